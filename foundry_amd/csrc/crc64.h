@@ -1,0 +1,136 @@
+// crc64.h -- CRC-64/XZ arithmetic for host and device.
+//
+// CRC-64/XZ is the code-object identity hash of the reference
+// (csrc/hook.cpp:315-321: width 64, poly 0x42F0E1EBA9EA3693, reflected in
+// and out, init and xorout all ones).  The restore path uses it for every
+// per-graph digest so that digests are checkable against any textbook
+// CRC-64/XZ implementation.
+//
+// Reflected representation: bit 63 holds the coefficient of x^0, so a
+// right shift multiplies by x.  Segments are combined with
+//   crc(A || B) = (crc(A) * x^(8|B|) mod P) xor crc(B)
+// (the method of zlib's crc32_combine, Adler 2011), which holds for raw
+// register values (init 0, no xorout) and for finished values alike.  For
+// fixed-size records the multipliers x^(8*S*2^k) are constants; device code
+// multiplies by them through 16 nibble tables per constant.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fdy {
+
+constexpr uint64_t kCrcPolyRefl = 0xC96C5795D7870F42ull;  // 0x42F0E1EBA9EA3693 bit-reversed
+constexpr uint64_t kX0 = 0x8000000000000000ull;           // the polynomial "1"
+
+// a * b mod P, reflected; 64 steps, branch-free in b.
+__host__ __device__ inline uint64_t gf2_mulmod(uint64_t a, uint64_t b) {
+  uint64_t p = 0;
+  for (int i = 0; i < 64; ++i) {
+    uint64_t bit = (a >> (63 - i)) & 1;
+    p ^= b & (0 - bit);
+    b = (b >> 1) ^ (kCrcPolyRefl & (0 - (b & 1)));
+  }
+  return p;
+}
+
+// x^(2^k) mod P for k = 0..63.
+struct X2nTable {
+  uint64_t v[64];
+};
+
+inline X2nTable make_x2n_table() {
+  X2nTable t;
+  uint64_t p = kX0 >> 1;  // x^1
+  for (int k = 0; k < 64; ++k) {
+    t.v[k] = p;
+    p = gf2_mulmod(p, p);
+  }
+  return t;
+}
+
+// x^(n * 2^k) mod P.
+__host__ __device__ inline uint64_t x2n_mod(const uint64_t* x2n, uint64_t n, unsigned k) {
+  uint64_t p = kX0;
+  while (n) {
+    if (n & 1) p = gf2_mulmod(x2n[k & 63], p);
+    n >>= 1;
+    ++k;
+  }
+  return p;
+}
+
+// Slicing-by-8 tables: t[0] is the byte table, t[k][i] = byte i followed by k zero bytes.
+struct SliceTables {
+  uint64_t t[8][256];
+};
+
+inline SliceTables make_slice_tables() {
+  SliceTables s;
+  for (int i = 0; i < 256; ++i) {
+    uint64_t c = (uint64_t)i;
+    for (int b = 0; b < 8; ++b) c = (c & 1) ? (c >> 1) ^ kCrcPolyRefl : c >> 1;
+    s.t[0][i] = c;
+  }
+  for (int k = 1; k < 8; ++k)
+    for (int i = 0; i < 256; ++i) s.t[k][i] = (s.t[k - 1][i] >> 8) ^ s.t[0][s.t[k - 1][i] & 0xFF];
+  return s;
+}
+
+// Register after absorbing 8 bytes (little-endian word w) into register c.
+__host__ __device__ inline uint64_t crc_slice8(const uint64_t (*t)[256], uint64_t c, uint64_t w) {
+  c ^= w;
+  return t[7][c & 0xFF] ^ t[6][(c >> 8) & 0xFF] ^ t[5][(c >> 16) & 0xFF] ^ t[4][(c >> 24) & 0xFF] ^
+         t[3][(c >> 32) & 0xFF] ^ t[2][(c >> 40) & 0xFF] ^ t[1][(c >> 48) & 0xFF] ^ t[0][c >> 56];
+}
+
+__host__ __device__ inline uint64_t crc_byte(const uint64_t* t0, uint64_t c, uint8_t b) {
+  return t0[(c ^ b) & 0xFF] ^ (c >> 8);
+}
+
+// Nibble tables for multiplying by a fixed constant X:
+//   z * X mod P = xor over i of tab[i][(z >> 4i) & 15]
+struct NibbleTable {
+  uint64_t t[16][16];
+};
+
+inline NibbleTable make_nibble_table(uint64_t X) {
+  NibbleTable n;
+  for (int i = 0; i < 16; ++i)
+    for (int v = 0; v < 16; ++v) n.t[i][v] = gf2_mulmod((uint64_t)v << (4 * i), X);
+  return n;
+}
+
+__host__ __device__ inline uint64_t nibble_mul(const uint64_t (*tab)[16], uint64_t z) {
+  uint64_t r = 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) r ^= tab[i][(z >> (4 * i)) & 15];
+  return r;
+}
+
+// Levels of the block combine tree: level k joins runs of 2^k records, so
+// its multiplier is x^(8 * S * 2^k); level 8 joins 256-record chunks.
+constexpr int kTreeLevels = 9;
+
+struct CrcConsts {
+  SliceTables slice;
+  NibbleTable rec8[kTreeLevels];   // S = 8-byte records (byte streams)
+  NibbleTable rec16[kTreeLevels];  // S = 16-byte records (node records)
+  X2nTable x2n;
+};
+
+inline void make_crc_consts(CrcConsts* c) {
+  c->slice = make_slice_tables();
+  c->x2n = make_x2n_table();
+  for (int k = 0; k < kTreeLevels; ++k) {
+    c->rec8[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)8 << k, 3));
+    c->rec16[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)16 << k, 3));
+  }
+}
+
+// Finish a raw CRC of an L-byte stream: crc = raw ^ (~0 * x^(8L)) ^ ~0.
+__host__ __device__ inline uint64_t crc_finish(const uint64_t* x2n, uint64_t raw, uint64_t len) {
+  return raw ^ gf2_mulmod(x2n_mod(x2n, len, 3), ~0ull) ^ ~0ull;
+}
+
+}  // namespace fdy

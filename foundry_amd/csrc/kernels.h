@@ -1,0 +1,66 @@
+// kernels.h -- launch wrappers for the restore kernels (kernels.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/foundry_restore.h"
+#include "restore_dev.h"
+
+namespace fdy {
+
+// Everything the restore kernels read or write for one archive.
+struct RestoreArgs {
+  const uint8_t* img;         // .cugraph images, each 256-B aligned
+  const DevGraph* graphs;
+  const CrcConsts* cc;
+  uint32_t num_graphs;
+  uint32_t num_slots;
+  uint16_t epoch;
+  uint64_t* digests;          // 4 per graph
+  const uint32_t* explicit_template;  // or null
+  uint32_t* template_of;
+  uint32_t* status;
+  uint32_t* gwords;
+  uint64_t* pbytes;           // param bytes per graph
+  uint8_t* node_flags;
+  NodeDesc* node_desc;
+  uint64_t* node_ptrs;        // 2 per node
+  uint32_t* tile_node;        // per slot
+  const uint32_t* slot_graph; // per slot
+  uint64_t* aux;              // ragged-word sources (per word)
+  uint64_t* image;            // relocated param images R
+  uint64_t* live;             // live images (template graphs)
+  uint32_t* live_src;         // per node
+  uint32_t* live_cur;         // per graph
+  fdy_override* ovr;
+  uint64_t* ovr_off;          // G+1
+  uint64_t* lookback;         // per slot
+  uint32_t* ticket;
+  RelocDev reloc;
+};
+
+hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_diff(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t v, hipStream_t s);
+
+struct SwitchArgs {
+  const fdy_override* ovr_cur;  // current graph's overrides
+  uint64_t n_cur;
+  const fdy_override* ovr_new;  // target graph's overrides
+  uint64_t n_new;
+  const uint64_t* tmpl_image;   // R of the template
+  uint64_t* live;               // live image of the template
+  const uint8_t* flags_new;     // node flags of the target
+  uint32_t* live_src;           // node sources of the template's group
+  uint32_t num_nodes;           // template's node count
+  uint32_t target;
+  uint32_t tmpl;
+};
+hipError_t launch_switch(const SwitchArgs& a, hipStream_t s);
+
+hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s);
+
+}  // namespace fdy

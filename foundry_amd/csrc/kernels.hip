@@ -1,0 +1,883 @@
+// kernels.hip -- the restore kernels for gfx950 (wave64, 160 KB LDS per CU).
+//
+//   k_hash    one workgroup per graph: CRC-64/XZ of the saved topology key and
+//             of the dependency table, as a block-wide segmented CRC (each
+//             lane absorbs one 8-byte record, lanes are joined by a combine
+//             tree whose multipliers are constants applied through nibble
+//             tables held in LDS).
+//   k_group   template_of[g] = lowest graph with the same key digest and length.
+//   k_node    one workgroup per graph: per node, the param layout, the compare
+//             against the template's node, memset/memcpy pointer relocation,
+//             node-type and kernel-entry digests, the node descriptors the
+//             diff pass consumes, and the diff-tile -> first-node table.
+//   k_diff    one workgroup per 4096-word tile of a graph's param image:
+//             coalesced 8-byte loads of the graph's and the template's words,
+//             relocation through an LDS-staged interval search, the relocated
+//             image store, and ballot + LDS prefix-sum compaction of the
+//             differing words; tiles are ordered by an atomic ticket and
+//             chained by a decoupled look-back so the override records land
+//             in canonical (graph, node, word) order in a single pass.
+//   k_switch  override scatter for one graph switch.
+//   k_reloc   streaming relocation of packed words.
+#include "kernels.h"
+
+namespace fdy {
+namespace {
+
+constexpr uint32_t kHashThreads = 256;
+constexpr uint32_t kNodeThreads = 256;
+constexpr uint32_t kGroupThreads = 1024;
+constexpr uint32_t kRelocThreads = 512;
+constexpr uint64_t kMask46 = (1ull << 46) - 1;
+
+__device__ inline uint64_t shfl_down64(uint64_t v, int d) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_down(lo, (unsigned)d, 64);
+  hi = __shfl_down(hi, (unsigned)d, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+__device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
+
+// Copy the slice tables and one family of combine multipliers into LDS.
+__device__ void stage_crc_tables(const CrcConsts* cc, bool rec16, uint64_t (*slice)[256],
+                                 uint64_t (*nib)[16][16]) {
+  const uint64_t* s = &cc->slice.t[0][0];
+  uint64_t* d = &slice[0][0];
+  for (uint32_t i = threadIdx.x; i < 8 * 256; i += blockDim.x) d[i] = s[i];
+  const uint64_t* ns = rec16 ? &cc->rec16[0].t[0][0] : &cc->rec8[0].t[0][0];
+  uint64_t* nd = &nib[0][0][0];
+  for (uint32_t i = threadIdx.x; i < kTreeLevels * 256; i += blockDim.x) nd[i] = ns[i];
+  __syncthreads();
+}
+
+// Join the raw CRCs of 256 consecutive records (one per thread, in thread
+// order) into the raw CRC of the whole run.  Valid in thread 0.
+__device__ uint64_t block_crc_combine(uint64_t z, const uint64_t (*nib)[16][16], uint64_t* s_wave) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int k = 0; k < 6; ++k) {
+    uint64_t o = shfl_down64(z, 1 << k);
+    uint64_t m = nibble_mul(nib[k], z) ^ o;
+    if ((lane & ((2u << k) - 1)) == 0) z = m;
+  }
+  if (lane == 0) s_wave[wave] = z;
+  __syncthreads();
+  uint64_t r = 0;
+  if (threadIdx.x == 0) {
+    r = s_wave[0];
+    for (uint32_t w = 1; w < blockDim.x / 64; ++w) r = nibble_mul(nib[6], r) ^ s_wave[w];
+  }
+  __syncthreads();
+  return r;
+}
+
+// The 8 bytes [b0, b0+8) of the L-byte stream at p (8-aligned), with bytes
+// outside [0, L) read as zero.
+__device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b0) {
+  const int64_t q = b0 >> 3;
+  const uint32_t sh = (uint32_t)(b0 & 7);
+  auto word = [&](int64_t qi) -> uint64_t {
+    if (qi < 0 || (uint64_t)qi * 8 >= L) return 0;
+    uint64_t v = *reinterpret_cast<const uint64_t*>(p + qi * 8);
+    uint64_t rem = L - (uint64_t)qi * 8;
+    if (rem < 8) v &= (1ull << (8 * rem)) - 1;
+    return v;
+  };
+  uint64_t w0 = word(q);
+  if (sh == 0) return w0;
+  return (w0 >> (8 * sh)) | (word(q + 1) << (64 - 8 * sh));
+}
+
+// CRC-64/XZ of an L-byte stream, front-padded with zeros to whole
+// 2048-byte chunks (leading zeros leave a zero-initialised register at
+// zero, and crc_finish adds the effect of the all-ones initial value).
+__device__ uint64_t block_crc_bytes(const uint8_t* p, uint64_t L, const uint64_t (*slice)[256],
+                                    const uint64_t (*nib)[16][16], const uint64_t* x2n, uint64_t* s_wave) {
+  constexpr uint64_t kChunk = kHashThreads * 8;
+  const uint64_t pad = (kChunk - L % kChunk) % kChunk;
+  const uint64_t nchunks = (L + pad) / kChunk;
+  uint64_t acc = 0;
+  for (uint64_t c = 0; c < nchunks; ++c) {
+    int64_t b0 = (int64_t)(c * kChunk + 8 * threadIdx.x) - (int64_t)pad;
+    uint64_t z = crc_slice8(slice, 0, stream_window(p, L, b0));
+    z = block_crc_combine(z, nib, s_wave);
+    if (threadIdx.x == 0) acc = nibble_mul(nib[8], acc) ^ z;
+  }
+  return threadIdx.x == 0 ? crc_finish(x2n, acc, L) : 0;
+}
+
+__global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
+  __shared__ uint64_t s_slice[8][256];
+  __shared__ uint64_t s_nib[kTreeLevels][16][16];
+  __shared__ uint64_t s_wave[kHashThreads / 64];
+  stage_crc_tables(a.cc, false, s_slice, s_nib);
+  const uint32_t g = blockIdx.x;
+  if (g == 0 && threadIdx.x == 0) *a.ticket = 0;
+  const DevGraph& G = a.graphs[g];
+  uint64_t dk = block_crc_bytes(a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY],
+                                s_slice, s_nib, a.cc->x2n.v, s_wave);
+  uint64_t de = block_crc_bytes(a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, s_slice, s_nib,
+                                a.cc->x2n.v, s_wave);
+  if (threadIdx.x == 0) {
+    a.digests[4ull * g + 0] = dk;
+    a.digests[4ull * g + 1] = de;
+  }
+}
+
+__global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
+  const uint32_t G = a.num_graphs;
+  if (a.explicit_template) {
+    for (uint32_t i = threadIdx.x; i < G; i += kGroupThreads) a.template_of[i] = a.explicit_template[i];
+    return;
+  }
+  constexpr uint32_t kChunk = 2048;
+  __shared__ uint64_t s_d[kChunk];
+  __shared__ uint64_t s_l[kChunk];
+  for (uint32_t i0 = 0; i0 < G; i0 += kGroupThreads) {
+    const uint32_t i = i0 + threadIdx.x;
+    const uint32_t lim = min(i0 + kGroupThreads, G);
+    uint64_t di = 0, li = 0;
+    if (i < G) {
+      di = a.digests[4ull * i];
+      li = a.graphs[i].sec_size[FDY_SEC_TOPOLOGY_KEY];
+    }
+    uint32_t found = 0xFFFFFFFFu;
+    for (uint32_t base = 0; base < lim; base += kChunk) {
+      __syncthreads();
+      const uint32_t end = min(base + kChunk, lim);
+      for (uint32_t j = base + threadIdx.x; j < end; j += kGroupThreads) {
+        s_d[j - base] = a.digests[4ull * j];
+        s_l[j - base] = a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY];
+      }
+      __syncthreads();
+      if (i < G && found == 0xFFFFFFFFu) {
+        const uint32_t stop = min(end, i + 1);
+        for (uint32_t j = base; j < stop; ++j) {
+          if (s_d[j - base] == di && s_l[j - base] == li) {
+            found = j;
+            break;
+          }
+        }
+      }
+    }
+    if (i < G) a.template_of[i] = found;
+  }
+}
+
+// ---- node pass ----------------------------------------------------------
+
+struct Side {
+  uint32_t words;
+  uint32_t num_params;
+  uint32_t arg_size;
+  bool bad, extra, ragged;
+  uint64_t src;        // absolute byte offset of the blob
+  const uint8_t* pidx; // param entries (per-param style)
+};
+
+__device__ Side kernel_side(const uint8_t* img, const DevGraph& G, const uint8_t* e) {
+  Side s{};
+  const uint32_t pio = ld_u32(e + FDY_KOFF_PARAM_INDEX), np = ld_u32(e + FDY_KOFF_NUM_PARAMS);
+  const uint32_t ao = ld_u32(e + FDY_KOFF_ARG_OFFSET), as = ld_u32(e + FDY_KOFF_ARG_SIZE);
+  const uint32_t no = ld_u32(e + FDY_KOFF_NAME_OFFSET), nl = ld_u32(e + FDY_KOFF_NAME_LENGTH);
+  bool bad = (uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS] ||
+             (uint64_t)pio + 8ull * np > G.sec_size[FDY_SEC_PARAM_INDEX];
+  s.extra = ao != FDY_NO_ARG_BUFFER;
+  s.num_params = np;
+  s.arg_size = as;
+  s.pidx = img + G.sec_off[FDY_SEC_PARAM_INDEX] + pio;
+  if (!bad && s.extra) {
+    bad = (uint64_t)ao + as > G.sec_size[FDY_SEC_ARG_DATA];
+    s.words = (as + 7) / 8;
+    s.src = G.sec_off[FDY_SEC_ARG_DATA] + ao;
+    s.ragged = (ao & 7) || (as & 7);
+  } else if (!bad) {
+    uint64_t prev = 0, words = 0;
+    for (uint32_t j = 0; j < np; ++j) {
+      const uint32_t o = ld_u32(s.pidx + 8ull * j), sz = ld_u32(s.pidx + 8ull * j + 4);
+      if ((uint64_t)o + sz > G.sec_size[FDY_SEC_PARAM_DATA]) {
+        bad = true;
+        break;
+      }
+      if (j == 0) {
+        s.src = G.sec_off[FDY_SEC_PARAM_DATA] + o;
+        prev = o;
+      }
+      if ((sz & 7) || (o & 7) || o != prev) s.ragged = true;
+      prev = (uint64_t)o + sz;
+      words += (sz + 7) / 8;
+    }
+    s.words = words > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)words;
+  }
+  if (bad) {
+    s.words = 0;
+    s.ragged = false;
+  }
+  s.bad = bad;
+  return s;
+}
+
+__device__ bool same_layout(const Side& a, const Side& b) {
+  if (a.bad || b.bad || a.extra != b.extra) return false;
+  if (a.extra) return a.arg_size == b.arg_size;
+  if (a.num_params != b.num_params) return false;
+  for (uint32_t j = 0; j < a.num_params; ++j)
+    if (ld_u32(a.pidx + 8ull * j + 4) != ld_u32(b.pidx + 8ull * j + 4)) return false;
+  return true;
+}
+
+// Effective launch attributes (csrc/CUDAGraphParallel.cpp:1211-1389): common
+// attrs, then per-node attrs when any are present, then required cluster dims.
+struct Attrs {
+  int32_t has_cluster, cx, cy, cz, has_pref, px, py, pz, sched, coop, prio, msd, has_map, map_def, map_remote,
+      has_carve, carve;
+};
+
+__device__ inline void attrs_from(const uint8_t* b, Attrs& a, bool merge) {
+  const uint32_t f = ld_u32(b);
+  if (f & FDY_KNA_CLUSTER_DIM) {
+    a.has_cluster = 1;
+    a.cx = (int32_t)ld_u32(b + 4);
+    a.cy = (int32_t)ld_u32(b + 8);
+    a.cz = (int32_t)ld_u32(b + 12);
+  }
+  if (f & FDY_KNA_PREFERRED_CLUSTER_DIM) {
+    a.has_pref = 1;
+    a.px = (int32_t)ld_u32(b + 16);
+    a.py = (int32_t)ld_u32(b + 20);
+    a.pz = (int32_t)ld_u32(b + 24);
+  }
+  // When merging per-node attrs over common ones, a negative value does not override.
+  auto take = [&](uint32_t flag, uint32_t off, int32_t& dst) {
+    if (!(f & flag)) return;
+    int32_t v = (int32_t)ld_u32(b + off);
+    if (!merge || v >= 0) dst = v;
+  };
+  take(FDY_KNA_CLUSTER_SCHEDULING, 28, a.sched);
+  take(FDY_KNA_COOPERATIVE, 32, a.coop);
+  take(FDY_KNA_PRIORITY, 36, a.prio);
+  take(FDY_KNA_MEM_SYNC_DOMAIN, 40, a.msd);
+  if (f & FDY_KNA_MEM_SYNC_DOMAIN_MAP) {
+    a.has_map = 1;
+    a.map_def = b[44];
+    a.map_remote = b[45];
+  }
+  if (f & FDY_KNA_SHARED_MEM_CARVEOUT) {
+    a.has_carve = 1;
+    a.carve = (int32_t)ld_u32(b + 48);
+  }
+}
+
+__device__ Attrs effective_attrs(const uint8_t* img, const DevGraph& G, const uint8_t* e) {
+  Attrs a{0, 0, 0, 0, 0, 0, 0, 0, -1, -1, -1, -1, 0, 0, 0, 0, 0};
+  if (G.flags & FDY_HAS_COMMON_ATTRS) attrs_from(img + G.sec_off[FDY_SEC_COMMON_ATTRS], a, false);
+  if (ld_u32(e + FDY_KOFF_KNA_FLAGS) != 0) attrs_from(e + FDY_KOFF_KNA_FLAGS, a, true);
+  const int32_t w = (int32_t)ld_u32(e + 64), h = (int32_t)ld_u32(e + 68), d = (int32_t)ld_u32(e + 72);
+  if (w > 0 || h > 0 || d > 0) {
+    a.has_cluster = 1;
+    a.cx = w > 0 ? w : 1;
+    a.cy = h > 0 ? h : 1;
+    a.cz = d > 0 ? d : 1;
+  }
+  return a;
+}
+
+__device__ bool attrs_equal(const Attrs& a, const Attrs& b) {
+  const int32_t* x = &a.has_cluster;
+  const int32_t* y = &b.has_cluster;
+  bool eq = true;
+  for (int i = 0; i < 17; ++i) eq &= x[i] == y[i];
+  return eq;
+}
+
+__device__ bool names_equal(const uint8_t* img, const DevGraph& A, const uint8_t* ea, const DevGraph& B,
+                            const uint8_t* eb, bool same_strings) {
+  const uint32_t ao = ld_u32(ea + FDY_KOFF_NAME_OFFSET), al = ld_u32(ea + FDY_KOFF_NAME_LENGTH);
+  const uint32_t bo = ld_u32(eb + FDY_KOFF_NAME_OFFSET), bl = ld_u32(eb + FDY_KOFF_NAME_LENGTH);
+  if (al != bl) return false;
+  if ((uint64_t)ao + al > A.sec_size[FDY_SEC_STRINGS] || (uint64_t)bo + bl > B.sec_size[FDY_SEC_STRINGS])
+    return false;
+  if (same_strings && ao == bo) return true;
+  const uint8_t* pa = img + A.sec_off[FDY_SEC_STRINGS] + ao;
+  const uint8_t* pb = img + B.sec_off[FDY_SEC_STRINGS] + bo;
+  for (uint32_t i = 0; i < al; ++i)
+    if (pa[i] != pb[i]) return false;
+  return true;
+}
+
+// CRC-64/XZ of a kernel's name.
+__device__ uint64_t name_crc(const uint8_t* img, const DevGraph& G, const uint8_t* e,
+                             const uint64_t (*slice)[256]) {
+  const uint32_t no = ld_u32(e + FDY_KOFF_NAME_OFFSET), nl = ld_u32(e + FDY_KOFF_NAME_LENGTH);
+  if ((uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS]) return 0;
+  const uint8_t* s = img + G.sec_off[FDY_SEC_STRINGS] + no;
+  uint64_t c = ~0ull;
+  uint32_t i = 0;
+  for (; i + 8 <= nl; i += 8) c = crc_slice8(slice, c, ld_u64(s + i));
+  for (; i < nl; ++i) c = crc_byte(slice[0], c, s[i]);
+  return ~c;
+}
+
+// Relocated memset dst / memcpy dst, src of node entry e (0 when not a pointer node).
+__device__ void node_pointers(const uint8_t* e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
+  const uint8_t type = e[FDY_NODE_OFF_TYPE];
+  const uint64_t* top = r.level[r.n_levels];
+  *p0 = 0;
+  *p1 = 0;
+  if (type == FDY_NODE_MEMSET) {
+    *p0 = reloc_word(r, top, ld_u64(e + FDY_MSOFF_DST));
+  } else if (type == FDY_NODE_MEMCPY) {
+    const uint64_t dst = ld_u64(e + FDY_MCOFF_DST), src = ld_u64(e + FDY_MCOFF_SRC);
+    const int32_t dt = (int32_t)ld_u32(e + FDY_MCOFF_DST_MEMTYPE), st = (int32_t)ld_u32(e + FDY_MCOFF_SRC_MEMTYPE);
+    *p0 = (dt == FDY_MEMTYPE_DEVICE || dt == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, top, dst) : dst;
+    *p1 = (st == FDY_MEMTYPE_DEVICE || st == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, top, src) : src;
+  }
+}
+
+__device__ bool u64_range_differs(const uint8_t* a, const uint8_t* b, uint32_t off, uint32_t n) {
+  bool d = false;
+  for (uint32_t i = 0; i < n; i += 8) d |= ld_u64(a + off + i) != ld_u64(b + off + i);
+  return d;
+}
+
+__device__ bool desc_differs(const uint8_t* img, const DevGraph& A, const uint8_t* ea, const DevGraph& B,
+                             const uint8_t* eb, bool same_strings, uint64_t pa0, uint64_t pa1, uint64_t pb0,
+                             uint64_t pb1) {
+  const uint8_t ta = ea[FDY_NODE_OFF_TYPE], tb = eb[FDY_NODE_OFF_TYPE];
+  if (ta != tb) return true;
+  switch (ta) {
+    case FDY_NODE_KERNEL: {
+      bool d = false;
+      for (uint32_t off = 8; off < 44; off += 4) d |= ld_u32(ea + off) != ld_u32(eb + off);
+      for (uint32_t off = 52; off < 76; off += 4) d |= ld_u32(ea + off) != ld_u32(eb + off);
+      if (d) return true;
+      if (!names_equal(img, A, ea, B, eb, same_strings)) return true;
+      return !attrs_equal(effective_attrs(img, A, ea), effective_attrs(img, B, eb));
+    }
+    case FDY_NODE_MEMSET:
+      return pa0 != pb0 || ld_u32(ea + 16) != ld_u32(eb + 16) || u64_range_differs(ea, eb, 24, 16) ||
+             ld_u32(ea + 40) != ld_u32(eb + 40) || ld_u64(ea + 48) != ld_u64(eb + 48);
+    case FDY_NODE_MEMCPY:
+      return pa0 != pb0 || pa1 != pb1 || u64_range_differs(ea, eb, 8, 24) || u64_range_differs(ea, eb, 40, 48) ||
+             ld_u32(ea + 88) != ld_u32(eb + 88) || u64_range_differs(ea, eb, 104, 48) ||
+             ld_u32(ea + 152) != ld_u32(eb + 152);
+    case FDY_NODE_EVENT_RECORD:
+    case FDY_NODE_EVENT_WAIT:
+      return ld_u32(ea + FDY_EVOFF_ID) != ld_u32(eb + FDY_EVOFF_ID);
+    default:
+      return false;
+  }
+}
+
+// Exclusive block-wide prefix sum of 256 u32 values; *total gets the sum.
+__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint32_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    uint32_t y = shfl_up32(x, d);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_tmp[wave] = x;
+  __syncthreads();
+  uint32_t before = 0, sum = 0;
+  for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
+    uint32_t t = s_tmp[w];
+    if (w < wave) before += t;
+    sum += t;
+  }
+  __syncthreads();
+  *total = sum;
+  return before + x - v;
+}
+
+__device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* e, const Side& s, uint64_t* aux,
+                          uint32_t gword) {
+  uint32_t idx = 0;
+  auto put = [&](uint64_t byte, uint32_t size) {
+    for (uint32_t m = 0; m < size; m += 8, ++idx) {
+      if ((uint64_t)gword + idx >= G.word_cap) return;
+      const uint32_t width = min(8u, size - m);
+      aux[G.word_base + gword + idx] = ((byte + m) << 4) | width;
+    }
+  };
+  if (s.extra) {
+    put(s.src, s.arg_size);
+  } else {
+    for (uint32_t j = 0; j < s.num_params; ++j)
+      put(G.sec_off[FDY_SEC_PARAM_DATA] + ld_u32(s.pidx + 8ull * j), ld_u32(s.pidx + 8ull * j + 4));
+  }
+  (void)img;
+  (void)e;
+}
+
+__global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
+  __shared__ uint64_t s_slice[8][256];
+  __shared__ uint64_t s_nib[kTreeLevels][16][16];
+  __shared__ uint64_t s_wave[kNodeThreads / 64];
+  __shared__ uint32_t s_tmp[kNodeThreads / 64];
+  __shared__ uint32_t s_status, s_key_differs, s_str_differs, s_words;
+  __shared__ unsigned long long s_pbytes;
+  stage_crc_tables(a.cc, true, s_slice, s_nib);
+
+  const uint32_t g = blockIdx.x;
+  const uint32_t t = a.template_of[g];
+  const bool is_t = t == g;
+  const DevGraph& Gg = a.graphs[g];
+  const DevGraph& Gt = a.graphs[t];
+  const uint32_t N = Gg.num_nodes, NT = Gt.num_nodes;
+  const uint8_t* img = a.img;
+
+  if (threadIdx.x == 0) {
+    s_status = 0;
+    s_key_differs = 0;
+    s_str_differs = 0;
+    s_pbytes = 0;
+  }
+  __syncthreads();
+  if (!is_t) {
+    // The template must carry the very same key bytes (digest collisions are
+    // reported, never silently merged).
+    const uint64_t L = Gg.sec_size[FDY_SEC_TOPOLOGY_KEY];
+    if (L != Gt.sec_size[FDY_SEC_TOPOLOGY_KEY]) {
+      if (threadIdx.x == 0) s_key_differs = 1;
+    } else {
+      const uint8_t* pg = img + Gg.sec_off[FDY_SEC_TOPOLOGY_KEY];
+      const uint8_t* pt = img + Gt.sec_off[FDY_SEC_TOPOLOGY_KEY];
+      for (uint64_t q = threadIdx.x; q * 8 < L; q += kNodeThreads)
+        if (stream_window(pg, L, (int64_t)q * 8) != stream_window(pt, L, (int64_t)q * 8)) s_key_differs = 1;
+    }
+    const uint64_t S = Gg.sec_size[FDY_SEC_STRINGS];
+    if (S != Gt.sec_size[FDY_SEC_STRINGS]) {
+      if (threadIdx.x == 0) s_str_differs = 1;
+    } else {
+      const uint8_t* pg = img + Gg.sec_off[FDY_SEC_STRINGS];
+      const uint8_t* pt = img + Gt.sec_off[FDY_SEC_STRINGS];
+      for (uint64_t q = threadIdx.x; q * 8 < S; q += kNodeThreads)
+        if (stream_window(pg, S, (int64_t)q * 8) != stream_window(pt, S, (int64_t)q * 8)) s_str_differs = 1;
+    }
+  }
+  __syncthreads();
+  const bool same_strings = !s_str_differs;
+  if (threadIdx.x == 0) {
+    if (s_key_differs) s_status |= FDY_GRAPH_COLLISION;
+    if (!is_t && N != NT) s_status |= kGraphNodeCount;
+  }
+
+  const uint32_t pad = (kNodeThreads - N % kNodeThreads) % kNodeThreads;
+  const uint32_t nchunks = (N + pad) / kNodeThreads;
+  uint32_t gcarry = 0, tcarry = 0;
+  uint64_t acc_type = 0, acc_kent = 0;
+  for (uint32_t c = 0; c < nchunks; ++c) {
+    const int64_t ns = (int64_t)c * kNodeThreads + threadIdx.x - pad;
+    const bool valid = ns >= 0 && ns < (int64_t)N;
+    const uint32_t n = valid ? (uint32_t)ns : 0;
+    uint32_t words_g = 0, words_t = 0, flags = 0;
+    uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0;
+    uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
+    Side sg{};
+    const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
+    if (valid) {
+      const uint8_t type = eg[FDY_NODE_OFF_TYPE];
+      tw0 = type;
+      if (type == FDY_NODE_KERNEL) {
+        // Cluster dims of the recomputed key (csrc/CUDAGraphParallel.cpp:1807-1833).
+        uint32_t cx = 0, cy = 0, cz = 0;
+        if (ld_u32(eg + FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
+          cx = ld_u32(eg + 80);
+          cy = ld_u32(eg + 84);
+          cz = ld_u32(eg + 88);
+        }
+        if (cx == 0 && (Gg.flags & FDY_HAS_COMMON_ATTRS)) {
+          const uint8_t* ca = img + Gg.sec_off[FDY_SEC_COMMON_ATTRS];
+          if (ld_u32(ca) & FDY_KNA_CLUSTER_DIM) {
+            cx = ld_u32(ca + 4);
+            cy = ld_u32(ca + 8);
+            cz = ld_u32(ca + 12);
+          }
+        }
+        if (cx == 0) {
+          cx = ld_u32(eg + 64);
+          cy = ld_u32(eg + 68);
+          cz = ld_u32(eg + 72);
+        }
+        tw0 |= (uint64_t)cx << 32;
+        tw1 = cy | ((uint64_t)cz << 32);
+        kw0 = ld_u64(eg + FDY_KOFF_BINARY_HASH);
+        kw1 = name_crc(img, Gg, eg, s_slice);
+        sg = kernel_side(img, Gg, eg);
+        words_g = sg.words;
+        if (!sg.bad) {
+          uint64_t pb = sg.extra ? sg.arg_size : 0;
+          if (!sg.extra)
+            for (uint32_t j = 0; j < sg.num_params; ++j) pb += ld_u32(sg.pidx + 8ull * j + 4);
+          if (pb) atomicAdd(&s_pbytes, (unsigned long long)pb);
+        }
+        src_g = sg.src;
+        if (sg.ragged) flags |= FDY_NODE_RAGGED;
+        if (sg.bad) flags |= kNodeBad;
+      }
+      node_pointers(eg, a.reloc, &p0, &p1);
+      if (is_t) {
+        flags |= FDY_NODE_TEMPLATE;
+      } else if (n < NT) {
+        const uint8_t* et = img + Gt.sec_off[FDY_SEC_NODES] + 168ull * n;
+        uint64_t q0, q1;
+        node_pointers(et, a.reloc, &q0, &q1);
+        bool layout = et[FDY_NODE_OFF_TYPE] != type;
+        if (et[FDY_NODE_OFF_TYPE] == FDY_NODE_KERNEL) {
+          const Side st = kernel_side(img, Gt, et);
+          words_t = st.words;
+          src_t = st.src;
+          if (st.ragged) flags |= kNodeRaggedT;
+          if (type == FDY_NODE_KERNEL) layout = !same_layout(sg, st);
+        }
+        if (layout) flags |= FDY_NODE_LAYOUT;
+        else if (words_g) flags |= kNodeCompare;
+        if (desc_differs(img, Gg, eg, Gt, et, same_strings, p0, p1, q0, q1)) flags |= FDY_NODE_DESC;
+      } else {
+        flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
+      }
+      if (flags & kNodeBad) atomicOr(&s_status, FDY_GRAPH_BAD_PARAMS);
+    }
+    uint32_t tot_g, tot_t;
+    const uint32_t gword = gcarry + block_excl_scan(words_g, s_tmp, &tot_g);
+    const uint32_t tword = tcarry + block_excl_scan(words_t, s_tmp, &tot_t);
+    // A template whose image overflows its capacity (overlapping param
+    // ranges) has no usable words past the capacity; never index them.
+    if ((flags & kNodeCompare) && (uint64_t)tword + words_t > Gt.word_cap) flags &= ~kNodeCompare;
+    if (valid) {
+      const uint64_t gi = Gg.node_base + n;
+      NodeDesc d;
+      d.gword = gword;
+      d.nwords = words_g;
+      d.tword = tword;
+      d.flags = flags;
+      d.src_g = src_g;
+      d.src_t = src_t;
+      a.node_desc[gi] = d;
+      a.node_flags[gi] = (uint8_t)(flags & 0x0F);
+      a.node_ptrs[2 * gi] = p0;
+      a.node_ptrs[2 * gi + 1] = p1;
+      if (is_t) a.live_src[gi] = g;
+      if (words_g) {
+        uint64_t k = ((uint64_t)gword + kTileWords - 1) / kTileWords;
+        const uint64_t k_last = ((uint64_t)gword + words_g - 1) / kTileWords;
+        for (; k <= k_last && k < Gg.tile_cap; ++k) a.tile_node[Gg.tile_base + k] = n;
+        if (flags & FDY_NODE_RAGGED) write_aux(img, Gg, eg, sg, a.aux, gword);
+      }
+    }
+    uint64_t zt = 0, zk = 0;
+    if (valid) {
+      zt = crc_slice8(s_slice, crc_slice8(s_slice, 0, tw0), tw1);
+      zk = crc_slice8(s_slice, crc_slice8(s_slice, 0, kw0), kw1);
+    }
+    zt = block_crc_combine(zt, s_nib, s_wave);
+    zk = block_crc_combine(zk, s_nib, s_wave);
+    if (threadIdx.x == 0) {
+      acc_type = nibble_mul(s_nib[8], acc_type) ^ zt;
+      acc_kent = nibble_mul(s_nib[8], acc_kent) ^ zk;
+    }
+    gcarry += tot_g;
+    tcarry += tot_t;
+  }
+  if (threadIdx.x == 0) {
+    const bool overflow = gcarry > Gg.word_cap;
+    s_words = overflow ? 0 : gcarry;
+    uint32_t st = s_status;
+    if (overflow) st |= FDY_GRAPH_BAD_PARAMS | kGraphOverflow;
+    a.status[g] = st;
+    a.gwords[g] = s_words;
+    a.pbytes[g] = s_pbytes;
+    a.digests[4ull * g + 2] = crc_finish(a.cc->x2n.v, acc_type, 16ull * N);
+    a.digests[4ull * g + 3] = crc_finish(a.cc->x2n.v, acc_kent, 16ull * N);
+    if (is_t) a.live_cur[g] = g;
+  }
+  __syncthreads();
+  const uint32_t first_unused = (s_words + kTileWords - 1) / kTileWords;
+  for (uint32_t k = first_unused + threadIdx.x; k < Gg.tile_cap; k += kNodeThreads)
+    a.tile_node[Gg.tile_base + k] = kNoTile;
+}
+
+// ---- diff pass ----------------------------------------------------------
+
+// The `width` bytes at byte offset `byte` of the image (any alignment).
+__device__ inline uint64_t load_bytes(const uint8_t* img, uint64_t byte, uint32_t width) {
+  const uint64_t a = byte & ~7ull;
+  const uint32_t sh = (uint32_t)(byte & 7);
+  uint64_t v = *reinterpret_cast<const uint64_t*>(img + a);
+  if (sh) {
+    v >>= 8 * sh;
+    if (sh + width > 8) v |= *reinterpret_cast<const uint64_t*>(img + a + 8) << (64 - 8 * sh);
+  }
+  return width >= 8 ? v : v & ((1ull << (8 * width)) - 1);
+}
+
+__device__ uint64_t lookback(uint64_t* lb, uint32_t slot, uint16_t epoch, uint64_t agg) {
+  const uint64_t ep = (uint64_t)epoch << 48;
+  if (slot == 0) {
+    __hip_atomic_store(&lb[0], ep | (2ull << 46) | (agg & kMask46), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return 0;
+  }
+  __hip_atomic_store(&lb[slot], ep | (1ull << 46) | (agg & kMask46), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint64_t excl = 0;
+  uint32_t p = slot - 1;
+  for (;;) {
+    const uint64_t s = __hip_atomic_load(&lb[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t flag = (s >> 46) & 3;
+    if ((s >> 48) != epoch || flag == 0) {
+      __builtin_amdgcn_s_sleep(1);
+      continue;
+    }
+    excl += s & kMask46;
+    if (flag == 2) break;
+    --p;
+  }
+  __hip_atomic_store(&lb[slot], ep | (2ull << 46) | ((excl + agg) & kMask46), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  return excl;
+}
+
+__global__ __launch_bounds__(kDiffThreads) void k_diff(RestoreArgs a) {
+  __shared__ NodeDesc s_nd[kDiffWindow];
+  __shared__ uint64_t s_top[kRelocLdsKeys];
+  __shared__ uint32_t s_cnt[kDiffWordsPerThread * (kDiffThreads / 64)];
+  __shared__ uint32_t s_slot, s_total;
+  __shared__ uint64_t s_excl;
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid == 0) s_slot = atomicAdd(a.ticket, 1u);
+  const RelocDev& R = a.reloc;
+  if (R.n)
+    for (uint32_t i = tid; i < R.n_top; i += kDiffThreads) s_top[i] = R.level[R.n_levels][i];
+  __syncthreads();
+  const uint32_t slot = s_slot;
+  const uint32_t g = a.slot_graph[slot];
+  const DevGraph& G = a.graphs[g];
+  const uint32_t t = a.template_of[g];
+  const DevGraph& T = a.graphs[t];
+  const bool is_t = t == g;
+  const uint32_t k = slot - G.tile_base;
+  const uint32_t n0 = a.tile_node[slot];
+  const bool active = n0 != kNoTile;
+  const uint32_t words = a.gwords[g];
+  const uint32_t N = G.num_nodes;
+  const uint32_t nwin = active ? min(kDiffWindow, N - n0) : 0;
+  const NodeDesc* nd = a.node_desc + G.node_base;
+  for (uint32_t i = tid; i < nwin; i += kDiffThreads) s_nd[i] = nd[n0 + i];
+  __syncthreads();
+
+  const uint64_t wbeg = (uint64_t)k * kTileWords;
+  uint32_t bits = 0;
+  uint64_t val[kDiffWordsPerThread];
+  uint32_t tw_of[kDiffWordsPerThread], node_of[kDiffWordsPerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
+    const uint64_t w = wbeg + (uint64_t)j * kDiffThreads + tid;
+    val[j] = 0;
+    tw_of[j] = 0;
+    node_of[j] = 0;
+    if (!active || w >= words) continue;
+    // Node holding word w: the last node whose first word is <= w.
+    uint32_t lo = 0, len = nwin;
+    while (len > 1) {
+      const uint32_t half = len >> 1;
+      if (s_nd[lo + half].gword <= w) lo += half;
+      len -= half;
+    }
+    NodeDesc d = s_nd[lo];
+    uint32_t node = n0 + lo;
+    if (lo == nwin - 1 && nwin == kDiffWindow && w >= (uint64_t)d.gword + d.nwords) {
+      uint32_t l2 = n0 + lo, h2 = N;  // beyond the staged window
+      while (h2 - l2 > 1) {
+        const uint32_t mid = (l2 + h2) >> 1;
+        if (nd[mid].gword <= w) l2 = mid;
+        else h2 = mid;
+      }
+      d = nd[l2];
+      node = l2;
+    }
+    const uint32_t off = (uint32_t)(w - d.gword);
+    uint64_t raw_g;
+    uint32_t width_g = 8;
+    if (d.flags & FDY_NODE_RAGGED) {
+      const uint64_t x = a.aux[G.word_base + w];
+      width_g = (uint32_t)(x & 15);
+      raw_g = load_bytes(a.img, x >> 4, width_g);
+    } else {
+      raw_g = *reinterpret_cast<const uint64_t*>(a.img + d.src_g + 8ull * off);
+    }
+    const uint64_t rg = width_g == 8 ? reloc_word(R, s_top, raw_g) : raw_g;
+    a.image[G.word_base + w] = rg;
+    if (is_t) a.live[G.word_base + w] = rg;
+    if (d.flags & kNodeCompare) {
+      const uint32_t tw = d.tword + off;
+      uint64_t raw_t;
+      uint32_t width_t = 8;
+      if (d.flags & kNodeRaggedT) {
+        const uint64_t x = a.aux[T.word_base + tw];
+        width_t = (uint32_t)(x & 15);
+        raw_t = load_bytes(a.img, x >> 4, width_t);
+      } else {
+        raw_t = *reinterpret_cast<const uint64_t*>(a.img + d.src_t + 8ull * off);
+      }
+      const uint64_t rt = (raw_t == raw_g && width_t == width_g) ? rg
+                          : (width_t == 8 ? reloc_word(R, s_top, raw_t) : raw_t);
+      if (rg != rt) {
+        bits |= 1u << j;
+        val[j] = rg;
+        tw_of[j] = tw;
+        node_of[j] = node;
+      }
+    }
+  }
+  // Compaction: records are ordered by (j, thread) = word order in the tile.
+#pragma unroll
+  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
+    const uint64_t m = __ballot((bits >> j) & 1);
+    if (lane == 0) s_cnt[j * (kDiffThreads / 64) + wave] = (uint32_t)__popcll(m);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const uint32_t v = s_cnt[lane];
+    uint32_t x = v;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const uint32_t y = shfl_up32(x, dd);
+      if (lane >= (uint32_t)dd) x += y;
+    }
+    s_cnt[lane] = x - v;
+    if (lane == 63) s_total = x;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const uint64_t excl = lookback(a.lookback, slot, a.epoch, s_total);
+    s_excl = excl;
+    if (k == 0) {
+      a.ovr_off[g] = excl;
+      if (!is_t && a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
+    }
+    if (slot == a.num_slots - 1) a.ovr_off[a.num_graphs] = excl + s_total;
+  }
+  __syncthreads();
+  const uint64_t base = s_excl;
+  const uint64_t lt = (1ull << lane) - 1;
+#pragma unroll
+  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
+    const uint64_t m = __ballot((bits >> j) & 1);
+    if ((bits >> j) & 1) {
+      const uint64_t pos = base + s_cnt[j * (kDiffThreads / 64) + wave] + (uint64_t)__popcll(m & lt);
+      fdy_override o;
+      o.word = tw_of[j];
+      o.node = node_of[j];
+      o.value = val[j];
+      a.ovr[pos] = o;
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void k_fill_u64(uint64_t* p, uint64_t n, uint64_t v) {
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) p[i] = v;
+}
+
+// ---- switch --------------------------------------------------------------
+
+__global__ __launch_bounds__(256) void k_switch(SwitchArgs a) {
+  const uint64_t total = a.n_cur + a.n_new;
+  const uint64_t lim = total > a.num_nodes ? total : a.num_nodes;
+  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < lim; i += (uint64_t)gridDim.x * 256) {
+    if (i < a.n_cur) {
+      const fdy_override r = a.ovr_cur[i];
+      uint64_t lo = 0, hi = a.n_new;  // does the target override this word too?
+      while (lo < hi) {
+        const uint64_t mid = (lo + hi) >> 1;
+        if (a.ovr_new[mid].word < r.word) lo = mid + 1;
+        else hi = mid;
+      }
+      if (lo == a.n_new || a.ovr_new[lo].word != r.word) a.live[r.word] = a.tmpl_image[r.word];
+    } else if (i < total) {
+      const fdy_override r = a.ovr_new[i - a.n_cur];
+      a.live[r.word] = r.value;
+    }
+    if (i < a.num_nodes)
+      a.live_src[i] = (a.flags_new[i] & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) ? a.target : a.tmpl;
+  }
+}
+
+// ---- standalone relocation ---------------------------------------------
+
+__global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint64_t* __restrict__ in,
+                                                         uint64_t* __restrict__ out, uint64_t n, int vec) {
+  __shared__ uint64_t s_top[kRelocLdsKeys];
+  if (R.n)
+    for (uint32_t i = threadIdx.x; i < R.n_top; i += kRelocThreads) s_top[i] = R.level[R.n_levels][i];
+  __syncthreads();
+  const uint64_t stride = (uint64_t)gridDim.x * kRelocThreads;
+  uint64_t i = (uint64_t)blockIdx.x * kRelocThreads + threadIdx.x;
+  if (vec) {
+    const uint64_t pairs = n / 2;
+    const ulonglong2* in2 = reinterpret_cast<const ulonglong2*>(in);
+    ulonglong2* out2 = reinterpret_cast<ulonglong2*>(out);
+    for (uint64_t p = i; p < pairs; p += stride) {
+      ulonglong2 v = in2[p];
+      v.x = reloc_word(R, s_top, v.x);
+      v.y = reloc_word(R, s_top, v.y);
+      out2[p] = v;
+    }
+    if (i == 0 && (n & 1)) out[n - 1] = reloc_word(R, s_top, in[n - 1]);
+  } else {
+    for (uint64_t p = i; p < n; p += stride) out[p] = reloc_word(R, s_top, in[p]);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_hash(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_hash, dim3(a.num_graphs), dim3(kHashThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(kGroupThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_node(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_node, dim3(a.num_graphs), dim3(kNodeThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_diff(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_diff, dim3(a.num_slots), dim3(kDiffThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t v, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  uint64_t blocks = (n + 255) / 256;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(k_fill_u64, dim3((uint32_t)blocks), dim3(256), 0, s, p, n, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_switch(const SwitchArgs& a, hipStream_t s) {
+  uint64_t lim = a.n_cur + a.n_new;
+  if (a.num_nodes > lim) lim = a.num_nodes;
+  if (lim == 0) return hipSuccess;
+  uint64_t blocks = (lim + 255) / 256;
+  if (blocks > 2048) blocks = 2048;
+  hipLaunchKernelGGL(k_switch, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const int vec = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  uint64_t per_block = (uint64_t)kRelocThreads * (vec ? 2 : 1);
+  uint64_t blocks = (n + per_block - 1) / per_block;
+  if (blocks > 256 * 16) blocks = 256 * 16;
+  hipLaunchKernelGGL(k_reloc, dim3((uint32_t)blocks), dim3(kRelocThreads), 0, s, r, in, out, n, vec);
+  return hipGetLastError();
+}
+
+}  // namespace fdy

@@ -1,0 +1,710 @@
+// restore.hip -- host side of the C ABI in include/foundry_restore.h.
+//
+// Host work is limited to what cannot run on the device: reading files,
+// validating section bounds (so device code never indexes outside an image),
+// sizing buffers, and enqueueing the kernels of kernels.hip.
+#include <hip/hip_runtime.h>
+#include <sys/stat.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/foundry_restore.h"
+#include "cugraph.h"
+#include "kernels.h"
+
+namespace fdy {
+namespace {
+
+thread_local std::string g_err;
+
+int err(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define FDY_HIP(call)                                                                                 \
+  do {                                                                                                \
+    hipError_t e_ = (call);                                                                           \
+    if (e_ != hipSuccess)                                                                             \
+      return err(FDY_E_HIP, std::string(#call) + " failed: " + hipGetErrorString(e_) + " (hipError_t " + \
+                                std::to_string((int)e_) + ")");                                       \
+  } while (0)
+
+template <typename F>
+void parallel_for(uint32_t n, uint32_t threads, F&& f) {
+  threads = std::max(1u, std::min(threads ? threads : 1u, std::max(1u, n)));
+  if (threads == 1) {
+    for (uint32_t i = 0; i < n; ++i) f(i);
+    return;
+  }
+  std::atomic<uint32_t> next{0};
+  std::vector<std::thread> pool;
+  for (uint32_t t = 0; t < threads; ++t)
+    pool.emplace_back([&] {
+      for (uint32_t i; (i = next.fetch_add(1)) < n;) f(i);
+    });
+  for (auto& t : pool) t.join();
+}
+
+uint32_t default_threads() { return std::max(1u, std::min(16u, std::thread::hardware_concurrency())); }
+
+// Device allocation owned by one archive or plan.
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+int dev_alloc(DevBuf& b, size_t bytes, const char* what) {
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(&b.p, bytes);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    return err(FDY_E_NOMEM, std::string("hipMalloc(") + std::to_string(bytes) + ") for " + what +
+                                " failed: " + hipGetErrorString(e));
+  }
+  b.bytes = bytes;
+  return FDY_OK;
+}
+
+// Host staging buffer: pinned when possible so the upload runs at full PCIe rate.
+struct HostStage {
+  uint8_t* p = nullptr;
+  bool pinned = false;
+  ~HostStage() {
+    if (!p) return;
+    if (pinned) (void)hipHostFree(p);
+    else std::free(p);
+  }
+  int alloc(size_t bytes) {
+    if (hipHostMalloc(reinterpret_cast<void**>(&p), bytes, hipHostMallocDefault) == hipSuccess) {
+      pinned = true;
+      return FDY_OK;
+    }
+    (void)hipGetLastError();
+    p = static_cast<uint8_t*>(std::malloc(bytes));
+    return p ? FDY_OK : err(FDY_E_NOMEM, "host staging buffer of " + std::to_string(bytes) + " bytes");
+  }
+};
+
+// The interval search structure: level 0 holds every interval's lo, each
+// higher level every 16th key of the level below, up to a top level small
+// enough for LDS.  Lower levels are padded with UINT64_MAX to whole nodes.
+struct RelocPlan {
+  DevBuf levels[8];
+  DevBuf hi, delta;
+  RelocDev dev{};
+};
+
+int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
+                     RelocPlan* out) {
+  std::memset(&out->dev, 0, sizeof(out->dev));
+  if (policy > FDY_RELOC_INCLUSIVE) return err(FDY_E_INVALID, "unknown relocation policy");
+  if (n == 0) return FDY_OK;
+  if (!lo || !hi || !nlo) return err(FDY_E_INVALID, "null interval array");
+  for (uint64_t i = 0; i < n; ++i) {
+    if (lo[i] >= hi[i]) return err(FDY_E_INVALID, "interval " + std::to_string(i) + " is empty (lo >= hi)");
+    if (hi[i] == UINT64_MAX) return err(FDY_E_INVALID, "interval " + std::to_string(i) + " ends at 2^64-1");
+    if (i && hi[i - 1] > lo[i])
+      return err(FDY_E_INVALID, "intervals " + std::to_string(i - 1) + " and " + std::to_string(i) +
+                                    " overlap or are not sorted by lo");
+  }
+  std::vector<std::vector<uint64_t>> lv;
+  lv.emplace_back(lo, lo + n);
+  while (lv.back().size() > kRelocLdsKeys) {
+    std::vector<uint64_t>& cur = lv.back();
+    std::vector<uint64_t> next;
+    for (size_t j = 0; j < cur.size(); j += kRelocFanout) next.push_back(cur[j]);
+    cur.resize((cur.size() + kRelocFanout - 1) / kRelocFanout * kRelocFanout, UINT64_MAX);
+    lv.push_back(std::move(next));
+    if (lv.size() > 8) return err(FDY_E_INVALID, "interval table too large");
+  }
+  for (size_t k = 0; k < lv.size(); ++k) {
+    int rc = dev_alloc(out->levels[k], lv[k].size() * 8, "interval search level");
+    if (rc) return rc;
+    FDY_HIP(hipMemcpy(out->levels[k].p, lv[k].data(), lv[k].size() * 8, hipMemcpyHostToDevice));
+    out->dev.level[k] = out->levels[k].as<uint64_t>();
+  }
+  std::vector<uint64_t> delta(n);
+  for (uint64_t i = 0; i < n; ++i) delta[i] = nlo[i] - lo[i];
+  int rc = dev_alloc(out->hi, n * 8, "interval hi");
+  if (!rc) rc = dev_alloc(out->delta, n * 8, "interval delta");
+  if (rc) return rc;
+  FDY_HIP(hipMemcpy(out->hi.p, hi, n * 8, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->delta.p, delta.data(), n * 8, hipMemcpyHostToDevice));
+  out->dev.hi = out->hi.as<uint64_t>();
+  out->dev.delta = out->delta.as<uint64_t>();
+  out->dev.n = n;
+  out->dev.lo_min = lo[0];
+  out->dev.hi_max = hi[n - 1];
+  out->dev.n_levels = (uint32_t)lv.size() - 1;
+  out->dev.n_top = (uint32_t)lv.back().size();
+  out->dev.policy = policy;
+  return FDY_OK;
+}
+
+uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
+
+}  // namespace
+}  // namespace fdy
+
+using namespace fdy;
+
+struct fdy_reloc_plan {
+  int device = 0;
+  RelocPlan plan;
+};
+
+struct fdy_archive {
+  int device = 0;
+  uint32_t G = 0;
+  std::vector<DevGraph> graphs;
+  uint64_t img_bytes = 0;
+  uint64_t total_nodes = 0;
+  uint64_t total_cap = 0;
+  uint32_t num_slots = 0;
+
+  DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
+  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, lookback, ticket, live_cur;
+  DevBuf aux, image, live, ovr, ovr_off;
+
+  RelocPlan reloc;
+  bool use_explicit = false;
+  uint16_t epoch = 0;
+  bool restored = false;
+
+  // Host copies taken after a restore (one synchronisation, then reused).
+  bool cached = false;
+  std::vector<uint32_t> h_tmpl, h_status, h_gwords;
+  std::vector<uint64_t> h_ovr_off, h_pbytes;
+  std::vector<uint32_t> h_current;
+
+  bool timing = false;
+  bool timed = false;
+  hipEvent_t ev[5] = {};
+
+  ~fdy_archive() {
+    for (hipEvent_t& e : ev)
+      if (e) (void)hipEventDestroy(e);
+  }
+};
+
+namespace {
+
+int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& off,
+                const std::vector<uint64_t>& sizes, const std::vector<std::string>& names) {
+  const uint32_t G = a->G;
+  a->graphs.resize(G);
+  std::vector<std::string> errs(G);
+  parallel_for(G, default_threads(), [&](uint32_t i) {
+    GraphView v;
+    errs[i] = validate_image(stage.p + off[i], sizes[i], &v);
+    if (!errs[i].empty()) return;
+    DevGraph& d = a->graphs[i];
+    std::memset(&d, 0, sizeof(d));
+    for (int s = 0; s < FDY_SEC_COUNT; ++s) {
+      d.sec_off[s] = off[i] + v.sec[s].offset;
+      d.sec_size[s] = v.sec[s].size;
+    }
+    d.num_nodes = v.hdr.num_nodes;
+    d.num_deps = v.hdr.num_deps;
+    d.flags = v.hdr.flags;
+    // Capacity of the param image: every param rounds up to whole words, and
+    // an extra-style node's arg buffer can end in a partial word.
+    uint64_t cap = (v.sec[FDY_SEC_PARAM_DATA].size + 7) / 8 + v.sec[FDY_SEC_PARAM_INDEX].size / 8 +
+                   (v.sec[FDY_SEC_ARG_DATA].size + 7) / 8 + v.hdr.num_nodes;
+    if (cap > 0xFFFFFFF0ull) {
+      errs[i] = "param image of more than 2^32 words";
+      return;
+    }
+    d.word_cap = (uint32_t)cap;
+  });
+  for (uint32_t i = 0; i < G; ++i)
+    if (!errs[i].empty()) return err(FDY_E_FORMAT, names[i] + ": " + errs[i]);
+
+  uint64_t nodes = 0, words = 0, slots = 0;
+  for (uint32_t i = 0; i < G; ++i) {
+    DevGraph& d = a->graphs[i];
+    d.node_base = nodes;
+    d.word_base = words;
+    d.tile_base = (uint32_t)slots;
+    d.tile_cap = (uint32_t)std::max<uint64_t>(1, (d.word_cap + kTileWords - 1) / kTileWords);
+    nodes += d.num_nodes;
+    words += d.word_cap;
+    slots += d.tile_cap;
+  }
+  if (slots > 0xFFFFFFF0ull) return err(FDY_E_FORMAT, "archive too large (diff tiles exceed 2^32)");
+  a->total_nodes = nodes;
+  a->total_cap = words;
+  a->num_slots = (uint32_t)slots;
+
+  std::vector<uint32_t> slot_graph(slots);
+  for (uint32_t i = 0; i < G; ++i)
+    std::fill(slot_graph.begin() + a->graphs[i].tile_base,
+              slot_graph.begin() + a->graphs[i].tile_base + a->graphs[i].tile_cap, i);
+
+  int rc = 0;
+  auto alloc = [&](DevBuf& b, size_t bytes, const char* what) {
+    if (!rc) rc = dev_alloc(b, bytes, what);
+  };
+  alloc(a->img, a->img_bytes + 4096, "archive images");
+  alloc(a->dgraphs, G * sizeof(DevGraph), "graph table");
+  alloc(a->cc, sizeof(CrcConsts), "CRC tables");
+  alloc(a->digests, 32ull * G, "digests");
+  alloc(a->tmpl, 4ull * G, "template_of");
+  alloc(a->explicit_tmpl, 4ull * G, "explicit groups");
+  alloc(a->status, 4ull * G, "status");
+  alloc(a->gwords, 4ull * G, "image words");
+  alloc(a->pbytes, 8ull * G, "param bytes");
+  alloc(a->live_cur, 4ull * G, "live current");
+  alloc(a->nflags, nodes, "node flags");
+  alloc(a->ndesc, nodes * sizeof(NodeDesc), "node descriptors");
+  alloc(a->nptrs, 16 * nodes, "node pointers");
+  alloc(a->live_src, 4 * nodes, "live node sources");
+  alloc(a->tile_node, 4 * slots, "tile table");
+  alloc(a->slot_graph, 4 * slots, "slot table");
+  alloc(a->lookback, 8 * slots, "look-back state");
+  alloc(a->ticket, 256, "tile ticket");
+  alloc(a->aux, 8 * words, "ragged word sources");
+  alloc(a->image, 8 * words, "param images");
+  alloc(a->live, 8 * words, "live images");
+  alloc(a->ovr, sizeof(fdy_override) * words, "override records");
+  alloc(a->ovr_off, 8ull * (G + 1), "override offsets");
+  if (rc) return rc;
+
+  FDY_HIP(hipMemcpy(a->img.p, stage.p, a->img_bytes, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemset(static_cast<uint8_t*>(a->img.p) + a->img_bytes, 0, 4096));
+  FDY_HIP(hipMemcpy(a->dgraphs.p, a->graphs.data(), G * sizeof(DevGraph), hipMemcpyHostToDevice));
+  auto consts = std::make_unique<CrcConsts>();
+  make_crc_consts(consts.get());
+  FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(a->slot_graph.p, slot_graph.data(), 4 * slots, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemset(a->lookback.p, 0, 8 * slots));
+  FDY_HIP(hipMemset(a->ticket.p, 0, 256));
+  return FDY_OK;
+}
+
+int ensure_cache(fdy_archive* a, hipStream_t s) {
+  if (!a->restored) return err(FDY_E_STATE, "call fdy_restore first");
+  if (a->cached) return FDY_OK;
+  FDY_HIP(hipStreamSynchronize(s));
+  const uint32_t G = a->G;
+  a->h_tmpl.resize(G);
+  a->h_status.resize(G);
+  a->h_gwords.resize(G);
+  a->h_pbytes.resize(G);
+  a->h_ovr_off.resize(G + 1);
+  FDY_HIP(hipMemcpy(a->h_tmpl.data(), a->tmpl.p, 4ull * G, hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(a->h_status.data(), a->status.p, 4ull * G, hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(a->h_gwords.data(), a->gwords.p, 4ull * G, hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(a->h_pbytes.data(), a->pbytes.p, 8ull * G, hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(a->h_ovr_off.data(), a->ovr_off.p, 8ull * (G + 1), hipMemcpyDeviceToHost));
+  a->h_current.resize(G);
+  for (uint32_t i = 0; i < G; ++i) a->h_current[i] = i;
+  a->cached = true;
+  return FDY_OK;
+}
+
+int check_graph(const fdy_archive* a, uint32_t g) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  if (g >= a->G) return err(FDY_E_RANGE, "graph " + std::to_string(g) + " out of range (num_graphs=" +
+                                             std::to_string(a->G) + ")");
+  return FDY_OK;
+}
+
+template <typename T>
+int copy_out(const void* dev, uint64_t n, T* out, uint64_t cap, uint64_t* n_out) {
+  if (n_out) *n_out = n;
+  if (!out) return FDY_OK;
+  if (cap < n) return err(FDY_E_CAPACITY, "output array holds " + std::to_string(cap) + ", needs " + std::to_string(n));
+  if (n) FDY_HIP(hipMemcpy(out, dev, n * sizeof(T), hipMemcpyDeviceToHost));
+  return FDY_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fdy_last_error(void) { return g_err.c_str(); }
+const char* fdy_version(void) { return "foundry-mi355x restore 0.1 (gfx950)"; }
+
+int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads, fdy_archive** out) {
+  if (!paths || !out || n == 0) return err(FDY_E_INVALID, "need at least one path and an output pointer");
+  *out = nullptr;
+  std::vector<std::string> names(n);
+  std::vector<uint64_t> sizes(n), off(n);
+  uint64_t at = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    std::string p = paths[i] ? paths[i] : "";
+    if (p.size() >= 5 && p.compare(p.size() - 5, 5, ".json") == 0) p = p.substr(0, p.size() - 5) + ".cugraph";
+    struct stat st;
+    if (p.empty() || stat(p.c_str(), &st) != 0 || !S_ISREG(st.st_mode))
+      return err(FDY_E_IO, "cannot open " + (p.empty() ? std::string("<null path>") : p));
+    names[i] = p;
+    sizes[i] = (uint64_t)st.st_size;
+    off[i] = at;
+    at = align_up(at + sizes[i], 256);
+  }
+  auto a = std::make_unique<fdy_archive>();
+  (void)hipGetDevice(&a->device);
+  a->G = n;
+  a->img_bytes = at;
+  HostStage stage;
+  int rc = stage.alloc(at ? at : 256);
+  if (rc) return rc;
+  std::vector<std::string> errs(n);
+  // Phase 1a: parallel reads (csrc/CUDAGraphParallel.cpp:1583-1620), straight into the staging buffer.
+  parallel_for(n, std::min(num_threads ? num_threads : 4u, n), [&](uint32_t i) {
+    FILE* f = std::fopen(names[i].c_str(), "rb");
+    if (!f) {
+      errs[i] = "cannot open";
+      return;
+    }
+    size_t got = std::fread(stage.p + off[i], 1, sizes[i], f);
+    std::fclose(f);
+    if (got != sizes[i]) errs[i] = "short read";
+    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
+  });
+  for (uint32_t i = 0; i < n; ++i)
+    if (!errs[i].empty()) return err(FDY_E_IO, names[i] + ": " + errs[i]);
+  rc = finish_open(a.get(), stage, off, sizes, names);
+  if (rc) return rc;
+  *out = a.release();
+  return FDY_OK;
+}
+
+int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes_in, uint32_t n, fdy_archive** out) {
+  if (!images || !sizes_in || !out || n == 0) return err(FDY_E_INVALID, "need at least one image and an output pointer");
+  *out = nullptr;
+  std::vector<std::string> names(n);
+  std::vector<uint64_t> sizes(sizes_in, sizes_in + n), off(n);
+  uint64_t at = 0;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!images[i] && sizes[i]) return err(FDY_E_INVALID, "null image " + std::to_string(i));
+    names[i] = "image " + std::to_string(i);
+    off[i] = at;
+    at = align_up(at + sizes[i], 256);
+  }
+  auto a = std::make_unique<fdy_archive>();
+  (void)hipGetDevice(&a->device);
+  a->G = n;
+  a->img_bytes = at;
+  HostStage stage;
+  int rc = stage.alloc(at ? at : 256);
+  if (rc) return rc;
+  parallel_for(n, default_threads(), [&](uint32_t i) {
+    if (sizes[i]) std::memcpy(stage.p + off[i], images[i], sizes[i]);
+    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
+  });
+  rc = finish_open(a.get(), stage, off, sizes, names);
+  if (rc) return rc;
+  *out = a.release();
+  return FDY_OK;
+}
+
+int fdy_archive_close(fdy_archive* a) {
+  if (!a) return FDY_OK;
+  (void)hipSetDevice(a->device);
+  (void)hipDeviceSynchronize();
+  delete a;
+  return FDY_OK;
+}
+
+int fdy_archive_info_get(const fdy_archive* a, fdy_archive_info* o) {
+  if (!a || !o) return err(FDY_E_INVALID, "null argument");
+  std::memset(o, 0, sizeof(*o));
+  o->num_graphs = a->G;
+  o->total_nodes = a->total_nodes;
+  o->file_bytes = a->img_bytes;
+  o->num_intervals = a->reloc.dev.n;
+  if (a->cached) {
+    for (uint32_t i = 0; i < a->G; ++i) {
+      o->num_groups += a->h_tmpl[i] == i;
+      o->total_words += a->h_gwords[i];
+      o->total_param_bytes += a->h_pbytes[i];
+    }
+    o->total_overrides = a->h_ovr_off[a->G];
+  }
+  return FDY_OK;
+}
+
+int fdy_archive_set_relocation(fdy_archive* a, const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo,
+                               uint64_t n, uint32_t policy) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  FDY_HIP(hipSetDevice(a->device));
+  FDY_HIP(hipDeviceSynchronize());  // kernels in flight may still read the old table
+  a->reloc.~RelocPlan();
+  new (&a->reloc) RelocPlan();
+  return build_reloc_plan(lo, hi, nlo, n, policy, &a->reloc);
+}
+
+int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  if (!template_of) {
+    a->use_explicit = false;
+    return FDY_OK;
+  }
+  for (uint32_t i = 0; i < a->G; ++i) {
+    const uint32_t t = template_of[i];
+    if (t >= a->G) return err(FDY_E_RANGE, "template_of[" + std::to_string(i) + "] out of range");
+    if (template_of[t] != t)
+      return err(FDY_E_INVALID, "template_of[" + std::to_string(i) + "] = " + std::to_string(t) +
+                                    " is not a template itself");
+  }
+  FDY_HIP(hipSetDevice(a->device));
+  FDY_HIP(hipMemcpy(a->explicit_tmpl.p, template_of, 4ull * a->G, hipMemcpyHostToDevice));
+  a->use_explicit = true;
+  return FDY_OK;
+}
+
+int fdy_restore(fdy_archive* a, void* stream) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  FDY_HIP(hipSetDevice(a->device));
+  if (++a->epoch == 0) {  // 16-bit epochs wrapped: clear stale look-back words
+    FDY_HIP(launch_fill_u64(a->lookback.as<uint64_t>(), a->num_slots, 0, s));
+    a->epoch = 1;
+  }
+  RestoreArgs r{};
+  r.img = a->img.as<uint8_t>();
+  r.graphs = a->dgraphs.as<DevGraph>();
+  r.cc = a->cc.as<CrcConsts>();
+  r.num_graphs = a->G;
+  r.num_slots = a->num_slots;
+  r.epoch = a->epoch;
+  r.digests = a->digests.as<uint64_t>();
+  r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
+  r.template_of = a->tmpl.as<uint32_t>();
+  r.status = a->status.as<uint32_t>();
+  r.gwords = a->gwords.as<uint32_t>();
+  r.pbytes = a->pbytes.as<uint64_t>();
+  r.node_flags = a->nflags.as<uint8_t>();
+  r.node_desc = a->ndesc.as<NodeDesc>();
+  r.node_ptrs = a->nptrs.as<uint64_t>();
+  r.tile_node = a->tile_node.as<uint32_t>();
+  r.slot_graph = a->slot_graph.as<uint32_t>();
+  r.aux = a->aux.as<uint64_t>();
+  r.image = a->image.as<uint64_t>();
+  r.live = a->live.as<uint64_t>();
+  r.live_src = a->live_src.as<uint32_t>();
+  r.live_cur = a->live_cur.as<uint32_t>();
+  r.ovr = a->ovr.as<fdy_override>();
+  r.ovr_off = a->ovr_off.as<uint64_t>();
+  r.lookback = a->lookback.as<uint64_t>();
+  r.ticket = a->ticket.as<uint32_t>();
+  r.reloc = a->reloc.dev;
+  if (a->timing) {
+    for (hipEvent_t& e : a->ev)
+      if (!e) FDY_HIP(hipEventCreate(&e));
+    FDY_HIP(hipEventRecord(a->ev[0], s));
+  }
+  FDY_HIP(launch_hash(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
+  FDY_HIP(launch_group(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
+  FDY_HIP(launch_node(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
+  FDY_HIP(launch_diff(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
+  a->timed = a->timing;
+  a->restored = true;
+  a->cached = false;
+  return FDY_OK;
+}
+
+int fdy_set_timing(fdy_archive* a, int enabled) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  a->timing = enabled != 0;
+  return FDY_OK;
+}
+
+int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
+  if (!a || !o) return err(FDY_E_INVALID, "null argument");
+  if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
+  FDY_HIP(hipEventSynchronize(a->ev[4]));
+  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
+  FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
+  FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
+  FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[3], a->ev[4]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[4]));
+  return FDY_OK;
+}
+
+int fdy_get_digests(fdy_archive* a, void* stream, uint64_t* out) {
+  if (!a || !out) return err(FDY_E_INVALID, "null argument");
+  int rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  FDY_HIP(hipMemcpy(out, a->digests.p, 32ull * a->G, hipMemcpyDeviceToHost));
+  return FDY_OK;
+}
+
+int fdy_get_groups(fdy_archive* a, void* stream, uint32_t* out) {
+  if (!a || !out) return err(FDY_E_INVALID, "null argument");
+  int rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  std::memcpy(out, a->h_tmpl.data(), 4ull * a->G);
+  return FDY_OK;
+}
+
+int fdy_get_graph_status(fdy_archive* a, void* stream, uint32_t* out) {
+  if (!a || !out) return err(FDY_E_INVALID, "null argument");
+  int rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  // TYPE_MISMATCH is set by the diff pass after the cache may have been taken.
+  FDY_HIP(hipMemcpy(a->h_status.data(), a->status.p, 4ull * a->G, hipMemcpyDeviceToHost));
+  std::memcpy(out, a->h_status.data(), 4ull * a->G);
+  return FDY_OK;
+}
+
+int fdy_get_override_offsets(fdy_archive* a, void* stream, uint64_t* out) {
+  if (!a || !out) return err(FDY_E_INVALID, "null argument");
+  int rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  std::memcpy(out, a->h_ovr_off.data(), 8ull * (a->G + 1));
+  return FDY_OK;
+}
+
+int fdy_get_param_bytes(fdy_archive* a, void* stream, uint64_t* out) {
+  if (!a || !out) return err(FDY_E_INVALID, "null argument");
+  int rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  std::memcpy(out, a->h_pbytes.data(), 8ull * a->G);
+  return FDY_OK;
+}
+
+int fdy_get_overrides(fdy_archive* a, void* stream, uint32_t g, fdy_override* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  const uint64_t b = a->h_ovr_off[g], n = a->h_ovr_off[g + 1] - b;
+  return copy_out(a->ovr.as<fdy_override>() + b, n, out, cap, n_out);
+}
+
+int fdy_get_node_flags(fdy_archive* a, void* stream, uint32_t g, uint8_t* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  return copy_out(a->nflags.as<uint8_t>() + a->graphs[g].node_base, a->graphs[g].num_nodes, out, cap, n_out);
+}
+
+int fdy_get_node_words(fdy_archive* a, void* stream, uint32_t g, uint32_t* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  const uint32_t N = a->graphs[g].num_nodes;
+  if (n_out) *n_out = N + 1ull;
+  if (!out) return FDY_OK;
+  if (cap < N + 1ull) return err(FDY_E_CAPACITY, "output array too small for N+1 word offsets");
+  std::vector<NodeDesc> d(N);
+  if (N) FDY_HIP(hipMemcpy(d.data(), a->ndesc.as<NodeDesc>() + a->graphs[g].node_base, N * sizeof(NodeDesc),
+                           hipMemcpyDeviceToHost));
+  for (uint32_t i = 0; i < N; ++i) out[i] = d[i].gword;
+  out[N] = a->h_gwords[g];
+  return FDY_OK;
+}
+
+int fdy_get_param_image(fdy_archive* a, void* stream, uint32_t g, uint64_t* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  return copy_out(a->image.as<uint64_t>() + a->graphs[g].word_base, a->h_gwords[g], out, cap, n_out);
+}
+
+int fdy_get_node_pointers(fdy_archive* a, void* stream, uint32_t g, uint64_t* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  return copy_out(a->nptrs.as<uint64_t>() + 2 * a->graphs[g].node_base, 2ull * a->graphs[g].num_nodes, out, cap,
+                  n_out);
+}
+
+int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, s);
+  if (rc) return rc;
+  const uint32_t t = a->h_tmpl[g];
+  if (a->h_status[g] & (FDY_GRAPH_NODE_COUNT | FDY_GRAPH_OVERFLOW))
+    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has " + std::to_string(a->graphs[g].num_nodes) +
+                                   " nodes but its template " + std::to_string(t) + " has " +
+                                   std::to_string(a->graphs[t].num_nodes));
+  const uint32_t c = a->h_current[t];
+  if (c == g) return FDY_OK;
+  FDY_HIP(hipSetDevice(a->device));
+  SwitchArgs w{};
+  w.ovr_cur = a->ovr.as<fdy_override>() + a->h_ovr_off[c];
+  w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
+  w.ovr_new = a->ovr.as<fdy_override>() + a->h_ovr_off[g];
+  w.n_new = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
+  w.tmpl_image = a->image.as<uint64_t>() + a->graphs[t].word_base;
+  w.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
+  w.flags_new = a->nflags.as<uint8_t>() + a->graphs[g].node_base;
+  w.live_src = a->live_src.as<uint32_t>() + a->graphs[t].node_base;
+  w.num_nodes = a->graphs[t].num_nodes;
+  w.target = g;
+  w.tmpl = t;
+  FDY_HIP(launch_switch(w, s));
+  a->h_current[t] = g;
+  return FDY_OK;
+}
+
+int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint64_t cap, uint32_t* node_src,
+                 uint64_t node_cap, uint32_t* current) {
+  int rc = check_graph(a, t);
+  if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
+  if (rc) return rc;
+  if (a->h_tmpl[t] != t) return err(FDY_E_INVALID, "graph " + std::to_string(t) + " is not a template");
+  FDY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
+  rc = copy_out(a->live.as<uint64_t>() + a->graphs[t].word_base, a->h_gwords[t], words, cap, nullptr);
+  if (!rc) rc = copy_out(a->live_src.as<uint32_t>() + a->graphs[t].node_base, a->graphs[t].num_nodes, node_src,
+                         node_cap, nullptr);
+  if (rc) return rc;
+  if (current) *current = a->h_current[t];
+  return FDY_OK;
+}
+
+int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
+                          fdy_reloc_plan** out) {
+  if (!out) return err(FDY_E_INVALID, "null output");
+  auto p = std::make_unique<fdy_reloc_plan>();
+  (void)hipGetDevice(&p->device);
+  int rc = build_reloc_plan(lo, hi, nlo, n, policy, &p->plan);
+  if (rc) return rc;
+  *out = p.release();
+  return FDY_OK;
+}
+
+int fdy_reloc_plan_destroy(fdy_reloc_plan* p) {
+  if (p) {
+    (void)hipSetDevice(p->device);
+    (void)hipDeviceSynchronize();
+  }
+  delete p;
+  return FDY_OK;
+}
+
+int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* in, uint64_t* out, uint64_t n, void* stream) {
+  if (!p || (!in && n) || (!out && n)) return err(FDY_E_INVALID, "null argument");
+  if (((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 7) != 0)
+    return err(FDY_E_INVALID, "word arrays must be 8-byte aligned");
+  FDY_HIP(launch_reloc_words(p->plan.dev, in, out, n, static_cast<hipStream_t>(stream)));
+  return FDY_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,244 @@
+"""Python view of the restore C ABI (include/foundry_restore.h).
+
+Every method is a thin wrapper over one `fdy_*` entry point; results come
+back as numpy arrays.  `stream` arguments accept a torch.cuda.Stream, a raw
+hipStream_t integer, or None for the null stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from typing import Sequence
+
+import numpy as np
+
+from . import _lib
+from ._lib import ArchiveInfo, Override, RestoreTiming, check, restore_lib
+
+OVERRIDE_DTYPE = np.dtype([("word", "<u4"), ("node", "<u4"), ("value", "<u8")])
+
+
+def _stream(s) -> C.c_void_p:
+    if s is None:
+        return C.c_void_p(0)
+    if isinstance(s, int):
+        return C.c_void_p(s)
+    return C.c_void_p(int(s.cuda_stream))
+
+
+def _u64(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
+
+
+class Archive:
+    """A set of `.cugraph` archives resident in HBM, and their restore state."""
+
+    def __init__(self, handle: C.c_void_p, keepalive=None):
+        self._h = handle
+        self._keep = keepalive
+
+    # ---- opening ---------------------------------------------------------
+    @classmethod
+    def open(cls, paths: Sequence[str], num_threads: int = 4) -> "Archive":
+        arr = (C.c_char_p * len(paths))(*[p.encode() for p in paths])
+        h = C.c_void_p()
+        check(restore_lib().fdy_archive_open(arr, len(paths), num_threads, C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_images(cls, images: Sequence[bytes]) -> "Archive":
+        bufs = [C.create_string_buffer(b, len(b)) if len(b) else C.create_string_buffer(1) for b in images]
+        ptrs = (_lib.u8p * len(images))(*[C.cast(b, _lib.u8p) for b in bufs])
+        sizes = (C.c_uint64 * len(images))(*[len(b) for b in images])
+        h = C.c_void_p()
+        check(restore_lib().fdy_archive_open_images(ptrs, sizes, len(images), C.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def from_synth(cls, synth) -> "Archive":
+        n = synth.num_graphs
+        addrs = [synth.image_ptr(i) for i in range(n)]
+        ptrs = (_lib.u8p * n)(*[C.cast(C.c_void_p(a), _lib.u8p) for a, _ in addrs])
+        sizes = (C.c_uint64 * n)(*[s for _, s in addrs])
+        h = C.c_void_p()
+        check(restore_lib().fdy_archive_open_images(ptrs, sizes, n, C.byref(h)))
+        return cls(h)
+
+    def close(self) -> None:
+        if self._h:
+            check(restore_lib().fdy_archive_close(self._h))
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- configuration ---------------------------------------------------
+    def set_relocation(self, lo, hi, new_lo, policy: int = _lib.RELOC_HALF_OPEN) -> None:
+        lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+        self._reloc_keep = (lo, hi, new_lo)
+        check(
+            restore_lib().fdy_archive_set_relocation(
+                self._h,
+                lo.ctypes.data_as(_lib.u64p),
+                hi.ctypes.data_as(_lib.u64p),
+                new_lo.ctypes.data_as(_lib.u64p),
+                len(lo),
+                policy,
+            )
+        )
+
+    def set_groups(self, template_of) -> None:
+        if template_of is None:
+            check(restore_lib().fdy_archive_set_groups(self._h, None))
+            return
+        t = np.ascontiguousarray(np.asarray(template_of, dtype=np.uint32))
+        check(restore_lib().fdy_archive_set_groups(self._h, t.ctypes.data_as(_lib.u32p)))
+
+    def set_timing(self, enabled: bool = True) -> None:
+        check(restore_lib().fdy_set_timing(self._h, 1 if enabled else 0))
+
+    # ---- the restore -----------------------------------------------------
+    def restore(self, stream=None) -> None:
+        check(restore_lib().fdy_restore(self._h, _stream(stream)))
+
+    def timing(self) -> dict:
+        t = RestoreTiming()
+        check(restore_lib().fdy_restore_timing_get(self._h, C.byref(t)))
+        return {k: getattr(t, k) for k, _ in RestoreTiming._fields_}
+
+    def info(self) -> dict:
+        i = ArchiveInfo()
+        check(restore_lib().fdy_archive_info_get(self._h, C.byref(i)))
+        return {k: getattr(i, k) for k, _ in ArchiveInfo._fields_}
+
+    @property
+    def num_graphs(self) -> int:
+        return self.info()["num_graphs"]
+
+    def digests(self, stream=None) -> np.ndarray:
+        out = np.zeros((self.num_graphs, 4), dtype=np.uint64)
+        check(restore_lib().fdy_get_digests(self._h, _stream(stream), out.ctypes.data_as(_lib.u64p)))
+        return out
+
+    def groups(self, stream=None) -> np.ndarray:
+        out = np.zeros(self.num_graphs, dtype=np.uint32)
+        check(restore_lib().fdy_get_groups(self._h, _stream(stream), out.ctypes.data_as(_lib.u32p)))
+        return out
+
+    def status(self, stream=None) -> np.ndarray:
+        out = np.zeros(self.num_graphs, dtype=np.uint32)
+        check(restore_lib().fdy_get_graph_status(self._h, _stream(stream), out.ctypes.data_as(_lib.u32p)))
+        return out
+
+    def override_offsets(self, stream=None) -> np.ndarray:
+        out = np.zeros(self.num_graphs + 1, dtype=np.uint64)
+        check(restore_lib().fdy_get_override_offsets(self._h, _stream(stream), out.ctypes.data_as(_lib.u64p)))
+        return out
+
+    def param_bytes(self, stream=None) -> np.ndarray:
+        out = np.zeros(self.num_graphs, dtype=np.uint64)
+        check(restore_lib().fdy_get_param_bytes(self._h, _stream(stream), out.ctypes.data_as(_lib.u64p)))
+        return out
+
+    def _sized(self, fn, g: int, dtype, stream, mult: int = 1):
+        n = C.c_uint64()
+        check(fn(self._h, _stream(stream), g, None, 0, C.byref(n)))
+        out = np.zeros(n.value, dtype=dtype)
+        ptr = out.ctypes.data_as(C.POINTER(np.ctypeslib.as_ctypes_type(dtype))) if n.value else None
+        check(fn(self._h, _stream(stream), g, ptr, n.value, C.byref(n)))
+        return out
+
+    def overrides(self, g: int, stream=None) -> np.ndarray:
+        n = C.c_uint64()
+        lib = restore_lib()
+        check(lib.fdy_get_overrides(self._h, _stream(stream), g, None, 0, C.byref(n)))
+        out = np.zeros(n.value, dtype=OVERRIDE_DTYPE)
+        if n.value:
+            check(
+                lib.fdy_get_overrides(
+                    self._h, _stream(stream), g, out.ctypes.data_as(C.POINTER(Override)), n.value, C.byref(n)
+                )
+            )
+        return out
+
+    def node_flags(self, g: int, stream=None) -> np.ndarray:
+        return self._sized(restore_lib().fdy_get_node_flags, g, np.uint8, stream)
+
+    def node_words(self, g: int, stream=None) -> np.ndarray:
+        return self._sized(restore_lib().fdy_get_node_words, g, np.uint32, stream)
+
+    def param_image(self, g: int, stream=None) -> np.ndarray:
+        return self._sized(restore_lib().fdy_get_param_image, g, np.uint64, stream)
+
+    def node_pointers(self, g: int, stream=None) -> np.ndarray:
+        return self._sized(restore_lib().fdy_get_node_pointers, g, np.uint64, stream)
+
+    # ---- switching -------------------------------------------------------
+    def switch(self, g: int, stream=None) -> None:
+        check(restore_lib().fdy_switch(self._h, g, _stream(stream)))
+
+    def live(self, template: int, stream=None) -> tuple[np.ndarray, np.ndarray, int]:
+        words = self.param_image(template, stream).size
+        nodes = self.node_flags(template, stream).size
+        w = np.zeros(words, dtype=np.uint64)
+        src = np.zeros(nodes, dtype=np.uint32)
+        cur = C.c_uint32()
+        check(
+            restore_lib().fdy_get_live(
+                self._h,
+                _stream(stream),
+                template,
+                w.ctypes.data_as(_lib.u64p) if words else None,
+                words,
+                src.ctypes.data_as(_lib.u32p) if nodes else None,
+                nodes,
+                C.byref(cur),
+            )
+        )
+        return w, src, cur.value
+
+
+class RelocPlan:
+    """Interval search structure for fdy_relocate_words."""
+
+    def __init__(self, lo, hi, new_lo, policy: int = _lib.RELOC_HALF_OPEN):
+        lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+        h = C.c_void_p()
+        check(
+            restore_lib().fdy_reloc_plan_create(
+                lo.ctypes.data_as(_lib.u64p),
+                hi.ctypes.data_as(_lib.u64p),
+                new_lo.ctypes.data_as(_lib.u64p),
+                len(lo),
+                policy,
+                C.byref(h),
+            )
+        )
+        self._h = h
+
+    def relocate(self, d_in: int, d_out: int, n_words: int, stream=None) -> None:
+        """Relocate n_words u64 words at device address d_in into d_out."""
+        check(restore_lib().fdy_relocate_words(self._h, C.c_void_p(d_in), C.c_void_p(d_out), n_words, _stream(stream)))
+
+    def close(self) -> None:
+        if self._h:
+            check(restore_lib().fdy_reloc_plan_destroy(self._h))
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def version() -> str:
+    return restore_lib().fdy_version().decode()

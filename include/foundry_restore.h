@@ -1,0 +1,192 @@
+/*
+ * foundry_restore.h -- C ABI of the MI355X graph-restore (LOAD) data path.
+ *
+ * libfoundry_restore.so turns a set of `.cugraph` archives into restorable
+ * graphs on one MI355X (gfx950).  Every data-parallel step runs as a
+ * hand-written HIP kernel on the device; the host side only reads files,
+ * validates section bounds and enqueues work.
+ *
+ * Conventions
+ *   - Every call returns int: FDY_OK (0) or a negative FDY_E_* code.
+ *     fdy_last_error() returns a message for the calling thread's last error.
+ *     No C++ exception crosses this boundary.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Enqueueing calls are asynchronous; calls that return host arrays
+ *     synchronize the stream they name and say so.
+ *   - One fdy_archive is not safe for concurrent use from several threads;
+ *     distinct archives are independent.
+ *   - Arrays are caller-owned; device buffers are owned by the archive.
+ *
+ * Where the reference does this work (paths relative to the reference root):
+ *   read .cugraph files          csrc/CUDAGraphParallel.cpp:1575-1620, csrc/BinaryGraphIO.cpp:710-737
+ *   topology grouping            csrc/CUDAGraphParallel.cpp:1720-1851
+ *   per-graph param materialise  csrc/CUDAGraphParallel.cpp:1192-1480 (prepare_on_demand_graph_binary)
+ *   switch to another graph      csrc/CUDAGraph.cpp:330-461 (CUDAGraph::replay, on-demand branch)
+ * The reference has no diff and no pointer relocation; their semantics are
+ * defined here (see the comments on each call).
+ */
+#ifndef FOUNDRY_RESTORE_H
+#define FOUNDRY_RESTORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------- */
+#define FDY_OK 0
+#define FDY_E_INVALID (-1)  /* bad argument */
+#define FDY_E_IO (-2)       /* file missing or unreadable */
+#define FDY_E_FORMAT (-3)   /* not a valid .cugraph v1, or a section out of bounds */
+#define FDY_E_HIP (-4)      /* a HIP runtime call failed (message carries hipError_t) */
+#define FDY_E_NOMEM (-5)    /* host or device allocation failed */
+#define FDY_E_RANGE (-6)    /* index out of range */
+#define FDY_E_STATE (-7)    /* call out of order (e.g. results before fdy_restore) */
+#define FDY_E_CAPACITY (-8) /* caller array too small; *_needed outputs say how big */
+#define FDY_E_MISMATCH (-9) /* graph and template disagree in node count (reference: TORCH_CHECK) */
+
+/* ---- relocation policy (fdy_archive_set_relocation / fdy_reloc_plan_create) ----
+ * A word w is relocated by interval i = the last i with lo[i] <= w, if
+ *   FDY_RELOC_HALF_OPEN:   w <  hi[i]   (one-past-end stays unchanged unless it is lo[i+1])
+ *   FDY_RELOC_INCLUSIVE:   w <= hi[i]   (one-past-end moves with its interval)
+ * and then w' = w - lo[i] + new_lo[i] (mod 2^64).  Otherwise w is unchanged. */
+#define FDY_RELOC_HALF_OPEN 0u
+#define FDY_RELOC_INCLUSIVE 1u
+
+/* ---- per-node diff flags (fdy_get_node_flags) -------------------------- */
+#define FDY_NODE_LAYOUT 0x01u  /* node type, param count or param sizes differ from the template */
+#define FDY_NODE_DESC 0x02u    /* launch config / function / attributes / memset-memcpy fields differ */
+#define FDY_NODE_RAGGED 0x04u  /* node has a param whose size is not a multiple of 8 */
+#define FDY_NODE_TEMPLATE 0x08u
+
+/* ---- per-graph status bits (fdy_get_graph_status) ---------------------- */
+#define FDY_GRAPH_TYPE_MISMATCH 0x01u /* recomputed node-type digest differs from the template's */
+#define FDY_GRAPH_BAD_PARAMS 0x02u    /* a param/arg/name range lies outside its section */
+#define FDY_GRAPH_COLLISION 0x08u     /* equal key digest but different key bytes */
+#define FDY_GRAPH_NODE_COUNT 0x10u    /* node count differs from the template (switch refused) */
+#define FDY_GRAPH_OVERFLOW 0x20u      /* param image larger than the capacity the sections allow */
+
+/* One override: the word `word` of the template's param image takes `value`. */
+typedef struct fdy_override {
+  uint32_t word; /* template-image word index (node-major, params padded to 8 B) */
+  uint32_t node; /* node index inside the graph */
+  uint64_t value;
+} fdy_override;
+
+typedef struct fdy_archive_info {
+  uint32_t num_graphs;
+  uint32_t num_groups;      /* valid after fdy_restore */
+  uint64_t total_nodes;
+  uint64_t total_param_bytes;  /* sum of kernel param sizes (+ extra arg buffers) */
+  uint64_t total_words;        /* param-image words (valid after fdy_restore) */
+  uint64_t total_overrides;    /* valid after fdy_restore */
+  uint64_t file_bytes;         /* bytes of .cugraph images resident in HBM */
+  uint64_t num_intervals;
+} fdy_archive_info;
+
+typedef struct fdy_archive fdy_archive;
+typedef struct fdy_reloc_plan fdy_reloc_plan;
+
+const char* fdy_last_error(void);
+const char* fdy_version(void);
+
+/* Open `n` archives given by path.  A path ending in ".json" names the
+ * sibling ".cugraph" (csrc/CUDAGraphParallel.cpp:1591-1594).  Files are read
+ * on min(num_threads, n) host threads (csrc/CUDAGraphParallel.cpp:1553,1584),
+ * validated, and copied to HBM in one transfer.  Replaces Phase 1a. */
+int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads, fdy_archive** out);
+
+/* Same, from archive images already in host memory. */
+int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes, uint32_t n,
+                            fdy_archive** out);
+
+int fdy_archive_close(fdy_archive* a);
+int fdy_archive_info_get(const fdy_archive* a, fdy_archive_info* out);
+
+/* Saved allocation intervals [lo, hi) -> new_lo, sorted by lo, non-overlapping.
+ * n == 0 disables relocation (words pass through).  The interval model is the
+ * allocator cursor of csrc/hook.cpp:2246-2441 recorded as alloc events
+ * (csrc/hook.cpp:3364-3392); the reference never moves them, the build can. */
+int fdy_archive_set_relocation(fdy_archive* a, const uint64_t* lo, const uint64_t* hi,
+                               const uint64_t* new_lo, uint64_t n, uint32_t policy);
+
+/* Use these template assignments instead of the key digests (the
+ * graph_manifest.json path, csrc/CUDAGraphParallel.cpp:1735-1786).
+ * template_of[i] == i marks a template.  Pass NULL to go back to digests. */
+int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of);
+
+/* The GPU restore, enqueued on `stream`:
+ *   1. digests per graph (CRC-64/XZ): saved topology key, dependency table,
+ *      recomputed node-type stream, kernel-entry stream;
+ *   2. template_of[g] = lowest index with an identical saved topology key
+ *      (csrc/CUDAGraphParallel.cpp:1788-1851), verified byte-exactly;
+ *   3. per node: layout/descriptor compare against the template, param-image
+ *      layout, memset/memcpy pointer relocation;
+ *   4. fused diff + relocate over every param word: writes the relocated
+ *      param image R_g of every graph and the override set O_g of every
+ *      non-template graph in canonical (node, word) order.
+ * Also resets every group's live image to its template. */
+int fdy_restore(fdy_archive* a, void* stream);
+
+/* Results.  Each synchronizes `stream`. */
+int fdy_get_digests(fdy_archive* a, void* stream, uint64_t* out /* 4*G: key,edge,type,kent */);
+int fdy_get_groups(fdy_archive* a, void* stream, uint32_t* template_of /* G */);
+int fdy_get_graph_status(fdy_archive* a, void* stream, uint32_t* status /* G */);
+int fdy_get_override_offsets(fdy_archive* a, void* stream, uint64_t* offsets /* G+1 */);
+/* Param bytes per graph: sum of kernel param sizes (or extra arg-buffer
+ * sizes) over nodes whose ranges are in bounds -- the bytes
+ * prepare_on_demand_graph_binary copies (csrc/CUDAGraphParallel.cpp:1391-1409). */
+int fdy_get_param_bytes(fdy_archive* a, void* stream, uint64_t* out /* G */);
+int fdy_get_overrides(fdy_archive* a, void* stream, uint32_t graph, fdy_override* out, uint64_t cap,
+                      uint64_t* n_out);
+int fdy_get_node_flags(fdy_archive* a, void* stream, uint32_t graph, uint8_t* flags, uint64_t cap,
+                       uint64_t* n_out);
+int fdy_get_node_words(fdy_archive* a, void* stream, uint32_t graph, uint32_t* word_offsets /* N+1 */,
+                       uint64_t cap, uint64_t* n_out);
+/* The relocated param image R_g (node-major; each param padded to 8 B with zeros). */
+int fdy_get_param_image(fdy_archive* a, void* stream, uint32_t graph, uint64_t* words, uint64_t cap,
+                        uint64_t* n_out);
+/* Relocated memset dst / memcpy dst,src per node (0 for other node types). */
+int fdy_get_node_pointers(fdy_archive* a, void* stream, uint32_t graph, uint64_t* ptrs /* 2*N */,
+                          uint64_t cap, uint64_t* n_out);
+
+/* Switch the live image of graph `graph`'s group to `graph`: restore the
+ * template's words under the current graph's overrides that `graph` does
+ * not override, write `graph`'s overrides, and point layout/descriptor-
+ * changed nodes at `graph`.  Afterwards the live image equals R_graph on
+ * every node without FDY_NODE_LAYOUT.  Counterpart of the all-node re-set
+ * in csrc/CUDAGraph.cpp:340-461.  Enqueued on `stream`; no-op if current. */
+int fdy_switch(fdy_archive* a, uint32_t graph, void* stream);
+/* Live state of the group whose template is `template_graph`.  Synchronizes.
+ * node_src[n] = graph whose own image supplies node n (template unless the
+ * node has a layout or descriptor difference). */
+int fdy_get_live(fdy_archive* a, void* stream, uint32_t template_graph, uint64_t* words, uint64_t cap,
+                 uint32_t* node_src, uint64_t node_cap, uint32_t* current_graph);
+
+/* Standalone relocation of packed u64 words already in device memory
+ * (in and out may alias).  The plan holds the interval search structure. */
+int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
+                          uint32_t policy, fdy_reloc_plan** out);
+int fdy_reloc_plan_destroy(fdy_reloc_plan* p);
+int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
+                       void* stream);
+
+/* Timing of the last fdy_restore, from HIP events recorded on its stream
+ * around each kernel (milliseconds).  Synchronizes. */
+typedef struct fdy_restore_timing {
+  float hash_ms;    /* saved-key and dependency digests */
+  float group_ms;   /* template assignment */
+  float node_ms;    /* per-node compare, layout, type and kernel-entry digests */
+  float diff_ms;    /* fused diff + relocate */
+  float total_ms;
+} fdy_restore_timing;
+int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
+int fdy_set_timing(fdy_archive* a, int enabled);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FOUNDRY_RESTORE_H */
