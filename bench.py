@@ -98,7 +98,7 @@ def main():
 
     # Per-kernel GPU time from HIP events recorded on the restore stream.
     arch.set_timing(True)
-    per = {"hash_ms": [], "group_ms": [], "node_ms": [], "diff_ms": [], "total_ms": []}
+    per = {"hash_ms": [], "group_ms": [], "node_ms": [], "diff_ms": [], "compact_ms": [], "total_ms": []}
     for _ in range(args.steps):
         arch.restore(stream)
         t = arch.timing()

@@ -66,6 +66,7 @@ class RestoreTiming(C.Structure):
         ("group_ms", C.c_float),
         ("node_ms", C.c_float),
         ("diff_ms", C.c_float),
+        ("compact_ms", C.c_float),
         ("total_ms", C.c_float),
     ]
 

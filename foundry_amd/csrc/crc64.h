@@ -109,13 +109,15 @@ __host__ __device__ inline uint64_t nibble_mul(const uint64_t (*tab)[16], uint64
 }
 
 // Levels of the block combine tree: level k joins runs of 2^k records, so
-// its multiplier is x^(8 * S * 2^k); level 8 joins 256-record chunks.
-constexpr int kTreeLevels = 9;
+// its multiplier is x^(8 * S * 2^k); levels 0-5 run inside a wave, 6-9
+// across the waves of a 1024-thread block, and level 10 joins 1024-record
+// chunks.
+constexpr int kTreeLevels = 11;
 
 struct CrcConsts {
   SliceTables slice;
-  NibbleTable rec8[kTreeLevels];   // S = 8-byte records (byte streams)
   NibbleTable rec16[kTreeLevels];  // S = 16-byte records (node records)
+  NibbleTable rec64[kTreeLevels];  // S = 64-byte records (byte streams, 8 words per lane)
   X2nTable x2n;
 };
 
@@ -123,14 +125,15 @@ inline void make_crc_consts(CrcConsts* c) {
   c->slice = make_slice_tables();
   c->x2n = make_x2n_table();
   for (int k = 0; k < kTreeLevels; ++k) {
-    c->rec8[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)8 << k, 3));
     c->rec16[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)16 << k, 3));
+    c->rec64[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)64 << k, 3));
   }
 }
 
 // Finish a raw CRC of an L-byte stream: crc = raw ^ (~0 * x^(8L)) ^ ~0.
-__host__ __device__ inline uint64_t crc_finish(const uint64_t* x2n, uint64_t raw, uint64_t len) {
-  return raw ^ gf2_mulmod(x2n_mod(x2n, len, 3), ~0ull) ^ ~0ull;
+// The term after `raw` depends on L only; hosts precompute it per stream.
+__host__ __device__ inline uint64_t crc_finish_term(const uint64_t* x2n, uint64_t len) {
+  return gf2_mulmod(x2n_mod(x2n, len, 3), ~0ull) ^ ~0ull;
 }
 
 }  // namespace fdy

@@ -16,7 +16,6 @@ struct RestoreArgs {
   const CrcConsts* cc;
   uint32_t num_graphs;
   uint32_t num_slots;
-  uint16_t epoch;
   uint64_t* digests;          // 4 per graph
   const uint32_t* explicit_template;  // or null
   uint32_t* template_of;
@@ -33,10 +32,11 @@ struct RestoreArgs {
   uint64_t* live;             // live images (template graphs)
   uint32_t* live_src;         // per node
   uint32_t* live_cur;         // per graph
-  fdy_override* ovr;
+  fdy_override* ovr;          // dense override records, canonical order
   uint64_t* ovr_off;          // G+1
-  uint64_t* lookback;         // per slot
-  uint32_t* ticket;
+  fdy_override* ovr_tile;     // per-slot record regions (kTileWords each)
+  uint32_t* tile_count;       // records per slot
+  uint64_t* tile_off;         // exclusive prefix of tile_count
   RelocDev reloc;
 };
 
@@ -44,7 +44,7 @@ hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff(const RestoreArgs& a, hipStream_t s);
-hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t v, hipStream_t s);
+hipError_t launch_compact(const RestoreArgs& a, hipStream_t s);
 
 struct SwitchArgs {
   const fdy_override* ovr_cur;  // current graph's overrides

@@ -2,21 +2,21 @@
 //
 //   k_hash    one workgroup per graph: CRC-64/XZ of the saved topology key and
 //             of the dependency table, as a block-wide segmented CRC (each
-//             lane absorbs one 8-byte record, lanes are joined by a combine
-//             tree whose multipliers are constants applied through nibble
-//             tables held in LDS).
+//             lane absorbs 64 bytes, lanes are joined by a combine tree whose
+//             multipliers are constants applied through nibble tables in LDS).
 //   k_group   template_of[g] = lowest graph with the same key digest and length.
 //   k_node    one workgroup per graph: per node, the param layout, the compare
 //             against the template's node, memset/memcpy pointer relocation,
 //             node-type and kernel-entry digests, the node descriptors the
 //             diff pass consumes, and the diff-tile -> first-node table.
 //   k_diff    one workgroup per 4096-word tile of a graph's param image:
-//             coalesced 8-byte loads of the graph's and the template's words,
-//             relocation through an LDS-staged interval search, the relocated
-//             image store, and ballot + LDS prefix-sum compaction of the
-//             differing words; tiles are ordered by an atomic ticket and
-//             chained by a decoupled look-back so the override records land
-//             in canonical (graph, node, word) order in a single pass.
+//             coalesced 8-byte loads of the graph's and the template's words
+//             (software-pipelined), relocation through a bucket-indexed
+//             interval search, the relocated image store, and ballot + LDS
+//             prefix-sum compaction of the differing words into the tile's
+//             own record region.
+//   k_scan    prefix of the per-tile record counts -> per-graph offsets.
+//   k_compact tile regions -> the dense override array, canonical order.
 //   k_switch  override scatter for one graph switch.
 //   k_reloc   streaming relocation of packed words.
 #include "kernels.h"
@@ -24,11 +24,13 @@
 namespace fdy {
 namespace {
 
-constexpr uint32_t kHashThreads = 256;
-constexpr uint32_t kNodeThreads = 256;
+constexpr uint32_t kHashThreads = 1024;
+constexpr uint32_t kNodeThreads = 1024;
+constexpr int kChunkLevel = 10;  // combine level joining 1024-record chunks (log2 of the block size)
+static_assert((1u << kChunkLevel) == kHashThreads && kHashThreads == kNodeThreads, "chunk level");
 constexpr uint32_t kGroupThreads = 1024;
-constexpr uint32_t kRelocThreads = 512;
-constexpr uint64_t kMask46 = (1ull << 46) - 1;
+constexpr uint32_t kRelocThreads = 256;
+constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
 
 __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -45,16 +47,18 @@ __device__ void stage_crc_tables(const CrcConsts* cc, bool rec16, uint64_t (*sli
   const uint64_t* s = &cc->slice.t[0][0];
   uint64_t* d = &slice[0][0];
   for (uint32_t i = threadIdx.x; i < 8 * 256; i += blockDim.x) d[i] = s[i];
-  const uint64_t* ns = rec16 ? &cc->rec16[0].t[0][0] : &cc->rec8[0].t[0][0];
+  const uint64_t* ns = rec16 ? &cc->rec16[0].t[0][0] : &cc->rec64[0].t[0][0];
   uint64_t* nd = &nib[0][0][0];
   for (uint32_t i = threadIdx.x; i < kTreeLevels * 256; i += blockDim.x) nd[i] = ns[i];
   __syncthreads();
 }
 
-// Join the raw CRCs of 256 consecutive records (one per thread, in thread
-// order) into the raw CRC of the whole run.  Valid in thread 0.
+// Join the raw CRCs of blockDim.x consecutive records (one per thread, in
+// thread order; blockDim.x a power of two) into the raw CRC of the whole
+// run: a shuffle tree inside each wave, then one across the waves.  Valid
+// in thread 0.
 __device__ uint64_t block_crc_combine(uint64_t z, const uint64_t (*nib)[16][16], uint64_t* s_wave) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
 #pragma unroll
   for (int k = 0; k < 6; ++k) {
     uint64_t o = shfl_down64(z, 1 << k);
@@ -64,9 +68,13 @@ __device__ uint64_t block_crc_combine(uint64_t z, const uint64_t (*nib)[16][16],
   if (lane == 0) s_wave[wave] = z;
   __syncthreads();
   uint64_t r = 0;
-  if (threadIdx.x == 0) {
-    r = s_wave[0];
-    for (uint32_t w = 1; w < blockDim.x / 64; ++w) r = nibble_mul(nib[6], r) ^ s_wave[w];
+  if (wave == 0) {
+    r = lane < nw ? s_wave[lane] : 0;
+    for (uint32_t k = 0; (1u << k) < nw; ++k) {
+      uint64_t o = shfl_down64(r, 1 << k);
+      uint64_t m = nibble_mul(nib[6 + k], r) ^ o;
+      if ((lane & ((2u << k) - 1)) == 0) r = m;
+    }
   }
   __syncthreads();
   return r;
@@ -89,22 +97,30 @@ __device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b
   return (w0 >> (8 * sh)) | (word(q + 1) << (64 - 8 * sh));
 }
 
-// CRC-64/XZ of an L-byte stream, front-padded with zeros to whole
-// 2048-byte chunks (leading zeros leave a zero-initialised register at
-// zero, and crc_finish adds the effect of the all-ones initial value).
+// CRC-64/XZ of an L-byte stream.  Each lane absorbs 64 consecutive bytes
+// (eight slicing steps), lanes are joined by the combine tree for 64-byte
+// records, and the stream is front-padded with zeros to whole 64 KB chunks
+// (leading zeros leave a zero-initialised register at zero; `fin`, the
+// stream's finishing term, adds the effect of the all-ones initial value).
 __device__ uint64_t block_crc_bytes(const uint8_t* p, uint64_t L, const uint64_t (*slice)[256],
-                                    const uint64_t (*nib)[16][16], const uint64_t* x2n, uint64_t* s_wave) {
-  constexpr uint64_t kChunk = kHashThreads * 8;
+                                    const uint64_t (*nib)[16][16], uint64_t fin, uint64_t* s_wave) {
+  constexpr uint64_t kLane = 64;
+  constexpr uint64_t kChunk = kHashThreads * kLane;
   const uint64_t pad = (kChunk - L % kChunk) % kChunk;
   const uint64_t nchunks = (L + pad) / kChunk;
   uint64_t acc = 0;
   for (uint64_t c = 0; c < nchunks; ++c) {
-    int64_t b0 = (int64_t)(c * kChunk + 8 * threadIdx.x) - (int64_t)pad;
-    uint64_t z = crc_slice8(slice, 0, stream_window(p, L, b0));
+    const int64_t b0 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad;
+    uint64_t v[kLane / 8];
+#pragma unroll
+    for (uint32_t q = 0; q < kLane / 8; ++q) v[q] = stream_window(p, L, b0 + 8 * q);
+    uint64_t z = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kLane / 8; ++q) z = crc_slice8(slice, z, v[q]);
     z = block_crc_combine(z, nib, s_wave);
-    if (threadIdx.x == 0) acc = nibble_mul(nib[8], acc) ^ z;
+    if (threadIdx.x == 0) acc = nibble_mul(nib[kChunkLevel], acc) ^ z;
   }
-  return threadIdx.x == 0 ? crc_finish(x2n, acc, L) : 0;
+  return threadIdx.x == 0 ? acc ^ fin : 0;
 }
 
 __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
@@ -113,12 +129,11 @@ __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
   __shared__ uint64_t s_wave[kHashThreads / 64];
   stage_crc_tables(a.cc, false, s_slice, s_nib);
   const uint32_t g = blockIdx.x;
-  if (g == 0 && threadIdx.x == 0) *a.ticket = 0;
   const DevGraph& G = a.graphs[g];
   uint64_t dk = block_crc_bytes(a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY],
-                                s_slice, s_nib, a.cc->x2n.v, s_wave);
+                                s_slice, s_nib, G.crc_fin[0], s_wave);
   uint64_t de = block_crc_bytes(a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, s_slice, s_nib,
-                                a.cc->x2n.v, s_wave);
+                                G.crc_fin[1], s_wave);
   if (threadIdx.x == 0) {
     a.digests[4ull * g + 0] = dk;
     a.digests[4ull * g + 1] = de;
@@ -152,12 +167,20 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
       }
       __syncthreads();
       if (i < G && found == 0xFFFFFFFFu) {
+        // Eight candidates per step with independent LDS loads (indices
+        // clamped inside the chunk), first match wins.
         const uint32_t stop = min(end, i + 1);
-        for (uint32_t j = base; j < stop; ++j) {
-          if (s_d[j - base] == di && s_l[j - base] == li) {
-            found = j;
-            break;
+        for (uint32_t j = base; j < stop && found == 0xFFFFFFFFu; j += 8) {
+          uint64_t d[8], l[8];
+#pragma unroll
+          for (uint32_t q = 0; q < 8; ++q) {
+            const uint32_t jj = min(j + q, stop - 1) - base;
+            d[q] = s_d[jj];
+            l[q] = s_l[jj];
           }
+#pragma unroll
+          for (uint32_t q = 0; q < 8; ++q)
+            if (found == 0xFFFFFFFFu && j + q < stop && d[q] == di && l[q] == li) found = j + q;
         }
       }
     }
@@ -311,27 +334,31 @@ __device__ uint64_t name_crc(const uint8_t* img, const DevGraph& G, const uint8_
                              const uint64_t (*slice)[256]) {
   const uint32_t no = ld_u32(e + FDY_KOFF_NAME_OFFSET), nl = ld_u32(e + FDY_KOFF_NAME_LENGTH);
   if ((uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS]) return 0;
-  const uint8_t* s = img + G.sec_off[FDY_SEC_STRINGS] + no;
+  // The string section starts 8-byte aligned: read it through aligned words.
+  const uint8_t* base = img + G.sec_off[FDY_SEC_STRINGS];
+  const uint64_t S = G.sec_size[FDY_SEC_STRINGS];
   uint64_t c = ~0ull;
   uint32_t i = 0;
-  for (; i + 8 <= nl; i += 8) c = crc_slice8(slice, c, ld_u64(s + i));
-  for (; i < nl; ++i) c = crc_byte(slice[0], c, s[i]);
+  for (; i + 8 <= nl; i += 8) c = crc_slice8(slice, c, stream_window(base, S, (int64_t)no + i));
+  if (i < nl) {
+    uint64_t tail = stream_window(base, S, (int64_t)no + i);
+    for (; i < nl; ++i, tail >>= 8) c = crc_byte(slice[0], c, (uint8_t)tail);
+  }
   return ~c;
 }
 
 // Relocated memset dst / memcpy dst, src of node entry e (0 when not a pointer node).
 __device__ void node_pointers(const uint8_t* e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
   const uint8_t type = e[FDY_NODE_OFF_TYPE];
-  const uint64_t* top = r.level[r.n_levels];
   *p0 = 0;
   *p1 = 0;
   if (type == FDY_NODE_MEMSET) {
-    *p0 = reloc_word(r, top, ld_u64(e + FDY_MSOFF_DST));
+    *p0 = reloc_word(r, ld_u64(e + FDY_MSOFF_DST));
   } else if (type == FDY_NODE_MEMCPY) {
     const uint64_t dst = ld_u64(e + FDY_MCOFF_DST), src = ld_u64(e + FDY_MCOFF_SRC);
     const int32_t dt = (int32_t)ld_u32(e + FDY_MCOFF_DST_MEMTYPE), st = (int32_t)ld_u32(e + FDY_MCOFF_SRC_MEMTYPE);
-    *p0 = (dt == FDY_MEMTYPE_DEVICE || dt == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, top, dst) : dst;
-    *p1 = (st == FDY_MEMTYPE_DEVICE || st == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, top, src) : src;
+    *p0 = (dt == FDY_MEMTYPE_DEVICE || dt == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, dst) : dst;
+    *p1 = (st == FDY_MEMTYPE_DEVICE || st == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, src) : src;
   }
 }
 
@@ -576,8 +603,8 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
     zt = block_crc_combine(zt, s_nib, s_wave);
     zk = block_crc_combine(zk, s_nib, s_wave);
     if (threadIdx.x == 0) {
-      acc_type = nibble_mul(s_nib[8], acc_type) ^ zt;
-      acc_kent = nibble_mul(s_nib[8], acc_kent) ^ zk;
+      acc_type = nibble_mul(s_nib[kChunkLevel], acc_type) ^ zt;
+      acc_kent = nibble_mul(s_nib[kChunkLevel], acc_kent) ^ zk;
     }
     gcarry += tot_g;
     tcarry += tot_t;
@@ -590,8 +617,8 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
     a.status[g] = st;
     a.gwords[g] = s_words;
     a.pbytes[g] = s_pbytes;
-    a.digests[4ull * g + 2] = crc_finish(a.cc->x2n.v, acc_type, 16ull * N);
-    a.digests[4ull * g + 3] = crc_finish(a.cc->x2n.v, acc_kent, 16ull * N);
+    a.digests[4ull * g + 2] = acc_type ^ Gg.crc_fin[2];
+    a.digests[4ull * g + 3] = acc_kent ^ Gg.crc_fin[3];
     if (is_t) a.live_cur[g] = g;
   }
   __syncthreads();
@@ -614,44 +641,106 @@ __device__ inline uint64_t load_bytes(const uint8_t* img, uint64_t byte, uint32_
   return width >= 8 ? v : v & ((1ull << (8 * width)) - 1);
 }
 
-__device__ uint64_t lookback(uint64_t* lb, uint32_t slot, uint16_t epoch, uint64_t agg) {
-  const uint64_t ep = (uint64_t)epoch << 48;
-  if (slot == 0) {
-    __hip_atomic_store(&lb[0], ep | (2ull << 46) | (agg & kMask46), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return 0;
+// The node holding graph-local word w: the last node whose first word is <= w,
+// searched in the LDS window first and in global memory past it.
+__device__ inline uint32_t find_node(const NodeDesc* s_nd, uint32_t nwin, const NodeDesc* nd, uint32_t n0,
+                                     uint32_t N, uint64_t w, NodeDesc* out) {
+  uint32_t lo = 0, len = nwin;
+  while (len > 1) {
+    const uint32_t half = len >> 1;
+    if (s_nd[lo + half].gword <= w) lo += half;
+    len -= half;
   }
-  __hip_atomic_store(&lb[slot], ep | (1ull << 46) | (agg & kMask46), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  uint64_t excl = 0;
-  uint32_t p = slot - 1;
-  for (;;) {
-    const uint64_t s = __hip_atomic_load(&lb[p], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t flag = (s >> 46) & 3;
-    if ((s >> 48) != epoch || flag == 0) {
-      __builtin_amdgcn_s_sleep(1);
-      continue;
+  NodeDesc d = s_nd[lo];
+  uint32_t node = n0 + lo;
+  if (lo == nwin - 1 && nwin == kDiffWindow && w >= (uint64_t)d.gword + d.nwords) {
+    uint32_t l2 = node, h2 = N;
+    while (h2 - l2 > 1) {
+      const uint32_t mid = (l2 + h2) >> 1;
+      if (nd[mid].gword <= w) l2 = mid;
+      else h2 = mid;
     }
-    excl += s & kMask46;
-    if (flag == 2) break;
-    --p;
+    d = nd[l2];
+    node = l2;
   }
-  __hip_atomic_store(&lb[slot], ep | (2ull << 46) | ((excl + agg) & kMask46), __ATOMIC_RELAXED,
-                     __HIP_MEMORY_SCOPE_AGENT);
-  return excl;
+  *out = d;
+  return node;
 }
 
+// Loads of one batch of B words per thread: the graph's raw word and, where
+// the node is compared, the template's raw word.  Bit j of *valid / *cmp /
+// *full marks word j present / compared / a whole 8-byte word.
+template <uint32_t B>
+__device__ inline void diff_load(const RestoreArgs& a, bool flat, const uint8_t* pg, const uint8_t* pt, bool cflat,
+                                 const NodeDesc* s_nd, uint32_t nwin, const NodeDesc* nd, uint32_t n0, uint32_t N,
+                                 const DevGraph& G, const DevGraph& T, uint64_t w0, uint64_t wend, uint64_t* rg,
+                                 uint64_t* rt, uint32_t* valid, uint32_t* cmp, uint32_t* full) {
+  uint32_t v = 0, c = 0, f = 0;
+  if (flat) {
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j) {
+      const uint64_t w = w0 + (uint64_t)j * kDiffThreads;
+      rg[j] = rt[j] = 0;
+      if (w < wend) {
+        v |= 1u << j;
+        rg[j] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
+        if (cflat) rt[j] = *reinterpret_cast<const uint64_t*>(pt + 8 * w);
+      }
+    }
+    f = v;
+    c = cflat ? v : 0;
+  } else {
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j) {
+      const uint64_t w = w0 + (uint64_t)j * kDiffThreads;
+      rg[j] = rt[j] = 0;
+      if (w >= wend) continue;
+      v |= 1u << j;
+      NodeDesc d;
+      find_node(s_nd, nwin, nd, n0, N, w, &d);
+      const uint32_t off = (uint32_t)(w - d.gword);
+      uint32_t width = 8;
+      if (d.flags & FDY_NODE_RAGGED) {
+        const uint64_t x = a.aux[G.word_base + w];
+        width = (uint32_t)(x & 15);
+        rg[j] = load_bytes(a.img, x >> 4, width);
+      } else {
+        rg[j] = *reinterpret_cast<const uint64_t*>(a.img + d.src_g + 8ull * off);
+      }
+      if (width == 8) f |= 1u << j;
+      if (d.flags & kNodeCompare) {
+        c |= 1u << j;
+        const uint32_t tw = d.tword + off;
+        if (d.flags & kNodeRaggedT) {
+          const uint64_t x = a.aux[T.word_base + tw];
+          rt[j] = load_bytes(a.img, x >> 4, (uint32_t)(x & 15));
+        } else {
+          rt[j] = *reinterpret_cast<const uint64_t*>(a.img + d.src_t + 8ull * off);
+        }
+      }
+    }
+  }
+  *valid = v;
+  *cmp = c;
+  *full = f;
+}
+
+// One workgroup per tile slot.  Tiles are independent: each writes its
+// override records, in word order, to its own kTileWords-record region and
+// their number to tile_count; k_scan and k_compact then pack the regions
+// into the dense canonical array.
 __global__ __launch_bounds__(kDiffThreads) void k_diff(RestoreArgs a) {
+  constexpr uint32_t J = kDiffWordsPerThread;
+  constexpr uint32_t B = 4;                      // words per thread per batch
+  constexpr uint32_t kWaves = kDiffThreads / 64;
+  constexpr uint32_t kCounts = J * kWaves;       // per-(batch word, wave) override counts
+  static_assert(kCounts == 64 && J % B == 0, "tile shape");
   __shared__ NodeDesc s_nd[kDiffWindow];
-  __shared__ uint64_t s_top[kRelocLdsKeys];
-  __shared__ uint32_t s_cnt[kDiffWordsPerThread * (kDiffThreads / 64)];
-  __shared__ uint32_t s_slot, s_total;
-  __shared__ uint64_t s_excl;
+  __shared__ uint32_t s_cnt[kCounts];
+  __shared__ uint32_t s_flat;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid == 0) s_slot = atomicAdd(a.ticket, 1u);
   const RelocDev& R = a.reloc;
-  if (R.n)
-    for (uint32_t i = tid; i < R.n_top; i += kDiffThreads) s_top[i] = R.level[R.n_levels][i];
-  __syncthreads();
-  const uint32_t slot = s_slot;
+  const uint32_t slot = blockIdx.x;
   const uint32_t g = a.slot_graph[slot];
   const DevGraph& G = a.graphs[g];
   const uint32_t t = a.template_of[g];
@@ -660,82 +749,94 @@ __global__ __launch_bounds__(kDiffThreads) void k_diff(RestoreArgs a) {
   const uint32_t k = slot - G.tile_base;
   const uint32_t n0 = a.tile_node[slot];
   const bool active = n0 != kNoTile;
-  const uint32_t words = a.gwords[g];
   const uint32_t N = G.num_nodes;
-  const uint32_t nwin = active ? min(kDiffWindow, N - n0) : 0;
+  // Nodes holding this tile's words run from n0 to the next tile's first
+  // node (which may also hold the tile's last words).
+  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
+  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
+  const uint32_t nwin = active ? min(kDiffWindow, n_last - n0 + 1) : 0;
   const NodeDesc* nd = a.node_desc + G.node_base;
+  const uint64_t wbeg = (uint64_t)k * kTileWords;
+  const uint64_t wend = active ? min(wbeg + kTileWords, (uint64_t)a.gwords[g]) : wbeg;
+  if (tid == 0) {
+    s_flat = active;
+    if (k == 0 && !is_t && a.digests[4ull * g + 2] != a.digests[4ull * t + 2])
+      atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
+  }
+  if (!active) {
+    if (tid == 0) a.tile_count[slot] = 0;
+    return;
+  }
   for (uint32_t i = tid; i < nwin; i += kDiffThreads) s_nd[i] = nd[n0 + i];
   __syncthreads();
 
-  const uint64_t wbeg = (uint64_t)k * kTileWords;
-  uint32_t bits = 0;
-  uint64_t val[kDiffWordsPerThread];
-  uint32_t tw_of[kDiffWordsPerThread], node_of[kDiffWordsPerThread];
-#pragma unroll
-  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
-    const uint64_t w = wbeg + (uint64_t)j * kDiffThreads + tid;
-    val[j] = 0;
-    tw_of[j] = 0;
-    node_of[j] = 0;
-    if (!active || w >= words) continue;
-    // Node holding word w: the last node whose first word is <= w.
-    uint32_t lo = 0, len = nwin;
-    while (len > 1) {
-      const uint32_t half = len >> 1;
-      if (s_nd[lo + half].gword <= w) lo += half;
-      len -= half;
-    }
-    NodeDesc d = s_nd[lo];
-    uint32_t node = n0 + lo;
-    if (lo == nwin - 1 && nwin == kDiffWindow && w >= (uint64_t)d.gword + d.nwords) {
-      uint32_t l2 = n0 + lo, h2 = N;  // beyond the staged window
-      while (h2 - l2 > 1) {
-        const uint32_t mid = (l2 + h2) >> 1;
-        if (nd[mid].gword <= w) l2 = mid;
-        else h2 = mid;
-      }
-      d = nd[l2];
-      node = l2;
-    }
-    const uint32_t off = (uint32_t)(w - d.gword);
-    uint64_t raw_g;
-    uint32_t width_g = 8;
-    if (d.flags & FDY_NODE_RAGGED) {
-      const uint64_t x = a.aux[G.word_base + w];
-      width_g = (uint32_t)(x & 15);
-      raw_g = load_bytes(a.img, x >> 4, width_g);
-    } else {
-      raw_g = *reinterpret_cast<const uint64_t*>(a.img + d.src_g + 8ull * off);
-    }
-    const uint64_t rg = width_g == 8 ? reloc_word(R, s_top, raw_g) : raw_g;
-    a.image[G.word_base + w] = rg;
-    if (is_t) a.live[G.word_base + w] = rg;
-    if (d.flags & kNodeCompare) {
-      const uint32_t tw = d.tword + off;
-      uint64_t raw_t;
-      uint32_t width_t = 8;
-      if (d.flags & kNodeRaggedT) {
-        const uint64_t x = a.aux[T.word_base + tw];
-        width_t = (uint32_t)(x & 15);
-        raw_t = load_bytes(a.img, x >> 4, width_t);
-      } else {
-        raw_t = *reinterpret_cast<const uint64_t*>(a.img + d.src_t + 8ull * off);
-      }
-      const uint64_t rt = (raw_t == raw_g && width_t == width_g) ? rg
-                          : (width_t == 8 ? reloc_word(R, s_top, raw_t) : raw_t);
-      if (rg != rt) {
-        bits |= 1u << j;
-        val[j] = rg;
-        tw_of[j] = tw;
-        node_of[j] = node;
-      }
-    }
+  // Flat tile: every node overlapping it is aligned in both images, shares
+  // node n0's compare status, and sits at the same offset from a common
+  // base, so word w is at byte kg + 8w of the graph's image (kt + 8w of
+  // the template's) and needs no node lookup.
+  const NodeDesc d0 = s_nd[0];
+  const uint64_t kg = d0.src_g - 8ull * d0.gword, kt = d0.src_t - 8ull * d0.gword;
+  for (uint32_t i = tid; i < nwin; i += kDiffThreads) {
+    const NodeDesc d = s_nd[i];
+    if (d.gword >= wend || d.nwords == 0) continue;
+    const bool ok = !(d.flags & (FDY_NODE_RAGGED | kNodeRaggedT)) && !((d.flags ^ d0.flags) & kNodeCompare) &&
+                    d.src_g - 8ull * d.gword == kg && (!(d.flags & kNodeCompare) || d.src_t - 8ull * d.gword == kt);
+    if (!ok) s_flat = 0;
   }
-  // Compaction: records are ordered by (j, thread) = word order in the tile.
+  if (tid == 0 && nwin == kDiffWindow && (uint64_t)s_nd[nwin - 1].gword + s_nd[nwin - 1].nwords < wend)
+    s_flat = 0;
+  __syncthreads();
+  const bool flat = s_flat != 0;
+  const bool cflat = (d0.flags & kNodeCompare) != 0;
+  const uint8_t* pg = a.img + kg;
+  const uint8_t* pt = a.img + kt;
+
+  // Batches of B words per thread, software-pipelined: batch b+1's loads
+  // are issued before batch b is relocated, compared and stored.
+  uint64_t* img_out = a.image + G.word_base;
+  uint64_t* live_out = a.live + G.word_base;
+  uint32_t bits = 0;
+  uint64_t rg[B], rt[B], ng[B], nt[B];
+  uint32_t valid, cmp, full, nvalid = 0, ncmp = 0, nfull = 0;
+  diff_load<B>(a, flat, pg, pt, cflat, s_nd, nwin, nd, n0, N, G, T, wbeg + tid, wend, rg, rt, &valid, &cmp, &full);
 #pragma unroll
-  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
+  for (uint32_t jb = 0; jb < J; jb += B) {
+    if (jb + B < J)
+      diff_load<B>(a, flat, pg, pt, cflat, s_nd, nwin, nd, n0, N, G, T,
+                   wbeg + (uint64_t)(jb + B) * kDiffThreads + tid, wend, ng, nt, &nvalid, &ncmp, &nfull);
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j) {
+      if (!((valid >> j) & 1)) continue;
+      const uint64_t raw = rg[j];
+      const bool f = (full >> j) & 1;
+      rg[j] = f ? reloc_word(R, raw) : raw;
+      if ((cmp >> j) & 1) {
+        const uint64_t r = rt[j] == raw ? rg[j] : (f ? reloc_word(R, rt[j]) : rt[j]);
+        if (r != rg[j]) bits |= 1u << (jb + j);
+      }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j) {
+      if (!((valid >> j) & 1)) continue;
+      const uint64_t w = wbeg + (uint64_t)(jb + j) * kDiffThreads + tid;
+      img_out[w] = rg[j];
+      if (is_t) live_out[w] = rg[j];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < B; ++j) {
+      rg[j] = ng[j];
+      rt[j] = nt[j];
+    }
+    valid = nvalid;
+    cmp = ncmp;
+    full = nfull;
+  }
+
+  // Compaction inside the tile: records ordered by (j, thread) = word order.
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) {
     const uint64_t m = __ballot((bits >> j) & 1);
-    if (lane == 0) s_cnt[j * (kDiffThreads / 64) + wave] = (uint32_t)__popcll(m);
+    if (lane == 0) s_cnt[j * kWaves + wave] = (uint32_t)__popcll(m);
   }
   __syncthreads();
   if (wave == 0) {
@@ -747,37 +848,70 @@ __global__ __launch_bounds__(kDiffThreads) void k_diff(RestoreArgs a) {
       if (lane >= (uint32_t)dd) x += y;
     }
     s_cnt[lane] = x - v;
-    if (lane == 63) s_total = x;
+    if (lane == 63) a.tile_count[slot] = x;
   }
   __syncthreads();
-  if (tid == 0) {
-    const uint64_t excl = lookback(a.lookback, slot, a.epoch, s_total);
-    s_excl = excl;
-    if (k == 0) {
-      a.ovr_off[g] = excl;
-      if (!is_t && a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
-    }
-    if (slot == a.num_slots - 1) a.ovr_off[a.num_graphs] = excl + s_total;
-  }
-  __syncthreads();
-  const uint64_t base = s_excl;
-  const uint64_t lt = (1ull << lane) - 1;
+  if (bits) {
+    fdy_override* out = a.ovr_tile + (uint64_t)slot * kTileWords;
+    const uint64_t lt = (1ull << lane) - 1;
 #pragma unroll
-  for (uint32_t j = 0; j < kDiffWordsPerThread; ++j) {
-    const uint64_t m = __ballot((bits >> j) & 1);
-    if ((bits >> j) & 1) {
-      const uint64_t pos = base + s_cnt[j * (kDiffThreads / 64) + wave] + (uint64_t)__popcll(m & lt);
-      fdy_override o;
-      o.word = tw_of[j];
-      o.node = node_of[j];
-      o.value = val[j];
-      a.ovr[pos] = o;
+    for (uint32_t j = 0; j < J; ++j) {
+      const uint64_t m = __ballot((bits >> j) & 1);
+      if ((bits >> j) & 1) {
+        const uint64_t w = wbeg + (uint64_t)j * kDiffThreads + tid;
+        NodeDesc d;
+        const uint32_t node = find_node(s_nd, nwin, nd, n0, N, w, &d);
+        fdy_override o;
+        o.word = d.tword + (uint32_t)(w - d.gword);
+        o.node = node;
+        o.value = img_out[w];  // written above by this thread
+        out[s_cnt[j * kWaves + wave] + (uint32_t)__popcll(m & lt)] = o;
+      }
     }
   }
 }
 
-__global__ __launch_bounds__(256) void k_fill_u64(uint64_t* p, uint64_t n, uint64_t v) {
-  for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) p[i] = v;
+// Exclusive prefix of the per-slot record counts (one workgroup), and the
+// per-graph override offsets it implies.
+__global__ __launch_bounds__(1024) void k_scan(RestoreArgs a) {
+  __shared__ uint64_t s_w[16];
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t n = a.num_slots;
+  const uint32_t per = (n + 1023) / 1024;
+  const uint32_t lo = min(n, tid * per), hi = min(n, lo + per);
+  uint64_t sum = 0;
+  for (uint32_t i = lo; i < hi; ++i) sum += a.tile_count[i];
+  uint64_t x = sum;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint32_t ylo = __shfl_up((uint32_t)x, (unsigned)d, 64), yhi = __shfl_up((uint32_t)(x >> 32), (unsigned)d, 64);
+    if (lane >= (uint32_t)d) x += ((uint64_t)yhi << 32) | ylo;
+  }
+  if (lane == 63) s_w[wave] = x;
+  __syncthreads();
+  uint64_t before = 0, total = 0;
+  for (uint32_t w = 0; w < 16; ++w) {
+    if (w < wave) before += s_w[w];
+    total += s_w[w];
+  }
+  uint64_t run = before + x - sum;
+  for (uint32_t i = lo; i < hi; ++i) {
+    a.tile_off[i] = run;
+    run += a.tile_count[i];
+  }
+  __syncthreads();
+  for (uint32_t g = tid; g < a.num_graphs; g += 1024) a.ovr_off[g] = a.tile_off[a.graphs[g].tile_base];
+  if (tid == 0) a.ovr_off[a.num_graphs] = total;
+}
+
+// Copy each slot's records to their place in the dense array.
+__global__ __launch_bounds__(256) void k_compact(RestoreArgs a) {
+  const uint32_t slot = blockIdx.x;
+  const uint32_t c = a.tile_count[slot];
+  if (c == 0) return;
+  const uint64_t base = a.tile_off[slot];
+  const fdy_override* src = a.ovr_tile + (uint64_t)slot * kTileWords;
+  for (uint32_t i = threadIdx.x; i < c; i += 256) a.ovr[base + i] = src[i];
 }
 
 // ---- switch --------------------------------------------------------------
@@ -808,25 +942,37 @@ __global__ __launch_bounds__(256) void k_switch(SwitchArgs a) {
 
 __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint64_t* __restrict__ in,
                                                          uint64_t* __restrict__ out, uint64_t n, int vec) {
-  __shared__ uint64_t s_top[kRelocLdsKeys];
-  if (R.n)
-    for (uint32_t i = threadIdx.x; i < R.n_top; i += kRelocThreads) s_top[i] = R.level[R.n_levels][i];
-  __syncthreads();
-  const uint64_t stride = (uint64_t)gridDim.x * kRelocThreads;
-  uint64_t i = (uint64_t)blockIdx.x * kRelocThreads + threadIdx.x;
+  // Each thread owns kRelocPairs 16-byte pairs per chunk (coalesced across
+  // the workgroup): all loads first, then the searches, then the stores, so
+  // the searches of 2 * kRelocPairs words overlap.
+  const uint64_t chunk = (uint64_t)kRelocThreads * kRelocPairs;
   if (vec) {
     const uint64_t pairs = n / 2;
     const ulonglong2* in2 = reinterpret_cast<const ulonglong2*>(in);
     ulonglong2* out2 = reinterpret_cast<ulonglong2*>(out);
-    for (uint64_t p = i; p < pairs; p += stride) {
-      ulonglong2 v = in2[p];
-      v.x = reloc_word(R, s_top, v.x);
-      v.y = reloc_word(R, s_top, v.y);
-      out2[p] = v;
+    for (uint64_t c = (uint64_t)blockIdx.x * chunk; c < pairs; c += (uint64_t)gridDim.x * chunk) {
+      ulonglong2 v[kRelocPairs];
+#pragma unroll
+      for (uint32_t q = 0; q < kRelocPairs; ++q) {
+        const uint64_t p = c + q * kRelocThreads + threadIdx.x;
+        v[q] = p < pairs ? in2[p] : ulonglong2{0, 0};
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kRelocPairs; ++q) {
+        v[q].x = reloc_word(R, v[q].x);
+        v[q].y = reloc_word(R, v[q].y);
+      }
+#pragma unroll
+      for (uint32_t q = 0; q < kRelocPairs; ++q) {
+        const uint64_t p = c + q * kRelocThreads + threadIdx.x;
+        if (p < pairs) out2[p] = v[q];
+      }
     }
-    if (i == 0 && (n & 1)) out[n - 1] = reloc_word(R, s_top, in[n - 1]);
+    if (blockIdx.x == 0 && threadIdx.x == 0 && (n & 1)) out[n - 1] = reloc_word(R, in[n - 1]);
   } else {
-    for (uint64_t p = i; p < n; p += stride) out[p] = reloc_word(R, s_top, in[p]);
+    const uint64_t stride = (uint64_t)gridDim.x * kRelocThreads;
+    for (uint64_t p = (uint64_t)blockIdx.x * kRelocThreads + threadIdx.x; p < n; p += stride)
+      out[p] = reloc_word(R, in[p]);
   }
 }
 
@@ -852,11 +998,11 @@ hipError_t launch_diff(const RestoreArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_fill_u64(uint64_t* p, uint64_t n, uint64_t v, hipStream_t s) {
-  if (n == 0) return hipSuccess;
-  uint64_t blocks = (n + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  hipLaunchKernelGGL(k_fill_u64, dim3((uint32_t)blocks), dim3(256), 0, s, p, n, v);
+hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -873,9 +1019,9 @@ hipError_t launch_switch(const SwitchArgs& a, hipStream_t s) {
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s) {
   if (n == 0) return hipSuccess;
   const int vec = ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-  uint64_t per_block = (uint64_t)kRelocThreads * (vec ? 2 : 1);
+  const uint64_t per_block = (uint64_t)kRelocThreads * (vec ? 2 * kRelocPairs : 1);
   uint64_t blocks = (n + per_block - 1) / per_block;
-  if (blocks > 256 * 16) blocks = 256 * 16;
+  if (blocks > 256 * 32) blocks = 256 * 32;
   hipLaunchKernelGGL(k_reloc, dim3((uint32_t)blocks), dim3(kRelocThreads), 0, s, r, in, out, n, vec);
   return hipGetLastError();
 }

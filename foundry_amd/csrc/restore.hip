@@ -103,12 +103,11 @@ struct HostStage {
   }
 };
 
-// The interval search structure: level 0 holds every interval's lo, each
-// higher level every 16th key of the level below, up to a top level small
-// enough for LDS.  Lower levels are padded with UINT64_MAX to whole nodes.
+// The interval search structure: a bucket index of 64-byte lines with about
+// one bucket per two intervals, 16-byte {hi, delta} records, and the lo keys
+// for crowded buckets (see RelocDev).
 struct RelocPlan {
-  DevBuf levels[8];
-  DevBuf hi, delta;
+  DevBuf bucket, rec, lo;
   RelocDev dev{};
 };
 
@@ -125,36 +124,50 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
       return err(FDY_E_INVALID, "intervals " + std::to_string(i - 1) + " and " + std::to_string(i) +
                                     " overlap or are not sorted by lo");
   }
-  std::vector<std::vector<uint64_t>> lv;
-  lv.emplace_back(lo, lo + n);
-  while (lv.back().size() > kRelocLdsKeys) {
-    std::vector<uint64_t>& cur = lv.back();
-    std::vector<uint64_t> next;
-    for (size_t j = 0; j < cur.size(); j += kRelocFanout) next.push_back(cur[j]);
-    cur.resize((cur.size() + kRelocFanout - 1) / kRelocFanout * kRelocFanout, UINT64_MAX);
-    lv.push_back(std::move(next));
-    if (lv.size() > 8) return err(FDY_E_INVALID, "interval table too large");
+  if (n > 0xFFFFFFF0ull) return err(FDY_E_INVALID, "more than 2^32 intervals");
+  const uint64_t span = hi[n - 1] - lo[0];
+  if (span >> 54) return err(FDY_E_INVALID, "intervals span more than 2^54 bytes");
+  std::vector<RelocRec> rec(n);
+  for (uint64_t i = 0; i < n; ++i) rec[i] = RelocRec{hi[i], nlo[i] - lo[i]};
+  // Bucket width: the smallest power of two giving at most ~n/2 buckets over
+  // [lo_min, hi_max], and at most 2^32 so in-bucket offsets fit in 32 bits.
+  uint64_t target = 1;
+  while (target * 2 < n) target <<= 1;
+  uint32_t shift = 0;
+  while ((span >> shift) + 1 > target) ++shift;
+  if (shift > 32) shift = 32;
+  const uint64_t nb = (span >> shift) + 1;  // w - lo_min <= span, so (w - lo_min) >> shift < nb
+  auto start = [&](uint64_t b) -> uint64_t {
+    const uint64_t off = b << shift;  // b <= nb, so no overflow below 2^55
+    return off > UINT64_MAX - lo[0] ? UINT64_MAX : lo[0] + off;
+  };
+  std::vector<RelocBucket> bucket(nb);
+  uint64_t i = 0, j = 0;  // i: last lo <= bucket start; j: last lo < next bucket's start
+  for (uint64_t b = 0; b < nb; ++b) {
+    const uint64_t s0 = start(b), s1 = start(b + 1);
+    while (i + 1 < n && lo[i + 1] <= s0) ++i;
+    if (j < i) j = i;
+    while (j + 1 < n && lo[j + 1] < s1) ++j;
+    RelocBucket& e = bucket[b];
+    e.first = (uint32_t)i;
+    e.count = (uint32_t)(j - i);
+    for (uint32_t k = 0; k < kBucketOffsets; ++k)
+      e.off[k] = k < e.count ? (uint32_t)(lo[i + 1 + k] - s0) : 0xFFFFFFFFu;
   }
-  for (size_t k = 0; k < lv.size(); ++k) {
-    int rc = dev_alloc(out->levels[k], lv[k].size() * 8, "interval search level");
-    if (rc) return rc;
-    FDY_HIP(hipMemcpy(out->levels[k].p, lv[k].data(), lv[k].size() * 8, hipMemcpyHostToDevice));
-    out->dev.level[k] = out->levels[k].as<uint64_t>();
-  }
-  std::vector<uint64_t> delta(n);
-  for (uint64_t i = 0; i < n; ++i) delta[i] = nlo[i] - lo[i];
-  int rc = dev_alloc(out->hi, n * 8, "interval hi");
-  if (!rc) rc = dev_alloc(out->delta, n * 8, "interval delta");
+  int rc = dev_alloc(out->bucket, nb * sizeof(RelocBucket), "interval buckets");
+  if (!rc) rc = dev_alloc(out->rec, n * sizeof(RelocRec), "interval records");
+  if (!rc) rc = dev_alloc(out->lo, n * 8, "interval starts");
   if (rc) return rc;
-  FDY_HIP(hipMemcpy(out->hi.p, hi, n * 8, hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(out->delta.p, delta.data(), n * 8, hipMemcpyHostToDevice));
-  out->dev.hi = out->hi.as<uint64_t>();
-  out->dev.delta = out->delta.as<uint64_t>();
+  FDY_HIP(hipMemcpy(out->bucket.p, bucket.data(), nb * sizeof(RelocBucket), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->rec.p, rec.data(), n * sizeof(RelocRec), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->lo.p, lo, n * 8, hipMemcpyHostToDevice));
+  out->dev.bucket = out->bucket.as<RelocBucket>();
+  out->dev.rec = out->rec.as<RelocRec>();
+  out->dev.lo = out->lo.as<uint64_t>();
   out->dev.n = n;
   out->dev.lo_min = lo[0];
   out->dev.hi_max = hi[n - 1];
-  out->dev.n_levels = (uint32_t)lv.size() - 1;
-  out->dev.n_top = (uint32_t)lv.back().size();
+  out->dev.shift = shift;
   out->dev.policy = policy;
   return FDY_OK;
 }
@@ -181,13 +194,13 @@ struct fdy_archive {
   uint32_t num_slots = 0;
 
   DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, lookback, ticket, live_cur;
-  DevBuf aux, image, live, ovr, ovr_off;
+  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, live_cur;
+  DevBuf aux, image, live, ovr, ovr_off, ovr_tile, tile_count, tile_off;
 
   RelocPlan reloc;
   bool use_explicit = false;
-  uint16_t epoch = 0;
   bool restored = false;
+  hipStream_t last_stream = nullptr;
 
   // Host copies taken after a restore (one synchronisation, then reused).
   bool cached = false;
@@ -197,7 +210,7 @@ struct fdy_archive {
 
   bool timing = false;
   bool timed = false;
-  hipEvent_t ev[5] = {};
+  hipEvent_t ev[6] = {};
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)
@@ -212,6 +225,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   const uint32_t G = a->G;
   a->graphs.resize(G);
   std::vector<std::string> errs(G);
+  const X2nTable x2n = make_x2n_table();
   parallel_for(G, default_threads(), [&](uint32_t i) {
     GraphView v;
     errs[i] = validate_image(stage.p + off[i], sizes[i], &v);
@@ -225,6 +239,10 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
     d.num_nodes = v.hdr.num_nodes;
     d.num_deps = v.hdr.num_deps;
     d.flags = v.hdr.flags;
+    // Digest streams: key bytes, dependency entries, 16-byte records per node (twice).
+    d.crc_fin[0] = crc_finish_term(x2n.v, v.sec[FDY_SEC_TOPOLOGY_KEY].size);
+    d.crc_fin[1] = crc_finish_term(x2n.v, 8ull * v.hdr.num_deps);
+    d.crc_fin[2] = d.crc_fin[3] = crc_finish_term(x2n.v, 16ull * v.hdr.num_nodes);
     // Capacity of the param image: every param rounds up to whole words, and
     // an extra-style node's arg buffer can end in a partial word.
     uint64_t cap = (v.sec[FDY_SEC_PARAM_DATA].size + 7) / 8 + v.sec[FDY_SEC_PARAM_INDEX].size / 8 +
@@ -279,8 +297,9 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->live_src, 4 * nodes, "live node sources");
   alloc(a->tile_node, 4 * slots, "tile table");
   alloc(a->slot_graph, 4 * slots, "slot table");
-  alloc(a->lookback, 8 * slots, "look-back state");
-  alloc(a->ticket, 256, "tile ticket");
+  alloc(a->tile_count, 4 * slots, "tile record counts");
+  alloc(a->tile_off, 8 * slots, "tile record offsets");
+  alloc(a->ovr_tile, sizeof(fdy_override) * (uint64_t)kTileWords * slots, "tile record regions");
   alloc(a->aux, 8 * words, "ragged word sources");
   alloc(a->image, 8 * words, "param images");
   alloc(a->live, 8 * words, "live images");
@@ -295,8 +314,6 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(a->slot_graph.p, slot_graph.data(), 4 * slots, hipMemcpyHostToDevice));
-  FDY_HIP(hipMemset(a->lookback.p, 0, 8 * slots));
-  FDY_HIP(hipMemset(a->ticket.p, 0, 256));
   return FDY_OK;
 }
 
@@ -426,14 +443,16 @@ int fdy_archive_close(fdy_archive* a) {
   return FDY_OK;
 }
 
-int fdy_archive_info_get(const fdy_archive* a, fdy_archive_info* o) {
+int fdy_archive_info_get(fdy_archive* a, fdy_archive_info* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   std::memset(o, 0, sizeof(*o));
   o->num_graphs = a->G;
   o->total_nodes = a->total_nodes;
   o->file_bytes = a->img_bytes;
   o->num_intervals = a->reloc.dev.n;
-  if (a->cached) {
+  if (a->restored) {
+    int rc = ensure_cache(a, a->last_stream);
+    if (rc) return rc;
     for (uint32_t i = 0; i < a->G; ++i) {
       o->num_groups += a->h_tmpl[i] == i;
       o->total_words += a->h_gwords[i];
@@ -477,17 +496,12 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (!a) return err(FDY_E_INVALID, "null archive");
   hipStream_t s = static_cast<hipStream_t>(stream);
   FDY_HIP(hipSetDevice(a->device));
-  if (++a->epoch == 0) {  // 16-bit epochs wrapped: clear stale look-back words
-    FDY_HIP(launch_fill_u64(a->lookback.as<uint64_t>(), a->num_slots, 0, s));
-    a->epoch = 1;
-  }
   RestoreArgs r{};
   r.img = a->img.as<uint8_t>();
   r.graphs = a->dgraphs.as<DevGraph>();
   r.cc = a->cc.as<CrcConsts>();
   r.num_graphs = a->G;
   r.num_slots = a->num_slots;
-  r.epoch = a->epoch;
   r.digests = a->digests.as<uint64_t>();
   r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
   r.template_of = a->tmpl.as<uint32_t>();
@@ -506,8 +520,9 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.live_cur = a->live_cur.as<uint32_t>();
   r.ovr = a->ovr.as<fdy_override>();
   r.ovr_off = a->ovr_off.as<uint64_t>();
-  r.lookback = a->lookback.as<uint64_t>();
-  r.ticket = a->ticket.as<uint32_t>();
+  r.ovr_tile = a->ovr_tile.as<fdy_override>();
+  r.tile_count = a->tile_count.as<uint32_t>();
+  r.tile_off = a->tile_off.as<uint64_t>();
   r.reloc = a->reloc.dev;
   if (a->timing) {
     for (hipEvent_t& e : a->ev)
@@ -522,9 +537,12 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
   FDY_HIP(launch_diff(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
+  FDY_HIP(launch_compact(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
   a->timed = a->timing;
   a->restored = true;
   a->cached = false;
+  a->last_stream = s;
   return FDY_OK;
 }
 
@@ -537,12 +555,13 @@ int fdy_set_timing(fdy_archive* a, int enabled) {
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
-  FDY_HIP(hipEventSynchronize(a->ev[4]));
+  FDY_HIP(hipEventSynchronize(a->ev[5]));
   FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
   FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[3], a->ev[4]));
-  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[4]));
+  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[4], a->ev[5]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[5]));
   return FDY_OK;
 }
 

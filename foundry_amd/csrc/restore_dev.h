@@ -11,12 +11,10 @@
 namespace fdy {
 
 // Words of the param image handled by one diff tile, and its thread count.
-constexpr uint32_t kDiffThreads = 512;
-constexpr uint32_t kDiffWordsPerThread = 8;
+constexpr uint32_t kDiffThreads = 256;
+constexpr uint32_t kDiffWordsPerThread = 16;
 constexpr uint32_t kTileWords = kDiffThreads * kDiffWordsPerThread;  // 4096
 constexpr uint32_t kDiffWindow = 512;    // node descriptors staged in LDS per tile
-constexpr uint32_t kRelocFanout = 16;    // keys per interval-search node
-constexpr uint32_t kRelocLdsKeys = 4096; // top search level kept in LDS (32 KB)
 constexpr uint32_t kNoTile = 0xFFFFFFFFu;
 
 // Internal node flag bits beyond the public FDY_NODE_* bits (0x0F).
@@ -40,6 +38,7 @@ struct DevGraph {
   uint64_t word_base;    // global index of word 0 in R / live / aux
   uint32_t tile_base;    // first diff-tile slot
   uint32_t tile_cap;     // number of diff-tile slots
+  uint64_t crc_fin[4];   // CRC-64/XZ finishing terms of the key, edge, type, kernel-entry streams
 };
 
 // Per-node work description written by the node pass for the diff pass.
@@ -53,18 +52,35 @@ struct NodeDesc {
 };
 static_assert(sizeof(NodeDesc) == 32, "NodeDesc is 32 B");
 
-// Interval search structure (see restore.hip: RelocPlanHost).
+// End and shift of one saved allocation interval (its lo is implied by the search).
+struct RelocRec {
+  uint64_t hi;
+  uint64_t delta;  // new_lo - lo (mod 2^64)
+};
+static_assert(sizeof(RelocRec) == 16, "RelocRec is 16 B");
+
+// One 64-byte line of the bucket index.  Bucket b covers addresses
+// [lo_min + b*2^shift, lo_min + (b+1)*2^shift).  `first` is the last
+// interval whose lo is <= the bucket's first address; intervals first+1 ..
+// first+count start inside the bucket, and off[k] holds lo - bucket start
+// of interval first+1+k for the first min(count, 14) of them.
+constexpr uint32_t kBucketOffsets = 14;
+struct RelocBucket {
+  uint32_t first;
+  uint32_t count;
+  uint32_t off[kBucketOffsets];
+};
+static_assert(sizeof(RelocBucket) == 64, "RelocBucket is one 64-byte line");
+
 struct RelocDev {
-  const uint64_t* level[8];  // level[0] = lo (padded); level[k] = every 16th key of level[k-1]
-  const uint64_t* hi;
-  const uint64_t* delta;     // new_lo - lo
-  uint64_t n;                // intervals; 0 = relocation off
+  const RelocBucket* bucket;
+  const RelocRec* rec;
+  const uint64_t* lo;  // every interval's lo (for buckets with > 14 starts)
+  uint64_t n;          // intervals; 0 = relocation off
   uint64_t lo_min;
   uint64_t hi_max;
-  uint32_t n_levels;         // global levels below the LDS top (level[n_levels] is the top)
-  uint32_t n_top;
+  uint32_t shift;      // <= 32, so offsets inside a bucket fit in 32 bits
   uint32_t policy;
-  uint32_t pad;
 };
 
 __device__ inline uint32_t ld_u32(const uint8_t* p) {
@@ -77,28 +93,42 @@ __device__ inline uint64_t ld_u64(const uint8_t* p) {
   return (uint64_t)ld_u32(p) | ((uint64_t)ld_u32(p + 4) << 32);
 }
 
-// Relocate one word.  `top` is the top search level (LDS or global).
-__device__ inline uint64_t reloc_word(const RelocDev& r, const uint64_t* top, uint64_t w) {
+// Relocate one word: the last interval with lo <= w moves w if w < hi
+// (w <= hi under the inclusive policy).
+__device__ inline uint64_t reloc_word(const RelocDev& r, uint64_t w) {
   if (r.n == 0 || w < r.lo_min) return w;
   if (r.policy ? (w > r.hi_max) : (w >= r.hi_max)) return w;
-  // Top level: last j with top[j] <= w (top[0] == lo_min <= w).
-  uint32_t lo = 0, len = r.n_top;
-  while (len > 1) {
-    uint32_t half = len >> 1;
-    if (top[lo + half] <= w) lo += half;
-    len -= half;
-  }
-  uint64_t j = lo;
-  for (int k = (int)r.n_levels - 1; k >= 0; --k) {
-    const uint64_t* node = r.level[k] + j * kRelocFanout;
-    uint32_t cnt = 0;
+  const uint64_t rel = w - r.lo_min;
+  const uint64_t b = rel >> r.shift;
+  const uint32_t x = (uint32_t)(rel - (b << r.shift));
+  // The first 16 bytes carry `first`, `count` and two offsets, which is the
+  // whole bucket most of the time; the other 48 are read only when needed.
+  const uint4* line = reinterpret_cast<const uint4*>(r.bucket + b);
+  const uint4 q0 = line[0];
+  const uint32_t count = q0.y;
+  uint32_t c = (count > 0 && q0.z <= x) + (count > 1 && q0.w <= x);
+  if (count > 2) {
+    const uint4 q1 = line[1], q2 = line[2], q3 = line[3];
+    const uint32_t m = count < kBucketOffsets ? count : kBucketOffsets;
+    const uint32_t off[kBucketOffsets - 2] = {q1.x, q1.y, q1.z, q1.w, q2.x, q2.y,
+                                              q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
 #pragma unroll
-    for (uint32_t q = 0; q < kRelocFanout; ++q) cnt += node[q] <= w;
-    j = j * kRelocFanout + cnt - 1;
+    for (uint32_t k = 0; k < kBucketOffsets - 2; ++k) c += (k + 2 < m) & (off[k] <= x);
   }
-  uint64_t hi = r.hi[j];
-  bool inside = r.policy ? (w <= hi) : (w < hi);
-  return inside ? w + r.delta[j] : w;
+  uint32_t i = q0.x + c;
+  if (count > kBucketOffsets && c == kBucketOffsets) {
+    // More starts than the line holds: binary search the rest of the bucket.
+    uint32_t lo = i, hi = q0.x + count;
+    while (hi > lo) {
+      const uint32_t mid = (lo + hi + 1) >> 1;
+      if (r.lo[mid] <= w) lo = mid;
+      else hi = mid - 1;
+    }
+    i = lo;
+  }
+  const RelocRec iv = r.rec[i];
+  const bool inside = r.policy ? (w <= iv.hi) : (w < iv.hi);
+  return inside ? w + iv.delta : w;
 }
 
 }  // namespace fdy

@@ -103,7 +103,8 @@ int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes,
                             fdy_archive** out);
 
 int fdy_archive_close(fdy_archive* a);
-int fdy_archive_info_get(const fdy_archive* a, fdy_archive_info* out);
+/* Sizes and counts.  After fdy_restore this synchronizes the restore's stream. */
+int fdy_archive_info_get(fdy_archive* a, fdy_archive_info* out);
 
 /* Saved allocation intervals [lo, hi) -> new_lo, sorted by lo, non-overlapping.
  * n == 0 disables relocation (words pass through).  The interval model is the
@@ -180,6 +181,7 @@ typedef struct fdy_restore_timing {
   float group_ms;   /* template assignment */
   float node_ms;    /* per-node compare, layout, type and kernel-entry digests */
   float diff_ms;    /* fused diff + relocate */
+  float compact_ms; /* per-tile override regions -> dense canonical array */
   float total_ms;
 } fdy_restore_timing;
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
