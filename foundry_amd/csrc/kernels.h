@@ -26,7 +26,10 @@ struct RestoreArgs {
   NodeDesc* node_desc;
   uint64_t* node_ptrs;        // 2 per node
   uint32_t* tile_node;        // per slot
+  uint32_t* tslots;           // slots of template graphs holding words (capacity: num_slots)
+  uint32_t* tslot_count;      // entries of tslots
   const uint32_t* slot_graph; // per slot
+  SlotDesc* slot_desc;        // per slot
   uint64_t* aux;              // ragged-word sources (per word)
   uint64_t* image;            // relocated param images R
   uint64_t* live;             // live images (template graphs)
@@ -34,9 +37,9 @@ struct RestoreArgs {
   uint32_t* live_cur;         // per graph
   fdy_override* ovr;          // dense override records, canonical order
   uint64_t* ovr_off;          // G+1
-  fdy_override* ovr_tile;     // per-slot record regions (kTileWords each)
-  uint32_t* tile_count;       // records per slot
-  uint64_t* tile_off;         // exclusive prefix of tile_count
+  fdy_override* ovr_tile;     // record regions, kSubWords records per (slot, sub-range)
+  uint32_t* sub_count;        // records per (slot, sub-range)
+  uint32_t* graph_count;      // records per graph
   RelocDev reloc;
 };
 

@@ -9,14 +9,17 @@
 //             against the template's node, memset/memcpy pointer relocation,
 //             node-type and kernel-entry digests, the node descriptors the
 //             diff pass consumes, and the diff-tile -> first-node table.
-//   k_diff    one workgroup per 4096-word tile of a graph's param image:
-//             coalesced 8-byte loads of the graph's and the template's words
-//             (software-pipelined), relocation through a bucket-indexed
-//             interval search, the relocated image store, and ballot + LDS
-//             prefix-sum compaction of the differing words into the tile's
-//             own record region.
-//   k_scan    prefix of the per-tile record counts -> per-graph offsets.
-//   k_compact tile regions -> the dense override array, canonical order.
+//   k_diff_t  the template graphs' words, relocated through a bucket-indexed
+//             interval search into R and the live image (1024-word units).
+//   k_diff_m  one workgroup per 4096-word tile of every other graph: coalesced
+//             8-byte loads of the graph's and the template's words, the
+//             template's relocated word reused where the raw words are equal,
+//             lockstep batched searches for the rest, the relocated image
+//             store, and per-wave ballot compaction of the differing words
+//             into override record regions.
+//   k_scan    prefix of the per-region record counts -> per-graph offsets.
+//   k_compact record regions -> the dense override array in canonical order,
+//             completing each record's node and template word index.
 //   k_switch  override scatter for one graph switch.
 //   k_reloc   streaming relocation of packed words.
 #include "kernels.h"
@@ -142,6 +145,7 @@ __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
 
 __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
   const uint32_t G = a.num_graphs;
+  if (threadIdx.x == 0) *a.tslot_count = 0;  // the node pass lists template slots here
   if (a.explicit_template) {
     for (uint32_t i = threadIdx.x; i < G; i += kGroupThreads) a.template_of[i] = a.explicit_template[i];
     return;
@@ -444,7 +448,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
   __shared__ uint64_t s_nib[kTreeLevels][16][16];
   __shared__ uint64_t s_wave[kNodeThreads / 64];
   __shared__ uint32_t s_tmp[kNodeThreads / 64];
-  __shared__ uint32_t s_status, s_key_differs, s_str_differs, s_words;
+  __shared__ uint32_t s_status, s_key_differs, s_str_differs, s_words, s_flat, s_tbase;
   __shared__ unsigned long long s_pbytes;
   stage_crc_tables(a.cc, true, s_slice, s_nib);
 
@@ -461,6 +465,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
     s_key_differs = 0;
     s_str_differs = 0;
     s_pbytes = 0;
+    s_flat = 1;
   }
   __syncthreads();
   if (!is_t) {
@@ -574,6 +579,15 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
     // A template whose image overflows its capacity (overlapping param
     // ranges) has no usable words past the capacity; never index them.
     if ((flags & kNodeCompare) && (uint64_t)tword + words_t > Gt.word_cap) flags &= ~kNodeCompare;
+    // The graph's image is flat when every node with words is aligned and
+    // placed canonically (word w of the image at param-data byte 8w), and
+    // likewise in the template's image for every compared node.
+    if (valid && words_g) {
+      const bool ok = !(flags & (FDY_NODE_RAGGED | kNodeRaggedT)) && src_g == Gg.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword &&
+                      (is_t || ((flags & kNodeCompare) && tword == gword &&
+                                src_t == Gt.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword));
+      if (!ok) s_flat = 0;
+    }
     if (valid) {
       const uint64_t gi = Gg.node_base + n;
       NodeDesc d;
@@ -619,12 +633,33 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
     a.pbytes[g] = s_pbytes;
     a.digests[4ull * g + 2] = acc_type ^ Gg.crc_fin[2];
     a.digests[4ull * g + 3] = acc_kent ^ Gg.crc_fin[3];
-    if (is_t) a.live_cur[g] = g;
+    if (is_t) {
+      a.live_cur[g] = g;
+      // List the template's slots that hold words for k_diff_t.
+      s_tbase = atomicAdd(a.tslot_count, (s_words + kTileWords - 1) / kTileWords);
+    }
   }
   __syncthreads();
-  const uint32_t first_unused = (s_words + kTileWords - 1) / kTileWords;
-  for (uint32_t k = first_unused + threadIdx.x; k < Gg.tile_cap; k += kNodeThreads)
-    a.tile_node[Gg.tile_base + k] = kNoTile;
+  const uint32_t words = s_words;
+  const uint32_t first_unused = (words + kTileWords - 1) / kTileWords;
+  const uint32_t sflags = (s_flat ? kSlotFlat | (is_t ? 0u : kSlotCompare) : 0u) | (is_t ? kSlotTemplate : 0u);
+  for (uint32_t k = threadIdx.x; k < Gg.tile_cap; k += kNodeThreads) {
+    if (k >= first_unused) a.tile_node[Gg.tile_base + k] = kNoTile;
+    SlotDesc sd;
+    sd.kg = Gg.sec_off[FDY_SEC_PARAM_DATA];
+    sd.kt = Gt.sec_off[FDY_SEC_PARAM_DATA];
+    sd.word_base = Gg.word_base;
+    sd.wbeg = (uint32_t)min((uint64_t)k * kTileWords, (uint64_t)words);
+    sd.wend = (uint32_t)min((uint64_t)(k + 1) * kTileWords, (uint64_t)words);
+    sd.graph = g;
+    sd.tmpl = t;
+    sd.flags = sflags | (k == 0 ? kSlotFirst : 0u);
+    sd.t_cap = Gt.word_cap;
+    sd.pad[0] = sd.pad[1] = 0;
+    sd.t_word_base = Gt.word_base;
+    a.slot_desc[Gg.tile_base + k] = sd;
+    if (is_t && k < first_unused) a.tslots[s_tbase + k] = Gg.tile_base + k;
+  }
 }
 
 // ---- diff pass ----------------------------------------------------------
@@ -641,246 +676,378 @@ __device__ inline uint64_t load_bytes(const uint8_t* img, uint64_t byte, uint32_
   return width >= 8 ? v : v & ((1ull << (8 * width)) - 1);
 }
 
-// The node holding graph-local word w: the last node whose first word is <= w,
-// searched in the LDS window first and in global memory past it.
-__device__ inline uint32_t find_node(const NodeDesc* s_nd, uint32_t nwin, const NodeDesc* nd, uint32_t n0,
-                                     uint32_t N, uint64_t w, NodeDesc* out) {
-  uint32_t lo = 0, len = nwin;
-  while (len > 1) {
-    const uint32_t half = len >> 1;
-    if (s_nd[lo + half].gword <= w) lo += half;
-    len -= half;
-  }
-  NodeDesc d = s_nd[lo];
-  uint32_t node = n0 + lo;
-  if (lo == nwin - 1 && nwin == kDiffWindow && w >= (uint64_t)d.gword + d.nwords) {
-    uint32_t l2 = node, h2 = N;
-    while (h2 - l2 > 1) {
-      const uint32_t mid = (l2 + h2) >> 1;
-      if (nd[mid].gword <= w) l2 = mid;
-      else h2 = mid;
-    }
-    d = nd[l2];
-    node = l2;
-  }
-  *out = d;
-  return node;
+// A slot descriptor, loaded whole before any branch: left to itself the
+// compiler loads each field at its first use, behind branches, and every
+// such load is another serial round trip before the tile's loads can start.
+__device__ inline SlotDesc load_slot(const SlotDesc* p) {
+  const uint4* q = reinterpret_cast<const uint4*>(p);
+  const uint4 v0 = q[0], v1 = q[1], v2 = q[2], v3 = q[3];
+  asm volatile("" ::"s"(v0.x), "s"(v0.y), "s"(v0.z), "s"(v0.w), "s"(v1.x), "s"(v1.y), "s"(v1.z), "s"(v1.w),
+               "s"(v2.x), "s"(v2.y), "s"(v2.z), "s"(v2.w), "s"(v3.x), "s"(v3.y), "s"(v3.z), "s"(v3.w));
+  SlotDesc d;
+  static_assert(sizeof(SlotDesc) == 4 * sizeof(uint4), "SlotDesc is four 16-byte words");
+  uint4* o = reinterpret_cast<uint4*>(&d);
+  o[0] = v0;
+  o[1] = v1;
+  o[2] = v2;
+  o[3] = v3;
+  return d;
 }
 
-// Loads of one batch of B words per thread: the graph's raw word and, where
-// the node is compared, the template's raw word.  Bit j of *valid / *cmp /
-// *full marks word j present / compared / a whole 8-byte word.
-template <uint32_t B>
-__device__ inline void diff_load(const RestoreArgs& a, bool flat, const uint8_t* pg, const uint8_t* pt, bool cflat,
-                                 const NodeDesc* s_nd, uint32_t nwin, const NodeDesc* nd, uint32_t n0, uint32_t N,
-                                 const DevGraph& G, const DevGraph& T, uint64_t w0, uint64_t wend, uint64_t* rg,
-                                 uint64_t* rt, uint32_t* valid, uint32_t* cmp, uint32_t* full) {
-  uint32_t v = 0, c = 0, f = 0;
-  if (flat) {
+// Stage the descriptors of the nodes holding slot `slot`'s words in LDS
+// (from its first node to the next slot's first node, at most kDiffWindow).
+struct NodeWindow {
+  const NodeDesc* nd;  // the graph's node descriptors
+  uint32_t n0, N, nwin;
+};
+
+__device__ inline NodeWindow stage_window(const RestoreArgs& a, const DevGraph& G, uint32_t slot, NodeDesc* s_nd) {
+  NodeWindow nw;
+  const uint32_t k = slot - G.tile_base;
+  nw.n0 = a.tile_node[slot];
+  nw.N = G.num_nodes;
+  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
+  const uint32_t n_last = n_next == kNoTile ? nw.N - 1 : n_next;
+  nw.nwin = min(kDiffWindow, n_last - nw.n0 + 1);
+  nw.nd = a.node_desc + G.node_base;
+  for (uint32_t i = threadIdx.x; i < nw.nwin; i += blockDim.x) s_nd[i] = nw.nd[nw.n0 + i];
+  return nw;
+}
+
+// The nodes holding graph-local words w[0..J): for each, the last node whose
+// first word is <= w[j].  The searches over the LDS window run in lockstep
+// (the window size is uniform), so their LDS reads overlap; a word past a
+// full window continues in global memory.  Nodes without words never
+// match, since the node holding w follows them.
+template <uint32_t J>
+__device__ inline void find_nodes(const NodeDesc* s_nd, const NodeWindow& nw, const uint64_t* w, uint32_t* node) {
+  uint32_t lo[J];
 #pragma unroll
-    for (uint32_t j = 0; j < B; ++j) {
-      const uint64_t w = w0 + (uint64_t)j * kDiffThreads;
-      rg[j] = rt[j] = 0;
-      if (w < wend) {
-        v |= 1u << j;
-        rg[j] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
-        if (cflat) rt[j] = *reinterpret_cast<const uint64_t*>(pt + 8 * w);
+  for (uint32_t j = 0; j < J; ++j) lo[j] = 0;
+  for (uint32_t len = nw.nwin; len > 1;) {
+    const uint32_t half = len >> 1;
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j)
+      if (s_nd[lo[j] + half].gword <= w[j]) lo[j] += half;
+    len -= half;
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) {
+    node[j] = nw.n0 + lo[j];
+    if (nw.nwin == kDiffWindow && lo[j] == kDiffWindow - 1) {
+      const NodeDesc& d = s_nd[lo[j]];
+      if (w[j] >= (uint64_t)d.gword + d.nwords) {
+        uint32_t l2 = node[j], h2 = nw.N;
+        while (h2 - l2 > 1) {
+          const uint32_t mid = (l2 + h2) >> 1;
+          if (nw.nd[mid].gword <= w[j]) l2 = mid;
+          else h2 = mid;
+        }
+        node[j] = l2;
       }
     }
-    f = v;
-    c = cflat ? v : 0;
-  } else {
+  }
+}
+
+__device__ inline NodeDesc window_desc(const NodeDesc* s_nd, const NodeWindow& nw, uint32_t node) {
+  const uint32_t i = node - nw.n0;
+  return i < nw.nwin ? s_nd[i] : nw.nd[node];
+}
+
+// Raw word w of a graph whose node descriptor is d (general path): ragged
+// words through their recorded byte position and width.
+__device__ inline uint64_t load_word(const RestoreArgs& a, const DevGraph& G, const NodeDesc& d, uint64_t w,
+                                     bool ragged, uint64_t src, uint32_t* width) {
+  if (ragged) {
+    const uint64_t x = a.aux[G.word_base + w];
+    *width = (uint32_t)(x & 15);
+    return load_bytes(a.img, x >> 4, *width);
+  }
+  *width = 8;
+  return *reinterpret_cast<const uint64_t*>(a.img + src + 8ull * (w - d.gword));
+}
+
+// Template graphs: relocate their words into R and the live image.  The
+// template slots listed by the node pass are cut into units of kTUnit words
+// (kTWords per thread, so one search batch), spread over the grid.
+constexpr uint32_t kTThreads = 256;
+constexpr uint32_t kTWords = 4;
+constexpr uint32_t kTUnit = kTThreads * kTWords;
+constexpr uint32_t kTUnitsPerTile = kTileWords / kTUnit;
+static_assert(kTileWords % kTUnit == 0, "template units tile a slot");
+
+__global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
+  __shared__ NodeDesc s_nd[kDiffWindow];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t units = *a.tslot_count * kTUnitsPerTile;
+  for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const uint32_t slot = a.tslots[u / kTUnitsPerTile];
+    const SlotDesc sd = load_slot(a.slot_desc + slot);
+    const uint64_t ubeg = (uint64_t)sd.wbeg + (u % kTUnitsPerTile) * kTUnit;
+    const uint64_t uend = min((uint64_t)sd.wend, ubeg + kTUnit);
+    if (ubeg >= uend) continue;  // uniform over the block
+    uint64_t v[kTWords], r[kTWords];
+    uint32_t m = 0;
+    if (sd.flags & kSlotFlat) {
+      const uint8_t* pg = a.img + sd.kg;
 #pragma unroll
-    for (uint32_t j = 0; j < B; ++j) {
-      const uint64_t w = w0 + (uint64_t)j * kDiffThreads;
-      rg[j] = rt[j] = 0;
-      if (w >= wend) continue;
-      v |= 1u << j;
-      NodeDesc d;
-      find_node(s_nd, nwin, nd, n0, N, w, &d);
-      const uint32_t off = (uint32_t)(w - d.gword);
-      uint32_t width = 8;
-      if (d.flags & FDY_NODE_RAGGED) {
-        const uint64_t x = a.aux[G.word_base + w];
-        width = (uint32_t)(x & 15);
-        rg[j] = load_bytes(a.img, x >> 4, width);
-      } else {
-        rg[j] = *reinterpret_cast<const uint64_t*>(a.img + d.src_g + 8ull * off);
+      for (uint32_t q = 0; q < kTWords; ++q) {
+        const uint64_t w = ubeg + q * kTThreads + tid;
+        v[q] = 0;
+        if (w < uend) {
+          v[q] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
+          m |= 1u << q;
+        }
       }
-      if (width == 8) f |= 1u << j;
-      if (d.flags & kNodeCompare) {
-        c |= 1u << j;
-        const uint32_t tw = d.tword + off;
-        if (d.flags & kNodeRaggedT) {
-          const uint64_t x = a.aux[T.word_base + tw];
-          rt[j] = load_bytes(a.img, x >> 4, (uint32_t)(x & 15));
-        } else {
-          rt[j] = *reinterpret_cast<const uint64_t*>(a.img + d.src_t + 8ull * off);
+    } else {
+      const DevGraph& G = a.graphs[sd.graph];
+      __syncthreads();  // the previous unit's lookups are done with s_nd
+      const NodeWindow nw = stage_window(a, G, slot, s_nd);
+      __syncthreads();
+      uint64_t wv[kTWords];
+      uint32_t node[kTWords];
+#pragma unroll
+      for (uint32_t q = 0; q < kTWords; ++q) wv[q] = ubeg + q * kTThreads + tid;
+      find_nodes<kTWords>(s_nd, nw, wv, node);
+#pragma unroll
+      for (uint32_t q = 0; q < kTWords; ++q) {
+        const uint64_t w = wv[q];
+        v[q] = 0;
+        if (w < uend) {
+          const NodeDesc d = window_desc(s_nd, nw, node[q]);
+          uint32_t width;
+          v[q] = load_word(a, G, d, w, (d.flags & FDY_NODE_RAGGED) != 0, d.src_g, &width);
+          if (width == 8) m |= 1u << q;  // partial words are never relocated
         }
       }
     }
+    reloc_batch<kTWords>(a.reloc, v, r, m);
+    uint64_t* img_out = a.image + sd.word_base;
+    uint64_t* live_out = a.live + sd.word_base;
+#pragma unroll
+    for (uint32_t q = 0; q < kTWords; ++q) {
+      const uint64_t w = ubeg + q * kTThreads + tid;
+      if (w < uend) {
+        img_out[w] = r[q];
+        live_out[w] = r[q];
+      }
+    }
   }
-  *valid = v;
-  *cmp = c;
-  *full = f;
 }
 
-// One workgroup per tile slot.  Tiles are independent: each writes its
-// override records, in word order, to its own kTileWords-record region and
-// their number to tile_count; k_scan and k_compact then pack the regions
-// into the dense canonical array.
-__global__ __launch_bounds__(kDiffThreads) void k_diff(RestoreArgs a) {
-  constexpr uint32_t J = kDiffWordsPerThread;
-  constexpr uint32_t B = 4;                      // words per thread per batch
-  constexpr uint32_t kWaves = kDiffThreads / 64;
-  constexpr uint32_t kCounts = J * kWaves;       // per-(batch word, wave) override counts
-  static_assert(kCounts == 64 && J % B == 0, "tile shape");
+// The other graphs: one workgroup per slot; wave v of the workgroup owns the
+// slot's sub-range v (kSubWords consecutive words), lane l its words
+// v*kSubWords + j*64 + l for j < kMWords.  Relocation is a function of the
+// raw word, so where a compared word equals the template's raw word the
+// template's relocated word is taken from R; the words left to search are
+// gathered kSlots per lane and searched in lockstep batches.  Each wave
+// compacts its override records, in word order, into its own sub-range's
+// kSubWords-record region (graph-local word index, node filled in later by
+// k_compact) and their number into sub_count; flat tiles need neither LDS
+// nor a barrier.  k_scan and k_compact then pack the regions into the dense
+// canonical array.
+constexpr uint32_t kMThreads = kSubsPerSlot * 64;
+constexpr uint32_t kSlots = 2;  // searches per lane per batch (64 VGPRs: 8 waves per SIMD)
+
+// Eight waves per SIMD (at most 64 VGPRs): two workgroups per CU.
+__global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
+  constexpr uint32_t J = kMWords;
   __shared__ NodeDesc s_nd[kDiffWindow];
-  __shared__ uint32_t s_cnt[kCounts];
-  __shared__ uint32_t s_flat;
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const RelocDev& R = a.reloc;
   const uint32_t slot = blockIdx.x;
-  const uint32_t g = a.slot_graph[slot];
-  const DevGraph& G = a.graphs[g];
-  const uint32_t t = a.template_of[g];
-  const DevGraph& T = a.graphs[t];
-  const bool is_t = t == g;
-  const uint32_t k = slot - G.tile_base;
-  const uint32_t n0 = a.tile_node[slot];
-  const bool active = n0 != kNoTile;
-  const uint32_t N = G.num_nodes;
-  // Nodes holding this tile's words run from n0 to the next tile's first
-  // node (which may also hold the tile's last words).
-  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
-  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
-  const uint32_t nwin = active ? min(kDiffWindow, n_last - n0 + 1) : 0;
-  const NodeDesc* nd = a.node_desc + G.node_base;
-  const uint64_t wbeg = (uint64_t)k * kTileWords;
-  const uint64_t wend = active ? min(wbeg + kTileWords, (uint64_t)a.gwords[g]) : wbeg;
-  if (tid == 0) {
-    s_flat = active;
-    if (k == 0 && !is_t && a.digests[4ull * g + 2] != a.digests[4ull * t + 2])
-      atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
-  }
-  if (!active) {
-    if (tid == 0) a.tile_count[slot] = 0;
+  const SlotDesc sd = load_slot(a.slot_desc + slot);
+  uint32_t* sub_count = a.sub_count + (uint64_t)slot * kSubsPerSlot;
+  if (sd.flags & kSlotTemplate) {  // relocated by k_diff_t; a template has no overrides
+    if (lane == 0) sub_count[wave] = 0;
     return;
   }
-  for (uint32_t i = tid; i < nwin; i += kDiffThreads) s_nd[i] = nd[n0 + i];
-  __syncthreads();
+  const uint32_t g = sd.graph, t = sd.tmpl;
+  const uint64_t wbeg = sd.wbeg, wend = sd.wend;
+  const uint64_t w0 = wbeg + (uint64_t)wave * kSubWords + lane;  // word j is w0 + 64j
+  const bool flat = (sd.flags & kSlotFlat) != 0;
+  const RelocDev& R = a.reloc;
+  uint64_t* img_out = a.image + sd.word_base;
+  // The template's relocated image (read within the template's capacity;
+  // with relocation off it equals the raw image and is not read).  Its
+  // words are usable unless the template overflowed its capacity (its image
+  // is then empty); that is checked once the loads are in flight.
+  const uint64_t* rimg_t = a.image + sd.t_word_base;
+  const uint32_t t_last = sd.t_cap ? sd.t_cap - 1 : 0;
 
-  // Flat tile: every node overlapping it is aligned in both images, shares
-  // node n0's compare status, and sits at the same offset from a common
-  // base, so word w is at byte kg + 8w of the graph's image (kt + 8w of
-  // the template's) and needs no node lookup.
-  const NodeDesc d0 = s_nd[0];
-  const uint64_t kg = d0.src_g - 8ull * d0.gword, kt = d0.src_t - 8ull * d0.gword;
-  for (uint32_t i = tid; i < nwin; i += kDiffThreads) {
-    const NodeDesc d = s_nd[i];
-    if (d.gword >= wend || d.nwords == 0) continue;
-    const bool ok = !(d.flags & (FDY_NODE_RAGGED | kNodeRaggedT)) && !((d.flags ^ d0.flags) & kNodeCompare) &&
-                    d.src_g - 8ull * d.gword == kg && (!(d.flags & kNodeCompare) || d.src_t - 8ull * d.gword == kt);
-    if (!ok) s_flat = 0;
-  }
-  if (tid == 0 && nwin == kDiffWindow && (uint64_t)s_nd[nwin - 1].gword + s_nd[nwin - 1].nwords < wend)
-    s_flat = 0;
-  __syncthreads();
-  const bool flat = s_flat != 0;
-  const bool cflat = (d0.flags & kNodeCompare) != 0;
-  const uint8_t* pg = a.img + kg;
-  const uint8_t* pt = a.img + kt;
-
-  // Batches of B words per thread, software-pipelined: batch b+1's loads
-  // are issued before batch b is relocated, compared and stored.
-  uint64_t* img_out = a.image + G.word_base;
-  uint64_t* live_out = a.live + G.word_base;
-  uint32_t bits = 0;
-  uint64_t rg[B], rt[B], ng[B], nt[B];
-  uint32_t valid, cmp, full, nvalid = 0, ncmp = 0, nfull = 0;
-  diff_load<B>(a, flat, pg, pt, cflat, s_nd, nwin, nd, n0, N, G, T, wbeg + tid, wend, rg, rt, &valid, &cmp, &full);
-#pragma unroll
-  for (uint32_t jb = 0; jb < J; jb += B) {
-    if (jb + B < J)
-      diff_load<B>(a, flat, pg, pt, cflat, s_nd, nwin, nd, n0, N, G, T,
-                   wbeg + (uint64_t)(jb + B) * kDiffThreads + tid, wend, ng, nt, &nvalid, &ncmp, &nfull);
-#pragma unroll
-    for (uint32_t j = 0; j < B; ++j) {
-      if (!((valid >> j) & 1)) continue;
-      const uint64_t raw = rg[j];
-      const bool f = (full >> j) & 1;
-      rg[j] = f ? reloc_word(R, raw) : raw;
-      if ((cmp >> j) & 1) {
-        const uint64_t r = rt[j] == raw ? rg[j] : (f ? reloc_word(R, rt[j]) : rt[j]);
-        if (r != rg[j]) bits |= 1u << (jb + j);
-      }
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < B; ++j) {
-      if (!((valid >> j) & 1)) continue;
-      const uint64_t w = wbeg + (uint64_t)(jb + j) * kDiffThreads + tid;
-      img_out[w] = rg[j];
-      if (is_t) live_out[w] = rg[j];
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < B; ++j) {
-      rg[j] = ng[j];
-      rt[j] = nt[j];
-    }
-    valid = nvalid;
-    cmp = ncmp;
-    full = nfull;
-  }
-
-  // Compaction inside the tile: records ordered by (j, thread) = word order.
-#pragma unroll
-  for (uint32_t j = 0; j < J; ++j) {
-    const uint64_t m = __ballot((bits >> j) & 1);
-    if (lane == 0) s_cnt[j * kWaves + wave] = (uint32_t)__popcll(m);
-  }
-  __syncthreads();
-  if (wave == 0) {
-    const uint32_t v = s_cnt[lane];
-    uint32_t x = v;
-#pragma unroll
-    for (int dd = 1; dd < 64; dd <<= 1) {
-      const uint32_t y = shfl_up32(x, dd);
-      if (lane >= (uint32_t)dd) x += y;
-    }
-    s_cnt[lane] = x - v;
-    if (lane == 63) a.tile_count[slot] = x;
-  }
-  __syncthreads();
-  if (bits) {
-    fdy_override* out = a.ovr_tile + (uint64_t)slot * kTileWords;
-    const uint64_t lt = (1ull << lane) - 1;
+  // fg: the graph's raw word; ft: the template's raw word; fr: the
+  // template's relocated word.  A flat tile's words all sit at kg + 8w (the
+  // template's at kt + 8w, word w of its image) and are all compared.
+  uint64_t fg[J], ft[J], fr[J];
+  uint32_t valid = 0, cmp = 0, full = 0;
+  if (flat) {
+    const uint8_t* pg = a.img + sd.kg;
+    const uint8_t* pt = a.img + sd.kt;
 #pragma unroll
     for (uint32_t j = 0; j < J; ++j) {
-      const uint64_t m = __ballot((bits >> j) & 1);
-      if ((bits >> j) & 1) {
-        const uint64_t w = wbeg + (uint64_t)j * kDiffThreads + tid;
-        NodeDesc d;
-        const uint32_t node = find_node(s_nd, nwin, nd, n0, N, w, &d);
-        fdy_override o;
-        o.word = d.tword + (uint32_t)(w - d.gword);
-        o.node = node;
-        o.value = img_out[w];  // written above by this thread
-        out[s_cnt[j * kWaves + wave] + (uint32_t)__popcll(m & lt)] = o;
+      const uint64_t w = w0 + 64 * j;
+      fg[j] = ft[j] = fr[j] = 0;
+      if (w < wend) {
+        valid |= 1u << j;
+        fg[j] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
+        ft[j] = *reinterpret_cast<const uint64_t*>(pt + 8 * w);
       }
     }
+    if (R.n != 0) {
+#pragma unroll
+      for (uint32_t j = 0; j < J; ++j)
+        if ((valid >> j) & 1) fr[j] = rimg_t[min(w0 + 64 * j, (uint64_t)t_last)];
+    }
+    cmp = full = valid;
+  }
+  if (tid == 0 && (sd.flags & kSlotFirst)) {
+    if (a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
+  }
+  if (!flat && wend > wbeg) {  // uniform over the workgroup
+    const DevGraph& G = a.graphs[g];
+    const DevGraph& T = a.graphs[t];
+    const NodeWindow nw = stage_window(a, G, slot, s_nd);
+    __syncthreads();
+    uint64_t wv[J];
+    uint32_t node[J];
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) wv[j] = w0 + 64 * j;
+    find_nodes<J>(s_nd, nw, wv, node);
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) {
+      const uint64_t w = wv[j];
+      fg[j] = ft[j] = fr[j] = 0;
+      if (w >= wend) continue;
+      valid |= 1u << j;
+      const NodeDesc d = window_desc(s_nd, nw, node[j]);
+      uint32_t width;
+      fg[j] = load_word(a, G, d, w, (d.flags & FDY_NODE_RAGGED) != 0, d.src_g, &width);
+      if (width == 8) full |= 1u << j;
+      if (d.flags & kNodeCompare) {
+        // Compared nodes have equal param sizes, so the template's word has
+        // the same width (and was relocated into R iff this one is).
+        cmp |= 1u << j;
+        const uint64_t tw = d.tword + (w - d.gword);
+        uint32_t wt;
+        NodeDesc dt = d;
+        dt.gword = d.tword;
+        ft[j] = load_word(a, T, dt, tw, (d.flags & kNodeRaggedT) != 0, d.src_t, &wt);
+        if (R.n != 0) fr[j] = rimg_t[min(tw, (uint64_t)t_last)];
+      }
+    }
+  }
+  if (R.n == 0 || (a.status[t] & kGraphOverflow)) {
+    // Relocation off: R equals the raw image.  Template overflowed: relocate
+    // its compared words here.
+#pragma unroll
+    for (uint32_t jb = 0; jb < J; jb += kSlots) {
+      uint64_t tin[kSlots], tout[kSlots];
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; ++k) tin[k] = ft[jb + k];
+      reloc_batch<kSlots>(R, tin, tout, ((cmp & full) >> jb) & ((1u << kSlots) - 1));
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; ++k) fr[jb + k] = tout[k];
+    }
+  }
+
+  // Words equal to the template's take its relocated word; partial words
+  // are never relocated; the rest need a search.  fg[j] ends as the word's
+  // value in R.
+  uint32_t need = 0, bits = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) {
+    if (!((valid >> j) & 1)) continue;
+    const bool c = (cmp >> j) & 1;
+    if (c && fg[j] == ft[j]) fg[j] = fr[j];
+    else if (!((full >> j) & 1)) bits |= (c && fg[j] != fr[j]) ? 1u << j : 0u;
+    else need |= 1u << j;
+  }
+  // Round r searches the lane's needed words of rank r*kSlots .. r*kSlots +
+  // kSlots-1 (rank: position among the lane's needed words).  Slots are
+  // filled and drained with compile-time word indexes only.
+  uint32_t rank[J];
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) rank[j] = (uint32_t)__popc(need & ((1u << j) - 1));
+  const uint32_t nneed = (uint32_t)__popc(need);
+  for (uint32_t base = 0; __ballot(base < nneed) != 0; base += kSlots) {
+    uint64_t sg[kSlots], st[kSlots], res[kSlots];
+    uint32_t m = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < kSlots; ++k) {
+      sg[k] = st[k] = 0;
+      if (base + k < nneed) m |= 1u << k;
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j)
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; ++k)
+        if (((need >> j) & 1) && rank[j] == base + k) {
+          sg[k] = fg[j];
+          st[k] = fr[j];
+        }
+    reloc_batch<kSlots>(R, sg, res, m);
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j)
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; ++k)
+        if (((need >> j) & 1) && rank[j] == base + k) {
+          fg[j] = res[k];
+          if (((cmp >> j) & 1) && res[k] != st[k]) bits |= 1u << j;
+        }
+  }
+
+  // Image store and this wave's records, in word order (j, lane).
+  fdy_override* out = a.ovr_tile + ((uint64_t)slot * kSubsPerSlot + wave) * kSubWords;
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t run = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) {
+    const uint64_t w = w0 + 64 * j;
+    if ((valid >> j) & 1) img_out[w] = fg[j];
+    const uint64_t mk = __ballot((bits >> j) & 1);
+    if ((bits >> j) & 1) {
+      fdy_override o;
+      o.word = (uint32_t)w;
+      o.node = 0;
+      o.value = fg[j];
+      out[run + (uint32_t)__popcll(mk & lt)] = o;
+    }
+    run += (uint32_t)__popcll(mk);
+  }
+  if (lane == 0) sub_count[wave] = run;
+}
+
+// Records per graph: the sum of its slots' sub-range counts (one workgroup
+// per graph).
+constexpr uint32_t kCountThreads = 256;
+
+__global__ __launch_bounds__(kCountThreads) void k_count(RestoreArgs a) {
+  __shared__ uint32_t s_part[kCountThreads / 64];
+  const uint32_t g = blockIdx.x, tid = threadIdx.x;
+  const DevGraph& G = a.graphs[g];
+  const uint64_t lo = (uint64_t)G.tile_base * kSubsPerSlot, hi = lo + (uint64_t)G.tile_cap * kSubsPerSlot;
+  uint32_t part = 0;
+  for (uint64_t i = lo + tid; i < hi; i += kCountThreads) part += a.sub_count[i];
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) part += __shfl_down(part, (unsigned)d, 64);
+  if ((tid & 63) == 0) s_part[tid >> 6] = part;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t total = 0;
+    for (uint32_t w = 0; w < kCountThreads / 64; ++w) total += s_part[w];
+    a.graph_count[g] = total;
   }
 }
 
-// Exclusive prefix of the per-slot record counts (one workgroup), and the
-// per-graph override offsets it implies.
+// Exclusive prefix of the per-graph record counts (one workgroup): the
+// per-graph override offsets.
 __global__ __launch_bounds__(1024) void k_scan(RestoreArgs a) {
   __shared__ uint64_t s_w[16];
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t n = a.num_slots;
+  const uint32_t n = a.num_graphs;
   const uint32_t per = (n + 1023) / 1024;
   const uint32_t lo = min(n, tid * per), hi = min(n, lo + per);
   uint64_t sum = 0;
-  for (uint32_t i = lo; i < hi; ++i) sum += a.tile_count[i];
+  for (uint32_t i = lo; i < hi; ++i) sum += a.graph_count[i];
   uint64_t x = sum;
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
@@ -896,22 +1063,63 @@ __global__ __launch_bounds__(1024) void k_scan(RestoreArgs a) {
   }
   uint64_t run = before + x - sum;
   for (uint32_t i = lo; i < hi; ++i) {
-    a.tile_off[i] = run;
-    run += a.tile_count[i];
+    a.ovr_off[i] = run;
+    run += a.graph_count[i];
   }
-  __syncthreads();
-  for (uint32_t g = tid; g < a.num_graphs; g += 1024) a.ovr_off[g] = a.tile_off[a.graphs[g].tile_base];
-  if (tid == 0) a.ovr_off[a.num_graphs] = total;
+  if (tid == 1023) a.ovr_off[n] = total;
 }
 
-// Copy each slot's records to their place in the dense array.
-__global__ __launch_bounds__(256) void k_compact(RestoreArgs a) {
-  const uint32_t slot = blockIdx.x;
-  const uint32_t c = a.tile_count[slot];
-  if (c == 0) return;
-  const uint64_t base = a.tile_off[slot];
-  const fdy_override* src = a.ovr_tile + (uint64_t)slot * kTileWords;
-  for (uint32_t i = threadIdx.x; i < c; i += 256) a.ovr[base + i] = src[i];
+// Move each slot's records to their place in the dense array, completing
+// them: the node holding the word (searched in the slot's node window) and
+// the word's index in the template's image.  A slot's records follow those
+// of the graph's earlier slots; one pass covers all its sub-ranges.
+constexpr uint32_t kCompactThreads = 256;
+
+__global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
+  __shared__ NodeDesc s_nd[kDiffWindow];
+  __shared__ uint32_t s_part[kCompactThreads / 64];
+  __shared__ uint32_t s_sub[kSubsPerSlot + 1];  // exclusive prefix of the slot's sub-range counts
+  const uint32_t slot = blockIdx.x, tid = threadIdx.x;
+  const uint32_t* cnt = a.sub_count + (uint64_t)slot * kSubsPerSlot;
+  if (tid == 0) {
+    uint32_t r = 0;
+    for (uint32_t q = 0; q < kSubsPerSlot; ++q) {
+      s_sub[q] = r;
+      r += cnt[q];
+    }
+    s_sub[kSubsPerSlot] = r;
+  }
+  __syncthreads();
+  const uint32_t total = s_sub[kSubsPerSlot];
+  if (total == 0) return;  // uniform over the workgroup
+  const SlotDesc sd = load_slot(a.slot_desc + slot);
+  const DevGraph& G = a.graphs[sd.graph];
+  uint32_t part = 0;
+  for (uint64_t i = (uint64_t)G.tile_base * kSubsPerSlot + tid; i < (uint64_t)slot * kSubsPerSlot; i += kCompactThreads)
+    part += a.sub_count[i];
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) part += __shfl_down(part, (unsigned)d, 64);
+  if ((tid & 63) == 0) s_part[tid >> 6] = part;
+  const NodeWindow nw = stage_window(a, G, slot, s_nd);
+  __syncthreads();
+  uint64_t base = a.ovr_off[sd.graph];
+#pragma unroll
+  for (uint32_t w = 0; w < kCompactThreads / 64; ++w) base += s_part[w];
+  const fdy_override* src = a.ovr_tile + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  for (uint32_t i = tid; i < total; i += kCompactThreads) {
+    uint32_t q = 0;  // the sub-range holding record i
+#pragma unroll
+    for (uint32_t b = kSubsPerSlot / 2; b >= 1; b >>= 1)
+      if (s_sub[q + b] <= i) q += b;
+    fdy_override o = src[(uint64_t)q * kSubWords + (i - s_sub[q])];
+    const uint64_t w = o.word;
+    uint32_t node;
+    find_nodes<1>(s_nd, nw, &w, &node);
+    const NodeDesc d = window_desc(s_nd, nw, node);
+    o.word = d.tword + (uint32_t)(w - d.gword);
+    o.node = node;
+    a.ovr[base + i] = o;
+  }
 }
 
 // ---- switch --------------------------------------------------------------
@@ -994,15 +1202,23 @@ hipError_t launch_node(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_diff(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_diff, dim3(a.num_slots), dim3(kDiffThreads), 0, s, a);
+  // Templates first: the other graphs read their relocated words.
+  const uint32_t tgrid = (uint32_t)std::min<uint64_t>((uint64_t)a.num_slots * kTUnitsPerTile, 2048);
+  hipLaunchKernelGGL(k_diff_t, dim3(tgrid), dim3(kTThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_diff_m, dim3(a.num_slots), dim3(kMThreads), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_count, dim3(a.num_graphs), dim3(kCountThreads), 0, s, a);
+  hipError_t e0 = hipGetLastError();
+  if (e0 != hipSuccess) return e0;
   hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(kCompactThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -104,8 +104,9 @@ struct HostStage {
 };
 
 // The interval search structure: a bucket index of 64-byte lines with about
-// one bucket per two intervals, 16-byte {hi, delta} records, and the lo keys
-// for crowded buckets (see RelocDev).
+// one root bucket per two intervals (crowded buckets split into sub-bucket
+// lines), 16-byte {hi, delta} records, and the lo keys for leaves still
+// crowded at the depth limit (see RelocDev).
 struct RelocPlan {
   DevBuf bucket, rec, lo;
   RelocDev dev{};
@@ -142,23 +143,81 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
     return off > UINT64_MAX - lo[0] ? UINT64_MAX : lo[0] + off;
   };
   std::vector<RelocBucket> bucket(nb);
-  uint64_t i = 0, j = 0;  // i: last lo <= bucket start; j: last lo < next bucket's start
+  auto leaf = [&](RelocBucket& e, uint64_t s0, uint64_t i, uint64_t j) {
+    e.first = (uint32_t)i;
+    e.count = (uint32_t)(j - i);
+    for (uint32_t k = 0; k < kBucketOffsets; ++k)
+      e.off[k] = k < e.count ? (uint32_t)(lo[i + 1 + k] - s0) : 0xFFFFFFFFu;
+  };
+  std::vector<uint64_t> crowded;  // root buckets with more starts than a line holds
+  uint64_t i = 0, j = 0;          // i: last lo <= bucket start; j: last lo < next bucket's start
   for (uint64_t b = 0; b < nb; ++b) {
     const uint64_t s0 = start(b), s1 = start(b + 1);
     while (i + 1 < n && lo[i + 1] <= s0) ++i;
     if (j < i) j = i;
     while (j + 1 < n && lo[j + 1] < s1) ++j;
-    RelocBucket& e = bucket[b];
-    e.first = (uint32_t)i;
-    e.count = (uint32_t)(j - i);
-    for (uint32_t k = 0; k < kBucketOffsets; ++k)
-      e.off[k] = k < e.count ? (uint32_t)(lo[i + 1 + k] - s0) : 0xFFFFFFFFu;
+    leaf(bucket[b], s0, i, j);
+    if (j - i > kBucketOffsets) crowded.push_back(b);
   }
-  int rc = dev_alloc(out->bucket, nb * sizeof(RelocBucket), "interval buckets");
+  // Split crowded buckets into 2^s sub-buckets: the smallest s whose
+  // sub-buckets all hold at most kBucketOffsets starts, at most
+  // log2(count) + 3 per level (so a level adds at most 8 lines per start),
+  // for at most kMaxSplitDepth levels; deeper leaves fall back to a binary
+  // search over lo[] on the device.
+  constexpr int kMaxSplitDepth = 6;
+  struct Pending {
+    uint64_t line, s0, i, j;
+    uint32_t width;
+    int depth;
+  };
+  std::vector<Pending> todo;
+  for (uint64_t b : crowded) {
+    const RelocBucket& e = bucket[b];
+    todo.push_back({b, start(b), e.first, (uint64_t)e.first + e.count, shift, 0});
+  }
+  while (!todo.empty()) {
+    const Pending p = todo.back();
+    todo.pop_back();
+    if (p.depth >= kMaxSplitDepth || p.width == 0) continue;  // stays a crowded leaf
+    const uint64_t cnt = p.j - p.i;
+    uint32_t smax = 1;
+    while (smax < p.width && (1ull << smax) < 8 * cnt) ++smax;
+    uint32_t s = 1;
+    for (; s < smax; ++s) {
+      // Largest number of starts in one sub-bucket of width 2^(width - s).
+      uint64_t best = 0, run = 0, cur = UINT64_MAX;
+      for (uint64_t q = p.i + 1; q <= p.j; ++q) {
+        const uint64_t sub = (lo[q] - p.s0) >> (p.width - s);
+        run = sub == cur ? run + 1 : 1;
+        cur = sub;
+        best = std::max(best, run);
+      }
+      if (best <= kBucketOffsets) break;
+    }
+    const uint64_t base = bucket.size();
+    if (base + (1ull << s) > 0xFFFFFFF0ull) return err(FDY_E_INVALID, "interval index too large");
+    bucket.resize(base + (1ull << s));
+    RelocBucket& e = bucket[p.line];
+    e.first = (uint32_t)base;
+    e.count = kBucketSplit | s;
+    for (uint32_t k = 0; k < kBucketOffsets; ++k) e.off[k] = 0xFFFFFFFFu;
+    const uint32_t cw = p.width - s;
+    uint64_t ci = p.i, cj = p.i;
+    for (uint64_t c = 0; c < (1ull << s); ++c) {
+      const uint64_t s0 = p.s0 + (c << cw);
+      const uint64_t s1 = s0 > UINT64_MAX - (1ull << cw) ? UINT64_MAX : s0 + (1ull << cw);
+      while (ci + 1 <= p.j && lo[ci + 1] <= s0) ++ci;
+      if (cj < ci) cj = ci;
+      while (cj + 1 <= p.j && lo[cj + 1] < s1) ++cj;
+      leaf(bucket[base + c], s0, ci, cj);
+      if (cj - ci > kBucketOffsets) todo.push_back({base + c, s0, ci, cj, cw, p.depth + 1});
+    }
+  }
+  int rc = dev_alloc(out->bucket, bucket.size() * sizeof(RelocBucket), "interval buckets");
   if (!rc) rc = dev_alloc(out->rec, n * sizeof(RelocRec), "interval records");
   if (!rc) rc = dev_alloc(out->lo, n * 8, "interval starts");
   if (rc) return rc;
-  FDY_HIP(hipMemcpy(out->bucket.p, bucket.data(), nb * sizeof(RelocBucket), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->bucket.p, bucket.data(), bucket.size() * sizeof(RelocBucket), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(out->rec.p, rec.data(), n * sizeof(RelocRec), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(out->lo.p, lo, n * 8, hipMemcpyHostToDevice));
   out->dev.bucket = out->bucket.as<RelocBucket>();
@@ -194,8 +253,8 @@ struct fdy_archive {
   uint32_t num_slots = 0;
 
   DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, live_cur;
-  DevBuf aux, image, live, ovr, ovr_off, ovr_tile, tile_count, tile_off;
+  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, slot_desc, live_cur, tslots;
+  DevBuf aux, image, live, ovr, ovr_off, ovr_tile, sub_count, graph_count;
 
   RelocPlan reloc;
   bool use_explicit = false;
@@ -297,8 +356,10 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->live_src, 4 * nodes, "live node sources");
   alloc(a->tile_node, 4 * slots, "tile table");
   alloc(a->slot_graph, 4 * slots, "slot table");
-  alloc(a->tile_count, 4 * slots, "tile record counts");
-  alloc(a->tile_off, 8 * slots, "tile record offsets");
+  alloc(a->slot_desc, sizeof(SlotDesc) * slots, "slot descriptors");
+  alloc(a->tslots, 4 * (slots + 1), "template slot list");
+  alloc(a->sub_count, 4 * slots * kSubsPerSlot, "record counts");
+  alloc(a->graph_count, 4ull * G, "graph record counts");
   alloc(a->ovr_tile, sizeof(fdy_override) * (uint64_t)kTileWords * slots, "tile record regions");
   alloc(a->aux, 8 * words, "ragged word sources");
   alloc(a->image, 8 * words, "param images");
@@ -512,7 +573,10 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.node_desc = a->ndesc.as<NodeDesc>();
   r.node_ptrs = a->nptrs.as<uint64_t>();
   r.tile_node = a->tile_node.as<uint32_t>();
+  r.tslots = a->tslots.as<uint32_t>();
+  r.tslot_count = a->tslots.as<uint32_t>() + a->num_slots;
   r.slot_graph = a->slot_graph.as<uint32_t>();
+  r.slot_desc = a->slot_desc.as<SlotDesc>();
   r.aux = a->aux.as<uint64_t>();
   r.image = a->image.as<uint64_t>();
   r.live = a->live.as<uint64_t>();
@@ -521,8 +585,8 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.ovr = a->ovr.as<fdy_override>();
   r.ovr_off = a->ovr_off.as<uint64_t>();
   r.ovr_tile = a->ovr_tile.as<fdy_override>();
-  r.tile_count = a->tile_count.as<uint32_t>();
-  r.tile_off = a->tile_off.as<uint64_t>();
+  r.sub_count = a->sub_count.as<uint32_t>();
+  r.graph_count = a->graph_count.as<uint32_t>();
   r.reloc = a->reloc.dev;
   if (a->timing) {
     for (hipEvent_t& e : a->ev)

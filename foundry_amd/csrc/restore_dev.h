@@ -10,10 +10,13 @@
 
 namespace fdy {
 
-// Words of the param image handled by one diff tile, and its thread count.
-constexpr uint32_t kDiffThreads = 256;
-constexpr uint32_t kDiffWordsPerThread = 16;
-constexpr uint32_t kTileWords = kDiffThreads * kDiffWordsPerThread;  // 4096
+// Words of the param image handled by one diff tile (one slot); words per
+// lane in the member diff; and the sub-ranges (one wave each) whose override
+// records are compacted independently.
+constexpr uint32_t kTileWords = 4096;
+constexpr uint32_t kMWords = 4;
+constexpr uint32_t kSubWords = 64 * kMWords;
+constexpr uint32_t kSubsPerSlot = kTileWords / kSubWords;
 constexpr uint32_t kDiffWindow = 512;    // node descriptors staged in LDS per tile
 constexpr uint32_t kNoTile = 0xFFFFFFFFu;
 
@@ -41,6 +44,25 @@ struct DevGraph {
   uint64_t crc_fin[4];   // CRC-64/XZ finishing terms of the key, edge, type, kernel-entry streams
 };
 
+// Per-slot work description written by the node pass for the diff pass.
+constexpr uint32_t kSlotFlat = 1;      // every word of the tile sits at kg + 8w (and kt + 8w)
+constexpr uint32_t kSlotCompare = 2;   // flat tile whose words are compared with the template
+constexpr uint32_t kSlotTemplate = 4;  // tile of a template graph (also writes the live image)
+constexpr uint32_t kSlotFirst = 8;     // the graph's first slot
+struct SlotDesc {
+  uint64_t kg;           // flat: byte offset of image word 0 of the graph in the file image
+  uint64_t kt;           // flat + compare: the same for the template
+  uint64_t word_base;    // the graph's first word in R / live / aux
+  uint64_t t_word_base;  // the template's first word in R
+  uint32_t wbeg, wend;   // graph-local word range of the tile (empty: inactive slot)
+  uint32_t graph;
+  uint32_t tmpl;         // the graph's template
+  uint32_t flags;        // kSlot*
+  uint32_t t_cap;        // the template's image capacity in words
+  uint32_t pad[2];
+};
+static_assert(sizeof(SlotDesc) == 64, "SlotDesc is one 64-byte line");
+
 // Per-node work description written by the node pass for the diff pass.
 struct NodeDesc {
   uint32_t gword;   // first word of this node in its graph's image
@@ -59,12 +81,17 @@ struct RelocRec {
 };
 static_assert(sizeof(RelocRec) == 16, "RelocRec is 16 B");
 
-// One 64-byte line of the bucket index.  Bucket b covers addresses
-// [lo_min + b*2^shift, lo_min + (b+1)*2^shift).  `first` is the last
-// interval whose lo is <= the bucket's first address; intervals first+1 ..
-// first+count start inside the bucket, and off[k] holds lo - bucket start
-// of interval first+1+k for the first min(count, 14) of them.
+// One 64-byte line of the bucket index.  Root bucket b covers addresses
+// [lo_min + b*2^shift, lo_min + (b+1)*2^shift).  A leaf line: `first` is
+// the last interval whose lo is <= the bucket's first address; intervals
+// first+1 .. first+count start inside the bucket, and off[k] holds
+// lo - bucket start of interval first+1+k for the first min(count, 14) of
+// them.  A split line (count has kBucketSplit set) stands for 2^s
+// sub-buckets, s = count & 63, of 2^(width - s) bytes each, whose lines
+// are bucket[first .. first + 2^s); crowded buckets are split until their
+// leaves hold at most 14 starts (or a depth limit is reached).
 constexpr uint32_t kBucketOffsets = 14;
+constexpr uint32_t kBucketSplit = 0x80000000u;
 struct RelocBucket {
   uint32_t first;
   uint32_t count;
@@ -93,42 +120,118 @@ __device__ inline uint64_t ld_u64(const uint8_t* p) {
   return (uint64_t)ld_u32(p) | ((uint64_t)ld_u32(p + 4) << 32);
 }
 
-// Relocate one word: the last interval with lo <= w moves w if w < hi
-// (w <= hi under the inclusive policy).
-__device__ inline uint64_t reloc_word(const RelocDev& r, uint64_t w) {
-  if (r.n == 0 || w < r.lo_min) return w;
-  if (r.policy ? (w > r.hi_max) : (w >= r.hi_max)) return w;
-  const uint64_t rel = w - r.lo_min;
-  const uint64_t b = rel >> r.shift;
-  const uint32_t x = (uint32_t)(rel - (b << r.shift));
-  // The first 16 bytes carry `first`, `count` and two offsets, which is the
-  // whole bucket most of the time; the other 48 are read only when needed.
-  const uint4* line = reinterpret_cast<const uint4*>(r.bucket + b);
-  const uint4 q0 = line[0];
-  const uint32_t count = q0.y;
-  uint32_t c = (count > 0 && q0.z <= x) + (count > 1 && q0.w <= x);
-  if (count > 2) {
-    const uint4 q1 = line[1], q2 = line[2], q3 = line[3];
-    const uint32_t m = count < kBucketOffsets ? count : kBucketOffsets;
-    const uint32_t off[kBucketOffsets - 2] = {q1.x, q1.y, q1.z, q1.w, q2.x, q2.y,
-                                              q2.z, q2.w, q3.x, q3.y, q3.z, q3.w};
+// Relocate K words at once (the words whose bit is set in `mask`; the others
+// pass through): the last interval with lo <= w moves w if w < hi (w <= hi
+// under the inclusive policy).  The K searches advance in lockstep, so each
+// step issues its K loads before waiting for any of them.
+template <int K>
+__device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_t* out, uint32_t mask) {
+  bool ok[K];
+  uint32_t x[K], width[K];
+  const uint4* line[K];
+  uint4 h[K];
 #pragma unroll
-    for (uint32_t k = 0; k < kBucketOffsets - 2; ++k) c += (k + 2 < m) & (off[k] <= x);
+  for (int k = 0; k < K; ++k) {
+    ok[k] = ((mask >> k) & 1) && r.n != 0 && w[k] >= r.lo_min &&
+            (r.policy ? w[k] <= r.hi_max : w[k] < r.hi_max);
+    const uint64_t rel = w[k] - r.lo_min;
+    const uint64_t b = ok[k] ? rel >> r.shift : 0;
+    x[k] = (uint32_t)(rel - (b << r.shift));
+    width[k] = r.shift;
+    line[k] = reinterpret_cast<const uint4*>(r.bucket + b);
+    h[k] = ok[k] ? line[k][0] : make_uint4(0, 0, 0, 0);
   }
-  uint32_t i = q0.x + c;
-  if (count > kBucketOffsets && c == kBucketOffsets) {
-    // More starts than the line holds: binary search the rest of the bucket.
-    uint32_t lo = i, hi = q0.x + count;
-    while (hi > lo) {
-      const uint32_t mid = (lo + hi + 1) >> 1;
-      if (r.lo[mid] <= w) lo = mid;
-      else hi = mid - 1;
+  // Descend through split lines (crowded buckets) to the leaves.
+  for (;;) {
+    bool any = false;
+#pragma unroll
+    for (int k = 0; k < K; ++k) any |= (h[k].y & kBucketSplit) != 0;
+    if (!any) break;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (h[k].y & kBucketSplit) {
+        width[k] -= h[k].y & 63;
+        const uint32_t sub = width[k] >= 32 ? 0u : x[k] >> width[k];
+        x[k] -= width[k] >= 32 ? 0u : sub << width[k];
+        line[k] = reinterpret_cast<const uint4*>(r.bucket + h[k].x + sub);
+        h[k] = line[k][0];
+      }
     }
-    i = lo;
   }
-  const RelocRec iv = r.rec[i];
-  const bool inside = r.policy ? (w <= iv.hi) : (w < iv.hi);
-  return inside ? w + iv.delta : w;
+  // `first`, `count` and two offsets are in the line's first 16 bytes; the
+  // other 48 are read only for leaves with more than two starts.
+  uint32_t c[K];
+  bool more = false;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    c[k] = (h[k].y > 0 && h[k].z <= x[k]) + (h[k].y > 1 && h[k].w <= x[k]);
+    more |= h[k].y > 2;
+  }
+  if (more) {
+    uint4 q1[K], q2[K], q3[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (h[k].y > 2) {
+        q1[k] = line[k][1];
+        q2[k] = line[k][2];
+        q3[k] = line[k][3];
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      if (h[k].y > 2) {
+        const uint32_t m = h[k].y < kBucketOffsets ? h[k].y : kBucketOffsets;
+        const uint32_t off[kBucketOffsets - 2] = {q1[k].x, q1[k].y, q1[k].z, q1[k].w, q2[k].x, q2[k].y,
+                                                  q2[k].z, q2[k].w, q3[k].x, q3[k].y, q3[k].z, q3[k].w};
+#pragma unroll
+        for (uint32_t e = 0; e < kBucketOffsets - 2; ++e) c[k] += (e + 2 < m) & (off[e] <= x[k]);
+      }
+    }
+  }
+  // A leaf with more starts than its line holds (depth limit reached):
+  // binary search over lo[] for the rest, in lockstep.
+  uint32_t i[K], lo[K], hi[K];
+  bool bs = false;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    i[k] = h[k].x + c[k];
+    const bool s = ok[k] && h[k].y > kBucketOffsets && c[k] == kBucketOffsets;
+    lo[k] = i[k];
+    hi[k] = s ? h[k].x + h[k].y : i[k];
+    bs |= s;
+  }
+  if (bs) {
+    for (;;) {
+      bool act = false;
+#pragma unroll
+      for (int k = 0; k < K; ++k) act |= hi[k] > lo[k];
+      if (!act) break;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        if (hi[k] > lo[k]) {
+          const uint32_t mid = (lo[k] + hi[k] + 1) >> 1;
+          if (r.lo[mid] <= w[k]) lo[k] = mid;
+          else hi[k] = mid - 1;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) i[k] = lo[k];
+  }
+  RelocRec iv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) iv[k] = ok[k] ? r.rec[i[k]] : RelocRec{0, 0};
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const bool inside = ok[k] && (r.policy ? (w[k] <= iv[k].hi) : (w[k] < iv[k].hi));
+    out[k] = inside ? w[k] + iv[k].delta : w[k];
+  }
+}
+
+__device__ inline uint64_t reloc_word(const RelocDev& r, uint64_t w) {
+  uint64_t o;
+  reloc_batch<1>(r, &w, &o, 1u);
+  return o;
 }
 
 }  // namespace fdy
