@@ -65,6 +65,7 @@ class RestoreTiming(C.Structure):
         ("hash_ms", C.c_float),
         ("group_ms", C.c_float),
         ("node_ms", C.c_float),
+        ("tmpl_ms", C.c_float),
         ("diff_ms", C.c_float),
         ("compact_ms", C.c_float),
         ("total_ms", C.c_float),

@@ -46,7 +46,8 @@ struct RestoreArgs {
 hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
-hipError_t launch_diff(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s);
 
 struct SwitchArgs {

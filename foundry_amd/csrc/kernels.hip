@@ -1201,12 +1201,14 @@ hipError_t launch_node(const RestoreArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_diff(const RestoreArgs& a, hipStream_t s) {
-  // Templates first: the other graphs read their relocated words.
+// Templates first: the other graphs read their relocated words.
+hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s) {
   const uint32_t tgrid = (uint32_t)std::min<uint64_t>((uint64_t)a.num_slots * kTUnitsPerTile, 2048);
   hipLaunchKernelGGL(k_diff_t, dim3(tgrid), dim3(kTThreads), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  return hipGetLastError();
+}
+
+hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_diff_m, dim3(a.num_slots), dim3(kMThreads), 0, s, a);
   return hipGetLastError();
 }

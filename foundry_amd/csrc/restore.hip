@@ -269,7 +269,7 @@ struct fdy_archive {
 
   bool timing = false;
   bool timed = false;
-  hipEvent_t ev[6] = {};
+  hipEvent_t ev[7] = {};
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)
@@ -599,10 +599,12 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
   FDY_HIP(launch_node(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
-  FDY_HIP(launch_diff(r, s));
+  FDY_HIP(launch_diff_templates(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
-  FDY_HIP(launch_compact(r, s));
+  FDY_HIP(launch_diff_members(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
+  FDY_HIP(launch_compact(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
   a->timed = a->timing;
   a->restored = true;
   a->cached = false;
@@ -619,13 +621,14 @@ int fdy_set_timing(fdy_archive* a, int enabled) {
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
-  FDY_HIP(hipEventSynchronize(a->ev[5]));
+  FDY_HIP(hipEventSynchronize(a->ev[6]));
   FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
-  FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[3], a->ev[4]));
-  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[4], a->ev[5]));
-  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[5]));
+  FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));
+  FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[4], a->ev[5]));
+  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[5], a->ev[6]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[6]));
   return FDY_OK;
 }
 

@@ -180,8 +180,9 @@ typedef struct fdy_restore_timing {
   float hash_ms;    /* saved-key and dependency digests */
   float group_ms;   /* template assignment */
   float node_ms;    /* per-node compare, layout, type and kernel-entry digests */
-  float diff_ms;    /* fused diff + relocate */
-  float compact_ms; /* per-tile override regions -> dense canonical array */
+  float tmpl_ms;    /* relocation of the template graphs' param words */
+  float diff_ms;    /* fused diff + relocate of every other graph's param words */
+  float compact_ms; /* record counts, offsets, dense canonical override array */
   float total_ms;
 } fdy_restore_timing;
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
