@@ -36,6 +36,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cctype>
+#include <exception>
 #include <chrono>
 #include <condition_variable>
 #include <cstdio>
@@ -643,7 +644,11 @@ int orc_group_by_keys(const char* const* keys, const uint64_t* lens, uint32_t n,
 int orc_group_manifest(const char* text, uint64_t len, const char* const* names, uint32_t n, uint32_t* out) {
   Json root;
   JsonParser jp{text, text + len};
-  if (!jp.val(&root, 0) || root.k != Json::OBJ) return -1;
+  try {
+    if (!jp.val(&root, 0) || root.k != Json::OBJ) return -1;
+  } catch (const std::exception&) {  // a malformed \u escape
+    return -1;
+  }
   const Json* groups = root.get("topology_groups");
   if (!groups || groups->k != Json::ARR) return -1;
   std::unordered_map<std::string, uint32_t> idx;
@@ -655,8 +660,9 @@ int orc_group_manifest(const char* text, uint64_t len, const char* const* names,
     const Json* m = grp.get("members");
     if (!t || t->k != Json::STR || !m || m->k != Json::ARR) return -1;
     auto ti = idx.find(t->s);
-    if (ti == idx.end()) continue;
-    res[ti->second] = ti->second;
+    if (ti == idx.end()) continue;  // unknown template: the group is skipped (1754-1755)
+    // The template's own entry is left alone (1759, 1771): a template listed
+    // as a member of an earlier group stays that group's member.
     for (const Json& mem : m->a) {
       if (mem.k != Json::STR) return -1;
       if (mem.s == t->s) continue;

@@ -47,9 +47,10 @@ int64_t orc_topology_key_recomputed(const uint8_t* image, uint64_t size, char* b
 int orc_group_by_keys(const char* const* keys, const uint64_t* lens, uint32_t n, uint32_t* template_for);
 
 /* Grouping from a graph_manifest.json text (csrc/CUDAGraphParallel.cpp:1727-1786).
- * names[i] = file name of graph i.  out[i] = template index, or i for
- * templates, or UINT32_MAX for a graph no group lists.  Returns 0, or -1 if
- * the manifest does not parse (the reference then falls back to keys). */
+ * names[i] = file name of graph i.  out[i] = the template of a member, or
+ * UINT32_MAX for a graph that builds its own exec (a template, or a graph no
+ * group lists), as template_for = SIZE_MAX there.  Returns 0, or -1 if the
+ * manifest does not parse (the reference then falls back to keys). */
 int orc_group_manifest(const char* manifest, uint64_t len, const char* const* names, uint32_t n,
                        uint32_t* out);
 

@@ -1,0 +1,40 @@
+"""The synthetic-archive generator: seeded and deterministic, and its
+archives read back through the independent reader."""
+import numpy as np
+
+from foundry_amd import synth
+from tests import cugraph_reader as R
+
+
+def test_same_seed_same_bytes():
+    p = synth.preset(2, num_graphs=6, nodes_per_graph=50, num_intervals=300)
+    a, b = synth.SynthArchive(p, threads=1), synth.SynthArchive(p, threads=4)
+    assert a.images() == b.images()
+    for x, y in zip(a.intervals(), b.intervals()):
+        np.testing.assert_array_equal(x, y)
+
+
+def test_other_seed_other_bytes():
+    p = synth.preset(2, num_graphs=4, nodes_per_graph=50, num_intervals=300)
+    q = synth.preset(2, num_graphs=4, nodes_per_graph=50, num_intervals=300, seed=p.seed + 1)
+    assert synth.SynthArchive(p).images() != synth.SynthArchive(q).images()
+
+
+def test_archives_parse_and_intervals_tile():
+    p = synth.preset(2, num_graphs=5, nodes_per_graph=60, num_intervals=500)
+    s = synth.SynthArchive(p)
+    for img in s.images():
+        arc = R.read(img)
+        assert len(arc.nodes) == 60
+        assert all(n.type == 0 for n in arc.nodes)
+    lo, hi, nlo = s.intervals()
+    assert len(lo) == 500 and (lo < hi).all() and (hi[:-1] <= lo[1:]).all()
+    # the intervals tile the region exactly
+    assert lo[0] == p.region_base and hi[-1] == p.region_base + p.region_size
+    assert (hi[:-1] == lo[1:]).all()
+
+
+def test_decode_preset_shape():
+    p = synth.preset(2)
+    assert (p.num_graphs, p.num_groups, p.nodes_per_graph, p.num_intervals) == (256, 4, 1200, 40000)
+    assert p.region_size == 64 << 30 and abs(p.pointer_frac - 0.25) < 1e-9
