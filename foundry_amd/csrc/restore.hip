@@ -726,10 +726,15 @@ int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
   if (!rc) rc = ensure_cache(a, s);
   if (rc) return rc;
   const uint32_t t = a->h_tmpl[g];
-  if (a->h_status[g] & (FDY_GRAPH_NODE_COUNT | FDY_GRAPH_OVERFLOW))
+  if (a->h_status[g] & FDY_GRAPH_NODE_COUNT)
     return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has " + std::to_string(a->graphs[g].num_nodes) +
                                    " nodes but its template " + std::to_string(t) + " has " +
                                    std::to_string(a->graphs[t].num_nodes));
+  if (a->h_status[g] & FDY_GRAPH_OVERFLOW)
+    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has a param image larger than its sections allow");
+  if (a->h_status[t] & FDY_GRAPH_OVERFLOW)
+    return err(FDY_E_MISMATCH, "the template " + std::to_string(t) + " of graph " + std::to_string(g) +
+                                   " has a param image larger than its sections allow");
   const uint32_t c = a->h_current[t];
   if (c == g) return FDY_OK;
   FDY_HIP(hipSetDevice(a->device));
