@@ -67,6 +67,7 @@ class RestoreTiming(C.Structure):
         ("node_ms", C.c_float),
         ("tmpl_ms", C.c_float),
         ("diff_ms", C.c_float),
+        ("search_ms", C.c_float),
         ("compact_ms", C.c_float),
         ("total_ms", C.c_float),
     ]

@@ -16,6 +16,9 @@ struct RestoreArgs {
   const CrcConsts* cc;
   uint32_t num_graphs;
   uint32_t num_slots;
+  uint32_t num_chunks;        // node chunks over all graphs
+  const uint32_t* chunk_graph;  // graph of each node chunk
+  NodeChunk* chunks;          // per node chunk
   uint64_t* digests;          // 4 per graph
   const uint32_t* explicit_template;  // or null
   uint32_t* template_of;
@@ -28,7 +31,6 @@ struct RestoreArgs {
   uint32_t* tile_node;        // per slot
   uint32_t* tslots;           // slots of template graphs holding words (capacity: num_slots)
   uint32_t* tslot_count;      // entries of tslots
-  const uint32_t* slot_graph; // per slot
   SlotDesc* slot_desc;        // per slot
   uint64_t* aux;              // ragged-word sources (per word)
   uint64_t* image;            // relocated param images R
@@ -37,7 +39,7 @@ struct RestoreArgs {
   uint32_t* live_cur;         // per graph
   fdy_override* ovr;          // dense override records, canonical order
   uint64_t* ovr_off;          // G+1
-  fdy_override* ovr_tile;     // record regions, kSubWords records per (slot, sub-range)
+  Candidate* cand;            // per (slot, sub-range): kSubWords candidates, then as many records
   uint32_t* sub_count;        // records per (slot, sub-range)
   uint32_t* graph_count;      // records per graph
   RelocDev reloc;
@@ -48,6 +50,7 @@ hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s);
 
 struct SwitchArgs {

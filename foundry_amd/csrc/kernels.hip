@@ -5,10 +5,13 @@
 //             lane absorbs 64 bytes, lanes are joined by a combine tree whose
 //             multipliers are constants applied through nibble tables in LDS).
 //   k_group   template_of[g] = lowest graph with the same key digest and length.
-//   k_node    one workgroup per graph: per node, the param layout, the compare
-//             against the template's node, memset/memcpy pointer relocation,
-//             node-type and kernel-entry digests, the node descriptors the
-//             diff pass consumes, and the diff-tile -> first-node table.
+//   k_node_a  one workgroup per 256-node chunk of a graph: per node, the
+//             param layout, the compare against the template's node,
+//             memset/memcpy pointer relocation, the node-type and kernel-entry
+//             records (raw CRC per chunk) and the node descriptor.
+//   k_node_b  one workgroup per graph: key check, chunk CRCs joined into the
+//             digests, word offsets by block scans, the diff-tile -> first-node
+//             table, ragged-word sources, slot descriptors.
 //   k_diff_t  the template graphs' words, relocated through a bucket-indexed
 //             interval search into R and the live image (1024-word units).
 //   k_diff_m  one workgroup per 4096-word tile of every other graph: coalesced
@@ -17,7 +20,8 @@
 //             lockstep batched searches for the rest, the relocated image
 //             store, and per-wave ballot compaction of the differing words
 //             into override record regions.
-//   k_scan    prefix of the per-region record counts -> per-graph offsets.
+//   k_count   override records per graph.
+//   k_scan    prefix of the per-graph record counts -> override offsets.
 //   k_compact record regions -> the dense override array in canonical order,
 //             completing each record's node and template word index.
 //   k_switch  override scatter for one graph switch.
@@ -45,14 +49,12 @@ __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
 __device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
 
 // Copy the slice tables and one family of combine multipliers into LDS.
+// `levels` combine levels are staged (log2 of the block size suffices
+// unless chunks of a block's records are joined too).
 __device__ void stage_crc_tables(const CrcConsts* cc, bool rec16, uint64_t (*slice)[256],
-                                 uint64_t (*nib)[16][16]) {
-  const uint64_t* s = &cc->slice.t[0][0];
-  uint64_t* d = &slice[0][0];
-  for (uint32_t i = threadIdx.x; i < 8 * 256; i += blockDim.x) d[i] = s[i];
-  const uint64_t* ns = rec16 ? &cc->rec16[0].t[0][0] : &cc->rec64[0].t[0][0];
-  uint64_t* nd = &nib[0][0][0];
-  for (uint32_t i = threadIdx.x; i < kTreeLevels * 256; i += blockDim.x) nd[i] = ns[i];
+                                 uint64_t (*nib)[16][16], uint32_t levels = kTreeLevels) {
+  stage_words(&slice[0][0], &cc->slice.t[0][0], 8 * 256);
+  stage_words(&nib[0][0][0], rec16 ? &cc->rec16[0].t[0][0] : &cc->rec64[0].t[0][0], levels * 256);
   __syncthreads();
 }
 
@@ -194,64 +196,121 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
 
 // ---- node pass ----------------------------------------------------------
 
+// A kernel node's params: layout, bounds and sizes.
 struct Side {
   uint32_t words;
   uint32_t num_params;
   uint32_t arg_size;
   bool bad, extra, ragged;
   uint64_t src;        // absolute byte offset of the blob
+  uint64_t pbytes;     // param bytes (0 when bad)
   const uint8_t* pidx; // param entries (per-param style)
 };
 
-__device__ Side kernel_side(const uint8_t* img, const DevGraph& G, const uint8_t* e) {
-  Side s{};
-  const uint32_t pio = ld_u32(e + FDY_KOFF_PARAM_INDEX), np = ld_u32(e + FDY_KOFF_NUM_PARAMS);
-  const uint32_t ao = ld_u32(e + FDY_KOFF_ARG_OFFSET), as = ld_u32(e + FDY_KOFF_ARG_SIZE);
-  const uint32_t no = ld_u32(e + FDY_KOFF_NAME_OFFSET), nl = ld_u32(e + FDY_KOFF_NAME_LENGTH);
-  bool bad = (uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS] ||
-             (uint64_t)pio + 8ull * np > G.sec_size[FDY_SEC_PARAM_INDEX];
+// The param references of kernel node entry e: the name, param-index and
+// arg-buffer bounds; an extra-style node's blob.  Per-param nodes are
+// completed by scan_params.
+__device__ __forceinline__ void side_header(const uint8_t* img, const DevGraph& G, const uint8_t* e, Side& s) {
+  s = Side{};
+  const uint32_t pio = f32(e, FDY_KOFF_PARAM_INDEX), np = f32(e, FDY_KOFF_NUM_PARAMS);
+  const uint32_t ao = f32(e, FDY_KOFF_ARG_OFFSET), as = f32(e, FDY_KOFF_ARG_SIZE);
+  const uint32_t no = f32(e, FDY_KOFF_NAME_OFFSET), nl = f32(e, FDY_KOFF_NAME_LENGTH);
+  s.bad = (uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS] ||
+          (uint64_t)pio + 8ull * np > G.sec_size[FDY_SEC_PARAM_INDEX];
   s.extra = ao != FDY_NO_ARG_BUFFER;
   s.num_params = np;
   s.arg_size = as;
   s.pidx = img + G.sec_off[FDY_SEC_PARAM_INDEX] + pio;
-  if (!bad && s.extra) {
-    bad = (uint64_t)ao + as > G.sec_size[FDY_SEC_ARG_DATA];
+  if (!s.bad && s.extra) {
+    s.bad = (uint64_t)ao + as > G.sec_size[FDY_SEC_ARG_DATA];
     s.words = (as + 7) / 8;
     s.src = G.sec_off[FDY_SEC_ARG_DATA] + ao;
     s.ragged = (ao & 7) || (as & 7);
-  } else if (!bad) {
-    uint64_t prev = 0, words = 0;
-    for (uint32_t j = 0; j < np; ++j) {
-      const uint32_t o = ld_u32(s.pidx + 8ull * j), sz = ld_u32(s.pidx + 8ull * j + 4);
-      if ((uint64_t)o + sz > G.sec_size[FDY_SEC_PARAM_DATA]) {
-        bad = true;
-        break;
-      }
-      if (j == 0) {
-        s.src = G.sec_off[FDY_SEC_PARAM_DATA] + o;
-        prev = o;
-      }
-      if ((sz & 7) || (o & 7) || o != prev) s.ragged = true;
-      prev = (uint64_t)o + sz;
-      words += (sz + 7) / 8;
-    }
-    s.words = words > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)words;
+    s.pbytes = as;
   }
-  if (bad) {
+  if (s.bad) {
     s.words = 0;
     s.ragged = false;
+    s.pbytes = 0;
   }
-  s.bad = bad;
-  return s;
 }
 
-__device__ bool same_layout(const Side& a, const Side& b) {
+// Param entry j ({u32 offset, u32 size}) into a side's running totals.
+__device__ inline void side_param(const DevGraph& G, Side& s, uint32_t j, uint64_t entry, uint64_t& prev,
+                                  uint64_t& words) {
+  const uint32_t o = (uint32_t)entry, sz = (uint32_t)(entry >> 32);
+  if ((uint64_t)o + sz > G.sec_size[FDY_SEC_PARAM_DATA]) {
+    s.bad = true;
+    return;
+  }
+  if (j == 0) {
+    s.src = G.sec_off[FDY_SEC_PARAM_DATA] + o;
+    prev = o;
+  }
+  if ((sz & 7) || (o & 7) || o != prev) s.ragged = true;
+  prev = (uint64_t)o + sz;
+  words += (sz + 7) / 8;
+  s.pbytes += sz;
+}
+
+// The per-param entries of a kernel node (with_g) and of its template's node
+// (with_t), walked together in batches of kParamBatch entries per side whose
+// loads are all issued before any is used.  *same_sizes: equal param counts
+// and sizes.
+constexpr uint32_t kParamBatch = 8;
+
+__device__ __forceinline__ void scan_params(const DevGraph& Gg, Side& g, bool with_g, const DevGraph& Gt, Side& t,
+                                            bool with_t, bool* same_sizes) {
+  const bool wg = with_g && !g.bad && !g.extra;
+  const bool wt = with_t && !t.bad && !t.extra;
+  const uint32_t ng = wg ? g.num_params : 0, nt = wt ? t.num_params : 0;
+  uint64_t prev_g = 0, prev_t = 0, words_g = 0, words_t = 0;
+  bool same = ng == nt;
+  // Entries of a side sit at one alignment: the common 8-byte-aligned case
+  // loads them directly, the rest through byte-safe loads.
+  const bool aligned = ((reinterpret_cast<uintptr_t>(g.pidx) | reinterpret_cast<uintptr_t>(t.pidx)) & 7) == 0;
+  for (uint32_t jb = 0; jb < max(ng, nt); jb += kParamBatch) {
+    uint64_t eg[kParamBatch], et[kParamBatch];
+    if (aligned) {
+#pragma unroll
+      for (uint32_t k = 0; k < kParamBatch; ++k) {
+        const uint32_t j = jb + k;
+        eg[k] = j < ng ? *reinterpret_cast<const uint64_t*>(g.pidx + 8ull * j) : 0;
+        et[k] = j < nt ? *reinterpret_cast<const uint64_t*>(t.pidx + 8ull * j) : 0;
+      }
+    } else {
+#pragma unroll
+      for (uint32_t k = 0; k < kParamBatch; ++k) {
+        const uint32_t j = jb + k;
+        eg[k] = j < ng ? ld_u64(g.pidx + 8ull * j) : 0;
+        et[k] = j < nt ? ld_u64(t.pidx + 8ull * j) : 0;
+      }
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kParamBatch; ++k) {
+      const uint32_t j = jb + k;
+      if (j < ng && !g.bad) side_param(Gg, g, j, eg[k], prev_g, words_g);
+      if (j < nt && !t.bad) side_param(Gt, t, j, et[k], prev_t, words_t);
+      if (j < ng && j < nt) same &= (eg[k] >> 32) == (et[k] >> 32);
+    }
+  }
+  auto finish = [](Side& s, bool walked, uint64_t words) {
+    if (walked) s.words = words > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)words;
+    if (s.bad) {
+      s.words = 0;
+      s.ragged = false;
+      s.pbytes = 0;
+    }
+  };
+  if (with_g) finish(g, wg, words_g);
+  if (with_t) finish(t, wt, words_t);
+  *same_sizes = same;
+}
+
+__device__ __forceinline__ bool same_layout(const Side& a, const Side& b, bool same_sizes) {
   if (a.bad || b.bad || a.extra != b.extra) return false;
   if (a.extra) return a.arg_size == b.arg_size;
-  if (a.num_params != b.num_params) return false;
-  for (uint32_t j = 0; j < a.num_params; ++j)
-    if (ld_u32(a.pidx + 8ull * j + 4) != ld_u32(b.pidx + 8ull * j + 4)) return false;
-  return true;
+  return same_sizes;
 }
 
 // Effective launch attributes (csrc/CUDAGraphParallel.cpp:1211-1389): common
@@ -262,23 +321,23 @@ struct Attrs {
 };
 
 __device__ inline void attrs_from(const uint8_t* b, Attrs& a, bool merge) {
-  const uint32_t f = ld_u32(b);
+  const uint32_t f = f32(b, 0);
   if (f & FDY_KNA_CLUSTER_DIM) {
     a.has_cluster = 1;
-    a.cx = (int32_t)ld_u32(b + 4);
-    a.cy = (int32_t)ld_u32(b + 8);
-    a.cz = (int32_t)ld_u32(b + 12);
+    a.cx = (int32_t)f32(b, 4);
+    a.cy = (int32_t)f32(b, 8);
+    a.cz = (int32_t)f32(b, 12);
   }
   if (f & FDY_KNA_PREFERRED_CLUSTER_DIM) {
     a.has_pref = 1;
-    a.px = (int32_t)ld_u32(b + 16);
-    a.py = (int32_t)ld_u32(b + 20);
-    a.pz = (int32_t)ld_u32(b + 24);
+    a.px = (int32_t)f32(b, 16);
+    a.py = (int32_t)f32(b, 20);
+    a.pz = (int32_t)f32(b, 24);
   }
   // When merging per-node attrs over common ones, a negative value does not override.
   auto take = [&](uint32_t flag, uint32_t off, int32_t& dst) {
     if (!(f & flag)) return;
-    int32_t v = (int32_t)ld_u32(b + off);
+    int32_t v = (int32_t)f32(b, off);
     if (!merge || v >= 0) dst = v;
   };
   take(FDY_KNA_CLUSTER_SCHEDULING, 28, a.sched);
@@ -292,15 +351,16 @@ __device__ inline void attrs_from(const uint8_t* b, Attrs& a, bool merge) {
   }
   if (f & FDY_KNA_SHARED_MEM_CARVEOUT) {
     a.has_carve = 1;
-    a.carve = (int32_t)ld_u32(b + 48);
+    a.carve = (int32_t)f32(b, 48);
   }
 }
 
-__device__ Attrs effective_attrs(const uint8_t* img, const DevGraph& G, const uint8_t* e) {
+// `common`: the graph's common kernel attrs, or null.
+__device__ __forceinline__ Attrs effective_attrs(const uint8_t* common, const uint8_t* e) {
   Attrs a{0, 0, 0, 0, 0, 0, 0, 0, -1, -1, -1, -1, 0, 0, 0, 0, 0};
-  if (G.flags & FDY_HAS_COMMON_ATTRS) attrs_from(img + G.sec_off[FDY_SEC_COMMON_ATTRS], a, false);
-  if (ld_u32(e + FDY_KOFF_KNA_FLAGS) != 0) attrs_from(e + FDY_KOFF_KNA_FLAGS, a, true);
-  const int32_t w = (int32_t)ld_u32(e + 64), h = (int32_t)ld_u32(e + 68), d = (int32_t)ld_u32(e + 72);
+  if (common) attrs_from(common, a, false);
+  if (f32(e, FDY_KOFF_KNA_FLAGS) != 0) attrs_from(e + FDY_KOFF_KNA_FLAGS, a, true);
+  const int32_t w = (int32_t)f32(e, 64), h = (int32_t)f32(e, 68), d = (int32_t)f32(e, 72);
   if (w > 0 || h > 0 || d > 0) {
     a.has_cluster = 1;
     a.cx = w > 0 ? w : 1;
@@ -310,7 +370,7 @@ __device__ Attrs effective_attrs(const uint8_t* img, const DevGraph& G, const ui
   return a;
 }
 
-__device__ bool attrs_equal(const Attrs& a, const Attrs& b) {
+__device__ __forceinline__ bool attrs_equal(const Attrs& a, const Attrs& b) {
   const int32_t* x = &a.has_cluster;
   const int32_t* y = &b.has_cluster;
   bool eq = true;
@@ -318,84 +378,88 @@ __device__ bool attrs_equal(const Attrs& a, const Attrs& b) {
   return eq;
 }
 
-__device__ bool names_equal(const uint8_t* img, const DevGraph& A, const uint8_t* ea, const DevGraph& B,
-                            const uint8_t* eb, bool same_strings) {
-  const uint32_t ao = ld_u32(ea + FDY_KOFF_NAME_OFFSET), al = ld_u32(ea + FDY_KOFF_NAME_LENGTH);
-  const uint32_t bo = ld_u32(eb + FDY_KOFF_NAME_OFFSET), bl = ld_u32(eb + FDY_KOFF_NAME_LENGTH);
+// A graph's string section (8-byte aligned start), in LDS or in the image.
+struct Strings {
+  const uint8_t* p;
+  uint64_t size;
+};
+
+// Equal kernel names, compared through 8-byte windows.
+__device__ __forceinline__ bool names_equal(const Strings& A, const uint8_t* ea, const Strings& B, const uint8_t* eb) {
+  const uint32_t ao = f32(ea, FDY_KOFF_NAME_OFFSET), al = f32(ea, FDY_KOFF_NAME_LENGTH);
+  const uint32_t bo = f32(eb, FDY_KOFF_NAME_OFFSET), bl = f32(eb, FDY_KOFF_NAME_LENGTH);
   if (al != bl) return false;
-  if ((uint64_t)ao + al > A.sec_size[FDY_SEC_STRINGS] || (uint64_t)bo + bl > B.sec_size[FDY_SEC_STRINGS])
-    return false;
-  if (same_strings && ao == bo) return true;
-  const uint8_t* pa = img + A.sec_off[FDY_SEC_STRINGS] + ao;
-  const uint8_t* pb = img + B.sec_off[FDY_SEC_STRINGS] + bo;
-  for (uint32_t i = 0; i < al; ++i)
-    if (pa[i] != pb[i]) return false;
-  return true;
+  if ((uint64_t)ao + al > A.size || (uint64_t)bo + bl > B.size) return false;
+  bool eq = true;
+  for (uint32_t i = 0; i < al && eq; i += 8) {
+    const uint32_t n = min(8u, al - i);
+    const uint64_t m = n == 8 ? ~0ull : (1ull << (8 * n)) - 1;
+    eq = ((stream_window(A.p, A.size, (int64_t)ao + i) ^ stream_window(B.p, B.size, (int64_t)bo + i)) & m) == 0;
+  }
+  return eq;
 }
 
 // CRC-64/XZ of a kernel's name.
-__device__ uint64_t name_crc(const uint8_t* img, const DevGraph& G, const uint8_t* e,
-                             const uint64_t (*slice)[256]) {
-  const uint32_t no = ld_u32(e + FDY_KOFF_NAME_OFFSET), nl = ld_u32(e + FDY_KOFF_NAME_LENGTH);
-  if ((uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS]) return 0;
-  // The string section starts 8-byte aligned: read it through aligned words.
-  const uint8_t* base = img + G.sec_off[FDY_SEC_STRINGS];
-  const uint64_t S = G.sec_size[FDY_SEC_STRINGS];
+__device__ __forceinline__ uint64_t name_crc(const Strings& S, const uint8_t* e, const uint64_t (*slice)[256]) {
+  const uint32_t no = f32(e, FDY_KOFF_NAME_OFFSET), nl = f32(e, FDY_KOFF_NAME_LENGTH);
+  if ((uint64_t)no + nl > S.size) return 0;
   uint64_t c = ~0ull;
   uint32_t i = 0;
-  for (; i + 8 <= nl; i += 8) c = crc_slice8(slice, c, stream_window(base, S, (int64_t)no + i));
+  for (; i + 8 <= nl; i += 8) c = crc_slice8(slice, c, stream_window(S.p, S.size, (int64_t)no + i));
   if (i < nl) {
-    uint64_t tail = stream_window(base, S, (int64_t)no + i);
+    uint64_t tail = stream_window(S.p, S.size, (int64_t)no + i);
     for (; i < nl; ++i, tail >>= 8) c = crc_byte(slice[0], c, (uint8_t)tail);
   }
   return ~c;
 }
 
 // Relocated memset dst / memcpy dst, src of node entry e (0 when not a pointer node).
-__device__ void node_pointers(const uint8_t* e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
+__device__ __forceinline__ void node_pointers(const uint8_t* e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
   const uint8_t type = e[FDY_NODE_OFF_TYPE];
   *p0 = 0;
   *p1 = 0;
   if (type == FDY_NODE_MEMSET) {
-    *p0 = reloc_word(r, ld_u64(e + FDY_MSOFF_DST));
+    *p0 = reloc_word(r, f64(e, FDY_MSOFF_DST));
   } else if (type == FDY_NODE_MEMCPY) {
-    const uint64_t dst = ld_u64(e + FDY_MCOFF_DST), src = ld_u64(e + FDY_MCOFF_SRC);
-    const int32_t dt = (int32_t)ld_u32(e + FDY_MCOFF_DST_MEMTYPE), st = (int32_t)ld_u32(e + FDY_MCOFF_SRC_MEMTYPE);
+    const uint64_t dst = f64(e, FDY_MCOFF_DST), src = f64(e, FDY_MCOFF_SRC);
+    const int32_t dt = (int32_t)f32(e, FDY_MCOFF_DST_MEMTYPE), st = (int32_t)f32(e, FDY_MCOFF_SRC_MEMTYPE);
     *p0 = (dt == FDY_MEMTYPE_DEVICE || dt == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, dst) : dst;
     *p1 = (st == FDY_MEMTYPE_DEVICE || st == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, src) : src;
   }
 }
 
-__device__ bool u64_range_differs(const uint8_t* a, const uint8_t* b, uint32_t off, uint32_t n) {
+__device__ __forceinline__ bool u64_range_differs(const uint8_t* a, const uint8_t* b, uint32_t off, uint32_t n) {
   bool d = false;
-  for (uint32_t i = 0; i < n; i += 8) d |= ld_u64(a + off + i) != ld_u64(b + off + i);
+  for (uint32_t i = 0; i < n; i += 8) d |= f64(a, off + i) != f64(b, off + i);
   return d;
 }
 
-__device__ bool desc_differs(const uint8_t* img, const DevGraph& A, const uint8_t* ea, const DevGraph& B,
-                             const uint8_t* eb, bool same_strings, uint64_t pa0, uint64_t pa1, uint64_t pb0,
+// Does node entry ea (strings A, common attrs ca) differ in its descriptor
+// from eb (strings B, common attrs cb)?  pa/pb: relocated pointers.
+__device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const uint8_t* ea, const Strings& B,
+                             const uint8_t* cb, const uint8_t* eb, uint64_t pa0, uint64_t pa1, uint64_t pb0,
                              uint64_t pb1) {
   const uint8_t ta = ea[FDY_NODE_OFF_TYPE], tb = eb[FDY_NODE_OFF_TYPE];
   if (ta != tb) return true;
   switch (ta) {
     case FDY_NODE_KERNEL: {
       bool d = false;
-      for (uint32_t off = 8; off < 44; off += 4) d |= ld_u32(ea + off) != ld_u32(eb + off);
-      for (uint32_t off = 52; off < 76; off += 4) d |= ld_u32(ea + off) != ld_u32(eb + off);
+      for (uint32_t off = 8; off < 44; off += 4) d |= f32(ea, off) != f32(eb, off);
+      for (uint32_t off = 52; off < 76; off += 4) d |= f32(ea, off) != f32(eb, off);
       if (d) return true;
-      if (!names_equal(img, A, ea, B, eb, same_strings)) return true;
-      return !attrs_equal(effective_attrs(img, A, ea), effective_attrs(img, B, eb));
+      if (!names_equal(A, ea, B, eb)) return true;
+      return !attrs_equal(effective_attrs(ca, ea), effective_attrs(cb, eb));
     }
     case FDY_NODE_MEMSET:
-      return pa0 != pb0 || ld_u32(ea + 16) != ld_u32(eb + 16) || u64_range_differs(ea, eb, 24, 16) ||
-             ld_u32(ea + 40) != ld_u32(eb + 40) || ld_u64(ea + 48) != ld_u64(eb + 48);
+      return pa0 != pb0 || f32(ea, 16) != f32(eb, 16) || u64_range_differs(ea, eb, 24, 16) ||
+             f32(ea, 40) != f32(eb, 40) || f64(ea, 48) != f64(eb, 48);
     case FDY_NODE_MEMCPY:
       return pa0 != pb0 || pa1 != pb1 || u64_range_differs(ea, eb, 8, 24) || u64_range_differs(ea, eb, 40, 48) ||
-             ld_u32(ea + 88) != ld_u32(eb + 88) || u64_range_differs(ea, eb, 104, 48) ||
-             ld_u32(ea + 152) != ld_u32(eb + 152);
+             f32(ea, 88) != f32(eb, 88) || u64_range_differs(ea, eb, 104, 48) ||
+             f32(ea, 152) != f32(eb, 152);
     case FDY_NODE_EVENT_RECORD:
     case FDY_NODE_EVENT_WAIT:
-      return ld_u32(ea + FDY_EVOFF_ID) != ld_u32(eb + FDY_EVOFF_ID);
+      return f32(ea, FDY_EVOFF_ID) != f32(eb, FDY_EVOFF_ID);
     default:
       return false;
   }
@@ -443,14 +507,199 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
   (void)e;
 }
 
-__global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
+// The node pass runs in two parts.
+//
+// Part A, k_node_a: one workgroup of kNodeChunk threads per chunk of a
+// graph's nodes, one node per thread.  A graph's chunks end at its last
+// node, so its first chunk is padded at the front (leading zero records
+// leave a zero-initialised CRC at zero).  Per node: type, params and their
+// bounds, layout and descriptor against the template's node, relocated
+// memset/memcpy pointers, the node-type and kernel-entry records; written
+// to the node descriptor with the node's word counts in place of its word
+// offsets.  Per chunk: the raw CRCs of the two record streams, word and
+// param-byte totals, status bits.
+//
+// Part B, k_node_b: one workgroup per graph: the template's key bytes, the
+// chunk CRCs shifted to their place, word offsets by block scans, the
+// tile -> first-node table, ragged-word sources, flatness, status, digests
+// and the slot descriptors of the diff pass.
+
+__global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
+  constexpr uint32_t kLevels = 8;      // combine levels for kNodeChunk records
+  constexpr uint32_t kStrStage = 2048; // string sections up to this size are staged in LDS
+  static_assert((1u << kLevels) == kNodeChunk, "one combine level per doubling");
   __shared__ uint64_t s_slice[8][256];
-  __shared__ uint64_t s_nib[kTreeLevels][16][16];
-  __shared__ uint64_t s_wave[kNodeThreads / 64];
+  __shared__ uint64_t s_nib[kLevels][16][16];
+  __shared__ uint64_t s_str[2][kStrStage / 8];
+  __shared__ uint64_t s_common[2][7];
+  __shared__ uint64_t s_wave[kNodeChunk / 64];
+  __shared__ uint32_t s_sum[2][kNodeChunk / 64];
+  __shared__ uint64_t s_pb[kNodeChunk / 64];
+  __shared__ uint32_t s_status;
+
+  const uint32_t chunk = blockIdx.x, tid = threadIdx.x;
+  const uint32_t g = a.chunk_graph[chunk];
+  const uint32_t t = a.template_of[g];
+  const bool is_t = t == g;
+  const DevGraph& Gg = a.graphs[g];
+  const DevGraph& Gt = a.graphs[t];
+  const uint32_t N = Gg.num_nodes, NT = Gt.num_nodes;
+  const uint8_t* img = a.img;
+  if (tid == 0) s_status = 0;
+
+  // CRC tables, the (small) string sections and the common attrs in LDS;
+  // sections start 8-byte aligned.
+  auto stage_strings = [&](const DevGraph& G, uint64_t* buf) -> Strings {
+    Strings S{img + G.sec_off[FDY_SEC_STRINGS], G.sec_size[FDY_SEC_STRINGS]};
+    if (S.size <= kStrStage) {
+      stage_words(buf, reinterpret_cast<const uint64_t*>(S.p), (uint32_t)((S.size + 7) / 8));
+      S.p = reinterpret_cast<const uint8_t*>(buf);
+    }
+    return S;
+  };
+  auto stage_common = [&](const DevGraph& G, uint64_t* buf) -> const uint8_t* {
+    if (!(G.flags & FDY_HAS_COMMON_ATTRS) || G.sec_size[FDY_SEC_COMMON_ATTRS] < 52) return nullptr;
+    if (tid < 7) buf[tid] = reinterpret_cast<const uint64_t*>(img + G.sec_off[FDY_SEC_COMMON_ATTRS])[tid];
+    return reinterpret_cast<const uint8_t*>(buf);
+  };
+  const Strings sg_str = stage_strings(Gg, s_str[0]);
+  const Strings st_str = is_t ? sg_str : stage_strings(Gt, s_str[1]);
+  const uint8_t* common_g = stage_common(Gg, s_common[0]);
+  const uint8_t* common_t = is_t ? common_g : stage_common(Gt, s_common[1]);
+  stage_crc_tables(a.cc, true, s_slice, s_nib, kLevels);  // ends with a barrier
+  const uint64_t (*slice)[256] = s_slice;
+
+  const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
+  const int64_t first = (int64_t)(chunk - Gg.chunk_base) * kNodeChunk - pad;  // node of thread 0
+  const int64_t ns = first + tid;
+  const bool valid = ns >= 0 && ns < (int64_t)N;
+  const uint32_t n = valid ? (uint32_t)ns : 0;
+  uint32_t words_g = 0, words_t = 0, flags = 0;
+  uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0, pbytes = 0;
+  uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
+  const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
+  const uint8_t* et = img + Gt.sec_off[FDY_SEC_NODES] + 168ull * (n < NT ? n : 0);
+  if (valid) {
+    const uint8_t type = eg[FDY_NODE_OFF_TYPE];
+    const bool has_t = !is_t && n < NT;
+    const uint8_t ttype = has_t ? et[FDY_NODE_OFF_TYPE] : 0xFF;
+    tw0 = type;
+    Side sg{}, st{};
+    bool same_sizes = false;
+    if (type == FDY_NODE_KERNEL) {
+      // Cluster dims of the recomputed key (csrc/CUDAGraphParallel.cpp:1807-1833).
+      uint32_t cx = 0, cy = 0, cz = 0;
+      if (f32(eg, FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
+        cx = f32(eg, 80);
+        cy = f32(eg, 84);
+        cz = f32(eg, 88);
+      }
+      if (cx == 0 && common_g && (f32(common_g, 0) & FDY_KNA_CLUSTER_DIM)) {
+        cx = f32(common_g, 4);
+        cy = f32(common_g, 8);
+        cz = f32(common_g, 12);
+      }
+      if (cx == 0) {
+        cx = f32(eg, 64);
+        cy = f32(eg, 68);
+        cz = f32(eg, 72);
+      }
+      tw0 |= (uint64_t)cx << 32;
+      tw1 = cy | ((uint64_t)cz << 32);
+      kw0 = f64(eg, FDY_KOFF_BINARY_HASH);
+      kw1 = name_crc(sg_str, eg, slice);
+      side_header(img, Gg, eg, sg);
+    }
+    const bool t_kernel = has_t && ttype == FDY_NODE_KERNEL;
+    if (t_kernel) side_header(img, Gt, et, st);
+    scan_params(Gg, sg, type == FDY_NODE_KERNEL, Gt, st, t_kernel, &same_sizes);
+    if (type == FDY_NODE_KERNEL) {
+      words_g = sg.words;
+      pbytes = sg.pbytes;
+      src_g = sg.src;
+      if (sg.ragged) flags |= FDY_NODE_RAGGED;
+      if (sg.bad) flags |= kNodeBad;
+    }
+    node_pointers(eg, a.reloc, &p0, &p1);
+    if (is_t) {
+      flags |= FDY_NODE_TEMPLATE;
+    } else if (has_t) {
+      uint64_t q0, q1;
+      node_pointers(et, a.reloc, &q0, &q1);
+      bool layout = ttype != type;
+      if (t_kernel) {
+        words_t = st.words;
+        src_t = st.src;
+        if (st.ragged) flags |= kNodeRaggedT;
+        if (type == FDY_NODE_KERNEL) layout = !same_layout(sg, st, same_sizes);
+      }
+      if (layout) flags |= FDY_NODE_LAYOUT;
+      else if (words_g) flags |= kNodeCompare;
+      if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, p0, p1, q0, q1)) flags |= FDY_NODE_DESC;
+    } else {
+      flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
+    }
+    if (flags & kNodeBad) atomicOr(&s_status, FDY_GRAPH_BAD_PARAMS);
+
+    const uint64_t gi = Gg.node_base + n;
+    NodeDesc d;
+    d.gword = 0;          // word offsets are filled in by k_node_b
+    d.nwords = words_g;
+    d.tword = words_t;    // the template node's word count until then
+    d.flags = flags;
+    d.src_g = src_g;
+    d.src_t = src_t;
+    a.node_desc[gi] = d;
+    a.node_flags[gi] = (uint8_t)(flags & 0x0F);
+    a.node_ptrs[2 * gi] = p0;
+    a.node_ptrs[2 * gi + 1] = p1;
+    if (is_t) a.live_src[gi] = g;
+  }
+
+  uint64_t zt = 0, zk = 0;
+  if (valid) {
+    zt = crc_slice8(slice, crc_slice8(slice, 0, tw0), tw1);
+    zk = crc_slice8(slice, crc_slice8(slice, 0, kw0), kw1);
+  }
+  zt = block_crc_combine(zt, s_nib, s_wave);
+  zk = block_crc_combine(zk, s_nib, s_wave);
+  uint32_t sum_g = words_g, sum_t = words_t;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    sum_g += __shfl_down(sum_g, (unsigned)d, 64);
+    sum_t += __shfl_down(sum_t, (unsigned)d, 64);
+    pbytes += shfl_down64(pbytes, d);
+  }
+  if ((tid & 63) == 0) {
+    s_sum[0][tid >> 6] = sum_g;
+    s_sum[1][tid >> 6] = sum_t;
+    s_pb[tid >> 6] = pbytes;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    NodeChunk c;
+    c.crc_type = zt;
+    c.crc_kent = zk;
+    c.pbytes = 0;
+    uint64_t wg = 0, wt = 0;
+    for (uint32_t w = 0; w < kNodeChunk / 64; ++w) {
+      wg += s_sum[0][w];
+      wt += s_sum[1][w];
+      c.pbytes += s_pb[w];
+    }
+    c.words_g = wg > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)wg;
+    c.words_t = wt > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)wt;
+    c.status = s_status;
+    c.pad_ = 0;
+    a.chunks[chunk] = c;
+  }
+}
+
+__global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   __shared__ uint32_t s_tmp[kNodeThreads / 64];
-  __shared__ uint32_t s_status, s_key_differs, s_str_differs, s_words, s_flat, s_tbase;
-  __shared__ unsigned long long s_pbytes;
-  stage_crc_tables(a.cc, true, s_slice, s_nib);
+  __shared__ uint64_t s_x[2][kNodeThreads / 64];
+  __shared__ unsigned long long s_pb;
+  __shared__ uint32_t s_status, s_key_differs, s_words, s_flat, s_tbase;
 
   const uint32_t g = blockIdx.x;
   const uint32_t t = a.template_of[g];
@@ -459,12 +708,11 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
   const DevGraph& Gt = a.graphs[t];
   const uint32_t N = Gg.num_nodes, NT = Gt.num_nodes;
   const uint8_t* img = a.img;
-
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (threadIdx.x == 0) {
     s_status = 0;
     s_key_differs = 0;
-    s_str_differs = 0;
-    s_pbytes = 0;
+    s_pb = 0;
     s_flat = 1;
   }
   __syncthreads();
@@ -480,157 +728,97 @@ __global__ __launch_bounds__(kNodeThreads) void k_node(RestoreArgs a) {
       for (uint64_t q = threadIdx.x; q * 8 < L; q += kNodeThreads)
         if (stream_window(pg, L, (int64_t)q * 8) != stream_window(pt, L, (int64_t)q * 8)) s_key_differs = 1;
     }
-    const uint64_t S = Gg.sec_size[FDY_SEC_STRINGS];
-    if (S != Gt.sec_size[FDY_SEC_STRINGS]) {
-      if (threadIdx.x == 0) s_str_differs = 1;
-    } else {
-      const uint8_t* pg = img + Gg.sec_off[FDY_SEC_STRINGS];
-      const uint8_t* pt = img + Gt.sec_off[FDY_SEC_STRINGS];
-      for (uint64_t q = threadIdx.x; q * 8 < S; q += kNodeThreads)
-        if (stream_window(pg, S, (int64_t)q * 8) != stream_window(pt, S, (int64_t)q * 8)) s_str_differs = 1;
-    }
-  }
-  __syncthreads();
-  const bool same_strings = !s_str_differs;
-  if (threadIdx.x == 0) {
-    if (s_key_differs) s_status |= FDY_GRAPH_COLLISION;
-    if (!is_t && N != NT) s_status |= kGraphNodeCount;
   }
 
-  const uint32_t pad = (kNodeThreads - N % kNodeThreads) % kNodeThreads;
-  const uint32_t nchunks = (N + pad) / kNodeThreads;
+  // Chunk results: each chunk's raw CRC times x^(8 * bytes after it),
+  // XOR-joined; param bytes and status bits.
+  const uint32_t nch = (N + kNodeChunk - 1) / kNodeChunk;
+  uint64_t xt = 0, xk = 0, pb = 0;
+  uint32_t st = 0;
+  for (uint32_t c = threadIdx.x; c < nch; c += kNodeThreads) {
+    const NodeChunk ch = a.chunks[Gg.chunk_base + c];
+    const uint64_t m = x2n_mod(a.cc->x2n.v, 16ull * kNodeChunk * (nch - 1 - c), 3);
+    xt ^= gf2_mulmod(m, ch.crc_type);
+    xk ^= gf2_mulmod(m, ch.crc_kent);
+    pb += ch.pbytes;
+    st |= ch.status;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    xt ^= shfl_down64(xt, d);
+    xk ^= shfl_down64(xk, d);
+  }
+  if (lane == 0) {
+    s_x[0][wave] = xt;
+    s_x[1][wave] = xk;
+  }
+  if (pb) atomicAdd(&s_pb, (unsigned long long)pb);
+  if (st) atomicOr(&s_status, st);
+
+  // Word offsets of every node in the graph's and in the template's image.
   uint32_t gcarry = 0, tcarry = 0;
-  uint64_t acc_type = 0, acc_kent = 0;
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    const int64_t ns = (int64_t)c * kNodeThreads + threadIdx.x - pad;
-    const bool valid = ns >= 0 && ns < (int64_t)N;
-    const uint32_t n = valid ? (uint32_t)ns : 0;
-    uint32_t words_g = 0, words_t = 0, flags = 0;
-    uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0;
-    uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
-    Side sg{};
-    const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
-    if (valid) {
-      const uint8_t type = eg[FDY_NODE_OFF_TYPE];
-      tw0 = type;
-      if (type == FDY_NODE_KERNEL) {
-        // Cluster dims of the recomputed key (csrc/CUDAGraphParallel.cpp:1807-1833).
-        uint32_t cx = 0, cy = 0, cz = 0;
-        if (ld_u32(eg + FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
-          cx = ld_u32(eg + 80);
-          cy = ld_u32(eg + 84);
-          cz = ld_u32(eg + 88);
-        }
-        if (cx == 0 && (Gg.flags & FDY_HAS_COMMON_ATTRS)) {
-          const uint8_t* ca = img + Gg.sec_off[FDY_SEC_COMMON_ATTRS];
-          if (ld_u32(ca) & FDY_KNA_CLUSTER_DIM) {
-            cx = ld_u32(ca + 4);
-            cy = ld_u32(ca + 8);
-            cz = ld_u32(ca + 12);
-          }
-        }
-        if (cx == 0) {
-          cx = ld_u32(eg + 64);
-          cy = ld_u32(eg + 68);
-          cz = ld_u32(eg + 72);
-        }
-        tw0 |= (uint64_t)cx << 32;
-        tw1 = cy | ((uint64_t)cz << 32);
-        kw0 = ld_u64(eg + FDY_KOFF_BINARY_HASH);
-        kw1 = name_crc(img, Gg, eg, s_slice);
-        sg = kernel_side(img, Gg, eg);
-        words_g = sg.words;
-        if (!sg.bad) {
-          uint64_t pb = sg.extra ? sg.arg_size : 0;
-          if (!sg.extra)
-            for (uint32_t j = 0; j < sg.num_params; ++j) pb += ld_u32(sg.pidx + 8ull * j + 4);
-          if (pb) atomicAdd(&s_pbytes, (unsigned long long)pb);
-        }
-        src_g = sg.src;
-        if (sg.ragged) flags |= FDY_NODE_RAGGED;
-        if (sg.bad) flags |= kNodeBad;
-      }
-      node_pointers(eg, a.reloc, &p0, &p1);
-      if (is_t) {
-        flags |= FDY_NODE_TEMPLATE;
-      } else if (n < NT) {
-        const uint8_t* et = img + Gt.sec_off[FDY_SEC_NODES] + 168ull * n;
-        uint64_t q0, q1;
-        node_pointers(et, a.reloc, &q0, &q1);
-        bool layout = et[FDY_NODE_OFF_TYPE] != type;
-        if (et[FDY_NODE_OFF_TYPE] == FDY_NODE_KERNEL) {
-          const Side st = kernel_side(img, Gt, et);
-          words_t = st.words;
-          src_t = st.src;
-          if (st.ragged) flags |= kNodeRaggedT;
-          if (type == FDY_NODE_KERNEL) layout = !same_layout(sg, st);
-        }
-        if (layout) flags |= FDY_NODE_LAYOUT;
-        else if (words_g) flags |= kNodeCompare;
-        if (desc_differs(img, Gg, eg, Gt, et, same_strings, p0, p1, q0, q1)) flags |= FDY_NODE_DESC;
-      } else {
-        flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
-      }
-      if (flags & kNodeBad) atomicOr(&s_status, FDY_GRAPH_BAD_PARAMS);
-    }
+  for (uint32_t base = 0; base < N; base += kNodeThreads) {
+    const uint32_t n = base + threadIdx.x;
+    const bool valid = n < N;
+    const uint64_t gi = Gg.node_base + n;
+    NodeDesc d{};
+    if (valid) d = a.node_desc[gi];
+    const uint32_t words_g = d.nwords, words_t = d.tword;
+    uint32_t flags = d.flags;
     uint32_t tot_g, tot_t;
     const uint32_t gword = gcarry + block_excl_scan(words_g, s_tmp, &tot_g);
     const uint32_t tword = tcarry + block_excl_scan(words_t, s_tmp, &tot_t);
     // A template whose image overflows its capacity (overlapping param
     // ranges) has no usable words past the capacity; never index them.
     if ((flags & kNodeCompare) && (uint64_t)tword + words_t > Gt.word_cap) flags &= ~kNodeCompare;
-    // The graph's image is flat when every node with words is aligned and
-    // placed canonically (word w of the image at param-data byte 8w), and
-    // likewise in the template's image for every compared node.
-    if (valid && words_g) {
-      const bool ok = !(flags & (FDY_NODE_RAGGED | kNodeRaggedT)) && src_g == Gg.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword &&
-                      (is_t || ((flags & kNodeCompare) && tword == gword &&
-                                src_t == Gt.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword));
-      if (!ok) s_flat = 0;
-    }
     if (valid) {
-      const uint64_t gi = Gg.node_base + n;
-      NodeDesc d;
+      // The graph's image is flat when every node with words is aligned and
+      // placed canonically (word w of the image at param-data byte 8w), and
+      // likewise in the template's image for every compared node.
+      if (words_g) {
+        const bool ok = !(flags & (FDY_NODE_RAGGED | kNodeRaggedT)) &&
+                        d.src_g == Gg.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword &&
+                        (is_t || ((flags & kNodeCompare) && tword == gword &&
+                                  d.src_t == Gt.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword));
+        if (!ok) s_flat = 0;
+      }
       d.gword = gword;
-      d.nwords = words_g;
       d.tword = tword;
       d.flags = flags;
-      d.src_g = src_g;
-      d.src_t = src_t;
       a.node_desc[gi] = d;
-      a.node_flags[gi] = (uint8_t)(flags & 0x0F);
-      a.node_ptrs[2 * gi] = p0;
-      a.node_ptrs[2 * gi + 1] = p1;
-      if (is_t) a.live_src[gi] = g;
       if (words_g) {
         uint64_t k = ((uint64_t)gword + kTileWords - 1) / kTileWords;
         const uint64_t k_last = ((uint64_t)gword + words_g - 1) / kTileWords;
         for (; k <= k_last && k < Gg.tile_cap; ++k) a.tile_node[Gg.tile_base + k] = n;
-        if (flags & FDY_NODE_RAGGED) write_aux(img, Gg, eg, sg, a.aux, gword);
+        if (flags & FDY_NODE_RAGGED) {
+          const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
+          Side sd_{}, none_{};
+          bool same_;
+          side_header(img, Gg, eg, sd_);
+          scan_params(Gg, sd_, true, Gg, none_, false, &same_);
+          write_aux(img, Gg, eg, sd_, a.aux, gword);
+        }
       }
-    }
-    uint64_t zt = 0, zk = 0;
-    if (valid) {
-      zt = crc_slice8(s_slice, crc_slice8(s_slice, 0, tw0), tw1);
-      zk = crc_slice8(s_slice, crc_slice8(s_slice, 0, kw0), kw1);
-    }
-    zt = block_crc_combine(zt, s_nib, s_wave);
-    zk = block_crc_combine(zk, s_nib, s_wave);
-    if (threadIdx.x == 0) {
-      acc_type = nibble_mul(s_nib[kChunkLevel], acc_type) ^ zt;
-      acc_kent = nibble_mul(s_nib[kChunkLevel], acc_kent) ^ zk;
     }
     gcarry += tot_g;
     tcarry += tot_t;
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    uint64_t acc_type = 0, acc_kent = 0;
+    for (uint32_t w = 0; w < kNodeThreads / 64; ++w) {
+      acc_type ^= s_x[0][w];
+      acc_kent ^= s_x[1][w];
+    }
     const bool overflow = gcarry > Gg.word_cap;
     s_words = overflow ? 0 : gcarry;
-    uint32_t st = s_status;
-    if (overflow) st |= FDY_GRAPH_BAD_PARAMS | kGraphOverflow;
-    a.status[g] = st;
+    uint32_t stat = s_status;
+    if (s_key_differs) stat |= FDY_GRAPH_COLLISION;
+    if (!is_t && N != NT) stat |= kGraphNodeCount;
+    if (overflow) stat |= FDY_GRAPH_BAD_PARAMS | kGraphOverflow;
+    a.status[g] = stat;
     a.gwords[g] = s_words;
-    a.pbytes[g] = s_pbytes;
+    a.pbytes[g] = s_pb;
     a.digests[4ull * g + 2] = acc_type ^ Gg.crc_fin[2];
     a.digests[4ull * g + 3] = acc_kent ^ Gg.crc_fin[3];
     if (is_t) {
@@ -839,15 +1027,14 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
 // slot's sub-range v (kSubWords consecutive words), lane l its words
 // v*kSubWords + j*64 + l for j < kMWords.  Relocation is a function of the
 // raw word, so where a compared word equals the template's raw word the
-// template's relocated word is taken from R; the words left to search are
-// gathered kSlots per lane and searched in lockstep batches.  Each wave
-// compacts its override records, in word order, into its own sub-range's
-// kSubWords-record region (graph-local word index, node filled in later by
-// k_compact) and their number into sub_count; flat tiles need neither LDS
-// nor a barrier.  k_scan and k_compact then pack the regions into the dense
-// canonical array.
+// template's relocated word is taken from R and stored at once, as are
+// partial words (never relocated).  The words left over (to be searched, or
+// possibly differing from the template) become candidates: each wave
+// compacts them, in word order, into its sub-range's region and their
+// number into sub_count, and k_diff_s settles them.  No wave waits for an
+// interval search, and flat tiles need neither LDS nor a barrier.
 constexpr uint32_t kMThreads = kSubsPerSlot * 64;
-constexpr uint32_t kSlots = 2;  // searches per lane per batch (64 VGPRs: 8 waves per SIMD)
+constexpr uint32_t kSlots = 2;  // searches per batch in the overflowed-template path
 
 // Eight waves per SIMD (at most 64 VGPRs): two workgroups per CU.
 __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
@@ -935,9 +1122,11 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
       }
     }
   }
-  if (R.n == 0 || (a.status[t] & kGraphOverflow)) {
-    // Relocation off: R equals the raw image.  Template overflowed: relocate
-    // its compared words here.
+  if (R.n == 0) {
+#pragma unroll
+    for (uint32_t j = 0; j < J; ++j) fr[j] = ft[j];  // relocation off: R equals the raw image
+  } else if (a.status[t] & kGraphOverflow) {
+    // The template overflowed its capacity: relocate its compared words here.
 #pragma unroll
     for (uint32_t jb = 0; jb < J; jb += kSlots) {
       uint64_t tin[kSlots], tout[kSlots];
@@ -949,71 +1138,124 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
     }
   }
 
-  // Words equal to the template's take its relocated word; partial words
-  // are never relocated; the rest need a search.  fg[j] ends as the word's
-  // value in R.
-  uint32_t need = 0, bits = 0;
+  // Store what is settled; the rest (whole words to relocate, and partial
+  // words that differ from the template's) are candidates.
+  uint32_t cand = 0, creloc = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
     if (!((valid >> j) & 1)) continue;
+    const uint64_t w = w0 + 64 * j;
     const bool c = (cmp >> j) & 1;
-    if (c && fg[j] == ft[j]) fg[j] = fr[j];
-    else if (!((full >> j) & 1)) bits |= (c && fg[j] != fr[j]) ? 1u << j : 0u;
-    else need |= 1u << j;
-  }
-  // Round r searches the lane's needed words of rank r*kSlots .. r*kSlots +
-  // kSlots-1 (rank: position among the lane's needed words).  Slots are
-  // filled and drained with compile-time word indexes only.
-  uint32_t rank[J];
-#pragma unroll
-  for (uint32_t j = 0; j < J; ++j) rank[j] = (uint32_t)__popc(need & ((1u << j) - 1));
-  const uint32_t nneed = (uint32_t)__popc(need);
-  for (uint32_t base = 0; __ballot(base < nneed) != 0; base += kSlots) {
-    uint64_t sg[kSlots], st[kSlots], res[kSlots];
-    uint32_t m = 0;
-#pragma unroll
-    for (uint32_t k = 0; k < kSlots; ++k) {
-      sg[k] = st[k] = 0;
-      if (base + k < nneed) m |= 1u << k;
+    if (c && fg[j] == ft[j]) {
+      img_out[w] = fr[j];
+    } else if (!((full >> j) & 1)) {
+      img_out[w] = fg[j];
+      if (c && fg[j] != fr[j]) cand |= 1u << j;
+    } else {
+      cand |= 1u << j;
+      creloc |= 1u << j;
     }
-#pragma unroll
-    for (uint32_t j = 0; j < J; ++j)
-#pragma unroll
-      for (uint32_t k = 0; k < kSlots; ++k)
-        if (((need >> j) & 1) && rank[j] == base + k) {
-          sg[k] = fg[j];
-          st[k] = fr[j];
-        }
-    reloc_batch<kSlots>(R, sg, res, m);
-#pragma unroll
-    for (uint32_t j = 0; j < J; ++j)
-#pragma unroll
-      for (uint32_t k = 0; k < kSlots; ++k)
-        if (((need >> j) & 1) && rank[j] == base + k) {
-          fg[j] = res[k];
-          if (((cmp >> j) & 1) && res[k] != st[k]) bits |= 1u << j;
-        }
   }
-
-  // Image store and this wave's records, in word order (j, lane).
-  fdy_override* out = a.ovr_tile + ((uint64_t)slot * kSubsPerSlot + wave) * kSubWords;
+  Candidate* out = a.cand + ((uint64_t)slot * kSubsPerSlot + wave) * kSubWords;
   const uint64_t lt = (1ull << lane) - 1;
   uint32_t run = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
-    const uint64_t w = w0 + 64 * j;
-    if ((valid >> j) & 1) img_out[w] = fg[j];
-    const uint64_t mk = __ballot((bits >> j) & 1);
-    if ((bits >> j) & 1) {
-      fdy_override o;
-      o.word = (uint32_t)w;
-      o.node = 0;
-      o.value = fg[j];
-      out[run + (uint32_t)__popcll(mk & lt)] = o;
+    const uint64_t mk = __ballot((cand >> j) & 1);
+    if ((cand >> j) & 1) {
+      Candidate c;
+      c.word = (uint32_t)(w0 + 64 * j);
+      c.flags = (((creloc >> j) & 1) ? kCandReloc : 0u) | (((cmp >> j) & 1) ? kCandCompare : 0u);
+      c.raw = fg[j];
+      c.tval = fr[j];
+      out[run + (uint32_t)__popcll(mk & lt)] = c;
     }
     run += (uint32_t)__popcll(mk);
   }
   if (lane == 0) sub_count[wave] = run;
+}
+
+// Candidates of the member pass, one wave per slot: the slot's sub-range
+// lists are taken as one list in word order, kSBatch / 64 candidates per
+// lane searched in one lockstep batch.  The relocated word goes to R, and
+// the words whose value differs from the template's become override records,
+// compacted in word order at the start of the slot's region; the slot's
+// record count replaces the first sub-range count (the others become 0).
+// Writing over the candidates is safe: record r takes bytes [16r, 16r + 16)
+// and every candidate at or after list index r lies at or past byte 24r of
+// its own sub-range region, hence past them; a batch reads all its
+// candidates before writing any record.
+constexpr uint32_t kSThreads = 256;  // four slots per workgroup
+constexpr uint32_t kSBatch = 256;
+
+__global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
+  constexpr uint32_t K = kSBatch / 64;
+  static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t slot = blockIdx.x * (kSThreads / 64) + (threadIdx.x >> 6);
+  if (slot >= a.num_slots) return;  // per wave: this kernel has no barrier
+  uint32_t* counts = a.sub_count + (uint64_t)slot * kSubsPerSlot;
+  // Lane q < kSubsPerSlot holds sub-range q's count; inclusive prefix over lanes.
+  const uint32_t cnt = lane < kSubsPerSlot ? counts[lane] : 0;
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int d = 1; d < (int)kSubsPerSlot; d <<= 1) {
+    const uint32_t y = shfl_up32(incl, d);
+    if (lane >= (uint32_t)d) incl += y;
+  }
+  const uint32_t total = __shfl(incl, kSubsPerSlot - 1, 64);
+  if (total == 0) return;
+  uint32_t start[kSubsPerSlot];  // exclusive prefix, the same in every lane
+#pragma unroll
+  for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __shfl(incl - cnt, q, 64);
+  const uint64_t word_base = a.slot_desc[slot].word_base;
+  uint64_t* img_out = a.image + word_base;
+  Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  fdy_override* rec = reinterpret_cast<fdy_override*>(base);
+  const uint64_t lt = (1ull << lane) - 1;
+  uint32_t run = 0;
+  for (uint32_t b = 0; b < total; b += kSBatch) {
+    uint64_t raw[K], tval[K], res[K];
+    uint32_t word[K], fl[K], m = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+      const uint32_t i = b + 64 * k + lane;  // list index
+      raw[k] = tval[k] = 0;
+      word[k] = fl[k] = 0;
+      if (i < total) {
+        uint32_t q = 0;
+#pragma unroll
+        for (uint32_t s = 1; s < kSubsPerSlot; ++s) q += start[s] <= i;
+        uint32_t sq = start[0];
+#pragma unroll
+        for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
+        const Candidate c = base[(uint64_t)q * kSubWords + (i - sq)];
+        raw[k] = c.raw;
+        tval[k] = c.tval;
+        word[k] = c.word;
+        fl[k] = c.flags;
+        if (c.flags & kCandReloc) m |= 1u << k;
+      }
+    }
+    reloc_batch<K>(a.reloc, raw, res, m);
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k)
+      if ((m >> k) & 1) img_out[word[k]] = res[k];
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+      const bool d = (fl[k] & kCandCompare) && res[k] != tval[k];
+      const uint64_t mk = __ballot(d);
+      if (d) {
+        fdy_override o;
+        o.word = word[k];
+        o.node = 0;
+        o.value = res[k];
+        rec[run + (uint32_t)__popcll(mk & lt)] = o;
+      }
+      run += (uint32_t)__popcll(mk);
+    }
+  }
+  if (lane < kSubsPerSlot) counts[lane] = lane == 0 ? run : 0u;
 }
 
 // Records per graph: the sum of its slots' sub-range counts (one workgroup
@@ -1105,13 +1347,13 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   uint64_t base = a.ovr_off[sd.graph];
 #pragma unroll
   for (uint32_t w = 0; w < kCompactThreads / 64; ++w) base += s_part[w];
-  const fdy_override* src = a.ovr_tile + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  const Candidate* regions = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
   for (uint32_t i = tid; i < total; i += kCompactThreads) {
     uint32_t q = 0;  // the sub-range holding record i
 #pragma unroll
     for (uint32_t b = kSubsPerSlot / 2; b >= 1; b >>= 1)
       if (s_sub[q + b] <= i) q += b;
-    fdy_override o = src[(uint64_t)q * kSubWords + (i - s_sub[q])];
+    fdy_override o = reinterpret_cast<const fdy_override*>(regions + (uint64_t)q * kSubWords)[i - s_sub[q]];
     const uint64_t w = o.word;
     uint32_t node;
     find_nodes<1>(s_nd, nw, &w, &node);
@@ -1197,7 +1439,12 @@ hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_node, dim3(a.num_graphs), dim3(kNodeThreads), 0, s, a);
+  if (a.num_chunks) {
+    hipLaunchKernelGGL(k_node_a, dim3(a.num_chunks), dim3(kNodeChunk), 0, s, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(k_node_b, dim3(a.num_graphs), dim3(kNodeThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1210,6 +1457,12 @@ hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s) {
 
 hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_diff_m, dim3(a.num_slots), dim3(kMThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
+  const uint32_t sgrid = (a.num_slots + kSThreads / 64 - 1) / (kSThreads / 64);
+  hipLaunchKernelGGL(k_diff_s, dim3(sgrid), dim3(kSThreads), 0, s, a);
   return hipGetLastError();
 }
 

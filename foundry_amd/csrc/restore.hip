@@ -251,10 +251,11 @@ struct fdy_archive {
   uint64_t total_nodes = 0;
   uint64_t total_cap = 0;
   uint32_t num_slots = 0;
+  uint32_t num_chunks = 0;
 
   DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  DevBuf nflags, ndesc, nptrs, live_src, tile_node, slot_graph, slot_desc, live_cur, tslots;
-  DevBuf aux, image, live, ovr, ovr_off, ovr_tile, sub_count, graph_count;
+  DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
+  DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count;
 
   RelocPlan reloc;
   bool use_explicit = false;
@@ -269,7 +270,7 @@ struct fdy_archive {
 
   bool timing = false;
   bool timed = false;
-  hipEvent_t ev[7] = {};
+  hipEvent_t ev[8] = {};
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)
@@ -315,26 +316,29 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   for (uint32_t i = 0; i < G; ++i)
     if (!errs[i].empty()) return err(FDY_E_FORMAT, names[i] + ": " + errs[i]);
 
-  uint64_t nodes = 0, words = 0, slots = 0;
+  uint64_t nodes = 0, words = 0, slots = 0, chunks = 0;
   for (uint32_t i = 0; i < G; ++i) {
     DevGraph& d = a->graphs[i];
     d.node_base = nodes;
     d.word_base = words;
     d.tile_base = (uint32_t)slots;
     d.tile_cap = (uint32_t)std::max<uint64_t>(1, (d.word_cap + kTileWords - 1) / kTileWords);
+    d.chunk_base = (uint32_t)chunks;
     nodes += d.num_nodes;
     words += d.word_cap;
     slots += d.tile_cap;
+    chunks += (d.num_nodes + kNodeChunk - 1) / kNodeChunk;
   }
   if (slots > 0xFFFFFFF0ull) return err(FDY_E_FORMAT, "archive too large (diff tiles exceed 2^32)");
   a->total_nodes = nodes;
   a->total_cap = words;
   a->num_slots = (uint32_t)slots;
+  a->num_chunks = (uint32_t)chunks;
 
-  std::vector<uint32_t> slot_graph(slots);
+  std::vector<uint32_t> chunk_graph(chunks);
   for (uint32_t i = 0; i < G; ++i)
-    std::fill(slot_graph.begin() + a->graphs[i].tile_base,
-              slot_graph.begin() + a->graphs[i].tile_base + a->graphs[i].tile_cap, i);
+    std::fill(chunk_graph.begin() + a->graphs[i].chunk_base,
+              chunk_graph.begin() + a->graphs[i].chunk_base + (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk, i);
 
   int rc = 0;
   auto alloc = [&](DevBuf& b, size_t bytes, const char* what) {
@@ -355,12 +359,13 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->nptrs, 16 * nodes, "node pointers");
   alloc(a->live_src, 4 * nodes, "live node sources");
   alloc(a->tile_node, 4 * slots, "tile table");
-  alloc(a->slot_graph, 4 * slots, "slot table");
+  alloc(a->chunk_graph, 4 * chunks, "node chunk table");
+  alloc(a->chunks, sizeof(NodeChunk) * chunks, "node chunk results");
   alloc(a->slot_desc, sizeof(SlotDesc) * slots, "slot descriptors");
   alloc(a->tslots, 4 * (slots + 1), "template slot list");
   alloc(a->sub_count, 4 * slots * kSubsPerSlot, "record counts");
   alloc(a->graph_count, 4ull * G, "graph record counts");
-  alloc(a->ovr_tile, sizeof(fdy_override) * (uint64_t)kTileWords * slots, "tile record regions");
+  alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * slots, "candidate and record regions");
   alloc(a->aux, 8 * words, "ragged word sources");
   alloc(a->image, 8 * words, "param images");
   alloc(a->live, 8 * words, "live images");
@@ -374,7 +379,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   auto consts = std::make_unique<CrcConsts>();
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(a->slot_graph.p, slot_graph.data(), 4 * slots, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(a->chunk_graph.p, chunk_graph.data(), 4 * chunks, hipMemcpyHostToDevice));
   return FDY_OK;
 }
 
@@ -563,6 +568,9 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.cc = a->cc.as<CrcConsts>();
   r.num_graphs = a->G;
   r.num_slots = a->num_slots;
+  r.num_chunks = a->num_chunks;
+  r.chunk_graph = a->chunk_graph.as<uint32_t>();
+  r.chunks = a->chunks.as<NodeChunk>();
   r.digests = a->digests.as<uint64_t>();
   r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
   r.template_of = a->tmpl.as<uint32_t>();
@@ -575,7 +583,6 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.tile_node = a->tile_node.as<uint32_t>();
   r.tslots = a->tslots.as<uint32_t>();
   r.tslot_count = a->tslots.as<uint32_t>() + a->num_slots;
-  r.slot_graph = a->slot_graph.as<uint32_t>();
   r.slot_desc = a->slot_desc.as<SlotDesc>();
   r.aux = a->aux.as<uint64_t>();
   r.image = a->image.as<uint64_t>();
@@ -584,7 +591,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.live_cur = a->live_cur.as<uint32_t>();
   r.ovr = a->ovr.as<fdy_override>();
   r.ovr_off = a->ovr_off.as<uint64_t>();
-  r.ovr_tile = a->ovr_tile.as<fdy_override>();
+  r.cand = a->cand.as<Candidate>();
   r.sub_count = a->sub_count.as<uint32_t>();
   r.graph_count = a->graph_count.as<uint32_t>();
   r.reloc = a->reloc.dev;
@@ -603,8 +610,10 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
   FDY_HIP(launch_diff_members(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
-  FDY_HIP(launch_compact(r, s));
+  FDY_HIP(launch_diff_search(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
+  FDY_HIP(launch_compact(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[7], s));
   a->timed = a->timing;
   a->restored = true;
   a->cached = false;
@@ -621,14 +630,15 @@ int fdy_set_timing(fdy_archive* a, int enabled) {
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
-  FDY_HIP(hipEventSynchronize(a->ev[6]));
+  FDY_HIP(hipEventSynchronize(a->ev[7]));
   FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
   FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));
   FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[4], a->ev[5]));
-  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[5], a->ev[6]));
-  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[6]));
+  FDY_HIP(hipEventElapsedTime(&o->search_ms, a->ev[5], a->ev[6]));
+  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[6], a->ev[7]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[7]));
   return FDY_OK;
 }
 

@@ -42,7 +42,20 @@ struct DevGraph {
   uint32_t tile_base;    // first diff-tile slot
   uint32_t tile_cap;     // number of diff-tile slots
   uint64_t crc_fin[4];   // CRC-64/XZ finishing terms of the key, edge, type, kernel-entry streams
+  uint32_t chunk_base;   // first node chunk (kNodeChunk nodes each)
+  uint32_t pad_;
 };
+
+// Nodes per chunk of the node pass, and what a chunk reports to its graph.
+constexpr uint32_t kNodeChunk = 256;
+struct NodeChunk {
+  uint64_t crc_type, crc_kent;  // raw CRCs (zero initial value) of the chunk's node-type and kernel-entry records
+  uint64_t pbytes;              // param bytes of the chunk's kernel nodes
+  uint32_t words_g, words_t;    // image words of the chunk's nodes in the graph and in its template
+  uint32_t status;              // FDY_GRAPH_* bits found in the chunk
+  uint32_t pad_;
+};
+static_assert(sizeof(NodeChunk) == 40, "NodeChunk is 40 B");
 
 // Per-slot work description written by the node pass for the diff pass.
 constexpr uint32_t kSlotFlat = 1;      // every word of the tile sits at kg + 8w (and kt + 8w)
@@ -62,6 +75,19 @@ struct SlotDesc {
   uint32_t pad[2];
 };
 static_assert(sizeof(SlotDesc) == 64, "SlotDesc is one 64-byte line");
+
+// A word the member pass leaves to k_diff_s: a whole word to relocate
+// (kCandReloc), possibly differing from the template's (kCandCompare).
+constexpr uint32_t kCandReloc = 1;
+constexpr uint32_t kCandCompare = 2;
+struct Candidate {
+  uint32_t word;   // graph-local word index
+  uint32_t flags;  // kCand*
+  uint64_t raw;    // the graph's raw word
+  uint64_t tval;   // the template's relocated word (kCandCompare)
+};
+static_assert(sizeof(Candidate) == 24, "Candidate is 24 B");
+static_assert(sizeof(Candidate) >= 16, "a region of candidates holds as many 16-byte records");
 
 // Per-node work description written by the node pass for the diff pass.
 struct NodeDesc {
@@ -118,6 +144,37 @@ __device__ inline uint32_t ld_u32(const uint8_t* p) {
 __device__ inline uint64_t ld_u64(const uint8_t* p) {
   if ((reinterpret_cast<uintptr_t>(p) & 7) == 0) return *reinterpret_cast<const uint64_t*>(p);
   return (uint64_t)ld_u32(p) | ((uint64_t)ld_u32(p + 4) << 32);
+}
+
+// Fields of a node entry, its kernel-attribute block or the common attrs:
+// these start 8-byte aligned (sections are validated 8-byte aligned and an
+// entry is 168 = 8 * 21 bytes), so every 4-byte field is 4-byte aligned and
+// its load needs no run-time alignment branch (which would keep the
+// compiler from issuing a node's loads together).
+__device__ __forceinline__ uint32_t f32(const uint8_t* e, uint32_t off) {
+  return *reinterpret_cast<const uint32_t*>(e + off);
+}
+__device__ __forceinline__ uint64_t f64(const uint8_t* e, uint32_t off) {
+  return (uint64_t)f32(e, off) | ((uint64_t)f32(e, off + 4) << 32);
+}
+
+// Copy n 8-byte words into LDS, kBatch loads per thread issued before any
+// store (a plain copy loop waits for each load in turn).
+template <uint32_t kBatch = 8>
+__device__ inline void stage_words(uint64_t* dst, const uint64_t* src, uint32_t n) {
+  for (uint32_t base = 0; base < n; base += kBatch * blockDim.x) {
+    uint64_t v[kBatch];
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      const uint32_t i = base + k * blockDim.x + threadIdx.x;
+      v[k] = i < n ? src[i] : 0;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kBatch; ++k) {
+      const uint32_t i = base + k * blockDim.x + threadIdx.x;
+      if (i < n) dst[i] = v[k];
+    }
+  }
 }
 
 // Relocate K words at once (the words whose bit is set in `mask`; the others

@@ -182,6 +182,7 @@ typedef struct fdy_restore_timing {
   float node_ms;    /* per-node compare, layout, type and kernel-entry digests */
   float tmpl_ms;    /* relocation of the template graphs' param words */
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
+  float search_ms;  /* interval searches and override records of the words left over by the diff */
   float compact_ms; /* record counts, offsets, dense canonical override array */
   float total_ms;
 } fdy_restore_timing;
