@@ -33,8 +33,10 @@ WORKLOADS = {
     1: "archive of 64 graphs x 120 kernel nodes, 1 topology group, 1 interval (uniform rebase)",
     2: "decode-style archive of 256 graphs x 1200 kernel nodes, 4 topology groups, 40k intervals",
     3: "MoE-style archive of 256 graphs x 3000 nodes (kernel/memset/memcpy), 16 groups, 40k intervals",
-    5: "archive of 1024 graphs x 5000 nodes, 32 groups, 40k intervals",
+    4: "relocation of 1 GiB of packed param words (40% pointers) against 2M intervals",
+    5: "archive of 1024 graphs x 5000 nodes, 32 groups, 40k intervals, then 10,000 seeded graph switches",
 }
+SWITCHES = 10000
 
 
 def parse():
@@ -48,6 +50,95 @@ def parse():
     ap.add_argument("--profile-loop", type=int, default=0,
                     help="only run this many restores (for rocprofv3), print nothing else")
     return ap.parse_args()
+
+
+def bench_relocation(args, s, iv, torch, np, stream):
+    """Standalone relocation of packed words (fdy_relocate_words): one step
+    relocates every word once, out of place, with inputs in HBM."""
+    from foundry_amd.restore import RelocPlan
+
+    words_host = np.asarray(s.words())
+    n = int(words_host.size)
+    w = torch.from_numpy(words_host.view(np.int64)).to("cuda")
+    o = torch.empty_like(w)
+    plan = RelocPlan(*iv)
+    for _ in range(max(1, args.warmup)):
+        plan.relocate(w.data_ptr(), o.data_ptr(), n, stream)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        plan.relocate(w.data_ptr(), o.data_ptr(), n, stream)
+    torch.cuda.synchronize()
+    ms = 1e3 * (time.perf_counter() - t0) / args.steps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        plan.relocate(w.data_ptr(), o.data_ptr(), n, stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    kms = e0.elapsed_time(e1) / args.steps
+    b_r = 16 * n + 16 * len(iv[0])  # read + write every word, the interval records once
+    value = b_r / (ms * 1e-3) / 1e9
+    result = {
+        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u64", "data": "synthetic (seeded packed words and interval table, in HBM)",
+        "config": {"workload": WORKLOADS[4], "preset": 4, "words": n, "intervals": int(len(iv[0]))},
+        "roofline": {"bound": "hbm", "kernel": "k_reloc", "achieved": round(b_r / (kms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(b_r / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": None, "algorithmic_bytes": b_r},
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+
+        threads = len(os.sched_getaffinity(0))
+        sample = words_host[: 1 << 25]
+        times = []
+        budget_end = time.perf_counter() + args.cpu_seconds
+        while len(times) < 3 or (time.perf_counter() < budget_end and len(times) < 20):
+            t1 = time.perf_counter()
+            oracle.relocate_words(sample, *iv, threads=threads)
+            times.append(time.perf_counter() - t1)
+        med = statistics.median(times)
+        result["cpu_baseline"] = {
+            "value": round(16 * sample.size / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"the oracle's relocation of the first {sample.size} words against all "
+                      f"{len(iv[0])} intervals, median of {len(times)} runs ({1e3 * med:.1f} ms)",
+        }
+    return result
+
+
+def bench_switches(arch, s, stream, torch, np):
+    """Sustained graph switches: a seeded sequence of SWITCHES targets over
+    all graphs, each scattering its override set into its group's live
+    image (after the restore)."""
+    from foundry_amd import synth
+
+    seq = synth.switch_sequence(s.params.seed, s.num_graphs, SWITCHES)
+    offs = arch.override_offsets().astype(np.int64)
+    groups = arch.groups()
+    count = np.diff(offs)
+    for g in seq[:100]:
+        arch.switch(int(g), stream)
+    torch.cuda.synchronize()
+    # Bytes: 16-B record read + 8-B word write for the outgoing and the incoming set.
+    current = {int(t): int(t) for t in np.unique(groups)}
+    for g in seq[:100]:
+        current[int(groups[g])] = int(g)
+    b_s = 0
+    for g in seq:
+        t = int(groups[g])
+        if current[t] != int(g):
+            b_s += 24 * (int(count[current[t]]) + int(count[g]))
+            current[t] = int(g)
+    t0 = time.perf_counter()
+    for g in seq:
+        arch.switch(int(g), stream)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    return {"switches": SWITCHES, "seconds": round(sec, 4), "switches_per_s": round(SWITCHES / sec, 1),
+            "scatter_bytes": b_s, "GBps": round(b_s / sec / 1e9, 3)}
 
 
 def main():
@@ -71,6 +162,9 @@ def main():
     params = synth.preset(args.preset)
     s = synth.SynthArchive(params)
     iv = s.intervals()
+    if args.preset == 4:
+        print(json.dumps(bench_relocation(args, s, iv, torch, np, stream)))
+        return
     t0 = time.perf_counter()
     arch = Archive.from_synth(s)
     open_s = time.perf_counter() - t0
@@ -132,8 +226,8 @@ def main():
     b_m = 8 * int(words[~templ].sum()) + 8 * int(tw[~templ].sum()) + 8 * int(words[~templ].sum())
     b_dr = b_m + 16 * n_ovr + 24 * int(words[templ].sum()) + 16 * len(iv[0])
     diff_m_gbs = b_m / (kern["diff_ms"] * 1e-3) / 1e9
-    traffic = None
-    if os.path.exists(TRAFFIC_FILE):
+    traffic = None  # measured for the default workload only
+    if args.preset == 2 and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 if line.startswith("hbm_bytes_per_launch:"):
@@ -186,11 +280,20 @@ def main():
         "cpu_baseline": None,
     }
 
+    if args.preset == 5:
+        result["switch"] = bench_switches(arch, s, stream, torch, np)
+
     if not args.no_cpu_baseline:
         import oracle
 
-        images = s.images()
         threads = len(os.sched_getaffinity(0))
+        # A bounded sample: all graphs when the archive is small, else the
+        # first graphs up to about 600 MB of params (whole groups are not
+        # needed: the oracle groups what it is given).
+        pb = arch.param_bytes().astype(np.int64)
+        n_cpu = G if P <= (1 << 30) else max(1, int(np.searchsorted(np.cumsum(pb), 600 << 20)))
+        images = [s.image(i) for i in range(n_cpu)]
+        p_cpu = int(pb[:n_cpu].sum())
         times = []
         budget_end = time.perf_counter() + args.cpu_seconds
         while len(times) < 3 or (time.perf_counter() < budget_end and len(times) < 30):
@@ -198,23 +301,24 @@ def main():
             oracle.Restore(images, iv, threads=threads)
             times.append(time.perf_counter() - t0)
         med = statistics.median(times)
+        what = "the whole workload" if n_cpu == G else f"the first {n_cpu} of {G} graphs ({p_cpu} param bytes)"
         cpu = {
-            "value": round(P / med / 1e9, 3),
+            "value": round(p_cpu / med / 1e9, 3),
             "unit": "GB/s",
             "cores": threads,
             "kind": "port",
-            "sample": f"the whole workload: oracle restore (digests, grouping, param extraction, "
-                      f"relocation, diff) of all {G} graphs, median of {len(times)} runs "
-                      f"({1e3 * med:.1f} ms per restore)",
+            "sample": f"{what}: oracle restore (digests, grouping, param extraction, relocation, diff), "
+                      f"median of {len(times)} runs ({1e3 * med:.1f} ms per restore)",
         }
-        with tempfile.TemporaryDirectory() as d:
-            paths = s.write_dir(d)
-            ref = {}
-            for t in sorted({threads, 4}):
-                ms, calls = oracle.reference_load_ms(paths, t, reps=5)
-                ref[f"T={t}"] = round(ms, 2)
-            cpu["reference_load_path_ms"] = ref
-            cpu["reference_load_path_driver_calls_skipped"] = calls
+        if n_cpu == G:
+            with tempfile.TemporaryDirectory() as d:
+                paths = s.write_dir(d)
+                ref = {}
+                for t in sorted({threads, 4}):
+                    ms, calls = oracle.reference_load_ms(paths, t, reps=5)
+                    ref[f"T={t}"] = round(ms, 2)
+                cpu["reference_load_path_ms"] = ref
+                cpu["reference_load_path_driver_calls_skipped"] = calls
         result["cpu_baseline"] = cpu
 
     arch.close()

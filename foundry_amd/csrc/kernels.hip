@@ -38,6 +38,8 @@ static_assert((1u << kChunkLevel) == kHashThreads && kHashThreads == kNodeThread
 constexpr uint32_t kGroupThreads = 1024;
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
+constexpr uint32_t kRelocBatch = 4;  // words searched in lockstep (8 and 2 measured no faster)
+static_assert(kRelocBatch % 2 == 0 && (2 * kRelocPairs) % kRelocBatch == 0, "whole pairs per batch");
 
 __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -1408,9 +1410,16 @@ __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint6
         v[q] = p < pairs ? in2[p] : ulonglong2{0, 0};
       }
 #pragma unroll
-      for (uint32_t q = 0; q < kRelocPairs; ++q) {
-        v[q].x = reloc_word(R, v[q].x);
-        v[q].y = reloc_word(R, v[q].y);
+      for (uint32_t q = 0; q < kRelocPairs; q += kRelocBatch / 2) {
+        uint64_t w[kRelocBatch], r[kRelocBatch];
+#pragma unroll
+        for (uint32_t k = 0; k < kRelocBatch / 2; ++k) {
+          w[2 * k] = v[q + k].x;
+          w[2 * k + 1] = v[q + k].y;
+        }
+        reloc_batch<kRelocBatch>(R, w, r, (1u << kRelocBatch) - 1);
+#pragma unroll
+        for (uint32_t k = 0; k < kRelocBatch / 2; ++k) v[q + k] = ulonglong2{r[2 * k], r[2 * k + 1]};
       }
 #pragma unroll
       for (uint32_t q = 0; q < kRelocPairs; ++q) {
