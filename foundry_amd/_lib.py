@@ -29,6 +29,8 @@ ERRORS = {
     -7: "FDY_E_STATE",
     -8: "FDY_E_CAPACITY",
     -9: "FDY_E_MISMATCH",
+    -10: "FDY_E_NOT_FOUND",
+    -11: "FDY_E_UNSUPPORTED",
 }
 
 NODE_LAYOUT, NODE_DESC, NODE_RAGGED, NODE_TEMPLATE = 0x01, 0x02, 0x04, 0x08
@@ -70,6 +72,33 @@ class RestoreTiming(C.Structure):
         ("search_ms", C.c_float),
         ("compact_ms", C.c_float),
         ("total_ms", C.c_float),
+    ]
+
+
+class GroupGraphInfo(C.Structure):
+    _fields_ = [
+        ("template_graph", C.c_uint32),
+        ("current_graph", C.c_uint32),
+        ("num_nodes", C.c_uint32),
+        ("num_kernel_nodes", C.c_uint32),
+        ("num_fill_nodes", C.c_uint32),
+        ("num_memcpy_nodes", C.c_uint32),
+        ("num_event_nodes", C.c_uint32),
+        ("num_deps", C.c_uint32),
+        ("num_events", C.c_uint32),
+        ("pad_", C.c_uint32),
+        ("build_ms", C.c_double),
+        ("instantiate_ms", C.c_double),
+    ]
+
+
+class SelectStats(C.Structure):
+    _fields_ = [
+        ("nodes_reset", C.c_uint32),
+        ("kernel_nodes_reset", C.c_uint32),
+        ("words_scattered", C.c_uint64),
+        ("host_us", C.c_double),
+        ("reset_us", C.c_double),
     ]
 
 
@@ -137,6 +166,22 @@ _SIGS = {
     "fdy_set_timing": (C.c_int, [_vp, C.c_int]),
 }
 
+_GRAPH_SIGS = {
+    "fdy_code_object_hash": (C.c_uint64, [_vp, C.c_uint64]),
+    "fdy_registry_create": (C.c_int, [C.POINTER(_vp)]),
+    "fdy_registry_destroy": (C.c_int, [_vp]),
+    "fdy_registry_add": (C.c_int, [_vp, _vp, C.c_uint64, u64p]),
+    "fdy_registry_add_file": (C.c_int, [_vp, C.c_char_p, u64p]),
+    "fdy_registry_lookup": (C.c_int, [_vp, C.c_uint64, C.c_char_p, C.POINTER(_vp)]),
+    "fdy_registry_global": (C.c_int, [_vp, C.c_uint64, C.c_char_p, C.POINTER(_vp), u64p]),
+    "fdy_group_graph_create": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
+    "fdy_group_graph_destroy": (C.c_int, [_vp]),
+    "fdy_group_graph_select": (C.c_int, [_vp, C.c_uint32, _vp, C.POINTER(SelectStats)]),
+    "fdy_group_graph_launch": (C.c_int, [_vp, _vp]),
+    "fdy_group_graph_info_get": (C.c_int, [_vp, C.POINTER(GroupGraphInfo)]),
+}
+_SIGS.update(_GRAPH_SIGS)
+
 _SYNTH_SIGS = {
     "fdy_synth_preset": (C.c_int, [C.c_uint32, C.POINTER(SynthParams)]),
     "fdy_synth_create": (C.c_int, [C.POINTER(SynthParams), C.c_uint32, C.POINTER(_vp)]),
@@ -193,4 +238,8 @@ def check_synth(rc: int) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return list(_SIGS)
+    return [k for k in _SIGS if k not in _GRAPH_SIGS]
+
+
+def graph_symbols() -> list[str]:
+    return list(_GRAPH_SIGS)

@@ -1,0 +1,120 @@
+// archive.h -- the archive object shared by the two host halves of the C ABI:
+// restore.hip (open, restore, results, switch) and graph.hip (code-object
+// registry and group graphs).  Internal to libfoundry_restore.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <vector>
+
+#include "../../include/foundry_restore.h"
+#include "kernels.h"
+
+struct fdy_group_graph;
+
+namespace fdy {
+
+// Message of the calling thread's last error (fdy_last_error).
+extern thread_local std::string g_err;
+
+inline int err(int code, const std::string& msg) {
+  g_err = msg;
+  return code;
+}
+
+#define FDY_HIP(call)                                                                                 \
+  do {                                                                                                \
+    hipError_t e_ = (call);                                                                           \
+    if (e_ != hipSuccess)                                                                             \
+      return ::fdy::err(FDY_E_HIP, std::string(#call) + " failed: " + hipGetErrorString(e_) +         \
+                                       " (hipError_t " + std::to_string((int)e_) + ")");              \
+  } while (0)
+
+// Device allocation owned by one archive, plan or group graph.
+struct DevBuf {
+  void* p = nullptr;
+  size_t bytes = 0;
+  DevBuf() = default;
+  DevBuf(const DevBuf&) = delete;
+  DevBuf& operator=(const DevBuf&) = delete;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(p);
+  }
+};
+
+int dev_alloc(DevBuf& b, size_t bytes, const char* what);
+
+// The interval search structure: a bucket index of 64-byte lines with about
+// one root bucket per two intervals (crowded buckets split into sub-bucket
+// lines), 16-byte {hi, delta} records, and the lo keys for leaves still
+// crowded at the depth limit (see RelocDev).
+struct RelocPlan {
+  DevBuf bucket, rec, lo;
+  RelocDev dev{};
+};
+
+}  // namespace fdy
+
+struct fdy_archive {
+  int device = 0;
+  uint32_t G = 0;
+  std::vector<fdy::DevGraph> graphs;
+  uint64_t img_bytes = 0;
+  uint64_t total_nodes = 0;
+  uint64_t total_cap = 0;
+  uint32_t num_slots = 0;
+  uint32_t num_chunks = 0;
+
+  fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
+  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
+  fdy::DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count;
+
+  fdy::RelocPlan reloc;
+  bool use_explicit = false;
+  bool restored = false;
+  hipStream_t last_stream = nullptr;
+
+  // Host copies taken after a restore (one synchronisation, then reused).
+  bool cached = false;
+  std::vector<uint32_t> h_tmpl, h_status, h_gwords;
+  std::vector<uint64_t> h_ovr_off, h_pbytes;
+  std::vector<uint32_t> h_current;
+
+  // Group graph bound to each template (null if none); while any is bound the
+  // archive refuses a new restore and close, and switches of a bound group go
+  // through its group graph so that the exec follows the live image.
+  std::vector<fdy_group_graph*> bound;
+  uint32_t num_bound = 0;
+
+  bool timing = false;
+  bool timed = false;
+  hipEvent_t ev[8] = {};
+
+  ~fdy_archive() {
+    for (hipEvent_t& e : ev)
+      if (e) (void)hipEventDestroy(e);
+  }
+};
+
+namespace fdy {
+
+// Host copies of the per-graph results; the first call after a restore
+// synchronizes `s`.
+int ensure_cache(fdy_archive* a, hipStream_t s);
+int check_graph(const fdy_archive* a, uint32_t g);
+// Whether graph g may take its group's live image; *t receives its template.
+int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t);
+// Enqueue the override scatter that moves the live image of g's group from
+// its current graph to g, and record g as current.  With `mirror` and
+// `dirty` (device-visible host memory of the group graph) the scatter also
+// writes every word it changes into mirror and marks the nodes to re-set.
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint64_t* mirror, uint8_t* dirty);
+// Switch of a group that has a bound group graph (graph.hip).
+int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* stats);
+
+}  // namespace fdy

@@ -1,0 +1,791 @@
+// graph.hip -- host side of include/foundry_graph.h: the code-object registry
+// and the group graphs (one hipGraph + hipGraphExec per topology group).
+//
+// The params a graph's nodes take come from the restore: the template's
+// relocated param image R_t when the group graph is built, and afterwards
+// the group's live image, which the device override scatter keeps equal to
+// the selected graph's R_g.  The scatter mirrors each word it writes into
+// device-visible host memory (h_live) and marks the node as dirty, so that
+// a switch re-sets exactly the nodes whose params changed, plus the nodes
+// whose descriptor or layout is the current or the new graph's own.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/fdy_format.h"
+#include "../../include/foundry_graph.h"
+#include "../../include/foundry_restore.h"
+#include "archive.h"
+#include "crc64.h"
+#include "kernels.h"
+
+using fdy::err;
+
+struct fdy_registry {
+  int device = 0;
+  struct Code {
+    uint64_t hash = 0;
+    std::vector<uint8_t> bytes;  // kept for the module's lifetime
+    hipModule_t mod = nullptr;
+  };
+  std::vector<std::unique_ptr<Code>> codes;
+  std::unordered_map<uint64_t, Code*> by_hash;
+  std::unordered_map<std::string, hipFunction_t> fns;  // key: 8 hash bytes + name
+  std::mutex mu;
+
+  ~fdy_registry() {
+    if (!codes.empty()) (void)hipSetDevice(device);
+    for (auto& c : codes)
+      if (c->mod) (void)hipModuleUnload(c->mod);
+  }
+};
+
+namespace fdy {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+double us_since(Clock::time_point t0) { return std::chrono::duration<double, std::micro>(Clock::now() - t0).count(); }
+
+const SliceTables& slice_tables() {
+  static const SliceTables t = make_slice_tables();
+  return t;
+}
+
+uint64_t crc64_xz(const uint8_t* p, uint64_t n) {
+  const SliceTables& t = slice_tables();
+  uint64_t c = ~0ull;
+  uint64_t i = 0;
+  for (; i + 8 <= n; i += 8) {
+    uint64_t w;
+    std::memcpy(&w, p + i, 8);
+    c = crc_slice8(t.t, c, w);
+  }
+  for (; i < n; ++i) c = crc_byte(t.t[0], c, p[i]);
+  return ~c;
+}
+
+int registry_lookup(fdy_registry* r, uint64_t hash, const char* name, size_t name_len, hipFunction_t* out) {
+  std::string key(reinterpret_cast<const char*>(&hash), 8);
+  key.append(name, name_len);
+  std::lock_guard<std::mutex> lk(r->mu);
+  auto f = r->fns.find(key);
+  if (f != r->fns.end()) {
+    *out = f->second;
+    return FDY_OK;
+  }
+  char hex[20];
+  std::snprintf(hex, sizeof hex, "%016llx", (unsigned long long)hash);
+  auto c = r->by_hash.find(hash);
+  if (c == r->by_hash.end())
+    return err(FDY_E_NOT_FOUND, std::string("no code object with binary_hash 0x") + hex + " is registered (kernel '" +
+                                    std::string(name, name_len) + "')");
+  hipFunction_t fn = nullptr;
+  const std::string nm(name, name_len);
+  hipError_t e = hipModuleGetFunction(&fn, c->second->mod, nm.c_str());
+  if (e != hipSuccess || !fn) {
+    (void)hipGetLastError();
+    return err(FDY_E_NOT_FOUND, "code object 0x" + std::string(hex) + " has no kernel '" + nm + "'");
+  }
+  r->fns.emplace(std::move(key), fn);
+  *out = fn;
+  return FDY_OK;
+}
+
+// Host copies of one graph's sections and restore results.  `flags` is
+// always present; the rest is fetched for the template and for members
+// that have nodes with their own descriptor or layout.
+struct HostGraph {
+  uint32_t g = 0;
+  bool full = false;
+  std::vector<uint8_t> flags;
+  std::vector<fdy_node> nodes;
+  std::vector<uint8_t> strings, pidx;
+  std::vector<fdy_dep> deps;
+  bool has_common = false;
+  fdy_common_attrs common{};
+  std::vector<NodeDesc> desc;
+  std::vector<uint64_t> ptrs;   // relocated memset dst / memcpy dst, src: 2 per node
+  std::vector<uint64_t> words;  // R_g
+};
+
+template <typename T>
+int fetch(const void* dev, uint64_t count, std::vector<T>& out) {
+  out.resize(count);
+  if (count) FDY_HIP(hipMemcpy(out.data(), dev, count * sizeof(T), hipMemcpyDeviceToHost));
+  return FDY_OK;
+}
+
+int fetch_section(fdy_archive* a, uint32_t g, int sec, std::vector<uint8_t>& out) {
+  return fetch(a->img.as<uint8_t>() + a->graphs[g].sec_off[sec], a->graphs[g].sec_size[sec], out);
+}
+
+int fetch_flags(fdy_archive* a, uint32_t g, HostGraph& h) {
+  h.g = g;
+  return fetch(a->nflags.as<uint8_t>() + a->graphs[g].node_base, a->graphs[g].num_nodes, h.flags);
+}
+
+int fetch_full(fdy_archive* a, uint32_t g, HostGraph& h) {
+  const DevGraph& d = a->graphs[g];
+  int rc = fetch_flags(a, g, h);
+  std::vector<uint8_t> raw;
+  if (!rc) rc = fetch_section(a, g, FDY_SEC_NODES, raw);
+  if (rc) return rc;
+  if (raw.size() < (uint64_t)d.num_nodes * sizeof(fdy_node)) return err(FDY_E_FORMAT, "node section too short");
+  h.nodes.resize(d.num_nodes);
+  if (d.num_nodes) std::memcpy(h.nodes.data(), raw.data(), (uint64_t)d.num_nodes * sizeof(fdy_node));
+  if (!rc) rc = fetch_section(a, g, FDY_SEC_STRINGS, h.strings);
+  if (!rc) rc = fetch_section(a, g, FDY_SEC_PARAM_INDEX, h.pidx);
+  if (!rc) rc = fetch_section(a, g, FDY_SEC_DEPS, raw);
+  if (rc) return rc;
+  const uint64_t ndeps = (d.flags & FDY_HAS_DEPS) ? d.num_deps : 0;
+  if (raw.size() < ndeps * sizeof(fdy_dep)) return err(FDY_E_FORMAT, "dependency section too short");
+  h.deps.resize(ndeps);
+  if (ndeps) std::memcpy(h.deps.data(), raw.data(), ndeps * sizeof(fdy_dep));
+  h.has_common = false;
+  if (d.flags & FDY_HAS_COMMON_ATTRS) {
+    rc = fetch_section(a, g, FDY_SEC_COMMON_ATTRS, raw);
+    if (rc) return rc;
+    if (raw.size() >= sizeof(fdy_common_attrs)) {
+      std::memcpy(&h.common, raw.data(), sizeof(fdy_common_attrs));
+      h.has_common = true;
+    }
+  }
+  rc = fetch(a->ndesc.as<NodeDesc>() + d.node_base, d.num_nodes, h.desc);
+  if (!rc) rc = fetch(a->nptrs.as<uint64_t>() + 2 * d.node_base, 2ull * d.num_nodes, h.ptrs);
+  if (!rc) rc = fetch(a->image.as<uint64_t>() + d.word_base, a->h_gwords[g], h.words);
+  if (rc) return rc;
+  h.full = true;
+  return FDY_OK;
+}
+
+// Cluster dims and cooperative flag of kernel node n: common attrs, then the
+// node's own attrs where set, then required cluster dims from the function
+// attrs (csrc/CUDAGraphParallel.cpp:1345-1389).
+struct LaunchAttrs {
+  uint32_t cx = 0, cy = 0, cz = 0;
+  int32_t coop = -1;
+};
+
+void read_attrs(const uint8_t* b, LaunchAttrs& a, bool merge) {
+  uint32_t f;
+  std::memcpy(&f, b, 4);
+  if (f & FDY_KNA_CLUSTER_DIM) {
+    std::memcpy(&a.cx, b + 4, 4);
+    std::memcpy(&a.cy, b + 8, 4);
+    std::memcpy(&a.cz, b + 12, 4);
+  }
+  if (f & FDY_KNA_COOPERATIVE) {
+    int32_t v;
+    std::memcpy(&v, b + 32, 4);
+    if (!merge || v >= 0) a.coop = v;
+  }
+}
+
+LaunchAttrs launch_attrs(const HostGraph& h, uint32_t n) {
+  LaunchAttrs a;
+  const uint8_t* e = reinterpret_cast<const uint8_t*>(&h.nodes[n]);
+  if (h.has_common) read_attrs(reinterpret_cast<const uint8_t*>(&h.common), a, false);
+  uint32_t kf;
+  std::memcpy(&kf, e + FDY_KOFF_KNA_FLAGS, 4);
+  if (kf) read_attrs(e + FDY_KOFF_KNA_FLAGS, a, true);
+  const fdy_kernel_body& k = h.nodes[n].u.kernel;
+  if (k.required_cluster[0] > 0 || k.required_cluster[1] > 0 || k.required_cluster[2] > 0) {
+    a.cx = k.required_cluster[0] > 0 ? k.required_cluster[0] : 1;
+    a.cy = k.required_cluster[1] > 0 ? k.required_cluster[1] : 1;
+    a.cz = k.required_cluster[2] > 0 ? k.required_cluster[2] : 1;
+  }
+  return a;
+}
+
+std::string node_name(uint32_t g, uint32_t n) { return "graph " + std::to_string(g) + " node " + std::to_string(n); }
+
+// Launch of one kernel node: params point into `words` (the node's words of
+// an image laid out param by param, each padded to 8 bytes).
+struct KernelLaunch {
+  hipFunction_t fn = nullptr;
+  dim3 grid, block;
+  uint32_t shmem = 0;
+  int32_t coop = -1;
+  bool extra = false;
+  size_t arg_size = 0;
+  void* extra_cfg[5] = {};
+  std::vector<void*> params;
+
+  hipKernelNodeParams node_params() {
+    hipKernelNodeParams p{};
+    p.func = reinterpret_cast<void*>(fn);
+    p.gridDim = grid;
+    p.blockDim = block;
+    p.sharedMemBytes = shmem;
+    if (extra) {
+      p.extra = extra_cfg;
+    } else {
+      p.kernelParams = params.empty() ? nullptr : params.data();
+    }
+    return p;
+  }
+};
+
+int kernel_launch(fdy_registry* r, const HostGraph& h, uint32_t n, uint64_t* words, uint32_t nwords,
+                  KernelLaunch& k) {
+  const fdy_kernel_body& b = h.nodes[n].u.kernel;
+  if ((uint64_t)b.name_offset + b.name_length > h.strings.size())
+    return err(FDY_E_FORMAT, node_name(h.g, n) + ": kernel name outside the string section");
+  size_t len = b.name_length;
+  const char* name = reinterpret_cast<const char*>(h.strings.data()) + b.name_offset;
+  while (len && name[len - 1] == '\0') --len;
+  int rc = registry_lookup(r, b.binary_hash, name, len, &k.fn);
+  if (rc) return rc;
+  const LaunchAttrs at = launch_attrs(h, n);
+  if (at.cx > 1 || at.cy > 1 || at.cz > 1)
+    return err(FDY_E_UNSUPPORTED, node_name(h.g, n) + ": cluster dims " + std::to_string(at.cx) + "x" +
+                                      std::to_string(at.cy) + "x" + std::to_string(at.cz) +
+                                      " (gfx950 has no thread-block clusters)");
+  k.coop = at.coop;
+  k.grid = dim3(b.grid[0], b.grid[1], b.grid[2]);
+  k.block = dim3(b.block[0], b.block[1], b.block[2]);
+  k.shmem = b.shared_mem_bytes;
+  k.params.clear();
+  uint64_t used = 0;
+  if (b.arg_offset != FDY_NO_ARG_BUFFER) {
+    k.extra = true;
+    k.arg_size = b.arg_size;
+    used = (b.arg_size + 7) / 8;
+    k.extra_cfg[0] = HIP_LAUNCH_PARAM_BUFFER_POINTER;
+    k.extra_cfg[1] = words;
+    k.extra_cfg[2] = HIP_LAUNCH_PARAM_BUFFER_SIZE;
+    k.extra_cfg[3] = &k.arg_size;
+    k.extra_cfg[4] = HIP_LAUNCH_PARAM_END;
+  } else {
+    k.extra = false;
+    if ((uint64_t)b.param_index_offset + 8ull * b.num_params > h.pidx.size())
+      return err(FDY_E_FORMAT, node_name(h.g, n) + ": param entries outside the param-index section");
+    k.params.resize(b.num_params);
+    for (uint32_t j = 0; j < b.num_params; ++j) {
+      fdy_param pe;
+      std::memcpy(&pe, h.pidx.data() + b.param_index_offset + 8ull * j, sizeof pe);
+      k.params[j] = words + used;
+      used += (pe.size + 7) / 8;
+    }
+  }
+  if (used != nwords)
+    return err(FDY_E_FORMAT, node_name(h.g, n) + ": params take " + std::to_string(used) +
+                                 " image words, the restore laid out " + std::to_string(nwords));
+  return FDY_OK;
+}
+
+int fill_args(const HostGraph& h, uint32_t n, FillArgs& f) {
+  const fdy_memset_body& m = h.nodes[n].u.memset;
+  const uint32_t es = m.element_size;
+  if (es != 1 && es != 2 && es != 4)
+    return err(FDY_E_FORMAT, node_name(h.g, n) + ": memset element size " + std::to_string(es));
+  f.dst = reinterpret_cast<uint8_t*>(h.ptrs[2ull * n]);
+  f.row_bytes = m.width * es;
+  f.height = m.height;
+  f.pitch = m.pitch;
+  f.pattern = es == 1 ? (m.value & 0xFFu) * 0x01010101u : es == 2 ? (m.value & 0xFFFFu) * 0x00010001u : m.value;
+  f.pad_ = 0;
+  if (f.height > 1 && f.pitch < f.row_bytes)
+    return err(FDY_E_FORMAT, node_name(h.g, n) + ": memset pitch below the row width");
+  return FDY_OK;
+}
+
+struct CopyDesc {
+  bool is3d = false;
+  void* dst = nullptr;
+  const void* src = nullptr;
+  size_t bytes = 0;
+  hipMemcpy3DParms p3{};
+};
+
+int copy_desc(const HostGraph& h, uint32_t n, CopyDesc& c) {
+  const fdy_memcpy_body& m = h.nodes[n].u.memcpy;
+  auto device_side = [](int32_t t) { return t == FDY_MEMTYPE_DEVICE || t == FDY_MEMTYPE_UNIFIED; };
+  if (!device_side(m.dst_mem_type) || !device_side(m.src_mem_type))
+    return err(FDY_E_UNSUPPORTED, node_name(h.g, n) + ": memcpy with a host or array endpoint (types " +
+                                      std::to_string(m.src_mem_type) + " -> " + std::to_string(m.dst_mem_type) +
+                                      ") has no address valid in another process");
+  const uint64_t dst = h.ptrs[2ull * n], src = h.ptrs[2ull * n + 1];
+  if (m.height <= 1 && m.depth <= 1) {
+    c.is3d = false;
+    c.dst = reinterpret_cast<void*>(dst + m.dst_x_bytes + m.dst_y * m.dst_pitch + m.dst_z * m.dst_pitch * m.dst_height);
+    c.src = reinterpret_cast<const void*>(src + m.src_x_bytes + m.src_y * m.src_pitch +
+                                          m.src_z * m.src_pitch * m.src_height);
+    c.bytes = m.width_bytes;
+    return FDY_OK;
+  }
+  if (m.src_pitch < m.width_bytes || m.dst_pitch < m.width_bytes ||
+      (m.depth > 1 && (m.src_height < m.height || m.dst_height < m.height)))
+    return err(FDY_E_FORMAT, node_name(h.g, n) + ": memcpy pitch or height below the copied extent");
+  c.is3d = true;
+  c.p3 = hipMemcpy3DParms{};
+  c.p3.srcPtr = make_hipPitchedPtr(reinterpret_cast<void*>(src), m.src_pitch, m.width_bytes, m.src_height);
+  c.p3.srcPos = make_hipPos(m.src_x_bytes, m.src_y, m.src_z);
+  c.p3.dstPtr = make_hipPitchedPtr(reinterpret_cast<void*>(dst), m.dst_pitch, m.width_bytes, m.dst_height);
+  c.p3.dstPos = make_hipPos(m.dst_x_bytes, m.dst_y, m.dst_z);
+  c.p3.extent = make_hipExtent(m.width_bytes, m.height, m.depth);
+  c.p3.kind = hipMemcpyDeviceToDevice;
+  return FDY_OK;
+}
+
+struct GNode {
+  hipGraphNode_t h = nullptr;
+  uint8_t type = 0;
+  bool copy3d = false;
+  int32_t coop = -1;
+  uint32_t tword = 0, nwords = 0;  // the node's words in the template's image
+};
+
+}  // namespace
+}  // namespace fdy
+
+using namespace fdy;
+
+struct fdy_group_graph {
+  fdy_archive* a = nullptr;
+  fdy_registry* reg = nullptr;
+  uint32_t t = 0;
+  uint32_t N = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<GNode> nodes;
+  HostGraph th;                                 // the template
+  std::unordered_map<uint32_t, std::unique_ptr<HostGraph>> members;
+  std::unordered_map<int32_t, hipEvent_t> events;  // saved event id -> event
+  uint64_t* h_live = nullptr;                   // host mirror of the group's live image
+  uint8_t* h_dirty = nullptr;                   // per node
+  uint64_t* d_live = nullptr;                   // device addresses of the two
+  uint8_t* d_dirty = nullptr;
+  hipEvent_t done = nullptr;                    // recorded after each launch
+  bool launched = false;
+  bool stale = false;                           // an update failed part-way: re-set every node next time
+  fdy_group_graph_info info{};
+
+  ~fdy_group_graph() {
+    (void)hipSetDevice(a ? a->device : 0);
+    if (done && launched) (void)hipEventSynchronize(done);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (auto& e : events) (void)hipEventDestroy(e.second);
+    if (done) (void)hipEventDestroy(done);
+    if (h_live) (void)hipHostFree(h_live);
+    if (h_dirty) (void)hipHostFree(h_dirty);
+  }
+};
+
+namespace fdy {
+namespace {
+
+int event_for(fdy_group_graph* gg, int32_t id, hipEvent_t* out) {
+  auto it = gg->events.find(id);
+  if (it == gg->events.end()) {
+    hipEvent_t e = nullptr;
+    FDY_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    it = gg->events.emplace(id, e).first;
+  }
+  *out = it->second;
+  return FDY_OK;
+}
+
+HostGraph* member(fdy_group_graph* gg, uint32_t g, int* rc) {
+  if (g == gg->t) return &gg->th;
+  auto it = gg->members.find(g);
+  if (it != gg->members.end()) return it->second.get();
+  auto h = std::make_unique<HostGraph>();
+  *rc = fetch_flags(gg->a, g, *h);
+  if (*rc) return nullptr;
+  bool own = false;
+  for (uint8_t f : h->flags) own |= (f & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) != 0;
+  if (own) {
+    *rc = fetch_full(gg->a, g, *h);
+    if (*rc) return nullptr;
+  }
+  HostGraph* p = h.get();
+  gg->members.emplace(g, std::move(h));
+  return p;
+}
+
+// Re-set exec node n to graph g's descriptor and the live params.
+int reset_node(fdy_group_graph* gg, uint32_t n, const HostGraph& hg) {
+  const GNode& x = gg->nodes[n];
+  const uint8_t fl = hg.flags[n];
+  const bool own = (fl & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) != 0;
+  const HostGraph& src = own ? hg : gg->th;
+  switch (x.type) {
+    case FDY_NODE_KERNEL: {
+      uint64_t* words = gg->h_live + x.tword;
+      uint32_t nw = x.nwords;
+      if (fl & FDY_NODE_LAYOUT) {
+        words = const_cast<uint64_t*>(hg.words.data()) + hg.desc[n].gword;
+        nw = hg.desc[n].nwords;
+      }
+      KernelLaunch k;
+      int rc = kernel_launch(gg->reg, src, n, words, nw, k);
+      if (rc) return rc;
+      if ((k.coop > 0) != (x.coop > 0))
+        return err(FDY_E_UNSUPPORTED, node_name(hg.g, n) + ": cooperative attribute differs from the template's");
+      hipKernelNodeParams p = k.node_params();
+      FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
+      return FDY_OK;
+    }
+    case FDY_NODE_MEMSET: {
+      FillArgs f;
+      int rc = fill_args(src, n, f);
+      if (rc) return rc;
+      void* args[1] = {&f};
+      hipKernelNodeParams p{};
+      p.func = fill_kernel();
+      p.gridDim = fill_grid(f);
+      p.blockDim = dim3(kFillThreads);
+      p.kernelParams = args;
+      FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
+      return FDY_OK;
+    }
+    case FDY_NODE_MEMCPY: {
+      CopyDesc c;
+      int rc = copy_desc(src, n, c);
+      if (rc) return rc;
+      if (c.is3d != x.copy3d)
+        return err(FDY_E_UNSUPPORTED, node_name(hg.g, n) + ": memcpy changes between 1-D and 3-D form");
+      if (c.is3d) FDY_HIP(hipGraphExecMemcpyNodeSetParams(gg->exec, x.h, &c.p3));
+      else FDY_HIP(hipGraphExecMemcpyNodeSetParams1D(gg->exec, x.h, c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice));
+      return FDY_OK;
+    }
+    case FDY_NODE_EVENT_RECORD:
+    case FDY_NODE_EVENT_WAIT: {
+      hipEvent_t e;
+      int rc = event_for(gg, src.nodes[n].u.event.event_id, &e);
+      if (rc) return rc;
+      if (x.type == FDY_NODE_EVENT_RECORD) FDY_HIP(hipGraphExecEventRecordNodeSetEvent(gg->exec, x.h, e));
+      else FDY_HIP(hipGraphExecEventWaitNodeSetEvent(gg->exec, x.h, e));
+      return FDY_OK;
+    }
+    default:
+      return FDY_OK;
+  }
+}
+
+int build(fdy_group_graph* gg, hipStream_t s) {
+  const auto t0 = Clock::now();
+  fdy_archive* a = gg->a;
+  const uint32_t t = gg->t;
+  HostGraph& th = gg->th;
+  int rc = fetch_full(a, t, th);
+  if (rc) return rc;
+  const uint32_t N = gg->N = a->graphs[t].num_nodes;
+  gg->nodes.assign(N, GNode{});
+
+  // Mirror of the live image (the template's R_t) and the dirty marks, in
+  // host memory the scatter kernel writes through.
+  const uint64_t cap = std::max<uint64_t>(a->graphs[t].word_cap, 1);
+  FDY_HIP(hipHostMalloc(reinterpret_cast<void**>(&gg->h_live), 8 * cap, hipHostMallocMapped | hipHostMallocCoherent));
+  FDY_HIP(hipHostMalloc(reinterpret_cast<void**>(&gg->h_dirty), std::max<uint32_t>(N, 1),
+                        hipHostMallocMapped | hipHostMallocCoherent));
+  FDY_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&gg->d_live), gg->h_live, 0));
+  FDY_HIP(hipHostGetDevicePointer(reinterpret_cast<void**>(&gg->d_dirty), gg->h_dirty, 0));
+  std::memset(gg->h_live, 0, 8 * cap);
+  std::memset(gg->h_dirty, 0, std::max<uint32_t>(N, 1));
+  if (!th.words.empty()) std::memcpy(gg->h_live, th.words.data(), 8 * th.words.size());
+  FDY_HIP(hipEventCreateWithFlags(&gg->done, hipEventDisableTiming));
+
+  FDY_HIP(hipGraphCreate(&gg->graph, 0));
+  fdy_group_graph_info& info = gg->info;
+  for (uint32_t n = 0; n < N; ++n) {
+    GNode& x = gg->nodes[n];
+    x.type = th.nodes[n].type;
+    x.tword = th.desc[n].gword;
+    x.nwords = th.desc[n].nwords;
+    switch (x.type) {
+      case FDY_NODE_KERNEL: {
+        if ((uint64_t)x.tword + x.nwords > cap) return err(FDY_E_FORMAT, node_name(t, n) + ": words beyond the image");
+        KernelLaunch k;
+        rc = kernel_launch(gg->reg, th, n, gg->h_live + x.tword, x.nwords, k);
+        if (rc) return rc;
+        x.coop = k.coop;
+        hipKernelNodeParams p = k.node_params();
+        FDY_HIP(hipGraphAddKernelNode(&x.h, gg->graph, nullptr, 0, &p));
+        if (k.coop > 0) {
+          hipKernelNodeAttrValue v{};
+          v.cooperative = 1;
+          FDY_HIP(hipGraphKernelNodeSetAttribute(x.h, hipLaunchAttributeCooperative, &v));
+        }
+        ++info.num_kernel_nodes;
+        break;
+      }
+      case FDY_NODE_MEMSET: {
+        FillArgs f;
+        rc = fill_args(th, n, f);
+        if (rc) return rc;
+        void* args[1] = {&f};
+        hipKernelNodeParams p{};
+        p.func = fill_kernel();
+        p.gridDim = fill_grid(f);
+        p.blockDim = dim3(kFillThreads);
+        p.kernelParams = args;
+        FDY_HIP(hipGraphAddKernelNode(&x.h, gg->graph, nullptr, 0, &p));
+        ++info.num_fill_nodes;
+        break;
+      }
+      case FDY_NODE_MEMCPY: {
+        CopyDesc c;
+        rc = copy_desc(th, n, c);
+        if (rc) return rc;
+        x.copy3d = c.is3d;
+        if (c.is3d) FDY_HIP(hipGraphAddMemcpyNode(&x.h, gg->graph, nullptr, 0, &c.p3));
+        else FDY_HIP(hipGraphAddMemcpyNode1D(&x.h, gg->graph, nullptr, 0, c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice));
+        ++info.num_memcpy_nodes;
+        break;
+      }
+      case FDY_NODE_EVENT_RECORD:
+      case FDY_NODE_EVENT_WAIT: {
+        hipEvent_t e;
+        rc = event_for(gg, th.nodes[n].u.event.event_id, &e);
+        if (rc) return rc;
+        if (x.type == FDY_NODE_EVENT_RECORD) FDY_HIP(hipGraphAddEventRecordNode(&x.h, gg->graph, nullptr, 0, e));
+        else FDY_HIP(hipGraphAddEventWaitNode(&x.h, gg->graph, nullptr, 0, e));
+        ++info.num_event_nodes;
+        break;
+      }
+      case FDY_NODE_EMPTY:
+        FDY_HIP(hipGraphAddEmptyNode(&x.h, gg->graph, nullptr, 0));
+        break;
+      default:
+        return err(FDY_E_FORMAT, node_name(t, n) + ": unknown node type " + std::to_string(x.type));
+    }
+  }
+
+  // Dependencies name node ids (csrc/CUDAGraphParallel.cpp:774-800).
+  std::unordered_map<uint32_t, uint32_t> index_of;
+  index_of.reserve(N * 2 + 1);
+  for (uint32_t n = 0; n < N; ++n)
+    if (!index_of.emplace(th.nodes[n].node_id, n).second)
+      return err(FDY_E_FORMAT, node_name(t, n) + ": node id " + std::to_string(th.nodes[n].node_id) + " repeats");
+  if (!th.deps.empty()) {
+    std::vector<hipGraphNode_t> from(th.deps.size()), to(th.deps.size());
+    for (size_t i = 0; i < th.deps.size(); ++i) {
+      auto f = index_of.find(th.deps[i].from), d = index_of.find(th.deps[i].to);
+      if (f == index_of.end() || d == index_of.end())
+        return err(FDY_E_FORMAT, "graph " + std::to_string(t) + " dependency " + std::to_string(i) +
+                                     " names a node id that does not exist");
+      from[i] = gg->nodes[f->second].h;
+      to[i] = gg->nodes[d->second].h;
+    }
+    FDY_HIP(hipGraphAddDependencies(gg->graph, from.data(), to.data(), from.size()));
+  }
+  const auto ti = Clock::now();
+  FDY_HIP(hipGraphInstantiate(&gg->exec, gg->graph, nullptr, nullptr, 0));
+  info.instantiate_ms = us_since(ti) / 1000.0;
+  info.template_graph = t;
+  info.current_graph = t;
+  info.num_nodes = N;
+  info.num_deps = (uint32_t)th.deps.size();
+  info.num_events = (uint32_t)gg->events.size();
+  info.build_ms = us_since(t0) / 1000.0;
+  (void)s;
+  return FDY_OK;
+}
+
+}  // namespace
+
+int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* stats_v) {
+  const auto t0 = Clock::now();
+  fdy_select_stats st{};
+  fdy_archive* a = gg->a;
+  int rc = check_graph(a, g);
+  if (!rc) rc = ensure_cache(a, s);
+  uint32_t t = 0;
+  if (!rc) rc = check_switchable(a, g, &t);
+  if (rc) return rc;
+  if (t != gg->t)
+    return err(FDY_E_INVALID, "graph " + std::to_string(g) + " belongs to the group of template " + std::to_string(t) +
+                                  ", not " + std::to_string(gg->t));
+  if (a->h_status[g] & FDY_GRAPH_TYPE_MISMATCH)
+    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has node types other than its template's");
+  if (a->h_status[g] & FDY_GRAPH_BAD_PARAMS)
+    return err(FDY_E_FORMAT, "graph " + std::to_string(g) + " has ranges outside its sections");
+  const uint32_t c = a->h_current[t];
+  if (c == g && !gg->stale) {
+    if (stats_v) *static_cast<fdy_select_stats*>(stats_v) = st;
+    return FDY_OK;
+  }
+  HostGraph* hg = member(gg, g, &rc);
+  if (!hg) return rc;
+  FDY_HIP(hipSetDevice(a->device));
+  if (gg->launched) FDY_HIP(hipEventSynchronize(gg->done));
+  st.words_scattered = (a->h_ovr_off[c + 1] - a->h_ovr_off[c]) + (a->h_ovr_off[g + 1] - a->h_ovr_off[g]);
+  rc = enqueue_switch(a, g, s, gg->d_live, gg->d_dirty);
+  if (rc) return rc;
+  FDY_HIP(hipStreamSynchronize(s));
+  const auto tr = Clock::now();
+  const bool all = gg->stale;
+  gg->stale = true;  // until every node below is set
+  for (uint32_t n = 0; n < gg->N; ++n) {
+    if (!all && !gg->h_dirty[n]) continue;
+    gg->h_dirty[n] = 0;
+    rc = reset_node(gg, n, *hg);
+    if (rc) return rc;
+    ++st.nodes_reset;
+    st.kernel_nodes_reset += gg->nodes[n].type == FDY_NODE_KERNEL;
+  }
+  gg->stale = false;
+  gg->info.current_graph = g;
+  st.reset_us = us_since(tr);
+  st.host_us = us_since(t0);
+  if (stats_v) *static_cast<fdy_select_stats*>(stats_v) = st;
+  return FDY_OK;
+}
+
+}  // namespace fdy
+
+extern "C" {
+
+uint64_t fdy_code_object_hash(const void* bytes, uint64_t size) {
+  return crc64_xz(static_cast<const uint8_t*>(bytes), bytes ? size : 0);
+}
+
+int fdy_registry_create(fdy_registry** out) {
+  if (!out) return err(FDY_E_INVALID, "null output pointer");
+  auto r = std::make_unique<fdy_registry>();
+  FDY_HIP(hipGetDevice(&r->device));
+  *out = r.release();
+  return FDY_OK;
+}
+
+int fdy_registry_destroy(fdy_registry* r) {
+  delete r;
+  return FDY_OK;
+}
+
+int fdy_registry_add(fdy_registry* r, const void* code_object, uint64_t size, uint64_t* hash_out) {
+  if (!r || !code_object || size == 0) return err(FDY_E_INVALID, "need a registry and a non-empty code object");
+  const uint64_t h = crc64_xz(static_cast<const uint8_t*>(code_object), size);
+  if (hash_out) *hash_out = h;
+  std::lock_guard<std::mutex> lk(r->mu);
+  if (r->by_hash.count(h)) return FDY_OK;
+  auto c = std::make_unique<fdy_registry::Code>();
+  c->hash = h;
+  c->bytes.assign(static_cast<const uint8_t*>(code_object), static_cast<const uint8_t*>(code_object) + size);
+  FDY_HIP(hipSetDevice(r->device));
+  hipError_t e = hipModuleLoadData(&c->mod, c->bytes.data());
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return err(FDY_E_FORMAT, std::string("hipModuleLoadData failed: ") + hipGetErrorString(e) +
+                                 " (not a code object for this device?)");
+  }
+  r->by_hash.emplace(h, c.get());
+  r->codes.push_back(std::move(c));
+  return FDY_OK;
+}
+
+int fdy_registry_add_file(fdy_registry* r, const char* path, uint64_t* hash_out) {
+  if (!r || !path) return err(FDY_E_INVALID, "need a registry and a path");
+  FILE* f = std::fopen(path, "rb");
+  if (!f) return err(FDY_E_IO, std::string("cannot open ") + path);
+  std::vector<uint8_t> b;
+  uint8_t buf[1 << 16];
+  size_t got;
+  while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) b.insert(b.end(), buf, buf + got);
+  const bool bad = std::ferror(f) != 0;
+  std::fclose(f);
+  if (bad) return err(FDY_E_IO, std::string("read error on ") + path);
+  return fdy_registry_add(r, b.data(), b.size(), hash_out);
+}
+
+int fdy_registry_lookup(fdy_registry* r, uint64_t hash, const char* name, void** fn) {
+  if (!r || !name || !fn) return err(FDY_E_INVALID, "need a registry, a name and an output pointer");
+  hipFunction_t f = nullptr;
+  int rc = registry_lookup(r, hash, name, std::strlen(name), &f);
+  if (rc) return rc;
+  *fn = reinterpret_cast<void*>(f);
+  return FDY_OK;
+}
+
+int fdy_registry_global(fdy_registry* r, uint64_t hash, const char* name, void** dptr, uint64_t* bytes) {
+  if (!r || !name || !dptr) return err(FDY_E_INVALID, "need a registry, a name and an output pointer");
+  std::lock_guard<std::mutex> lk(r->mu);
+  auto c = r->by_hash.find(hash);
+  if (c == r->by_hash.end()) return err(FDY_E_NOT_FOUND, "no code object with that binary_hash is registered");
+  hipDeviceptr_t p = nullptr;
+  size_t sz = 0;
+  FDY_HIP(hipSetDevice(r->device));
+  hipError_t e = hipModuleGetGlobal(&p, &sz, c->second->mod, name);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    return err(FDY_E_NOT_FOUND, std::string("the code object has no global '") + name + "'");
+  }
+  *dptr = p;
+  if (bytes) *bytes = sz;
+  return FDY_OK;
+}
+
+int fdy_group_graph_create(fdy_archive* a, uint32_t t, fdy_registry* r, void* stream, fdy_group_graph** out) {
+  if (!a || !r || !out) return err(FDY_E_INVALID, "need an archive, a registry and an output pointer");
+  *out = nullptr;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = check_graph(a, t);
+  if (!rc) rc = ensure_cache(a, s);
+  if (rc) return rc;
+  if (a->h_tmpl[t] != t) return err(FDY_E_INVALID, "graph " + std::to_string(t) + " is not a template");
+  if (a->h_status[t] & (FDY_GRAPH_BAD_PARAMS | FDY_GRAPH_OVERFLOW))
+    return err(FDY_E_FORMAT, "template " + std::to_string(t) + " has ranges outside its sections");
+  if (a->bound.size() != a->G) a->bound.assign(a->G, nullptr);
+  if (a->bound[t]) return err(FDY_E_STATE, "template " + std::to_string(t) + " already has a group graph");
+  FDY_HIP(hipSetDevice(a->device));
+  // The exec starts from the template's params: move the live image back first.
+  rc = enqueue_switch(a, t, s, nullptr, nullptr);
+  if (rc) return rc;
+  FDY_HIP(hipStreamSynchronize(s));
+  auto gg = std::make_unique<fdy_group_graph>();
+  gg->a = a;
+  gg->reg = r;
+  gg->t = t;
+  rc = build(gg.get(), s);
+  if (rc) return rc;
+  a->bound[t] = gg.get();
+  ++a->num_bound;
+  *out = gg.release();
+  return FDY_OK;
+}
+
+int fdy_group_graph_destroy(fdy_group_graph* gg) {
+  if (!gg) return FDY_OK;
+  fdy_archive* a = gg->a;
+  if (a && a->bound.size() == a->G && a->bound[gg->t] == gg) {
+    a->bound[gg->t] = nullptr;
+    --a->num_bound;
+  }
+  delete gg;
+  return FDY_OK;
+}
+
+int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fdy_select_stats* stats) {
+  if (!gg) return err(FDY_E_INVALID, "null group graph");
+  return group_graph_select(gg, graph, static_cast<hipStream_t>(stream), stats);
+}
+
+int fdy_group_graph_launch(fdy_group_graph* gg, void* stream) {
+  if (!gg) return err(FDY_E_INVALID, "null group graph");
+  if (gg->stale) return err(FDY_E_STATE, "the last select failed part-way; select a graph again before launching");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  FDY_HIP(hipSetDevice(gg->a->device));
+  FDY_HIP(hipGraphLaunch(gg->exec, s));
+  FDY_HIP(hipEventRecord(gg->done, s));
+  gg->launched = true;
+  return FDY_OK;
+}
+
+int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out) {
+  if (!gg || !out) return err(FDY_E_INVALID, "need a group graph and an output pointer");
+  *out = gg->info;
+  return FDY_OK;
+}
+
+}  // extern "C"

@@ -60,8 +60,11 @@ struct SwitchArgs {
   uint64_t n_new;
   const uint64_t* tmpl_image;   // R of the template
   uint64_t* live;               // live image of the template
+  const uint8_t* flags_cur;     // node flags of the current graph
   const uint8_t* flags_new;     // node flags of the target
   uint32_t* live_src;           // node sources of the template's group
+  uint64_t* mirror;             // or null: host copy of the live image (device-visible host memory)
+  uint8_t* dirty;               // with mirror: per node, set to 1 when the node must be re-set
   uint32_t num_nodes;           // template's node count
   uint32_t target;
   uint32_t tmpl;
@@ -69,5 +72,21 @@ struct SwitchArgs {
 hipError_t launch_switch(const SwitchArgs& a, hipStream_t s);
 
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s);
+
+// A memset node of a restored graph, run as a kernel node: `height` rows of
+// `row_bytes` bytes, `pitch` bytes apart, each byte k of a row taking byte
+// k % 4 of `pattern` (the value replicated to 32 bits).
+struct FillArgs {
+  uint8_t* dst;
+  uint64_t pitch;
+  uint64_t row_bytes;
+  uint64_t height;
+  uint32_t pattern;
+  uint32_t pad_;
+};
+constexpr uint32_t kFillThreads = 256;
+// Host handle of the fill kernel, for hipKernelNodeParams::func.
+void* fill_kernel();
+dim3 fill_grid(const FillArgs& f);
 
 }  // namespace fdy

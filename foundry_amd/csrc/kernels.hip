@@ -25,6 +25,7 @@
 //   k_compact record regions -> the dense override array in canonical order,
 //             completing each record's node and template word index.
 //   k_switch  override scatter for one graph switch.
+//   k_fill    memset node of a restored graph, as a kernel node.
 //   k_reloc   streaming relocation of packed words.
 #include "kernels.h"
 
@@ -1380,13 +1381,53 @@ __global__ __launch_bounds__(256) void k_switch(SwitchArgs a) {
         if (a.ovr_new[mid].word < r.word) lo = mid + 1;
         else hi = mid;
       }
-      if (lo == a.n_new || a.ovr_new[lo].word != r.word) a.live[r.word] = a.tmpl_image[r.word];
+      if (lo == a.n_new || a.ovr_new[lo].word != r.word) {
+        const uint64_t v = a.tmpl_image[r.word];
+        a.live[r.word] = v;
+        if (a.mirror) a.mirror[r.word] = v;
+      }
+      if (a.mirror) a.dirty[r.node] = 1;
     } else if (i < total) {
       const fdy_override r = a.ovr_new[i - a.n_cur];
       a.live[r.word] = r.value;
+      if (a.mirror) {
+        a.mirror[r.word] = r.value;
+        a.dirty[r.node] = 1;
+      }
     }
-    if (i < a.num_nodes)
-      a.live_src[i] = (a.flags_new[i] & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) ? a.target : a.tmpl;
+    if (i < a.num_nodes) {
+      const uint32_t fn = a.flags_new[i];
+      a.live_src[i] = (fn & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) ? a.target : a.tmpl;
+      // A node whose descriptor or layout comes from the current or the
+      // target graph is re-set even without word changes.
+      if (a.mirror && ((fn | a.flags_cur[i]) & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) a.dirty[i] = 1;
+    }
+  }
+}
+
+// ---- fill (memset nodes of restored graphs) -----------------------------
+
+// Row r starts at dst + r * pitch.  Its bytes up to the first 16-byte
+// boundary and after the last one are stored singly; the rest as 16-byte
+// vectors of the pattern rotated to the phase of the row offset.
+__global__ __launch_bounds__(kFillThreads) void k_fill(FillArgs a) {
+  const uint64_t tid = (uint64_t)blockIdx.x * kFillThreads + threadIdx.x;
+  const uint64_t stride = (uint64_t)gridDim.x * kFillThreads;
+  for (uint64_t r = blockIdx.y; r < a.height; r += gridDim.y) {
+    uint8_t* row = a.dst + r * a.pitch;
+    const uint64_t mis = (16 - ((uintptr_t)row & 15)) & 15;
+    const uint64_t head = mis < a.row_bytes ? mis : a.row_bytes;
+    const uint64_t nvec = (a.row_bytes - head) >> 4;
+    const uint64_t tail = head + (nvec << 4);
+    const uint32_t sh = 8 * (uint32_t)(head & 3);
+    const uint32_t w = sh ? (a.pattern >> sh) | (a.pattern << (32 - sh)) : a.pattern;
+    const uint4 q = make_uint4(w, w, w, w);
+    for (uint64_t v = tid; v < nvec; v += stride) *reinterpret_cast<uint4*>(row + head + (v << 4)) = q;
+    const uint64_t singles = head + (a.row_bytes - tail);
+    for (uint64_t k = tid; k < singles; k += stride) {
+      const uint64_t off = k < head ? k : tail + (k - head);
+      row[off] = (uint8_t)(a.pattern >> (8 * (off & 3)));
+    }
   }
 }
 
@@ -1494,6 +1535,15 @@ hipError_t launch_switch(const SwitchArgs& a, hipStream_t s) {
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(k_switch, dim3((uint32_t)blocks), dim3(256), 0, s, a);
   return hipGetLastError();
+}
+
+void* fill_kernel() { return reinterpret_cast<void*>(&k_fill); }
+
+dim3 fill_grid(const FillArgs& f) {
+  const uint64_t vec = (f.row_bytes >> 4) + 1;
+  const uint64_t x = std::min<uint64_t>((vec + kFillThreads - 1) / kFillThreads, 1024);
+  const uint64_t y = std::min<uint64_t>(std::max<uint64_t>(f.height, 1), 65535);
+  return dim3((uint32_t)std::max<uint64_t>(x, 1), (uint32_t)y);
 }
 
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s) {

@@ -16,26 +16,27 @@
 #include <vector>
 
 #include "../../include/foundry_restore.h"
+#include "archive.h"
 #include "cugraph.h"
 #include "kernels.h"
 
 namespace fdy {
-namespace {
 
 thread_local std::string g_err;
 
-int err(int code, const std::string& msg) {
-  g_err = msg;
-  return code;
+int dev_alloc(DevBuf& b, size_t bytes, const char* what) {
+  if (bytes == 0) bytes = 256;
+  hipError_t e = hipMalloc(&b.p, bytes);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    return err(FDY_E_NOMEM, std::string("hipMalloc(") + std::to_string(bytes) + ") for " + what +
+                                " failed: " + hipGetErrorString(e));
+  }
+  b.bytes = bytes;
+  return FDY_OK;
 }
 
-#define FDY_HIP(call)                                                                                 \
-  do {                                                                                                \
-    hipError_t e_ = (call);                                                                           \
-    if (e_ != hipSuccess)                                                                             \
-      return err(FDY_E_HIP, std::string(#call) + " failed: " + hipGetErrorString(e_) + " (hipError_t " + \
-                                std::to_string((int)e_) + ")");                                       \
-  } while (0)
+namespace {
 
 template <typename F>
 void parallel_for(uint32_t n, uint32_t threads, F&& f) {
@@ -55,34 +56,6 @@ void parallel_for(uint32_t n, uint32_t threads, F&& f) {
 
 uint32_t default_threads() { return std::max(1u, std::min(16u, std::thread::hardware_concurrency())); }
 
-// Device allocation owned by one archive or plan.
-struct DevBuf {
-  void* p = nullptr;
-  size_t bytes = 0;
-  DevBuf() = default;
-  DevBuf(const DevBuf&) = delete;
-  DevBuf& operator=(const DevBuf&) = delete;
-  ~DevBuf() {
-    if (p) (void)hipFree(p);
-  }
-  template <typename T>
-  T* as() const {
-    return static_cast<T*>(p);
-  }
-};
-
-int dev_alloc(DevBuf& b, size_t bytes, const char* what) {
-  if (bytes == 0) bytes = 256;
-  hipError_t e = hipMalloc(&b.p, bytes);
-  if (e != hipSuccess) {
-    b.p = nullptr;
-    return err(FDY_E_NOMEM, std::string("hipMalloc(") + std::to_string(bytes) + ") for " + what +
-                                " failed: " + hipGetErrorString(e));
-  }
-  b.bytes = bytes;
-  return FDY_OK;
-}
-
 // Host staging buffer: pinned when possible so the upload runs at full PCIe rate.
 struct HostStage {
   uint8_t* p = nullptr;
@@ -101,15 +74,6 @@ struct HostStage {
     p = static_cast<uint8_t*>(std::malloc(bytes));
     return p ? FDY_OK : err(FDY_E_NOMEM, "host staging buffer of " + std::to_string(bytes) + " bytes");
   }
-};
-
-// The interval search structure: a bucket index of 64-byte lines with about
-// one root bucket per two intervals (crowded buckets split into sub-bucket
-// lines), 16-byte {hi, delta} records, and the lo keys for leaves still
-// crowded at the depth limit (see RelocDev).
-struct RelocPlan {
-  DevBuf bucket, rec, lo;
-  RelocDev dev{};
 };
 
 int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
@@ -243,41 +207,6 @@ struct fdy_reloc_plan {
   RelocPlan plan;
 };
 
-struct fdy_archive {
-  int device = 0;
-  uint32_t G = 0;
-  std::vector<DevGraph> graphs;
-  uint64_t img_bytes = 0;
-  uint64_t total_nodes = 0;
-  uint64_t total_cap = 0;
-  uint32_t num_slots = 0;
-  uint32_t num_chunks = 0;
-
-  DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
-  DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count;
-
-  RelocPlan reloc;
-  bool use_explicit = false;
-  bool restored = false;
-  hipStream_t last_stream = nullptr;
-
-  // Host copies taken after a restore (one synchronisation, then reused).
-  bool cached = false;
-  std::vector<uint32_t> h_tmpl, h_status, h_gwords;
-  std::vector<uint64_t> h_ovr_off, h_pbytes;
-  std::vector<uint32_t> h_current;
-
-  bool timing = false;
-  bool timed = false;
-  hipEvent_t ev[8] = {};
-
-  ~fdy_archive() {
-    for (hipEvent_t& e : ev)
-      if (e) (void)hipEventDestroy(e);
-  }
-};
-
 namespace {
 
 int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& off,
@@ -383,6 +312,10 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   return FDY_OK;
 }
 
+}  // namespace
+
+namespace fdy {
+
 int ensure_cache(fdy_archive* a, hipStream_t s) {
   if (!a->restored) return err(FDY_E_STATE, "call fdy_restore first");
   if (a->cached) return FDY_OK;
@@ -410,6 +343,50 @@ int check_graph(const fdy_archive* a, uint32_t g) {
                                              std::to_string(a->G) + ")");
   return FDY_OK;
 }
+
+int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t_out) {
+  const uint32_t t = a->h_tmpl[g];
+  if (a->h_status[g] & FDY_GRAPH_NODE_COUNT)
+    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has " + std::to_string(a->graphs[g].num_nodes) +
+                                   " nodes but its template " + std::to_string(t) + " has " +
+                                   std::to_string(a->graphs[t].num_nodes));
+  if (a->h_status[g] & FDY_GRAPH_OVERFLOW)
+    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has a param image larger than its sections allow");
+  if (a->h_status[t] & FDY_GRAPH_OVERFLOW)
+    return err(FDY_E_MISMATCH, "the template " + std::to_string(t) + " of graph " + std::to_string(g) +
+                                   " has a param image larger than its sections allow");
+  *t_out = t;
+  return FDY_OK;
+}
+
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint64_t* mirror, uint8_t* dirty) {
+  const uint32_t t = a->h_tmpl[g];
+  const uint32_t c = a->h_current[t];
+  if (c == g) return FDY_OK;
+  FDY_HIP(hipSetDevice(a->device));
+  SwitchArgs w{};
+  w.ovr_cur = a->ovr.as<fdy_override>() + a->h_ovr_off[c];
+  w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
+  w.ovr_new = a->ovr.as<fdy_override>() + a->h_ovr_off[g];
+  w.n_new = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
+  w.tmpl_image = a->image.as<uint64_t>() + a->graphs[t].word_base;
+  w.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
+  w.flags_cur = a->nflags.as<uint8_t>() + a->graphs[c].node_base;
+  w.flags_new = a->nflags.as<uint8_t>() + a->graphs[g].node_base;
+  w.live_src = a->live_src.as<uint32_t>() + a->graphs[t].node_base;
+  w.mirror = mirror;
+  w.dirty = dirty;
+  w.num_nodes = a->graphs[t].num_nodes;
+  w.target = g;
+  w.tmpl = t;
+  FDY_HIP(launch_switch(w, s));
+  a->h_current[t] = g;
+  return FDY_OK;
+}
+
+}  // namespace fdy
+
+namespace {
 
 template <typename T>
 int copy_out(const void* dev, uint64_t n, T* out, uint64_t cap, uint64_t* n_out) {
@@ -503,6 +480,8 @@ int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes_
 
 int fdy_archive_close(fdy_archive* a) {
   if (!a) return FDY_OK;
+  if (a->num_bound)
+    return err(FDY_E_STATE, std::to_string(a->num_bound) + " group graph(s) still use this archive; destroy them first");
   (void)hipSetDevice(a->device);
   (void)hipDeviceSynchronize();
   delete a;
@@ -560,6 +539,8 @@ int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of) {
 
 int fdy_restore(fdy_archive* a, void* stream) {
   if (!a) return err(FDY_E_INVALID, "null archive");
+  if (a->num_bound)
+    return err(FDY_E_STATE, "group graphs hold the restored params; destroy them before restoring again");
   hipStream_t s = static_cast<hipStream_t>(stream);
   FDY_HIP(hipSetDevice(a->device));
   RestoreArgs r{};
@@ -734,35 +715,11 @@ int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = check_graph(a, g);
   if (!rc) rc = ensure_cache(a, s);
+  uint32_t t = 0;
+  if (!rc) rc = check_switchable(a, g, &t);
   if (rc) return rc;
-  const uint32_t t = a->h_tmpl[g];
-  if (a->h_status[g] & FDY_GRAPH_NODE_COUNT)
-    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has " + std::to_string(a->graphs[g].num_nodes) +
-                                   " nodes but its template " + std::to_string(t) + " has " +
-                                   std::to_string(a->graphs[t].num_nodes));
-  if (a->h_status[g] & FDY_GRAPH_OVERFLOW)
-    return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has a param image larger than its sections allow");
-  if (a->h_status[t] & FDY_GRAPH_OVERFLOW)
-    return err(FDY_E_MISMATCH, "the template " + std::to_string(t) + " of graph " + std::to_string(g) +
-                                   " has a param image larger than its sections allow");
-  const uint32_t c = a->h_current[t];
-  if (c == g) return FDY_OK;
-  FDY_HIP(hipSetDevice(a->device));
-  SwitchArgs w{};
-  w.ovr_cur = a->ovr.as<fdy_override>() + a->h_ovr_off[c];
-  w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
-  w.ovr_new = a->ovr.as<fdy_override>() + a->h_ovr_off[g];
-  w.n_new = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
-  w.tmpl_image = a->image.as<uint64_t>() + a->graphs[t].word_base;
-  w.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
-  w.flags_new = a->nflags.as<uint8_t>() + a->graphs[g].node_base;
-  w.live_src = a->live_src.as<uint32_t>() + a->graphs[t].node_base;
-  w.num_nodes = a->graphs[t].num_nodes;
-  w.target = g;
-  w.tmpl = t;
-  FDY_HIP(launch_switch(w, s));
-  a->h_current[t] = g;
-  return FDY_OK;
+  if (a->bound.size() == a->G && a->bound[t]) return group_graph_select(a->bound[t], g, s, nullptr);
+  return enqueue_switch(a, g, s, nullptr, nullptr);
 }
 
 int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint64_t cap, uint32_t* node_src,

@@ -1,0 +1,124 @@
+/*
+ * foundry_graph.h -- C ABI of the group graphs built from restored archives.
+ *
+ * A group graph is one hipGraph and one instantiated hipGraphExec per
+ * topology group, built from the template's `.cugraph` nodes and dependency
+ * table with the template's restored (relocated) param image.  Any graph of
+ * the group is made runnable by fdy_group_graph_select: the device-side
+ * override scatter (fdy_switch) moves the group's live param image to that
+ * graph and mirrors every word it changes into host memory, and only the
+ * nodes whose params or descriptor differ between the previous and the new
+ * graph are re-set in the exec.
+ *
+ * Where the reference does this work (paths relative to the reference root):
+ *   template graph from JSON      csrc/CUDAGraphParallel.cpp:171-834 (build_graph_from_parsed),
+ *                                 run sequentially per template at 1944-1990
+ *   shared exec per group         include/CUDAGraph.h:155-170 (SharedGraphExec),
+ *                                 csrc/CUDAGraph.cpp:553-572 (link_on_demand_shared_exec)
+ *   switch = re-set every node    csrc/CUDAGraph.cpp:330-461 (CUDAGraph::replay, on-demand branch)
+ *   kernel identity               csrc/hook.cpp:315-321 (compute_hash: CRC-64/XZ of the module image),
+ *                                 csrc/hook.cpp:3514-3551 (query_function_handle)
+ *
+ * Conventions are those of foundry_restore.h (int status, fdy_last_error,
+ * streams passed as void*).  In addition:
+ *   - A group graph keeps its archive alive in the sense that the archive
+ *     refuses fdy_restore and fdy_archive_close until every group graph built
+ *     on it is destroyed.  While a group graph exists, fdy_switch on its
+ *     group behaves as fdy_group_graph_select.
+ *   - Node kinds on gfx950: kernel nodes become kernel nodes; memset nodes
+ *     become kernel nodes of the library's own fill kernel; memcpy nodes
+ *     between device (or unified) memory become memcpy nodes; event record and
+ *     wait nodes use one hipEvent per saved event id and group graph; empty
+ *     nodes stay empty.  Dependencies name node ids (csrc/CUDAGraphParallel.cpp:774-800).
+ *   - Launch attributes: cooperative is applied; cluster dimensions other
+ *     than 1 are refused (gfx950 has no thread-block clusters); preferred
+ *     cluster, scheduling policy, priority, memory-sync domain and shared
+ *     memory carveout have no gfx950 counterpart and are not applied.
+ */
+#ifndef FOUNDRY_GRAPH_H
+#define FOUNDRY_GRAPH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "foundry_restore.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FDY_E_NOT_FOUND (-10)   /* no code object with that hash, or no function of that name in it */
+#define FDY_E_UNSUPPORTED (-11) /* a node or attribute with no gfx950 counterpart */
+
+typedef struct fdy_registry fdy_registry;
+typedef struct fdy_group_graph fdy_group_graph;
+
+/* ---- code-object registry ------------------------------------------------
+ * Code objects (gfx950 ELF images) are opaque bytes.  A code object's
+ * identity is the CRC-64/XZ of its bytes, the `binary_hash` a kernel node of
+ * a `.cugraph` names (csrc/hook.cpp:315-321); a kernel is (binary_hash, name)
+ * (csrc/hook.cpp:3514-3551).  Loading happens on the device current at
+ * fdy_registry_create. */
+int fdy_registry_create(fdy_registry** out);
+int fdy_registry_destroy(fdy_registry* r);
+/* CRC-64/XZ of `size` bytes (no device needed). */
+uint64_t fdy_code_object_hash(const void* bytes, uint64_t size);
+/* Load a code object (hipModuleLoadData) and register it under its hash.
+ * Adding bytes whose hash is already registered is a no-op. */
+int fdy_registry_add(fdy_registry* r, const void* code_object, uint64_t size, uint64_t* binary_hash);
+int fdy_registry_add_file(fdy_registry* r, const char* path, uint64_t* binary_hash);
+/* hipFunction_t of kernel `name` in the code object `binary_hash`. */
+int fdy_registry_lookup(fdy_registry* r, uint64_t binary_hash, const char* name, void** function);
+/* Device address and size of the global variable `name` of the code object
+ * `binary_hash` (hipModuleGetGlobal). */
+int fdy_registry_global(fdy_registry* r, uint64_t binary_hash, const char* name, void** device_ptr,
+                        uint64_t* bytes);
+
+/* ---- group graphs ------------------------------------------------------- */
+typedef struct fdy_group_graph_info {
+  uint32_t template_graph;
+  uint32_t current_graph;   /* graph whose params the exec holds */
+  uint32_t num_nodes;
+  uint32_t num_kernel_nodes;   /* kernel nodes of the archive */
+  uint32_t num_fill_nodes;     /* memset nodes, run by the fill kernel */
+  uint32_t num_memcpy_nodes;
+  uint32_t num_event_nodes;
+  uint32_t num_deps;
+  uint32_t num_events;         /* distinct saved event ids */
+  uint32_t pad_;
+  double build_ms;             /* host time of fdy_group_graph_create */
+  double instantiate_ms;       /* of which hipGraphInstantiate */
+} fdy_group_graph_info;
+
+typedef struct fdy_select_stats {
+  uint32_t nodes_reset;   /* nodes re-set in the exec */
+  uint32_t kernel_nodes_reset;
+  uint64_t words_scattered;  /* override records applied by the scatter: |O_prev| + |O_new| */
+  double host_us;            /* wall time of the call, including the scatter's synchronization */
+  double reset_us;           /* of which the exec node updates */
+} fdy_select_stats;
+
+/* Build the group graph of template graph `template_graph` after
+ * fdy_restore: the group's live image goes back to the template, the nodes
+ * are added in archive order with the template's relocated params, the
+ * dependencies are added, and the graph is instantiated.  Synchronizes
+ * `stream`.  Replaces the per-template JSON build
+ * (csrc/CUDAGraphParallel.cpp:171-834, 1944-1990). */
+int fdy_group_graph_create(fdy_archive* a, uint32_t template_graph, fdy_registry* r, void* stream,
+                           fdy_group_graph** out);
+int fdy_group_graph_destroy(fdy_group_graph* gg);
+/* Make the exec run graph `graph` (a member of the group): the override
+ * scatter on `stream`, then the exec updates of the changed nodes.  Waits
+ * for the group graph's previous launch and for the scatter.  No-op if
+ * `graph` is current.  `stats` may be NULL.  Counterpart of the on-demand
+ * branch of csrc/CUDAGraph.cpp:330-461, which re-sets every node. */
+int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fdy_select_stats* stats);
+/* Launch the exec on `stream` (csrc/CUDAGraph.cpp:476-477). */
+int fdy_group_graph_launch(fdy_group_graph* gg, void* stream);
+int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FOUNDRY_GRAPH_H */

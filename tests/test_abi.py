@@ -25,6 +25,28 @@ def test_restore_library_exports_every_declared_symbol():
     assert declared == set(_lib.exported_symbols())
 
 
+def test_graph_half_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.RESTORE_LIB)
+    declared = _declared("foundry_graph.h", "fdy_")
+    assert len(declared) >= 10
+    missing = [s for s in sorted(declared) if not hasattr(lib, s)]
+    assert not missing, missing
+    assert declared == set(_lib.graph_symbols())
+
+
+def test_code_object_hash_is_crc64_xz_without_gpu():
+    """fdy_code_object_hash is CRC-64/XZ (the identity of csrc/hook.cpp:315-321):
+    the standard check value, and agreement with the bit-serial reference."""
+    from refcrc import crc64_xz
+
+    lib = _lib.restore_lib()
+    check = b"123456789"
+    assert lib.fdy_code_object_hash(check, len(check)) == 0x995DC9BBDF1939FA
+    blob = bytes((i * 131 + 7) & 0xFF for i in range(1237))
+    for n in (0, 1, 7, 8, 9, 63, 64, 1237):
+        assert lib.fdy_code_object_hash(blob[:n], n) == crc64_xz(blob[:n])
+
+
 def test_synth_library_exports_every_declared_symbol():
     lib = ctypes.CDLL(_lib.SYNTH_LIB)
     declared = _declared("fdy_synth.h", "fdy_synth_")

@@ -1,0 +1,200 @@
+"""Group graphs on the GPU: build one hipGraph per topology group from the
+restored template, switch it between member graphs, and check what the
+graphs compute against the values the graphs' params determine.
+
+Before the first launch, the restored param images and node pointers are
+compared with the values graph_cases restates, so every pointer a kernel,
+fill or copy node dereferences is known to lie inside the test's buffer."""
+import ctypes
+import random
+
+import numpy as np
+import pytest
+import torch
+
+import graph_cases as GC
+import refcrc
+from foundry_amd import _lib
+from foundry_amd.graph import GroupGraph, Registry, code_object_hash
+from foundry_amd.restore import Archive
+
+pytestmark = pytest.mark.gpu
+
+_hip = None
+
+
+def _hip_memcpy(dst: int, src: int, n: int, kind: int) -> None:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("libamdhip64.so")
+        _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert _hip.hipMemcpy(dst, src, n, kind) == 0
+
+
+class Env:
+    def __init__(self):
+        torch.cuda.set_device(0)
+        self.stream = torch.cuda.current_stream()
+        self.reg = Registry()
+        data = open(GC.PROBE_CO, "rb").read()
+        self.bhash = self.reg.add_file(GC.PROBE_CO)
+        assert self.bhash == refcrc.crc64_xz(data) == code_object_hash(data)
+        self.slots, nbytes = self.reg.global_address(self.bhash, "probe_slots")
+        assert nbytes == 256 * 8
+        self.buf = torch.zeros(GC.BUF_BYTES // 8, dtype=torch.int64, device="cuda")
+        self.base = self.buf.data_ptr()
+        self.arch = Archive.from_images(GC.images(self.bhash))
+        self.arch.set_relocation([GC.SAVED], [GC.SAVED + GC.BUF_BYTES], [self.base])
+        self.arch.restore(self.stream)
+        self.check_restored()
+
+    def check_restored(self):
+        assert list(self.arch.groups(self.stream)) == [0, 0, 0, 0, 0, 5]
+        for g, s in enumerate(GC.SPECS):
+            img = [int(x) for x in self.arch.param_image(g, self.stream)]
+            assert img == GC.expected_image(s, self.bhash, self.base), f"graph {g}: restored params"
+            ptrs = [int(x) for x in self.arch.node_pointers(g, self.stream)]
+            assert ptrs == GC.expected_pointers(s, self.base), f"graph {g}: restored node pointers"
+
+    def poison_slot2(self):
+        v = np.array([0xDEADDEADDEADDEAD], dtype=np.uint64)
+        _hip_memcpy(self.slots + 16, v.ctypes.data, 8, 1)
+
+    def read_slot2(self) -> int:
+        v = np.zeros(1, dtype=np.uint64)
+        _hip_memcpy(v.ctypes.data, self.slots + 16, 8, 2)
+        return int(v[0])
+
+    def run(self, gg: GroupGraph, g: int) -> dict:
+        """Zero the buffer, replay graph g, and check every result."""
+        torch.cuda.synchronize()
+        self.buf.zero_()
+        self.poison_slot2()
+        torch.cuda.synchronize()
+        st = gg.replay(g, self.stream)
+        torch.cuda.synchronize()
+        self.check(g)
+        return st
+
+    def check(self, g: int):
+        s = GC.SPECS[g]
+        raw = self.buf.cpu().numpy().view(np.uint64)
+        slots, fill, copy = GC.expected_buffer(s)
+        for i in range(GC.CAP):
+            assert int(raw[i]) == slots.get(i, 0), f"graph {g}: result slot {i}"
+        b = raw.tobytes()
+        assert b[GC.FILL_OFF:GC.FILL_OFF + len(fill)] == fill, f"graph {g}: fill node"
+        assert b[GC.FILL_OFF + len(fill):GC.COPY_OFF] == bytes(GC.COPY_OFF - GC.FILL_OFF - len(fill))
+        assert b[GC.COPY_OFF:GC.COPY_OFF + len(copy)] == copy, f"graph {g}: copy node"
+        assert b[GC.COPY_OFF + len(copy):] == bytes(GC.BUF_BYTES - GC.COPY_OFF - len(copy))
+        assert self.read_slot2() == GC.expected_slot2(s), f"graph {g}: extra-style node"
+
+    def expected_resets(self, prev: int, new: int) -> int:
+        def nodes(g):
+            o = {int(x) for x in self.arch.overrides(g, self.stream)["node"]}
+            fl = self.arch.node_flags(g, self.stream)
+            return o | {n for n in range(len(fl)) if fl[n] & (_lib.NODE_LAYOUT | _lib.NODE_DESC)}
+        return len(nodes(prev) | nodes(new))
+
+
+@pytest.fixture(scope="module")
+def env():
+    e = Env()
+    yield e
+
+
+def test_registry_lookup_and_errors(env):
+    assert env.reg.lookup(env.bhash, "probe_mix") != 0
+    with pytest.raises(_lib.FoundryError, match="FDY_E_NOT_FOUND"):
+        env.reg.lookup(env.bhash, "no_such_kernel")
+    with pytest.raises(_lib.FoundryError, match="FDY_E_NOT_FOUND"):
+        env.reg.lookup(env.bhash ^ 1, "probe_mix")
+    # Adding the same bytes again keeps one module.
+    assert env.reg.add(open(GC.PROBE_CO, "rb").read()) == env.bhash
+
+
+def test_build_shape(env):
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        info = gg.info()
+        assert info["num_nodes"] == 11
+        assert info["num_kernel_nodes"] == 6
+        assert info["num_fill_nodes"] == 1
+        assert info["num_memcpy_nodes"] == 1
+        assert info["num_event_nodes"] == 2
+        assert info["num_deps"] == len(GC.EDGES)
+        assert info["num_events"] == 1
+        assert info["current_graph"] == 0
+
+
+def test_each_member_runs_its_own_params(env):
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        for g in GC.GROUP_A:
+            env.run(gg, g)
+        env.run(gg, 0)
+
+
+def test_only_changed_nodes_are_reset(env):
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        prev = 0
+        for g in [1, 2, 3, 4, 1, 0, 4, 3, 2]:
+            st = env.run(gg, g)
+            assert st["nodes_reset"] == env.expected_resets(prev, g), (prev, g)
+            prev = g
+        assert gg.select(prev, env.stream)["nodes_reset"] == 0  # already current
+
+
+def test_seeded_switch_sequence(env):
+    rng = random.Random(0x5EED)
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        for _ in range(24):
+            env.run(gg, rng.choice(GC.GROUP_A))
+
+
+def test_archive_switch_goes_through_the_group_graph(env):
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        for g in (3, 1, 0):
+            env.arch.switch(g, env.stream)
+            torch.cuda.synchronize()
+            env.buf.zero_()
+            env.poison_slot2()
+            torch.cuda.synchronize()
+            gg.launch(env.stream)
+            torch.cuda.synchronize()
+            env.check(g)
+            assert gg.info()["current_graph"] == g
+
+
+def test_second_group_and_misuse(env):
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        with pytest.raises(_lib.FoundryError, match="FDY_E_INVALID"):
+            gg.select(5, env.stream)  # graph of another group
+        with pytest.raises(_lib.FoundryError, match="FDY_E_STATE"):
+            GroupGraph(env.arch, 0, env.reg, env.stream)  # one group graph per template
+        with pytest.raises(_lib.FoundryError, match="FDY_E_STATE"):
+            env.arch.restore(env.stream)  # restored params are in use
+        with GroupGraph(env.arch, 5, env.reg, env.stream) as gb:
+            assert gb.info()["num_nodes"] == 12
+    with pytest.raises(_lib.FoundryError, match="FDY_E_INVALID"):
+        GroupGraph(env.arch, 1, env.reg, env.stream)  # not a template
+
+
+def test_unresolvable_templates_are_refused_before_launch(env):
+    import cugraph_writer as W
+    from cugraph_writer import le
+
+    out = le(GC.SAVED)
+    cases = [
+        ([W.Kernel("no_such_kernel", env.bhash, params=[out])], "FDY_E_NOT_FOUND"),
+        ([W.Kernel("probe_mix", env.bhash ^ 0xFF, params=[out])], "FDY_E_NOT_FOUND"),
+        ([W.Kernel("probe_mix", env.bhash, cluster=(2, 1, 1),
+                   params=[out, le(0, 4), le(1, 4), le(0), le(0)])], "FDY_E_UNSUPPORTED"),
+        ([W.Memcpy(dst=GC.SAVED, src=0x1000, width_bytes=8, src_type=1)], "FDY_E_UNSUPPORTED"),
+        ([W.Memset(dst=GC.SAVED, value=0, width=4, element_size=3)], "FDY_E_FORMAT"),
+    ]
+    for nodes, code in cases:
+        arch = Archive.from_images([W.write(nodes)])
+        arch.set_relocation([GC.SAVED], [GC.SAVED + GC.BUF_BYTES], [env.base])
+        arch.restore(env.stream)
+        with pytest.raises(_lib.FoundryError, match=code):
+            GroupGraph(arch, 0, env.reg, env.stream)
+        arch.close()
