@@ -37,6 +37,8 @@ WORKLOADS = {
     5: "archive of 1024 graphs x 5000 nodes, 32 groups, 40k intervals, then 10,000 seeded graph switches",
 }
 SWITCHES = 10000
+GRAPH_SWITCHES = 200  # switches timed through group graphs
+PROBE_CO = os.path.join(ROOT, "tests", "native", "_build", "probe.co")
 
 
 def parse():
@@ -47,6 +49,7 @@ def parse():
     ap.add_argument("--preset", type=int, default=2, choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="CPU baseline sample budget")
+    ap.add_argument("--no-group-graphs", action="store_true", help="skip the group-graph host measurement")
     ap.add_argument("--profile-loop", type=int, default=0,
                     help="only run this many restores (for rocprofv3), print nothing else")
     return ap.parse_args()
@@ -141,6 +144,84 @@ def bench_switches(arch, s, stream, torch, np):
             "scatter_bytes": b_s, "GBps": round(b_s / sec / 1e9, 3)}
 
 
+def _progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _pct(v, q):
+    v = sorted(v)
+    return v[min(len(v) - 1, int(q * (len(v) - 1) + 0.5))] if v else None
+
+
+def bench_group_graphs(preset, torch, np, stream):
+    """Group graphs (one hipGraph + exec per topology group) of an archive of
+    the same shape whose kernel nodes all resolve to one sink kernel: host
+    time to build each group's graph from its restored template, host time
+    per switch of the sparse exec update (device scatter + re-set of the
+    changed nodes) once every graph has been selected, and, on the same
+    execs, the re-set of every node that the reference performs on each
+    switch.  The graphs are built and switched,
+    never launched (their saved pointers are synthetic)."""
+    from foundry_amd import synth
+    from foundry_amd.graph import GroupGraph, Registry
+    from foundry_amd.restore import Archive
+
+    reg = Registry()
+    params = synth.preset(preset)
+    if preset == 5:
+        params.num_graphs = 256  # 8 of the 32 groups: bounds build time and memory
+        params.num_groups = 8
+    params.sink_hash = reg.add_file(PROBE_CO)
+    s = synth.SynthArchive(params)
+    arch = Archive.from_synth(s)
+    arch.set_relocation(*s.intervals())
+    arch.restore(stream)
+    groups = arch.groups(stream)
+    ggs, build_ms, inst_ms = {}, [], []
+    for t in np.unique(groups):
+        t0 = time.perf_counter()
+        gg = GroupGraph(arch, int(t), reg, stream)
+        build_ms.append(1e3 * (time.perf_counter() - t0))
+        inst_ms.append(gg.info()["instantiate_ms"])
+        ggs[int(t)] = gg
+    nodes = int(gg.info()["num_nodes"])
+    # First selection of each graph: includes fetching its host copies
+    # (flags; node table, strings and param index for graphs with nodes of
+    # their own descriptor) and preparing its own nodes' updates.
+    first_us = []
+    for g in range(s.num_graphs):
+        st = ggs[int(groups[g])].select(g, stream)
+        if st["nodes_reset"]:
+            first_us.append(st["host_us"])
+    seq = synth.switch_sequence(params.seed ^ 0x6A, s.num_graphs, GRAPH_SWITCHES)
+    sel_us, reset_n = [], []
+    for g in seq:
+        st = ggs[int(groups[g])].select(int(g), stream)
+        if st["nodes_reset"]:
+            sel_us.append(st["host_us"])
+            reset_n.append(st["nodes_reset"])
+    full_us = []
+    for i in range(40):
+        st = ggs[int(groups[seq[i]])].reset_all(stream)
+        full_us.append(st["reset_us"])
+    for gg in ggs.values():
+        gg.close()
+    arch.close()
+    reg.close()
+    return {
+        "sample": f"{s.num_graphs} graphs x {nodes} nodes, {len(ggs)} groups; {len(sel_us)} switches that changed "
+                  f"the exec out of {GRAPH_SWITCHES} seeded targets",
+        "build_ms_per_group": round(statistics.mean(build_ms), 3),
+        "instantiate_ms_per_group": round(statistics.mean(inst_ms), 3),
+        "first_select_us_p50": round(_pct(first_us, 0.5), 1),
+        "switch_us_p50": round(_pct(sel_us, 0.5), 1),
+        "switch_us_p99": round(_pct(sel_us, 0.99), 1),
+        "nodes_reset_mean": round(statistics.mean(reset_n), 1),
+        "nodes_per_graph": nodes,
+        "all_node_reset_us_p50": round(_pct(full_us, 0.5), 1),
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -162,6 +243,7 @@ def main():
     params = synth.preset(args.preset)
     s = synth.SynthArchive(params)
     iv = s.intervals()
+    _progress(f"synthetic archive for preset {args.preset} generated")
     if args.preset == 4:
         print(json.dumps(bench_relocation(args, s, iv, torch, np, stream)))
         return
@@ -280,8 +362,13 @@ def main():
         "cpu_baseline": None,
     }
 
+    _progress("restore timed")
     if args.preset == 5:
         result["switch"] = bench_switches(arch, s, stream, torch, np)
+        _progress("switches timed")
+    if args.preset in (1, 2, 5) and not args.no_group_graphs:
+        result["group_graph"] = bench_group_graphs(args.preset, torch, np, stream)
+        _progress("group graphs timed")
 
     if not args.no_cpu_baseline:
         import oracle

@@ -133,6 +133,7 @@ class SynthParams(C.Structure):
         ("interval_max", C.c_uint64),
         ("num_words", C.c_uint64),
         ("boundary_frac", C.c_double),
+        ("sink_hash", C.c_uint64),
     ]
 
 
@@ -177,6 +178,7 @@ _GRAPH_SIGS = {
     "fdy_group_graph_create": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),
     "fdy_group_graph_destroy": (C.c_int, [_vp]),
     "fdy_group_graph_select": (C.c_int, [_vp, C.c_uint32, _vp, C.POINTER(SelectStats)]),
+    "fdy_group_graph_reset_all": (C.c_int, [_vp, _vp, C.POINTER(SelectStats)]),
     "fdy_group_graph_launch": (C.c_int, [_vp, _vp]),
     "fdy_group_graph_info_get": (C.c_int, [_vp, C.POINTER(GroupGraphInfo)]),
 }

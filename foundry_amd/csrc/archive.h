@@ -110,10 +110,10 @@ int check_graph(const fdy_archive* a, uint32_t g);
 // Whether graph g may take its group's live image; *t receives its template.
 int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t);
 // Enqueue the override scatter that moves the live image of g's group from
-// its current graph to g, and record g as current.  With `mirror` and
-// `dirty` (device-visible host memory of the group graph) the scatter also
-// writes every word it changes into mirror and marks the nodes to re-set.
-int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint64_t* mirror, uint8_t* dirty);
+// its current graph to g, and record g as current.  With `dirty` (device
+// memory, one byte per node of the group) the scatter also marks the nodes
+// whose params, descriptor or layout change.
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty);
 // Switch of a group that has a bound group graph (graph.hip).
 int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* stats);
 

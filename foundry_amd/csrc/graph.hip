@@ -4,10 +4,11 @@
 // The params a graph's nodes take come from the restore: the template's
 // relocated param image R_t when the group graph is built, and afterwards
 // the group's live image, which the device override scatter keeps equal to
-// the selected graph's R_g.  The scatter mirrors each word it writes into
-// device-visible host memory (h_live) and marks the node as dirty, so that
-// a switch re-sets exactly the nodes whose params changed, plus the nodes
-// whose descriptor or layout is the current or the new graph's own.
+// the selected graph's R_g.  The scatter marks each node it touches as
+// dirty (device memory), and k_mirror then copies the dirty nodes' words
+// into device-visible host memory (h_live) as whole lines, so that a switch
+// re-sets exactly the nodes whose params changed, plus the nodes whose
+// descriptor or layout is the current or the new graph's own.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -100,11 +101,14 @@ int registry_lookup(fdy_registry* r, uint64_t hash, const char* name, size_t nam
 }
 
 // Host copies of one graph's sections and restore results.  `flags` is
-// always present; the rest is fetched for the template and for members
-// that have nodes with their own descriptor or layout.
+// always present.  The node table, strings, param index and common attrs
+// come with `desc_loaded` (the template, and members with nodes whose
+// descriptor or layout is their own); node descriptors and the param image
+// R_g with `layout_loaded` (members with layout changes, and the template);
+// relocated memset/memcpy pointers with `ptrs_loaded`.
 struct HostGraph {
   uint32_t g = 0;
-  bool full = false;
+  bool desc_loaded = false, layout_loaded = false, ptrs_loaded = false;
   std::vector<uint8_t> flags;
   std::vector<fdy_node> nodes;
   std::vector<uint8_t> strings, pidx;
@@ -132,11 +136,10 @@ int fetch_flags(fdy_archive* a, uint32_t g, HostGraph& h) {
   return fetch(a->nflags.as<uint8_t>() + a->graphs[g].node_base, a->graphs[g].num_nodes, h.flags);
 }
 
-int fetch_full(fdy_archive* a, uint32_t g, HostGraph& h) {
+int fetch_desc(fdy_archive* a, uint32_t g, HostGraph& h) {
   const DevGraph& d = a->graphs[g];
-  int rc = fetch_flags(a, g, h);
   std::vector<uint8_t> raw;
-  if (!rc) rc = fetch_section(a, g, FDY_SEC_NODES, raw);
+  int rc = fetch_section(a, g, FDY_SEC_NODES, raw);
   if (rc) return rc;
   if (raw.size() < (uint64_t)d.num_nodes * sizeof(fdy_node)) return err(FDY_E_FORMAT, "node section too short");
   h.nodes.resize(d.num_nodes);
@@ -158,12 +161,22 @@ int fetch_full(fdy_archive* a, uint32_t g, HostGraph& h) {
       h.has_common = true;
     }
   }
-  rc = fetch(a->ndesc.as<NodeDesc>() + d.node_base, d.num_nodes, h.desc);
-  if (!rc) rc = fetch(a->nptrs.as<uint64_t>() + 2 * d.node_base, 2ull * d.num_nodes, h.ptrs);
-  if (!rc) rc = fetch(a->image.as<uint64_t>() + d.word_base, a->h_gwords[g], h.words);
-  if (rc) return rc;
-  h.full = true;
+  h.desc_loaded = true;
   return FDY_OK;
+}
+
+int fetch_layout(fdy_archive* a, uint32_t g, HostGraph& h) {
+  const DevGraph& d = a->graphs[g];
+  int rc = fetch(a->ndesc.as<NodeDesc>() + d.node_base, d.num_nodes, h.desc);
+  if (!rc) rc = fetch(a->image.as<uint64_t>() + d.word_base, a->h_gwords[g], h.words);
+  if (!rc) h.layout_loaded = true;
+  return rc;
+}
+
+int fetch_ptrs(fdy_archive* a, uint32_t g, HostGraph& h) {
+  int rc = fetch(a->nptrs.as<uint64_t>() + 2 * a->graphs[g].node_base, 2ull * a->graphs[g].num_nodes, h.ptrs);
+  if (!rc) h.ptrs_loaded = true;
+  return rc;
 }
 
 // Cluster dims and cooperative flag of kernel node n: common attrs, then the
@@ -207,35 +220,67 @@ LaunchAttrs launch_attrs(const HostGraph& h, uint32_t n) {
 
 std::string node_name(uint32_t g, uint32_t n) { return "graph " + std::to_string(g) + " node " + std::to_string(n); }
 
-// Launch of one kernel node: params point into `words` (the node's words of
-// an image laid out param by param, each padded to 8 bytes).
-struct KernelLaunch {
+// Everything one exec node needs to be added or re-set, computed once: for
+// every node of the template when the group graph is built, and for each
+// member graph's own-descriptor nodes when that graph is first selected.
+// Kernel params point into `words` (the node's words of an image laid out
+// param by param, each padded to 8 bytes) through the owner's pointer array
+// (pfirst, pcount), so an update is a single exec call.
+struct NodeUpdate {
+  uint8_t type = 0;
+  bool copy3d = false;
+  int32_t coop = -1;
   hipFunction_t fn = nullptr;
   dim3 grid, block;
   uint32_t shmem = 0;
-  int32_t coop = -1;
   bool extra = false;
   size_t arg_size = 0;
   void* extra_cfg[5] = {};
-  std::vector<void*> params;
+  uint32_t pfirst = 0, pcount = 0;
+  FillArgs fill{};
+  hipEvent_t event = nullptr;
+  // memcpy
+  void* dst = nullptr;
+  const void* src = nullptr;
+  size_t bytes = 0;
+  hipMemcpy3DParms p3{};
 
-  hipKernelNodeParams node_params() {
-    hipKernelNodeParams p{};
-    p.func = reinterpret_cast<void*>(fn);
-    p.gridDim = grid;
-    p.blockDim = block;
-    p.sharedMemBytes = shmem;
-    if (extra) {
-      p.extra = extra_cfg;
-    } else {
-      p.kernelParams = params.empty() ? nullptr : params.data();
-    }
-    return p;
-  }
+  NodeUpdate() = default;
+  NodeUpdate(const NodeUpdate&) = delete;  // extra_cfg points at arg_size
+  NodeUpdate& operator=(const NodeUpdate&) = delete;
 };
 
-int kernel_launch(fdy_registry* r, const HostGraph& h, uint32_t n, uint64_t* words, uint32_t nwords,
-                  KernelLaunch& k) {
+// The updates of one graph's nodes and the param pointer array they index.
+struct UpdateSet {
+  std::vector<std::unique_ptr<NodeUpdate>> u;
+  std::vector<void*> params;
+};
+
+hipKernelNodeParams kernel_params(const NodeUpdate& u, void** params) {
+  hipKernelNodeParams p{};
+  p.func = reinterpret_cast<void*>(u.fn);
+  p.gridDim = u.grid;
+  p.blockDim = u.block;
+  p.sharedMemBytes = u.shmem;
+  if (u.extra) p.extra = const_cast<void**>(u.extra_cfg);
+  else p.kernelParams = u.pcount ? params + u.pfirst : nullptr;
+  return p;
+}
+
+hipKernelNodeParams fill_params(NodeUpdate& u) {
+  hipKernelNodeParams p{};
+  p.func = fill_kernel();
+  p.gridDim = fill_grid(u.fill);
+  p.blockDim = dim3(kFillThreads);
+  // HIP copies the argument when the node is added or set.
+  static thread_local void* arg[1];
+  arg[0] = &u.fill;
+  p.kernelParams = arg;
+  return p;
+}
+
+int kernel_update(fdy_registry* r, const HostGraph& h, uint32_t n, uint64_t* words, uint32_t nwords, NodeUpdate& k,
+                  std::vector<void*>& params) {
   const fdy_kernel_body& b = h.nodes[n].u.kernel;
   if ((uint64_t)b.name_offset + b.name_length > h.strings.size())
     return err(FDY_E_FORMAT, node_name(h.g, n) + ": kernel name outside the string section");
@@ -253,7 +298,6 @@ int kernel_launch(fdy_registry* r, const HostGraph& h, uint32_t n, uint64_t* wor
   k.grid = dim3(b.grid[0], b.grid[1], b.grid[2]);
   k.block = dim3(b.block[0], b.block[1], b.block[2]);
   k.shmem = b.shared_mem_bytes;
-  k.params.clear();
   uint64_t used = 0;
   if (b.arg_offset != FDY_NO_ARG_BUFFER) {
     k.extra = true;
@@ -268,11 +312,12 @@ int kernel_launch(fdy_registry* r, const HostGraph& h, uint32_t n, uint64_t* wor
     k.extra = false;
     if ((uint64_t)b.param_index_offset + 8ull * b.num_params > h.pidx.size())
       return err(FDY_E_FORMAT, node_name(h.g, n) + ": param entries outside the param-index section");
-    k.params.resize(b.num_params);
+    k.pfirst = (uint32_t)params.size();
+    k.pcount = b.num_params;
     for (uint32_t j = 0; j < b.num_params; ++j) {
       fdy_param pe;
       std::memcpy(&pe, h.pidx.data() + b.param_index_offset + 8ull * j, sizeof pe);
-      k.params[j] = words + used;
+      params.push_back(words + used);
       used += (pe.size + 7) / 8;
     }
   }
@@ -344,6 +389,14 @@ struct GNode {
   uint32_t tword = 0, nwords = 0;  // the node's words in the template's image
 };
 
+// A member graph: its host copies, and the updates of its own-descriptor
+// nodes (own[n] indexes `set`, or -1).
+struct Member {
+  HostGraph h;
+  std::vector<int32_t> own;
+  UpdateSet set;
+};
+
 }  // namespace
 }  // namespace fdy
 
@@ -358,12 +411,14 @@ struct fdy_group_graph {
   hipGraphExec_t exec = nullptr;
   std::vector<GNode> nodes;
   HostGraph th;                                 // the template
-  std::unordered_map<uint32_t, std::unique_ptr<HostGraph>> members;
+  UpdateSet tset;                               // the template's updates, one per node
+  std::unordered_map<uint32_t, std::unique_ptr<Member>> members;
   std::unordered_map<int32_t, hipEvent_t> events;  // saved event id -> event
   uint64_t* h_live = nullptr;                   // host mirror of the group's live image
   uint8_t* h_dirty = nullptr;                   // per node
   uint64_t* d_live = nullptr;                   // device addresses of the two
   uint8_t* d_dirty = nullptr;
+  DevBuf dirty;                                 // per node, device memory: the scatter's marks
   hipEvent_t done = nullptr;                    // recorded after each launch
   bool launched = false;
   bool stale = false;                           // an update failed part-way: re-set every node next time
@@ -395,96 +450,139 @@ int event_for(fdy_group_graph* gg, int32_t id, hipEvent_t* out) {
   return FDY_OK;
 }
 
-HostGraph* member(fdy_group_graph* gg, uint32_t g, int* rc) {
-  if (g == gg->t) return &gg->th;
-  auto it = gg->members.find(g);
-  if (it != gg->members.end()) return it->second.get();
-  auto h = std::make_unique<HostGraph>();
-  *rc = fetch_flags(gg->a, g, *h);
-  if (*rc) return nullptr;
-  bool own = false;
-  for (uint8_t f : h->flags) own |= (f & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) != 0;
-  if (own) {
-    *rc = fetch_full(gg->a, g, *h);
-    if (*rc) return nullptr;
+// The update of node n of graph h: params from `words` (nwords of them).
+int make_update(fdy_group_graph* gg, const HostGraph& h, uint32_t n, uint64_t* words, uint32_t nwords, NodeUpdate& u,
+                std::vector<void*>& params) {
+  u.type = h.nodes[n].type;
+  switch (u.type) {
+    case FDY_NODE_KERNEL:
+      return kernel_update(gg->reg, h, n, words, nwords, u, params);
+    case FDY_NODE_MEMSET:
+      return fill_args(h, n, u.fill);
+    case FDY_NODE_MEMCPY: {
+      CopyDesc c;
+      int rc = copy_desc(h, n, c);
+      if (rc) return rc;
+      u.copy3d = c.is3d;
+      u.dst = c.dst;
+      u.src = c.src;
+      u.bytes = c.bytes;
+      u.p3 = c.p3;
+      return FDY_OK;
+    }
+    case FDY_NODE_EVENT_RECORD:
+    case FDY_NODE_EVENT_WAIT:
+      return event_for(gg, h.nodes[n].u.event.event_id, &u.event);
+    case FDY_NODE_EMPTY:
+      return FDY_OK;
+    default:
+      return err(FDY_E_FORMAT, node_name(h.g, n) + ": unknown node type " + std::to_string(u.type));
   }
-  HostGraph* p = h.get();
-  gg->members.emplace(g, std::move(h));
-  return p;
 }
 
-// Re-set exec node n to graph g's descriptor and the live params.
-int reset_node(fdy_group_graph* gg, uint32_t n, const HostGraph& hg) {
-  const GNode& x = gg->nodes[n];
-  const uint8_t fl = hg.flags[n];
-  const bool own = (fl & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) != 0;
-  const HostGraph& src = own ? hg : gg->th;
+int apply_update(fdy_group_graph* gg, const GNode& x, NodeUpdate& u, void** params) {
   switch (x.type) {
     case FDY_NODE_KERNEL: {
-      uint64_t* words = gg->h_live + x.tword;
-      uint32_t nw = x.nwords;
-      if (fl & FDY_NODE_LAYOUT) {
-        words = const_cast<uint64_t*>(hg.words.data()) + hg.desc[n].gword;
-        nw = hg.desc[n].nwords;
-      }
-      KernelLaunch k;
-      int rc = kernel_launch(gg->reg, src, n, words, nw, k);
-      if (rc) return rc;
-      if ((k.coop > 0) != (x.coop > 0))
-        return err(FDY_E_UNSUPPORTED, node_name(hg.g, n) + ": cooperative attribute differs from the template's");
-      hipKernelNodeParams p = k.node_params();
+      hipKernelNodeParams p = kernel_params(u, params);
       FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
       return FDY_OK;
     }
     case FDY_NODE_MEMSET: {
-      FillArgs f;
-      int rc = fill_args(src, n, f);
-      if (rc) return rc;
-      void* args[1] = {&f};
-      hipKernelNodeParams p{};
-      p.func = fill_kernel();
-      p.gridDim = fill_grid(f);
-      p.blockDim = dim3(kFillThreads);
-      p.kernelParams = args;
+      hipKernelNodeParams p = fill_params(u);
       FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
       return FDY_OK;
     }
-    case FDY_NODE_MEMCPY: {
-      CopyDesc c;
-      int rc = copy_desc(src, n, c);
-      if (rc) return rc;
-      if (c.is3d != x.copy3d)
-        return err(FDY_E_UNSUPPORTED, node_name(hg.g, n) + ": memcpy changes between 1-D and 3-D form");
-      if (c.is3d) FDY_HIP(hipGraphExecMemcpyNodeSetParams(gg->exec, x.h, &c.p3));
-      else FDY_HIP(hipGraphExecMemcpyNodeSetParams1D(gg->exec, x.h, c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice));
+    case FDY_NODE_MEMCPY:
+      if (u.copy3d) FDY_HIP(hipGraphExecMemcpyNodeSetParams(gg->exec, x.h, &u.p3));
+      else FDY_HIP(hipGraphExecMemcpyNodeSetParams1D(gg->exec, x.h, u.dst, u.src, u.bytes, hipMemcpyDeviceToDevice));
       return FDY_OK;
-    }
     case FDY_NODE_EVENT_RECORD:
-    case FDY_NODE_EVENT_WAIT: {
-      hipEvent_t e;
-      int rc = event_for(gg, src.nodes[n].u.event.event_id, &e);
-      if (rc) return rc;
-      if (x.type == FDY_NODE_EVENT_RECORD) FDY_HIP(hipGraphExecEventRecordNodeSetEvent(gg->exec, x.h, e));
-      else FDY_HIP(hipGraphExecEventWaitNodeSetEvent(gg->exec, x.h, e));
+      FDY_HIP(hipGraphExecEventRecordNodeSetEvent(gg->exec, x.h, u.event));
       return FDY_OK;
-    }
+    case FDY_NODE_EVENT_WAIT:
+      FDY_HIP(hipGraphExecEventWaitNodeSetEvent(gg->exec, x.h, u.event));
+      return FDY_OK;
     default:
       return FDY_OK;
   }
 }
 
-int build(fdy_group_graph* gg, hipStream_t s) {
+// Member g's host state, fetched and prepared on its first use.
+Member* member(fdy_group_graph* gg, uint32_t g, int* rc) {
+  auto it = gg->members.find(g);
+  if (it != gg->members.end()) return it->second.get();
+  auto m = std::make_unique<Member>();
+  HostGraph& h = m->h;
+  *rc = fetch_flags(gg->a, g, h);
+  if (*rc) return nullptr;
+  const uint32_t N = (uint32_t)h.flags.size();
+  m->own.assign(N, -1);
+  uint32_t n_own = 0;
+  bool layout = false, ptr_nodes = false;
+  for (uint32_t n = 0; n < N; ++n) {
+    const uint8_t f = h.flags[n];
+    if (!(f & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) continue;
+    ++n_own;
+    layout |= (f & FDY_NODE_LAYOUT) != 0;
+    const uint8_t ty = gg->nodes[n].type;
+    ptr_nodes |= ty == FDY_NODE_MEMSET || ty == FDY_NODE_MEMCPY;
+  }
+  if (n_own) {
+    *rc = fetch_desc(gg->a, g, h);
+    if (!*rc && layout) *rc = fetch_layout(gg->a, g, h);
+    if (!*rc && ptr_nodes) *rc = fetch_ptrs(gg->a, g, h);
+    if (*rc) return nullptr;
+    m->set.u.reserve(n_own);
+    for (uint32_t n = 0; n < N; ++n) {
+      const uint8_t f = h.flags[n];
+      if (!(f & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) continue;
+      const GNode& x = gg->nodes[n];
+      uint64_t* words = gg->h_live + x.tword;
+      uint32_t nw = x.nwords;
+      if (f & FDY_NODE_LAYOUT) {
+        words = h.words.data() + h.desc[n].gword;
+        nw = h.desc[n].nwords;
+      }
+      auto u = std::make_unique<NodeUpdate>();
+      *rc = make_update(gg, h, n, words, nw, *u, m->set.params);
+      if (*rc) return nullptr;
+      if (u->type != x.type) {
+        *rc = err(FDY_E_MISMATCH, node_name(g, n) + ": node type differs from the template's");
+        return nullptr;
+      }
+      if (u->type == FDY_NODE_KERNEL && (u->coop > 0) != (x.coop > 0)) {
+        *rc = err(FDY_E_UNSUPPORTED, node_name(g, n) + ": cooperative attribute differs from the template's");
+        return nullptr;
+      }
+      if (u->type == FDY_NODE_MEMCPY && u->copy3d != x.copy3d) {
+        *rc = err(FDY_E_UNSUPPORTED, node_name(g, n) + ": memcpy changes between 1-D and 3-D form");
+        return nullptr;
+      }
+      m->own[n] = (int32_t)m->set.u.size();
+      m->set.u.push_back(std::move(u));
+    }
+  }
+  Member* p = m.get();
+  gg->members.emplace(g, std::move(m));
+  return p;
+}
+
+int build(fdy_group_graph* gg) {
   const auto t0 = Clock::now();
   fdy_archive* a = gg->a;
   const uint32_t t = gg->t;
   HostGraph& th = gg->th;
-  int rc = fetch_full(a, t, th);
+  th.g = t;
+  int rc = fetch_flags(a, t, th);
+  if (!rc) rc = fetch_desc(a, t, th);
+  if (!rc) rc = fetch_layout(a, t, th);
+  if (!rc) rc = fetch_ptrs(a, t, th);
   if (rc) return rc;
   const uint32_t N = gg->N = a->graphs[t].num_nodes;
   gg->nodes.assign(N, GNode{});
 
   // Mirror of the live image (the template's R_t) and the dirty marks, in
-  // host memory the scatter kernel writes through.
+  // host memory k_mirror writes through.
   const uint64_t cap = std::max<uint64_t>(a->graphs[t].word_cap, 1);
   FDY_HIP(hipHostMalloc(reinterpret_cast<void**>(&gg->h_live), 8 * cap, hipHostMallocMapped | hipHostMallocCoherent));
   FDY_HIP(hipHostMalloc(reinterpret_cast<void**>(&gg->h_dirty), std::max<uint32_t>(N, 1),
@@ -494,25 +592,36 @@ int build(fdy_group_graph* gg, hipStream_t s) {
   std::memset(gg->h_live, 0, 8 * cap);
   std::memset(gg->h_dirty, 0, std::max<uint32_t>(N, 1));
   if (!th.words.empty()) std::memcpy(gg->h_live, th.words.data(), 8 * th.words.size());
+  rc = dev_alloc(gg->dirty, std::max<uint32_t>(N, 1), "group graph dirty marks");
+  if (rc) return rc;
+  FDY_HIP(hipMemset(gg->dirty.p, 0, std::max<uint32_t>(N, 1)));
   FDY_HIP(hipEventCreateWithFlags(&gg->done, hipEventDisableTiming));
 
   FDY_HIP(hipGraphCreate(&gg->graph, 0));
   fdy_group_graph_info& info = gg->info;
+  gg->tset.u.reserve(N);
   for (uint32_t n = 0; n < N; ++n) {
     GNode& x = gg->nodes[n];
     x.type = th.nodes[n].type;
     x.tword = th.desc[n].gword;
     x.nwords = th.desc[n].nwords;
+    if ((uint64_t)x.tword + x.nwords > cap) return err(FDY_E_FORMAT, node_name(t, n) + ": words beyond the image");
+    auto up = std::make_unique<NodeUpdate>();
+    NodeUpdate& u = *up;
+    rc = make_update(gg, th, n, gg->h_live + x.tword, x.nwords, u, gg->tset.params);
+    if (rc) return rc;
+    x.coop = u.coop;
+    x.copy3d = u.copy3d;
+    gg->tset.u.push_back(std::move(up));
+  }
+  for (uint32_t n = 0; n < N; ++n) {
+    GNode& x = gg->nodes[n];
+    NodeUpdate& u = *gg->tset.u[n];
     switch (x.type) {
       case FDY_NODE_KERNEL: {
-        if ((uint64_t)x.tword + x.nwords > cap) return err(FDY_E_FORMAT, node_name(t, n) + ": words beyond the image");
-        KernelLaunch k;
-        rc = kernel_launch(gg->reg, th, n, gg->h_live + x.tword, x.nwords, k);
-        if (rc) return rc;
-        x.coop = k.coop;
-        hipKernelNodeParams p = k.node_params();
+        hipKernelNodeParams p = kernel_params(u, gg->tset.params.data());
         FDY_HIP(hipGraphAddKernelNode(&x.h, gg->graph, nullptr, 0, &p));
-        if (k.coop > 0) {
+        if (u.coop > 0) {
           hipKernelNodeAttrValue v{};
           v.cooperative = 1;
           FDY_HIP(hipGraphKernelNodeSetAttribute(x.h, hipLaunchAttributeCooperative, &v));
@@ -521,44 +630,27 @@ int build(fdy_group_graph* gg, hipStream_t s) {
         break;
       }
       case FDY_NODE_MEMSET: {
-        FillArgs f;
-        rc = fill_args(th, n, f);
-        if (rc) return rc;
-        void* args[1] = {&f};
-        hipKernelNodeParams p{};
-        p.func = fill_kernel();
-        p.gridDim = fill_grid(f);
-        p.blockDim = dim3(kFillThreads);
-        p.kernelParams = args;
+        hipKernelNodeParams p = fill_params(u);
         FDY_HIP(hipGraphAddKernelNode(&x.h, gg->graph, nullptr, 0, &p));
         ++info.num_fill_nodes;
         break;
       }
-      case FDY_NODE_MEMCPY: {
-        CopyDesc c;
-        rc = copy_desc(th, n, c);
-        if (rc) return rc;
-        x.copy3d = c.is3d;
-        if (c.is3d) FDY_HIP(hipGraphAddMemcpyNode(&x.h, gg->graph, nullptr, 0, &c.p3));
-        else FDY_HIP(hipGraphAddMemcpyNode1D(&x.h, gg->graph, nullptr, 0, c.dst, c.src, c.bytes, hipMemcpyDeviceToDevice));
+      case FDY_NODE_MEMCPY:
+        if (u.copy3d) FDY_HIP(hipGraphAddMemcpyNode(&x.h, gg->graph, nullptr, 0, &u.p3));
+        else FDY_HIP(hipGraphAddMemcpyNode1D(&x.h, gg->graph, nullptr, 0, u.dst, u.src, u.bytes, hipMemcpyDeviceToDevice));
         ++info.num_memcpy_nodes;
         break;
-      }
       case FDY_NODE_EVENT_RECORD:
-      case FDY_NODE_EVENT_WAIT: {
-        hipEvent_t e;
-        rc = event_for(gg, th.nodes[n].u.event.event_id, &e);
-        if (rc) return rc;
-        if (x.type == FDY_NODE_EVENT_RECORD) FDY_HIP(hipGraphAddEventRecordNode(&x.h, gg->graph, nullptr, 0, e));
-        else FDY_HIP(hipGraphAddEventWaitNode(&x.h, gg->graph, nullptr, 0, e));
+        FDY_HIP(hipGraphAddEventRecordNode(&x.h, gg->graph, nullptr, 0, u.event));
         ++info.num_event_nodes;
         break;
-      }
-      case FDY_NODE_EMPTY:
-        FDY_HIP(hipGraphAddEmptyNode(&x.h, gg->graph, nullptr, 0));
+      case FDY_NODE_EVENT_WAIT:
+        FDY_HIP(hipGraphAddEventWaitNode(&x.h, gg->graph, nullptr, 0, u.event));
+        ++info.num_event_nodes;
         break;
       default:
-        return err(FDY_E_FORMAT, node_name(t, n) + ": unknown node type " + std::to_string(x.type));
+        FDY_HIP(hipGraphAddEmptyNode(&x.h, gg->graph, nullptr, 0));
+        break;
     }
   }
 
@@ -589,7 +681,6 @@ int build(fdy_group_graph* gg, hipStream_t s) {
   info.num_deps = (uint32_t)th.deps.size();
   info.num_events = (uint32_t)gg->events.size();
   info.build_ms = us_since(t0) / 1000.0;
-  (void)s;
   return FDY_OK;
 }
 
@@ -616,21 +707,35 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
     if (stats_v) *static_cast<fdy_select_stats*>(stats_v) = st;
     return FDY_OK;
   }
-  HostGraph* hg = member(gg, g, &rc);
-  if (!hg) return rc;
+  Member* m = nullptr;
+  if (g != gg->t) {
+    m = member(gg, g, &rc);
+    if (!m) return rc;
+  }
   FDY_HIP(hipSetDevice(a->device));
   if (gg->launched) FDY_HIP(hipEventSynchronize(gg->done));
   st.words_scattered = (a->h_ovr_off[c + 1] - a->h_ovr_off[c]) + (a->h_ovr_off[g + 1] - a->h_ovr_off[g]);
-  rc = enqueue_switch(a, g, s, gg->d_live, gg->d_dirty);
+  rc = enqueue_switch(a, g, s, gg->dirty.as<uint8_t>());
   if (rc) return rc;
+  const bool all = gg->stale;
+  MirrorArgs mr{};
+  mr.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
+  mr.desc = a->ndesc.as<NodeDesc>() + a->graphs[t].node_base;
+  mr.dirty = gg->dirty.as<uint8_t>();
+  mr.h_live = gg->d_live;
+  mr.h_dirty = gg->d_dirty;
+  mr.num_nodes = gg->N;
+  mr.all = all ? 1 : 0;
+  FDY_HIP(launch_mirror(mr, s));
   FDY_HIP(hipStreamSynchronize(s));
   const auto tr = Clock::now();
-  const bool all = gg->stale;
   gg->stale = true;  // until every node below is set
   for (uint32_t n = 0; n < gg->N; ++n) {
-    if (!all && !gg->h_dirty[n]) continue;
+    if (!gg->h_dirty[n]) continue;
     gg->h_dirty[n] = 0;
-    rc = reset_node(gg, n, *hg);
+    const int32_t k = m ? m->own[n] : -1;
+    if (k >= 0) rc = apply_update(gg, gg->nodes[n], *m->set.u[k], m->set.params.data());
+    else rc = apply_update(gg, gg->nodes[n], *gg->tset.u[n], gg->tset.params.data());
     if (rc) return rc;
     ++st.nodes_reset;
     st.kernel_nodes_reset += gg->nodes[n].type == FDY_NODE_KERNEL;
@@ -740,14 +845,14 @@ int fdy_group_graph_create(fdy_archive* a, uint32_t t, fdy_registry* r, void* st
   if (a->bound[t]) return err(FDY_E_STATE, "template " + std::to_string(t) + " already has a group graph");
   FDY_HIP(hipSetDevice(a->device));
   // The exec starts from the template's params: move the live image back first.
-  rc = enqueue_switch(a, t, s, nullptr, nullptr);
+  rc = enqueue_switch(a, t, s, nullptr);
   if (rc) return rc;
   FDY_HIP(hipStreamSynchronize(s));
   auto gg = std::make_unique<fdy_group_graph>();
   gg->a = a;
   gg->reg = r;
   gg->t = t;
-  rc = build(gg.get(), s);
+  rc = build(gg.get());
   if (rc) return rc;
   a->bound[t] = gg.get();
   ++a->num_bound;
@@ -769,6 +874,12 @@ int fdy_group_graph_destroy(fdy_group_graph* gg) {
 int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fdy_select_stats* stats) {
   if (!gg) return err(FDY_E_INVALID, "null group graph");
   return group_graph_select(gg, graph, static_cast<hipStream_t>(stream), stats);
+}
+
+int fdy_group_graph_reset_all(fdy_group_graph* gg, void* stream, fdy_select_stats* stats) {
+  if (!gg) return err(FDY_E_INVALID, "null group graph");
+  gg->stale = true;
+  return group_graph_select(gg, gg->a->h_current[gg->t], static_cast<hipStream_t>(stream), stats);
 }
 
 int fdy_group_graph_launch(fdy_group_graph* gg, void* stream) {

@@ -63,13 +63,26 @@ struct SwitchArgs {
   const uint8_t* flags_cur;     // node flags of the current graph
   const uint8_t* flags_new;     // node flags of the target
   uint32_t* live_src;           // node sources of the template's group
-  uint64_t* mirror;             // or null: host copy of the live image (device-visible host memory)
-  uint8_t* dirty;               // with mirror: per node, set to 1 when the node must be re-set
+  uint8_t* dirty;               // or null: per node, set to 1 when the node must be re-set
   uint32_t num_nodes;           // template's node count
   uint32_t target;
   uint32_t tmpl;
 };
 hipError_t launch_switch(const SwitchArgs& a, hipStream_t s);
+
+// Copy of the dirty nodes' live words (or of every node's) into the host
+// mirror of a group graph, with the dirty marks; clears the device marks.
+struct MirrorArgs {
+  const uint64_t* live;   // the group's live image
+  const NodeDesc* desc;   // the template's node descriptors (gword, nwords)
+  uint8_t* dirty;         // per node (device memory)
+  uint64_t* h_live;       // device-visible host memory, same indexing as live
+  uint8_t* h_dirty;       // device-visible host memory, per node
+  uint32_t num_nodes;
+  uint32_t all;           // 1: copy every node and mark it dirty
+};
+constexpr uint32_t kMirrorNodes = 64;  // nodes per block
+hipError_t launch_mirror(const MirrorArgs& a, hipStream_t s);
 
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s);
 

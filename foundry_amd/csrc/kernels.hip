@@ -25,6 +25,7 @@
 //   k_compact record regions -> the dense override array in canonical order,
 //             completing each record's node and template word index.
 //   k_switch  override scatter for one graph switch.
+//   k_mirror  dirty nodes' live words -> a group graph's host mirror.
 //   k_fill    memset node of a restored graph, as a kernel node.
 //   k_reloc   streaming relocation of packed words.
 #include "kernels.h"
@@ -1381,27 +1382,45 @@ __global__ __launch_bounds__(256) void k_switch(SwitchArgs a) {
         if (a.ovr_new[mid].word < r.word) lo = mid + 1;
         else hi = mid;
       }
-      if (lo == a.n_new || a.ovr_new[lo].word != r.word) {
-        const uint64_t v = a.tmpl_image[r.word];
-        a.live[r.word] = v;
-        if (a.mirror) a.mirror[r.word] = v;
-      }
-      if (a.mirror) a.dirty[r.node] = 1;
+      if (lo == a.n_new || a.ovr_new[lo].word != r.word) a.live[r.word] = a.tmpl_image[r.word];
+      if (a.dirty) a.dirty[r.node] = 1;
     } else if (i < total) {
       const fdy_override r = a.ovr_new[i - a.n_cur];
       a.live[r.word] = r.value;
-      if (a.mirror) {
-        a.mirror[r.word] = r.value;
-        a.dirty[r.node] = 1;
-      }
+      if (a.dirty) a.dirty[r.node] = 1;
     }
     if (i < a.num_nodes) {
       const uint32_t fn = a.flags_new[i];
       a.live_src[i] = (fn & (FDY_NODE_LAYOUT | FDY_NODE_DESC)) ? a.target : a.tmpl;
       // A node whose descriptor or layout comes from the current or the
       // target graph is re-set even without word changes.
-      if (a.mirror && ((fn | a.flags_cur[i]) & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) a.dirty[i] = 1;
+      if (a.dirty && ((fn | a.flags_cur[i]) & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) a.dirty[i] = 1;
     }
+  }
+}
+
+// ---- host mirror of a group graph's live image ---------------------------
+
+// Block b covers nodes [64b, 64b + 64): the first wave moves their marks to
+// the host as one 64-byte line, then each wave copies whole dirty nodes, so
+// the words reach host memory as full lines rather than as single words.
+__global__ __launch_bounds__(256) void k_mirror(MirrorArgs a) {
+  __shared__ uint8_t s_dirty[kMirrorNodes];
+  const uint32_t n0 = blockIdx.x * kMirrorNodes;
+  const uint32_t cnt = min(kMirrorNodes, a.num_nodes - n0);
+  if (threadIdx.x < cnt) {
+    const uint32_t n = n0 + threadIdx.x;
+    const uint8_t d = a.all ? 1 : a.dirty[n];
+    s_dirty[threadIdx.x] = d;
+    a.h_dirty[n] = d;
+    if (d) a.dirty[n] = 0;
+  }
+  __syncthreads();
+  const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  for (uint32_t i = wave; i < cnt; i += 4) {
+    if (!s_dirty[i]) continue;
+    const NodeDesc d = a.desc[n0 + i];
+    for (uint32_t w = lane; w < d.nwords; w += 64) a.h_live[d.gword + w] = a.live[d.gword + w];
   }
 }
 
@@ -1534,6 +1553,12 @@ hipError_t launch_switch(const SwitchArgs& a, hipStream_t s) {
   uint64_t blocks = (lim + 255) / 256;
   if (blocks > 2048) blocks = 2048;
   hipLaunchKernelGGL(k_switch, dim3((uint32_t)blocks), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_mirror(const MirrorArgs& a, hipStream_t s) {
+  if (a.num_nodes == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_mirror, dim3((a.num_nodes + kMirrorNodes - 1) / kMirrorNodes), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -359,7 +359,7 @@ int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t_out) {
   return FDY_OK;
 }
 
-int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint64_t* mirror, uint8_t* dirty) {
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty) {
   const uint32_t t = a->h_tmpl[g];
   const uint32_t c = a->h_current[t];
   if (c == g) return FDY_OK;
@@ -374,7 +374,6 @@ int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint64_t* mirror, 
   w.flags_cur = a->nflags.as<uint8_t>() + a->graphs[c].node_base;
   w.flags_new = a->nflags.as<uint8_t>() + a->graphs[g].node_base;
   w.live_src = a->live_src.as<uint32_t>() + a->graphs[t].node_base;
-  w.mirror = mirror;
   w.dirty = dirty;
   w.num_nodes = a->graphs[t].num_nodes;
   w.target = g;
@@ -719,7 +718,7 @@ int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
   if (!rc) rc = check_switchable(a, g, &t);
   if (rc) return rc;
   if (a->bound.size() == a->G && a->bound[t]) return group_graph_select(a->bound[t], g, s, nullptr);
-  return enqueue_switch(a, g, s, nullptr, nullptr);
+  return enqueue_switch(a, g, s, nullptr);
 }
 
 int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint64_t cap, uint32_t* node_src,

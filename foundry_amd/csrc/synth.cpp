@@ -219,7 +219,11 @@ Group make_group(const fdy_synth_params& p, uint32_t g, const Intervals& iv) {
   for (uint32_t n = 0; n < N; ++n) {
     NodeLayout& L = grp.nodes[n];
     uint64_t roll = r.below(100);
-    if (n > 0 && roll < p.memset_pct) L.type = FDY_NODE_MEMSET;
+    if (p.sink_hash && n >= 1 && n <= 6 && n + 1 < N) {
+      // The group's key: node n is empty where bit n-1 of the group index is set.
+      L.type = ((g >> (n - 1)) & 1) ? FDY_NODE_EMPTY : FDY_NODE_KERNEL;
+      if (L.type == FDY_NODE_EMPTY) continue;
+    } else if (n > 0 && roll < p.memset_pct) L.type = FDY_NODE_MEMSET;
     else if (n > 0 && roll < p.memset_pct + p.memcpy_pct) L.type = FDY_NODE_MEMCPY;
     else if (n > 0 && n + 1 < N && roll < p.memset_pct + p.memcpy_pct + p.event_pct &&
              grp.nodes[n - 1].type != FDY_NODE_EVENT_RECORD)
@@ -240,6 +244,10 @@ Group make_group(const fdy_synth_params& p, uint32_t g, const Intervals& iv) {
     uint32_t pos = n % 25;
     L.binary_hash = mix(p.seed ^ 0xC0DEull, (uint64_t)g * 4096 + pos);
     L.name = kernel_name(g, pos, L.binary_hash);
+    if (p.sink_hash) {
+      L.binary_hash = p.sink_hash;
+      L.name = "fdy_sink";
+    }
     L.block = r.below(2) ? 256 : 128;
     L.grid[0] = 1 + (uint32_t)r.below(512);
     L.grid[1] = 1 + (uint32_t)r.below(4);
@@ -247,7 +255,7 @@ Group make_group(const fdy_synth_params& p, uint32_t g, const Intervals& iv) {
     L.grid_bs = r.below(100) < p.grid_bs_pct;
     L.extra = r.below(100) < p.extra_style_pct;
     L.layout_var = r.below(100) < p.layout_var_pct;
-    if (n == 0 && p.num_groups > 1) L.cluster_x = g + 1;
+    if (n == 0 && p.num_groups > 1 && !p.sink_hash) L.cluster_x = g + 1;
     uint32_t lo = std::max<uint32_t>(8, p.min_blob_bytes) / 8, hi = std::max<uint32_t>(lo * 8, p.max_blob_bytes) / 8;
     for (int v = 0; v < 2; ++v) {
       uint32_t blob = 8 * (uint32_t)r.range(lo, hi);
@@ -458,6 +466,7 @@ int fdy_synth_preset(uint32_t preset, fdy_synth_params* o) {
 
 int fdy_synth_create(const fdy_synth_params* p, uint32_t num_threads, fdy_synth** out) {
   if (!p || !out) return fail("null argument");
+  if (p->sink_hash && p->num_groups > 64) return fail("sink mode tells at most 64 groups apart");
   if (p->num_groups == 0 && p->num_graphs) return fail("num_groups must be >= 1");
   if (p->num_intervals == 0) return fail("num_intervals must be >= 1");
   if (p->region_size / std::max<uint32_t>(16, p->interval_granule) < p->num_intervals)

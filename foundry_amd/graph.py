@@ -77,6 +77,11 @@ class GroupGraph:
         check(restore_lib().fdy_group_graph_select(self._h, graph, _stream(stream), C.byref(st)))
         return {k: getattr(st, k) for k, _ in SelectStats._fields_}
 
+    def reset_all(self, stream=None) -> dict:
+        st = SelectStats()
+        check(restore_lib().fdy_group_graph_reset_all(self._h, _stream(stream), C.byref(st)))
+        return {k: getattr(st, k) for k, _ in SelectStats._fields_}
+
     def launch(self, stream=None) -> None:
         check(restore_lib().fdy_group_graph_launch(self._h, _stream(stream)))
 

@@ -61,6 +61,9 @@ typedef struct fdy_synth_params {
   uint64_t interval_max;
   uint64_t num_words;        /* preset 4: packed words to generate */
   double boundary_frac;      /* preset 4: fraction of pointers on interval edges */
+  uint64_t sink_hash;        /* nonzero: every kernel node names kernel "fdy_sink" of the code object
+                                with this hash, and groups differ by a kernel/empty pattern in nodes
+                                1..6 instead of by cluster dims (graphs a gfx950 group graph can build) */
 } fdy_synth_params;
 
 typedef struct fdy_synth fdy_synth;

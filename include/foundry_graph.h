@@ -113,6 +113,10 @@ int fdy_group_graph_destroy(fdy_group_graph* gg);
  * `graph` is current.  `stats` may be NULL.  Counterpart of the on-demand
  * branch of csrc/CUDAGraph.cpp:330-461, which re-sets every node. */
 int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fdy_select_stats* stats);
+/* Re-set every node of the exec from the current graph, as the reference
+ * does on every switch (csrc/CUDAGraph.cpp:345-441).  Use after an update
+ * failed part-way; the bench uses it as the all-node baseline. */
+int fdy_group_graph_reset_all(fdy_group_graph* gg, void* stream, fdy_select_stats* stats);
 /* Launch the exec on `stream` (csrc/CUDAGraph.cpp:476-477). */
 int fdy_group_graph_launch(fdy_group_graph* gg, void* stream);
 int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out);

@@ -198,3 +198,44 @@ def test_unresolvable_templates_are_refused_before_launch(env):
         with pytest.raises(_lib.FoundryError, match=code):
             GroupGraph(arch, 0, env.reg, env.stream)
         arch.close()
+
+
+def test_synthetic_groups_build_and_switch_without_launch(env):
+    """Group graphs of a synthetic decode-style archive whose kernels all
+    resolve to the probe's sink kernel (built and switched, never launched:
+    the saved pointers are synthetic).  Every switch re-sets exactly the
+    nodes the override sets and flags name."""
+    from foundry_amd import synth
+
+    p = synth.preset(2, num_graphs=24, num_groups=3, nodes_per_graph=300, num_intervals=2000)
+    p.sink_hash = env.bhash
+    s = synth.SynthArchive(p)
+    arch = Archive.from_synth(s)
+    arch.set_relocation(*s.intervals())
+    arch.restore(env.stream)
+    groups = arch.groups(env.stream)
+    temps = sorted(set(int(t) for t in groups))
+    assert len(temps) == 3
+    ggs = {t: GroupGraph(arch, t, env.reg, env.stream) for t in temps}
+
+    def touched(g):
+        o = {int(x) for x in arch.overrides(g, env.stream)["node"]}
+        fl = arch.node_flags(g, env.stream)
+        return o | {n for n in range(len(fl)) if fl[n] & (_lib.NODE_LAYOUT | _lib.NODE_DESC)}
+
+    current = {t: t for t in temps}
+    rng = random.Random(7)
+    for _ in range(30):
+        g = rng.randrange(s.num_graphs)
+        t = int(groups[g])
+        st = ggs[t].select(g, env.stream)
+        want = 0 if current[t] == g else len(touched(current[t]) | touched(g))
+        assert st["nodes_reset"] == want, (current[t], g)
+        current[t] = g
+    full = ggs[temps[0]].reset_all(env.stream)
+    assert full["nodes_reset"] == 300
+    _, _, cur = arch.live(temps[0], env.stream)
+    assert cur == current[temps[0]]
+    for gg in ggs.values():
+        gg.close()
+    arch.close()

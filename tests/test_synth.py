@@ -38,3 +38,20 @@ def test_decode_preset_shape():
     p = synth.preset(2)
     assert (p.num_graphs, p.num_groups, p.nodes_per_graph, p.num_intervals) == (256, 4, 1200, 40000)
     assert p.region_size == 64 << 30 and abs(p.pointer_frac - 0.25) < 1e-9
+
+
+def test_sink_mode_names_one_kernel_and_keeps_groups_apart():
+    import oracle
+
+    p = synth.preset(5, num_graphs=16, num_groups=8, nodes_per_graph=40, num_intervals=200)
+    p.sink_hash = 0xFEEDFACE12345678
+    s = synth.SynthArchive(p)
+    imgs = s.images()
+    for img in imgs:
+        arc = R.read(img)
+        for n in arc.nodes:
+            if n.type == 0:
+                assert n.kernel.name == b"fdy_sink" and n.kernel.binary_hash == p.sink_hash
+                assert n.kernel.kna_flags == 0  # no cluster dims
+    ref = oracle.Restore(imgs, s.intervals())
+    assert len(set(int(t) for t in ref.groups())) == 8
