@@ -102,6 +102,23 @@ class SelectStats(C.Structure):
     ]
 
 
+class RegionInfo(C.Structure):
+    _fields_ = [
+        ("saved_base", C.c_uint64),
+        ("base", C.c_uint64),
+        ("size", C.c_uint64),
+        ("offset", C.c_uint64),
+        ("granularity", C.c_uint64),
+        ("mapped_bytes", C.c_uint64),
+        ("live_allocations", C.c_uint64),
+        ("prealloc_begin", C.c_uint64),
+        ("prealloc_end", C.c_uint64),
+        ("num_events", C.c_uint64),
+        ("recording", C.c_uint32),
+        ("flags", C.c_uint32),
+    ]
+
+
 class SynthParams(C.Structure):
     _fields_ = [
         ("preset", C.c_uint32),
@@ -184,6 +201,28 @@ _GRAPH_SIGS = {
 }
 _SIGS.update(_GRAPH_SIGS)
 
+_REGION_SIGS = {
+    "fdy_region_create": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.POINTER(_vp)]),
+    "fdy_region_create_plan": (C.c_int, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.POINTER(_vp)]),
+    "fdy_region_destroy": (C.c_int, [_vp]),
+    "fdy_region_info_get": (C.c_int, [_vp, C.POINTER(RegionInfo)]),
+    "fdy_region_alloc": (C.c_int, [_vp, C.c_uint64, u64p]),
+    "fdy_region_free": (C.c_int, [_vp, C.c_uint64]),
+    "fdy_region_reserve": (C.c_int, [_vp, C.c_uint64, C.c_uint64, u64p]),
+    "fdy_region_preallocate": (C.c_int, [_vp, C.c_uint64]),
+    "fdy_region_free_preallocated": (C.c_int, [_vp]),
+    "fdy_region_get_offset": (C.c_int, [_vp, u64p]),
+    "fdy_region_set_offset": (C.c_int, [_vp, C.c_uint64]),
+    "fdy_region_record": (C.c_int, [_vp, C.c_int]),
+    "fdy_region_clear_events": (C.c_int, [_vp]),
+    "fdy_region_events_json": (C.c_int, [_vp, C.c_char_p, C.c_uint64, u64p]),
+    "fdy_region_replay": (C.c_int, [_vp, C.c_char_p, C.c_uint64]),
+    "fdy_region_intervals": (C.c_int, [_vp, C.c_uint32, u64p, u64p, u64p, C.c_uint64, u64p]),
+}
+_SIGS.update(_REGION_SIGS)
+REGION_EXACT_BASE = 0x1
+REGION_IV_REGION, REGION_IV_ALLOCATIONS = 0, 1
+
 _SYNTH_SIGS = {
     "fdy_synth_preset": (C.c_int, [C.c_uint32, C.POINTER(SynthParams)]),
     "fdy_synth_create": (C.c_int, [C.POINTER(SynthParams), C.c_uint32, C.POINTER(_vp)]),
@@ -240,7 +279,11 @@ def check_synth(rc: int) -> None:
 
 
 def exported_symbols() -> list[str]:
-    return [k for k in _SIGS if k not in _GRAPH_SIGS]
+    return [k for k in _SIGS if k not in _GRAPH_SIGS and k not in _REGION_SIGS]
+
+
+def region_symbols() -> list[str]:
+    return list(_REGION_SIGS)
 
 
 def graph_symbols() -> list[str]:

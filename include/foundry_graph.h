@@ -47,9 +47,6 @@
 extern "C" {
 #endif
 
-#define FDY_E_NOT_FOUND (-10)   /* no code object with that hash, or no function of that name in it */
-#define FDY_E_UNSUPPORTED (-11) /* a node or attribute with no gfx950 counterpart */
-
 typedef struct fdy_registry fdy_registry;
 typedef struct fdy_group_graph fdy_group_graph;
 

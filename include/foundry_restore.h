@@ -45,7 +45,10 @@ extern "C" {
 #define FDY_E_RANGE (-6)    /* index out of range */
 #define FDY_E_STATE (-7)    /* call out of order (e.g. results before fdy_restore) */
 #define FDY_E_CAPACITY (-8) /* caller array too small; *_needed outputs say how big */
-#define FDY_E_MISMATCH (-9) /* graph and template disagree in node count (reference: TORCH_CHECK) */
+#define FDY_E_MISMATCH (-9) /* graph and template disagree in node count (reference: TORCH_CHECK), or a
+                               replayed allocation lands elsewhere than it was saved */
+#define FDY_E_NOT_FOUND (-10)   /* no code object with that hash, or no function of that name in it */
+#define FDY_E_UNSUPPORTED (-11) /* a node, attribute or request with no gfx950 counterpart */
 
 /* ---- relocation policy (fdy_archive_set_relocation / fdy_reloc_plan_create) ----
  * A word w is relocated by interval i = the last i with lo[i] <= w, if

@@ -64,6 +64,8 @@ def lib() -> C.CDLL:
             "orc_relocate_word": (C.c_uint64, [C.c_uint64, u64p, u64p, u64p, C.c_uint64, C.c_uint32]),
             "orc_relocate_words": (C.c_int, [u64p, u64p, C.c_uint64, u64p, u64p, u64p, C.c_uint64, C.c_uint32, C.c_uint32]),
             "orc_reference_load_ms": (C.c_double, [C.POINTER(C.c_char_p), C.c_uint32, C.c_uint32, C.c_uint32, u64p]),
+            "orc_region_replay": (C.c_int64, [C.c_char_p, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, u64p, u64p,
+                                              C.c_uint64]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -75,6 +77,21 @@ def lib() -> C.CDLL:
 
 def _err() -> str:
     return lib().orc_last_error().decode(errors="replace")
+
+
+def region_replay(events: str, saved_base: int, base: int, size: int, cursor: int):
+    """Replay one graph's allocator events: (placements as (saved lo, saved hi,
+    new lo) rows, new cursor), or (error code, cursor) with -1 parse, -2
+    mismatch, -3 region too small."""
+    data = events.encode()
+    cur = C.c_uint64(cursor)
+    n = lib().orc_region_replay(data, len(data), saved_base, base, size, C.byref(cur), None, 0)
+    if n < 0:
+        return int(n), cursor
+    out = np.zeros(3 * max(1, n), dtype=np.uint64)
+    cur = C.c_uint64(cursor)
+    lib().orc_region_replay(data, len(data), saved_base, base, size, C.byref(cur), out.ctypes.data_as(u64p), n)
+    return out[: 3 * n].reshape(n, 3), cur.value
 
 
 def crc64(data: bytes) -> int:

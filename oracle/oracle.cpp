@@ -838,6 +838,68 @@ int orc_relocate_words(const uint64_t* in, uint64_t* out, uint64_t n_words, cons
   return 0;
 }
 
+
+// Allocator-event replay.  Follows csrc/hook.cpp:
+//   3397-3421 start_base_addr: move the cursor forward to it, abort if behind
+//   3432-3461 alloc: cuMemAlloc_v2 at the cursor, abort unless at the saved ptr
+//   2272-2291, 2424 placement: ptr = align_up(cursor, 2 MiB); cursor = align_up(ptr + size, 2 MiB)
+//   3463-3478 reserve: ptr = align_up(cursor, alignment), abort unless saved ptr; cursor = align_up(ptr + size, 2 MiB)
+//   3480-3488 free: no placement
+int64_t orc_region_replay(const char* json, uint64_t len, uint64_t saved_base, uint64_t base, uint64_t size,
+                          uint64_t* cursor, uint64_t* out, uint64_t cap) {
+  const uint64_t A = 2ull << 20;
+  auto up = [](uint64_t v, uint64_t a) { return (v + a - 1) / a * a; };
+  Json doc;
+  JsonParser jp{json, json + len};
+  if (!jp.val(&doc, 0) || doc.k != Json::OBJ) return -1;
+  auto num = [](const Json* j, uint64_t* v) {
+    if (!j || j->k != Json::NUM || j->s.empty() || j->s[0] == '-') return false;
+    for (char c : j->s)
+      if (c < '0' || c > '9') return false;
+    *v = std::stoull(j->s);
+    return true;
+  };
+  uint64_t cur = *cursor;
+  if (const Json* s0 = doc.get("start_base_addr")) {
+    uint64_t st;
+    if (!num(s0, &st)) return -1;
+    const uint64_t target = base + (st - saved_base);
+    if (target < cur) return -2;
+    cur = target;
+  }
+  const Json* evs = doc.get("events");
+  if (!evs || evs->k != Json::ARR) return -1;
+  int64_t n = 0;
+  for (const Json& ev : evs->a) {
+    const Json* ty = ev.get("type");
+    if (!ty || ty->k != Json::STR) return -1;
+    uint64_t ptr, sz, al;
+    if (!num(ev.get("ptr"), &ptr)) return -1;
+    if (ty->s == "free") continue;
+    if (!num(ev.get("size"), &sz)) return -1;
+    uint64_t at;
+    if (ty->s == "alloc") {
+      at = up(cur, A);
+    } else if (ty->s == "reserve") {
+      if (!num(ev.get("alignment"), &al) || al == 0) return -1;
+      at = up(cur, al);
+    } else {
+      return -1;
+    }
+    if (at + sz > base + size) return -3;
+    if (ptr < saved_base || at - base != ptr - saved_base) return -2;
+    cur = up(at + sz, A);
+    if ((uint64_t)n < cap && out) {
+      out[3 * n] = ptr;
+      out[3 * n + 1] = ptr + sz;
+      out[3 * n + 2] = at;
+    }
+    ++n;
+  }
+  *cursor = cur;
+  return n;
+}
+
 }  // extern "C"
 
 // ---- the reference's CPU LOAD data work, restated ----------------------

@@ -88,6 +88,17 @@ int orc_relocate_words(const uint64_t* in, uint64_t* out, uint64_t n_words, cons
                        const uint64_t* hi, const uint64_t* new_lo, uint64_t n, uint32_t policy,
                        uint32_t num_threads);
 
+/* Replay of one graph's allocator events (csrc/hook.cpp:3394-3492) on a
+ * region whose cursor is *cursor (absolute address), with the placement rule
+ * of cuMemAlloc_v2 (csrc/hook.cpp:2272-2291, 2424) and the reserve carve
+ * (2705-2721).  Saved addresses are offsets from saved_base, placements
+ * offsets from base.  Writes (saved lo, saved hi, new lo) per alloc or
+ * reserve into out (3 per placement, at most cap placements) and advances
+ * *cursor.  Returns the number of placements, -1 if the text does not parse,
+ * -2 on a mismatch (the reference aborts), -3 if the region is too small. */
+int64_t orc_region_replay(const char* json, uint64_t len, uint64_t saved_base, uint64_t base, uint64_t size,
+                          uint64_t* cursor, uint64_t* out, uint64_t cap);
+
 /* The reference's CPU LOAD data work, restated (csrc/CUDAGraphParallel.cpp):
  * read files (1583-1620), build key strings and group (1788-1851), and per
  * node the prep of prepare_on_demand_graph_binary (1288-1473) minus driver

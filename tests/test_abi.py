@@ -34,6 +34,15 @@ def test_graph_half_exports_every_declared_symbol():
     assert declared == set(_lib.graph_symbols())
 
 
+def test_region_half_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_lib.RESTORE_LIB)
+    declared = _declared("foundry_region.h", "fdy_")
+    assert len(declared) >= 15
+    missing = [s for s in sorted(declared) if not hasattr(lib, s)]
+    assert not missing, missing
+    assert declared == set(_lib.region_symbols())
+
+
 def test_code_object_hash_is_crc64_xz_without_gpu():
     """fdy_code_object_hash is CRC-64/XZ (the identity of csrc/hook.cpp:315-321):
     the standard check value, and agreement with the bit-serial reference."""
