@@ -164,6 +164,9 @@ _SIGS = {
     "fdy_archive_info_get": (C.c_int, [_vp, C.POINTER(ArchiveInfo)]),
     "fdy_archive_set_relocation": (C.c_int, [_vp, u64p, u64p, u64p, C.c_uint64, C.c_uint32]),
     "fdy_archive_set_groups": (C.c_int, [_vp, u32p]),
+    "fdy_manifest_groups": (C.c_int, [C.c_char_p, C.c_uint64, C.POINTER(C.c_char_p), C.c_uint32, u32p,
+                                      C.POINTER(C.c_int)]),
+    "fdy_archive_set_manifest": (C.c_int, [_vp, C.c_char_p, C.c_uint64, C.POINTER(C.c_char_p), C.POINTER(C.c_int)]),
     "fdy_restore": (C.c_int, [_vp, _vp]),
     "fdy_get_digests": (C.c_int, [_vp, _vp, u64p]),
     "fdy_get_groups": (C.c_int, [_vp, _vp, u32p]),

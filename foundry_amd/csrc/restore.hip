@@ -13,11 +13,13 @@
 #include <memory>
 #include <string>
 #include <thread>
+#include <unordered_map>
 #include <vector>
 
 #include "../../include/foundry_restore.h"
 #include "archive.h"
 #include "cugraph.h"
+#include "json_min.h"
 #include "kernels.h"
 
 namespace fdy {
@@ -534,6 +536,59 @@ int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of) {
   FDY_HIP(hipMemcpy(a->explicit_tmpl.p, template_of, 4ull * a->G, hipMemcpyHostToDevice));
   a->use_explicit = true;
   return FDY_OK;
+}
+
+int fdy_manifest_groups(const char* text, uint64_t len, const char* const* names, uint32_t n, uint32_t* template_of,
+                        int* used) {
+  if ((!text && len) || (!names && n) || (!template_of && n) || !used)
+    return err(FDY_E_INVALID, "need the manifest text, the names, the output array and the used flag");
+  *used = 0;
+  std::unordered_map<std::string, uint32_t> index;
+  for (uint32_t i = 0; i < n; ++i) {
+    if (!names[i]) return err(FDY_E_INVALID, "null name " + std::to_string(i));
+    index.emplace(names[i], i);  // a repeated name resolves to its first graph
+  }
+  json::Value doc;
+  std::string perr;
+  json::Reader reader(text ? text : "", len);
+  // Any shape the reference's parse would throw on means "no manifest" (1776-1783).
+  if (!reader.parse(doc, perr) || doc.kind != json::Value::Object) return FDY_OK;
+  const json::Value* groups = doc.get("topology_groups");
+  if (!groups || groups->kind != json::Value::Array) return FDY_OK;
+  std::vector<uint32_t> res(n, UINT32_MAX);
+  for (const json::Value& g : groups->items) {
+    if (g.kind != json::Value::Object) return FDY_OK;
+    const json::Value* t = g.get("template");
+    if (!t || t->kind != json::Value::String) return FDY_OK;
+    auto ti = index.find(t->s);
+    if (ti == index.end()) continue;  // members of a skipped group are not read (1754-1755)
+    const json::Value* m = g.get("members");
+    if (!m || m->kind != json::Value::Array) return FDY_OK;
+    for (const json::Value& mem : m->items) {
+      if (mem.kind != json::Value::String) return FDY_OK;
+      if (mem.s == t->s) continue;
+      auto mi = index.find(mem.s);
+      if (mi == index.end()) continue;
+      res[mi->second] = ti->second;
+    }
+  }
+  for (uint32_t i = 0; i < n; ++i) {
+    const uint32_t t = res[i];
+    if (t != UINT32_MAX && res[t] != UINT32_MAX)
+      return err(FDY_E_INVALID, std::string("manifest: ") + names[i] + " has template " + names[t] +
+                                    ", which is itself a member of another group");
+  }
+  for (uint32_t i = 0; i < n; ++i) template_of[i] = res[i] == UINT32_MAX ? i : res[i];
+  *used = 1;
+  return FDY_OK;
+}
+
+int fdy_archive_set_manifest(fdy_archive* a, const char* text, uint64_t len, const char* const* names, int* used) {
+  if (!a || !used) return err(FDY_E_INVALID, "need an archive and the used flag");
+  std::vector<uint32_t> t(a->G);
+  int rc = fdy_manifest_groups(text, len, names, a->G, t.data(), used);
+  if (rc) return rc;
+  return *used ? fdy_archive_set_groups(a, t.data()) : fdy_archive_set_groups(a, nullptr);
 }
 
 int fdy_restore(fdy_archive* a, void* stream) {

@@ -102,6 +102,15 @@ class Archive:
         t = np.ascontiguousarray(np.asarray(template_of, dtype=np.uint32))
         check(restore_lib().fdy_archive_set_groups(self._h, t.ctypes.data_as(_lib.u32p)))
 
+    def set_manifest(self, text, names: Sequence[str]) -> bool:
+        """Group by a graph_manifest.json text; False if the reference would
+        ignore it (and group by keys)."""
+        data = text.encode() if isinstance(text, str) else bytes(text)
+        arr = (C.c_char_p * len(names))(*[n.encode() for n in names])
+        used = C.c_int()
+        check(restore_lib().fdy_archive_set_manifest(self._h, data, len(data), arr, C.byref(used)))
+        return bool(used.value)
+
     def set_timing(self, enabled: bool = True) -> None:
         check(restore_lib().fdy_set_timing(self._h, 1 if enabled else 0))
 
@@ -242,3 +251,15 @@ class RelocPlan:
 
 def version() -> str:
     return restore_lib().fdy_version().decode()
+
+
+def manifest_groups(text, names: Sequence[str]):
+    """template_of from a graph_manifest.json text (no device), or None when
+    the reference would ignore the manifest."""
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    arr = (C.c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+    out = np.zeros(max(1, len(names)), dtype=np.uint32)
+    used = C.c_int()
+    check(restore_lib().fdy_manifest_groups(data, len(data), arr, len(names), out.ctypes.data_as(_lib.u32p),
+                                            C.byref(used)))
+    return out[: len(names)] if used.value else None

@@ -121,6 +121,26 @@ int fdy_archive_set_relocation(fdy_archive* a, const uint64_t* lo, const uint64_
  * template_of[i] == i marks a template.  Pass NULL to go back to digests. */
 int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of);
 
+/* Template assignments from the text of a graph_manifest.json
+ * (csrc/CUDAGraphParallel.cpp:1727-1786, written by python/foundry/graph.py:
+ * 170-242).  names[i] is graph i's file name as the manifest lists it (the
+ * ".json" name).  A group whose template is not among the names is skipped;
+ * members not among the names are skipped; a later group overrides an
+ * earlier one for the same member; a template's own entry is never set by
+ * its group.  template_of[i] = i for templates and unlisted graphs.
+ * If the text is not a manifest the reference accepts (not JSON, no
+ * topology_groups array, a group without a string template or members
+ * array), *used = 0 and template_of is untouched: the reference then groups
+ * by keys.  A graph that ends up a member whose template is itself a member
+ * (the reference builds no exec for such a template) is FDY_E_INVALID.
+ * No device needed. */
+int fdy_manifest_groups(const char* text, uint64_t len, const char* const* names, uint32_t n,
+                        uint32_t* template_of, int* used);
+/* fdy_manifest_groups, then fdy_archive_set_groups when the manifest is used
+ * (otherwise the archive keeps grouping by keys). */
+int fdy_archive_set_manifest(fdy_archive* a, const char* text, uint64_t len, const char* const* names,
+                             int* used);
+
 /* The GPU restore, enqueued on `stream`:
  *   1. digests per graph (CRC-64/XZ): saved topology key, dependency table,
  *      recomputed node-type stream, kernel-entry stream;

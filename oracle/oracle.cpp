@@ -657,10 +657,13 @@ int orc_group_manifest(const char* text, uint64_t len, const char* const* names,
   for (const Json& grp : groups->a) {
     if (grp.k != Json::OBJ) return -1;
     const Json* t = grp.get("template");
-    const Json* m = grp.get("members");
-    if (!t || t->k != Json::STR || !m || m->k != Json::ARR) return -1;
+    if (!t || t->k != Json::STR) return -1;
     auto ti = idx.find(t->s);
-    if (ti == idx.end()) continue;  // unknown template: the group is skipped (1754-1755)
+    // Unknown template: the group is skipped before its members are read
+    // (1754-1755), so they are not checked either.
+    if (ti == idx.end()) continue;
+    const Json* m = grp.get("members");
+    if (!m || m->k != Json::ARR) return -1;
     // The template's own entry is left alone (1759, 1771): a template listed
     // as a member of an earlier group stays that group's member.
     for (const Json& mem : m->a) {

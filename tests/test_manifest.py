@@ -1,0 +1,84 @@
+"""The product's graph_manifest.json grouping (fdy_manifest_groups, no device
+needed) against the oracle's restatement of csrc/CUDAGraphParallel.cpp:
+1727-1786, on the hand cases the oracle is pinned with and on seeded random
+manifests."""
+import json
+import random
+
+import numpy as np
+import pytest
+
+import oracle
+from foundry_amd import _lib
+from foundry_amd.restore import manifest_groups
+
+NAMES = [f"graph_{i}.json" for i in range(6)]
+NONE = 0xFFFFFFFF
+
+
+def manifest(groups):
+    return json.dumps({"topology_groups": groups})
+
+
+def _expect(text, names):
+    """The oracle's result in the product's convention (template_of[i] = i for
+    templates and unlisted graphs), or None when the manifest is not used."""
+    o = oracle.group_manifest(text.encode() if isinstance(text, str) else text, names)
+    if o is None:
+        return None
+    return np.array([i if t == NONE else t for i, t in enumerate(o.tolist())], dtype=np.uint32)
+
+
+CASES = [
+    manifest([{"topology_key": "k0", "template": "graph_0.json", "members": ["graph_0.json", "graph_2.json", "graph_4.json"]},
+              {"topology_key": "k1", "template": "graph_1.json", "members": ["graph_1.json", "graph_3.json"]}]),
+    manifest([{"template": "graph_9.json", "members": ["graph_9.json", "graph_2.json"]},
+              {"template": "graph_1.json", "members": ["graph_5.json", "graph_nope.json"]}]),
+    manifest([{"template": "graph_9.json", "members": 7}, {"template": "graph_0.json", "members": ["graph_3.json"]}]),
+    manifest([{"template": "graph_0.json", "members": ["graph_2.json"]},
+              {"template": "graph_1.json", "members": ["graph_2.json", "graph_3.json"]}]),
+    manifest([]),
+    "{", "[]", "{}", manifest([{"members": []}]), manifest([{"template": "graph_0.json"}]),
+    manifest([{"template": 3, "members": []}]), manifest([{"template": "graph_0.json", "members": [1]}]),
+    manifest(["graph_0.json"]),
+    '{"topology_groups": [{"template": "graph_0.json", "members": ["graph_\\u0031.json"]}]}',
+]
+
+
+@pytest.mark.parametrize("i", range(len(CASES)))
+def test_hand_cases_match_the_oracle(i):
+    got = manifest_groups(CASES[i], NAMES)
+    want = _expect(CASES[i], NAMES)
+    if want is None:
+        assert got is None
+    else:
+        np.testing.assert_array_equal(got, want)
+
+
+def test_a_template_that_is_a_member_is_refused():
+    # The oracle (like the reference) leaves graph_1 a member of group 0 while
+    # graph_2 points at it; the reference builds no exec for graph_1 then.
+    m = manifest([{"template": "graph_0.json", "members": ["graph_1.json"]},
+                  {"template": "graph_1.json", "members": ["graph_2.json"]}])
+    assert oracle.group_manifest(m.encode(), NAMES).tolist()[1:3] == [0, 1]
+    with pytest.raises(_lib.FoundryError, match="FDY_E_INVALID"):
+        manifest_groups(m, NAMES)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_random_manifests_match_the_oracle(seed):
+    rng = random.Random(seed)
+    names = [f"graph_{i}.json" for i in range(40)]
+    perm = rng.sample(names, len(names))
+    groups, at = [], 0
+    while at < len(perm):
+        k = rng.randrange(1, 8)
+        mem = perm[at:at + k]
+        at += k
+        tmpl = mem[0] if rng.random() < 0.9 else f"missing_{at}.json"
+        members = list(mem) + ([f"stray_{at}.json"] if rng.random() < 0.2 else [])
+        rng.shuffle(members)
+        groups.append({"topology_key": f"k{at}", "template": tmpl, "members": members})
+    text = json.dumps({"topology_groups": groups}, indent=rng.choice([None, 2]))
+    got = manifest_groups(text, names)
+    np.testing.assert_array_equal(got, _expect(text, names))

@@ -69,3 +69,11 @@ def test_manifest_parse_failures_fall_back():
 
 def test_manifest_empty_groups_list():
     assert oracle.group_manifest(manifest([]), NAMES).tolist() == [NONE] * 6
+
+
+def test_manifest_unknown_template_is_skipped_before_its_members_are_read():
+    # csrc/CUDAGraphParallel.cpp:1752-1760: the template lookup `continue`s before
+    # group.at("members") is reached, so a bad members entry there does not throw.
+    m = manifest([{"template": "graph_9.json", "members": 7},
+                  {"template": "graph_0.json", "members": ["graph_3.json"]}])
+    assert oracle.group_manifest(m, NAMES).tolist() == [NONE, NONE, NONE, 0, NONE, NONE]
