@@ -765,6 +765,14 @@ int fdy_get_node_pointers(fdy_archive* a, void* stream, uint32_t g, uint64_t* ou
                   n_out);
 }
 
+int fdy_get_section(fdy_archive* a, uint32_t g, uint32_t sec, uint8_t* out, uint64_t cap, uint64_t* n_out) {
+  int rc = check_graph(a, g);
+  if (rc) return rc;
+  if (sec >= FDY_SEC_COUNT) return err(FDY_E_RANGE, "section " + std::to_string(sec) + " out of range");
+  FDY_HIP(hipSetDevice(a->device));
+  return copy_out(a->img.as<uint8_t>() + a->graphs[g].sec_off[sec], a->graphs[g].sec_size[sec], out, cap, n_out);
+}
+
 int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = check_graph(a, g);

@@ -1,0 +1,399 @@
+"""The reference's `foundry.ops` LOAD surface, on the MI355X restore path.
+
+Mirrors the names, arguments and error behaviour of the compiled module the
+reference binds in csrc/binding.cpp:13-338 for the LOAD side:
+
+  allocation region   set_allocation_region / stop_ / resume_allocation_region,
+                      preallocate_region / free_preallocated_region,
+                      get_ / set_current_alloc_offset        (csrc/binding.cpp:16-69)
+  code objects        load_cuda_modules_and_libraries(dir)   (csrc/binding.cpp:81-86)
+  graphs              CUDAGraph.load / start_graph_builds / finish_graph_loads /
+                      finish_one_graph_load, CUDAGraph.replay / reset
+                                                             (csrc/binding.cpp:118-338)
+
+Underneath: the archives are opened and restored on the GPU in one pass
+(`Archive`), each topology group gets one hipGraph exec (`GroupGraph`), and a
+graph's replay switches its group's exec to it and launches.  When the
+allocation region could not sit at its saved base, the restore relocates
+every saved pointer by the region's interval, and output tensors are views at
+the relocated addresses.
+
+Capture and SAVE (capture_begin / capture_end / save) are not part of this
+build: they raise NotImplementedError.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import json
+import os
+import threading
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .graph import GroupGraph, Registry
+from .region import Region
+from .restore import Archive
+
+MiB = 1 << 20
+SEC_ALLOC_EVENTS, SEC_OUTPUT_TENSORS = 8, 9
+
+# ---- allocation region (per thread, as the reference's TLS state, csrc/hook.cpp:218-251) ----
+
+_tls = threading.local()
+
+
+def _region() -> Region | None:
+    return getattr(_tls, "region", None)
+
+
+def set_allocation_region(base: int, size: int) -> None:
+    """Reserve the region (csrc/hook.cpp:3088-3142).  The base is rounded up to
+    2 MiB as the reference does; when the device cannot hold the region there,
+    it is placed elsewhere and graphs restored later are relocated."""
+    old = _region()
+    if old is not None:
+        old.close()
+    base = (int(base) + 2 * MiB - 1) // (2 * MiB) * (2 * MiB)
+    size = (int(size) + 2 * MiB - 1) // (2 * MiB) * (2 * MiB)
+    _tls.region = Region(base, size)
+    _tls.enabled = True
+
+
+def release_allocation_region() -> None:
+    """Unmap and unreserve this thread's region (no counterpart in the
+    reference, whose region lives as long as the process).  Views into it
+    must be dropped first."""
+    r = _region()
+    if r is not None:
+        r.close()
+    _tls.region = None
+    _tls.enabled = False
+
+
+def stop_allocation_region() -> None:
+    _tls.enabled = False
+
+
+def resume_allocation_region() -> None:
+    _tls.enabled = True
+
+
+def allocation_region_enabled() -> bool:
+    return _region() is not None and getattr(_tls, "enabled", False)
+
+
+def preallocate_region(size: int) -> bool:
+    """csrc/hook.cpp:3161-3275: False (not an exception) when it cannot."""
+    r = _region()
+    if r is None:
+        return False
+    try:
+        r.preallocate(int(size))
+    except _lib.FoundryError:
+        return False
+    return True
+
+
+def free_preallocated_region() -> None:
+    r = _region()
+    if r is not None:
+        r.free_preallocated()
+
+
+def get_current_alloc_offset() -> int:
+    r = _region()
+    return r.offset if r is not None else 0
+
+
+def set_current_alloc_offset(offset: int) -> None:
+    r = _region()
+    if r is None:
+        raise RuntimeError("set_current_alloc_offset: no allocation region is set")
+    r.offset = int(offset)
+
+
+def region_alloc(nbytes: int) -> int:
+    """An allocation placed by the region's cursor rule (what the reference's
+    cuMemAlloc_v2 interposer does for every driver allocation)."""
+    r = _region()
+    if r is None or not allocation_region_enabled():
+        raise RuntimeError("no enabled allocation region")
+    return r.alloc(int(nbytes))
+
+
+def region_free(ptr: int) -> None:
+    r = _region()
+    if r is None:
+        raise RuntimeError("no allocation region")
+    r.free(int(ptr))
+
+
+def graph_pool_handle():
+    return torch.cuda.graph_pool_handle()
+
+
+# ---- code objects -----------------------------------------------------------
+
+_registry: Registry | None = None
+_registry_lock = threading.Lock()
+
+
+def registry() -> Registry:
+    global _registry
+    with _registry_lock:
+        if _registry is None:
+            _registry = Registry()
+        return _registry
+
+
+def load_cuda_modules_and_libraries(directory: str) -> int:
+    """Load every gfx950 code object (*.co, *.hsaco) in `directory` into the
+    process registry; kernels resolve by CRC-64/XZ of the code object and
+    name (csrc/hook.cpp:3514-3551).  Returns the number loaded."""
+    n = 0
+    for name in sorted(os.listdir(directory)):
+        if name.endswith((".co", ".hsaco")):
+            registry().add_file(os.path.join(directory, name))
+            n += 1
+    return n
+
+
+# ---- output tensors ---------------------------------------------------------
+
+# c10::ScalarType numbering, as the reference saves `dtype` (csrc/CUDAGraph.cpp:961).
+_SCALAR_TYPES = {
+    0: torch.uint8, 1: torch.int8, 2: torch.int16, 3: torch.int32, 4: torch.int64, 5: torch.float16,
+    6: torch.float32, 7: torch.float64, 9: torch.complex64, 10: torch.complex128, 11: torch.bool,
+    15: torch.bfloat16, 23: torch.float8_e5m2, 24: torch.float8_e4m3fn, 25: torch.float8_e5m2fnuz,
+    26: torch.float8_e4m3fnuz,
+}
+
+
+class _DLDevice(C.Structure):
+    _fields_ = [("device_type", C.c_int32), ("device_id", C.c_int32)]
+
+
+class _DLDataType(C.Structure):
+    _fields_ = [("code", C.c_uint8), ("bits", C.c_uint8), ("lanes", C.c_uint16)]
+
+
+class _DLTensor(C.Structure):
+    _fields_ = [("data", C.c_void_p), ("device", _DLDevice), ("ndim", C.c_int32), ("dtype", _DLDataType),
+                ("shape", C.POINTER(C.c_int64)), ("strides", C.POINTER(C.c_int64)), ("byte_offset", C.c_uint64)]
+
+
+class _DLManagedTensor(C.Structure):
+    pass
+
+
+_DELETER = C.CFUNCTYPE(None, C.POINTER(_DLManagedTensor))
+_DLManagedTensor._fields_ = [("dl_tensor", _DLTensor), ("manager_ctx", C.c_void_p), ("deleter", _DELETER)]
+_live_views: dict[int, tuple] = {}
+
+
+@_DELETER
+def _release_view(p):
+    _live_views.pop(C.addressof(p.contents), None)
+
+
+_PyCapsule_New = C.pythonapi.PyCapsule_New
+_PyCapsule_New.restype = C.py_object
+_PyCapsule_New.argtypes = [C.c_void_p, C.c_char_p, C.c_void_p]
+_kDLROCM = 10
+
+
+def tensor_at(ptr: int, sizes: Sequence[int], strides: Sequence[int], dtype: torch.dtype, device_index: int = 0,
+              requires_grad: bool = False) -> torch.Tensor:
+    """A non-owning view of device memory at `ptr` (at::from_blob,
+    csrc/CUDAGraph.cpp:996): built through DLPack as unsigned integers of the
+    element size, then viewed as `dtype`."""
+    esize = torch.empty((), dtype=dtype).element_size()
+    nd = len(sizes)
+    shape = (C.c_int64 * max(1, nd))(*sizes)
+    strd = (C.c_int64 * max(1, nd))(*strides)
+    m = _DLManagedTensor()
+    m.dl_tensor.data = ptr
+    m.dl_tensor.device = _DLDevice(_kDLROCM, device_index)
+    m.dl_tensor.ndim = nd
+    m.dl_tensor.dtype = _DLDataType(1, 8 * esize, 1)
+    m.dl_tensor.shape = C.cast(shape, C.POINTER(C.c_int64))
+    m.dl_tensor.strides = C.cast(strd, C.POINTER(C.c_int64))
+    m.dl_tensor.byte_offset = 0
+    m.manager_ctx = None
+    m.deleter = _release_view
+    _live_views[C.addressof(m)] = (m, shape, strd)
+    cap = _PyCapsule_New(C.addressof(m), b"dltensor", None)
+    t = torch.from_dlpack(cap).view(dtype)
+    if requires_grad:
+        t.requires_grad_(True)
+    return t
+
+
+def _relocate(ptr: int, intervals) -> int:
+    lo, hi, nlo = intervals
+    if not len(lo):
+        return ptr
+    i = int(np.searchsorted(lo, np.uint64(ptr), side="right")) - 1
+    if i >= 0 and ptr < int(hi[i]):
+        return (ptr - int(lo[i]) + int(nlo[i])) & ((1 << 64) - 1)
+    return ptr
+
+
+def _outputs_from(text: bytes, intervals):
+    """OUTPUT_TENSORS metadata -> None, a tensor, or a list/tuple of tensors
+    (csrc/CUDAGraph.cpp:971-999, csrc/CUDAGraphParallel.cpp:2077-2095)."""
+    if not text:
+        return None
+    obj = json.loads(text)
+    kind = int(obj.get("type", 0))
+    metas = obj.get("tensors", [])
+
+    def one(m):
+        dt = _SCALAR_TYPES.get(int(m["dtype"]))
+        if dt is None:
+            raise RuntimeError(f"output tensor of unsupported scalar type {m['dtype']}")
+        return tensor_at(_relocate(int(m["data_ptr"]), intervals), [int(s) for s in m["sizes"]],
+                         [int(s) for s in m["strides"]], dt, int(m.get("device_index", 0) or 0),
+                         bool(m.get("requires_grad", False)))
+
+    if kind == 1 and len(metas) == 1:
+        return one(metas[0])
+    if kind in (2, 3):
+        ts = [one(m) for m in metas]
+        return tuple(ts) if kind == 3 else ts
+    return None
+
+
+# ---- graphs -----------------------------------------------------------------
+
+
+class PendingGraphLoads:
+    """The split-load state (include/CUDAGraphInternal.h:13-28): the restored
+    archive, one group graph per topology group, and one CUDAGraph per graph."""
+
+    def __init__(self, json_paths: Sequence[str], num_threads: int, stream):
+        self.json_paths = list(json_paths)
+        self.names = [os.path.basename(p) for p in self.json_paths]
+        self.archive = Archive.open(self.json_paths, max(1, int(num_threads)))
+        self.used_manifest = False
+        manifest = os.path.join(os.path.dirname(self.json_paths[0]) or ".", "graph_manifest.json")
+        if os.path.exists(manifest):
+            with open(manifest, "rb") as f:
+                self.used_manifest = self.archive.set_manifest(f.read(), self.names)
+        r = _region()
+        self.intervals = (np.zeros(0, np.uint64),) * 3
+        if r is not None:
+            info = r.info()
+            if info["base"] != info["saved_base"]:
+                self.intervals = r.intervals()
+                self.archive.set_relocation(*self.intervals)
+        self.archive.restore(stream)
+        self.template_of = self.archive.groups(stream)
+        self.group_graphs = {int(t): GroupGraph(self.archive, int(t), registry(), stream)
+                             for t in sorted(set(int(x) for x in self.template_of))}
+        self.graphs = [CUDAGraph._restored(self, i) for i in range(len(self.json_paths))]
+        self.finished = [False] * len(self.json_paths)
+        self.outputs: list = [None] * len(self.json_paths)
+
+    def group_graph(self, index: int) -> GroupGraph:
+        return self.group_graphs[int(self.template_of[index])]
+
+    def close(self) -> None:
+        for gg in self.group_graphs.values():
+            gg.close()
+        self.group_graphs = {}
+        self.archive.close()
+
+
+class CUDAGraph:
+    """A restored graph (csrc/CUDAGraph.cpp).  Graphs of one topology group
+    share their group's exec; replay() makes it run this graph's params."""
+
+    def __init__(self, keep_graph: bool = False):
+        self.keep_graph = keep_graph
+        self._pending: PendingGraphLoads | None = None
+        self._index = -1
+
+    @classmethod
+    def _restored(cls, pending: PendingGraphLoads, index: int) -> "CUDAGraph":
+        g = cls()
+        g._pending = pending
+        g._index = index
+        return g
+
+    # capture and SAVE are out of scope
+    def capture_begin(self, pool=None, capture_error_mode: str = "global") -> None:
+        raise NotImplementedError("graph capture is not part of this build (LOAD path only)")
+
+    def capture_end(self) -> None:
+        raise NotImplementedError("graph capture is not part of this build (LOAD path only)")
+
+    def save(self, json_path: str, output_tensors=None) -> None:
+        raise NotImplementedError("SAVE is not part of this build (LOAD path only)")
+
+    def replay(self) -> None:
+        """csrc/CUDAGraph.cpp:330-483: switch the group's exec to this graph
+        (only the nodes that differ are re-set), then launch on the current
+        stream."""
+        if self._pending is None:
+            raise RuntimeError("replay: this CUDAGraph holds no restored graph")
+        gg = self._pending.group_graph(self._index)
+        stream = torch.cuda.current_stream()
+        gg.select(self._index, stream)
+        gg.launch(stream)
+
+    def reset(self) -> None:
+        self._pending = None
+        self._index = -1
+
+    def raw_cuda_graph_exec(self) -> int:
+        raise NotImplementedError("the exec belongs to the topology group (GroupGraph)")
+
+    @property
+    def index(self) -> int:
+        return self._index
+
+    # ---- split load -------------------------------------------------------
+    @staticmethod
+    def start_graph_builds(json_paths: Sequence[str], pool=None, num_threads: int = 4) -> PendingGraphLoads:
+        """Open and restore every archive on the GPU and build one exec per
+        topology group (csrc/CUDAGraphParallel.cpp:1543-2015).  A
+        graph_manifest.json beside the first path groups the graphs; without
+        it, graphs group by their saved topology keys.  Everything is done
+        when this returns."""
+        if not json_paths:
+            raise RuntimeError("start_graph_builds: no graphs given")
+        torch.cuda.synchronize()
+        return PendingGraphLoads(json_paths, num_threads, torch.cuda.current_stream())
+
+    @staticmethod
+    def finish_one_graph_load(pending: PendingGraphLoads, index: int):
+        """csrc/CUDAGraphParallel.cpp:2034-2069: replay graph `index`'s
+        allocator events into the region (in SAVE order), then rebuild its
+        output tensors.  Raises IndexError out of range, as the reference's
+        std::out_of_range does through pybind."""
+        if index < 0 or index >= len(pending.graphs):
+            raise IndexError(f"finish_one_graph_load: index {index} out of range "
+                             f"(num_graphs={len(pending.graphs)})")
+        if not pending.finished[index]:
+            events = pending.archive.section(index, SEC_ALLOC_EVENTS)
+            r = _region()
+            if events and r is not None:
+                r.replay(events)
+            pending.outputs[index] = _outputs_from(pending.archive.section(index, SEC_OUTPUT_TENSORS),
+                                                   pending.intervals)
+            pending.finished[index] = True
+        return pending.graphs[index], pending.outputs[index]
+
+    @staticmethod
+    def finish_graph_loads(pending: PendingGraphLoads):
+        return [CUDAGraph.finish_one_graph_load(pending, i) for i in range(len(pending.graphs))]
+
+    @staticmethod
+    def load(json_path: str, pool=None):
+        """One graph: (graph, outputs or None) (csrc/CUDAGraph.cpp:1520-1560)."""
+        pending = CUDAGraph.start_graph_builds([json_path], pool, 1)
+        return CUDAGraph.finish_one_graph_load(pending, 0)

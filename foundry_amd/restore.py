@@ -190,6 +190,15 @@ class Archive:
     def node_pointers(self, g: int, stream=None) -> np.ndarray:
         return self._sized(restore_lib().fdy_get_node_pointers, g, np.uint64, stream)
 
+    def section(self, g: int, section: int) -> bytes:
+        """Raw bytes of one section of graph g's archive."""
+        n = C.c_uint64()
+        check(restore_lib().fdy_get_section(self._h, g, section, None, 0, C.byref(n)))
+        buf = (C.c_uint8 * max(1, n.value))()
+        if n.value:
+            check(restore_lib().fdy_get_section(self._h, g, section, buf, n.value, C.byref(n)))
+        return bytes(buf)[: n.value]
+
     # ---- switching -------------------------------------------------------
     def switch(self, g: int, stream=None) -> None:
         check(restore_lib().fdy_switch(self._h, g, _stream(stream)))

@@ -176,6 +176,12 @@ int fdy_get_param_image(fdy_archive* a, void* stream, uint32_t graph, uint64_t* 
 int fdy_get_node_pointers(fdy_archive* a, void* stream, uint32_t graph, uint64_t* ptrs /* 2*N */,
                           uint64_t cap, uint64_t* n_out);
 
+/* The bytes of one section (FDY_SEC_*, include/fdy_format.h) of graph
+ * `graph`'s archive, e.g. the ALLOCATOR_EVENTS or OUTPUT_TENSORS JSON text
+ * (csrc/CUDAGraphParallel.cpp:1664-1690 reads the same).  Works before
+ * fdy_restore.  Synchronizes the device copy. */
+int fdy_get_section(fdy_archive* a, uint32_t graph, uint32_t section, uint8_t* out, uint64_t cap, uint64_t* n_out);
+
 /* Switch the live image of graph `graph`'s group to `graph`: restore the
  * template's words under the current graph's overrides that `graph` does
  * not override, write `graph`'s overrides, and point layout/descriptor-

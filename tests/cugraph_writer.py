@@ -111,8 +111,13 @@ def saved_key(nodes) -> bytes:
     return ",".join(parts).encode()
 
 
-def write(nodes, deps=(), node_ids=None, common_cluster=None) -> bytes:
-    """Archive bytes for `nodes` (Kernel/Memset/...); deps are (from_id, to_id)."""
+FLAG_ALLOC_EVENTS, FLAG_OUTPUT_TENSORS = 4, 8
+
+
+def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: bytes = b"",
+          output_tensors: bytes = b"") -> bytes:
+    """Archive bytes for `nodes` (Kernel/Memset/...); deps are (from_id, to_id).
+    alloc_events / output_tensors are the JSON texts of those sections."""
     ids = list(node_ids) if node_ids is not None else list(range(len(nodes)))
     strings = b""
     name_at = {}
@@ -156,7 +161,8 @@ def write(nodes, deps=(), node_ids=None, common_cluster=None) -> bytes:
         common = struct.pack("<4I", KNA_CLUSTER_DIM, *common_cluster) + struct.pack("<3I", 0, 0, 0)
         common += struct.pack("<4i", -1, -1, -1, -1) + struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
     secs = [strings, b"".join(entries), b"".join(struct.pack("<II", *d) for d in deps),
-            b"".join(struct.pack("<II", *p) for p in pidx), pdata, arg_data, common, b"", b"", b"", saved_key(nodes)]
+            b"".join(struct.pack("<II", *p) for p in pidx), pdata, arg_data, common, b"", alloc_events,
+            output_tensors, saved_key(nodes)]
     off = 64 + 11 * 24
     table, body = b"", b""
     for i, s in enumerate(secs):
@@ -165,6 +171,7 @@ def write(nodes, deps=(), node_ids=None, common_cluster=None) -> bytes:
         body += s + b"\0" * pad
         off += len(s) + pad
     flags = (FLAG_COMMON if common else 0) | (FLAG_DEPS if deps else 0)
+    flags |= (FLAG_ALLOC_EVENTS if alloc_events else 0) | (FLAG_OUTPUT_TENSORS if output_tensors else 0)
     header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, flags, len(nodes), len(deps), 0, 11, len(name_at))
     return header + table + body
 

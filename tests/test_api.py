@@ -1,0 +1,79 @@
+"""The reference's `foundry` names on this build (python/foundry/__init__.py,
+pinned by the reference's tests/test_imports.py:41-69), its size parser, and
+save_graph_manifest's output -- all without a GPU."""
+import json
+import os
+
+import pytest
+
+import cugraph_writer as W
+import foundry_amd
+from foundry_amd import api
+
+PUBLIC_NAMES_FROM_FOUNDRY = [
+    "CUDAGraph", "allocation_region", "free_preallocated_region", "get_current_alloc_offset", "graph",
+    "parse_size", "preallocate_region", "resume_allocation_region", "save_graph_manifest",
+    "set_current_alloc_offset", "set_allocation_region", "stop_allocation_region",
+]
+
+
+def test_re_exports_present():
+    missing = [n for n in PUBLIC_NAMES_FROM_FOUNDRY if not hasattr(foundry_amd, n)]
+    assert not missing
+    ops = __import__("foundry_amd.ops", fromlist=["CUDAGraph"])
+    for name in ("start_graph_builds", "finish_graph_loads", "finish_one_graph_load", "load", "replay"):
+        assert hasattr(ops.CUDAGraph, name)
+
+
+@pytest.mark.parametrize("text,value", [
+    (4096, 4096), ("1GB", 1 << 30), ("16MB", 16 << 20), ("24KB", 24 << 10), (" 2tb ", 2 << 40), ("1.5GB", 3 << 29),
+    ("512", 512), ("7 b", 7),
+])
+def test_parse_size(text, value):
+    assert api.parse_size(text) == value
+
+
+@pytest.mark.parametrize("bad", ["", "GB", "1XB", "-1GB", "1,5GB"])
+def test_parse_size_rejects(bad):
+    with pytest.raises(ValueError):
+        api.parse_size(bad)
+
+
+def test_capture_is_refused_clearly():
+    g = api.CUDAGraph()
+    with pytest.raises(NotImplementedError):
+        g.capture_begin()
+    with pytest.raises(NotImplementedError):
+        with api.graph(g):
+            pass
+
+
+def _kern(name):
+    return W.Kernel(name, 0x1234, params=[W.le(0)])
+
+
+def test_save_graph_manifest_groups_by_key_in_capture_order(tmp_path):
+    a = [_kern("k"), W.Empty()]
+    b = [_kern("k"), _kern("k")]
+    specs = {0: a, 1: b, 2: a, 3: b, 10: a}
+    for i, nodes in specs.items():
+        (tmp_path / f"graph_{i}_bs{i}.cugraph").write_bytes(W.write(nodes))
+    # one graph also has its JSON, whose dependencies are stripped (not a template)
+    (tmp_path / "graph_2_bs2.json").write_text(json.dumps({"topology_key": W.saved_key(a).decode(),
+                                                           "dependencies": [{"from": 0, "to": 1}]}))
+    api.save_graph_manifest(str(tmp_path))
+    text = (tmp_path / "graph_manifest.json").read_text()
+    key_a, key_b = W.saved_key(a).decode(), W.saved_key(b).decode()
+    expect = {"topology_groups": [
+        {"topology_key": key_a, "template": "graph_0_bs0.json",
+         "members": ["graph_0_bs0.json", "graph_2_bs2.json", "graph_10_bs10.json"]},
+        {"topology_key": key_b, "template": "graph_1_bs1.json", "members": ["graph_1_bs1.json", "graph_3_bs3.json"]},
+    ]}
+    assert text == json.dumps(expect, indent=2)  # the reference writes with json.dump(indent=2)
+    assert "dependencies" not in json.loads((tmp_path / "graph_2_bs2.json").read_text())
+
+
+def test_save_graph_manifest_needs_every_key(tmp_path):
+    (tmp_path / "graph_0.json").write_text(json.dumps({"topology_key": ""}))
+    api.save_graph_manifest(str(tmp_path))
+    assert not os.path.exists(tmp_path / "graph_manifest.json")
