@@ -114,11 +114,16 @@ __host__ __device__ inline uint64_t nibble_mul(const uint64_t (*tab)[16], uint64
 // chunks.
 constexpr int kTreeLevels = 11;
 
+// Records per node-pass chunk, and the multiplier of record i's raw CRC in
+// its chunk's CRC: x^(8 * 16 * (kPosRecords - 1 - i)) mod P.
+constexpr int kPosRecords = 256;
+
 struct CrcConsts {
   SliceTables slice;
   NibbleTable rec16[kTreeLevels];  // S = 16-byte records (node records)
   NibbleTable rec64[kTreeLevels];  // S = 64-byte records (byte streams, 8 words per lane)
   X2nTable x2n;
+  uint64_t pos16[kPosRecords];
 };
 
 inline void make_crc_consts(CrcConsts* c) {
@@ -128,6 +133,7 @@ inline void make_crc_consts(CrcConsts* c) {
     c->rec16[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)16 << k, 3));
     c->rec64[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)64 << k, 3));
   }
+  for (int i = 0; i < kPosRecords; ++i) c->pos16[i] = x2n_mod(c->x2n.v, 16ull * (kPosRecords - 1 - i), 3);
 }
 
 // Finish a raw CRC of an L-byte stream: crc = raw ^ (~0 * x^(8L)) ^ ~0.

@@ -89,6 +89,27 @@ __device__ uint64_t block_crc_combine(uint64_t z, const uint64_t (*nib)[16][16],
   return r;
 }
 
+// XOR of two values over the block (blockDim.x a multiple of 64); valid in
+// thread 0.
+__device__ void block_xor2(uint64_t& x, uint64_t& y, uint64_t (*s_wave)[2]) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    x ^= shfl_down64(x, d);
+    y ^= shfl_down64(y, d);
+  }
+  if (lane == 0) {
+    s_wave[wave][0] = x;
+    s_wave[wave][1] = y;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (uint32_t w = 1; w < nw; ++w) {
+      x ^= s_wave[w][0];
+      y ^= s_wave[w][1];
+    }
+}
+
 // The 8 bytes [b0, b0+8) of the L-byte stream at p (8-aligned), with bytes
 // outside [0, L) read as zero.
 __device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b0) {
@@ -440,13 +461,17 @@ __device__ __forceinline__ bool u64_range_differs(const uint8_t* a, const uint8_
 
 // Does node entry ea (strings A, common attrs ca) differ in its descriptor
 // from eb (strings B, common attrs cb)?  pa/pb: relocated pointers.
+// same_ctx: both graphs have byte-identical string sections and common
+// attrs, so equal entry bytes [8, 128) (launch config, function hash, name
+// offset and length, function attrs, per-node attrs) mean equal descriptors.
 __device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const uint8_t* ea, const Strings& B,
                              const uint8_t* cb, const uint8_t* eb, uint64_t pa0, uint64_t pa1, uint64_t pb0,
-                             uint64_t pb1) {
+                             uint64_t pb1, bool same_ctx) {
   const uint8_t ta = ea[FDY_NODE_OFF_TYPE], tb = eb[FDY_NODE_OFF_TYPE];
   if (ta != tb) return true;
   switch (ta) {
     case FDY_NODE_KERNEL: {
+      if (same_ctx && !u64_range_differs(ea, eb, 8, 120)) return false;
       bool d = false;
       for (uint32_t off = 8; off < 44; off += 4) d |= f32(ea, off) != f32(eb, off);
       for (uint32_t off = 52; off < 76; off += 4) d |= f32(ea, off) != f32(eb, off);
@@ -529,14 +554,13 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
 // and the slot descriptors of the diff pass.
 
 __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
-  constexpr uint32_t kLevels = 8;      // combine levels for kNodeChunk records
   constexpr uint32_t kStrStage = 2048; // string sections up to this size are staged in LDS
-  static_assert((1u << kLevels) == kNodeChunk, "one combine level per doubling");
+  static_assert(kNodeChunk == kPosRecords, "one position multiplier per record of a chunk");
   __shared__ uint64_t s_slice[8][256];
-  __shared__ uint64_t s_nib[kLevels][16][16];
   __shared__ uint64_t s_str[2][kStrStage / 8];
   __shared__ uint64_t s_common[2][7];
-  __shared__ uint64_t s_wave[kNodeChunk / 64];
+  __shared__ uint64_t s_wave[kNodeChunk / 64][2];
+  __shared__ uint32_t s_diff;
   __shared__ uint32_t s_sum[2][kNodeChunk / 64];
   __shared__ uint64_t s_pb[kNodeChunk / 64];
   __shared__ uint32_t s_status;
@@ -570,8 +594,22 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
   const Strings st_str = is_t ? sg_str : stage_strings(Gt, s_str[1]);
   const uint8_t* common_g = stage_common(Gg, s_common[0]);
   const uint8_t* common_t = is_t ? common_g : stage_common(Gt, s_common[1]);
-  stage_crc_tables(a.cc, true, s_slice, s_nib, kLevels);  // ends with a barrier
+  if (tid == 0) s_diff = 0;
+  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  __syncthreads();
   const uint64_t (*slice)[256] = s_slice;
+  // Identical string sections and common attrs (both staged in LDS) let the
+  // descriptor compare use the entry bytes alone.
+  bool same_ctx = false;
+  if (!is_t && sg_str.size == st_str.size && sg_str.size <= kStrStage && (common_g == nullptr) == (common_t == nullptr)) {
+    const uint32_t nw = (uint32_t)((sg_str.size + 7) / 8);
+    uint32_t d = 0;
+    for (uint32_t w = tid; w < nw; w += kNodeChunk) d |= s_str[0][w] != s_str[1][w];
+    if (common_g && tid < 7) d |= s_common[0][tid] != s_common[1][tid];
+    if (d) atomicOr(&s_diff, 1u);
+    __syncthreads();
+    same_ctx = s_diff == 0;
+  }
 
   const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
   const int64_t first = (int64_t)(chunk - Gg.chunk_base) * kNodeChunk - pad;  // node of thread 0
@@ -639,7 +677,7 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
       }
       if (layout) flags |= FDY_NODE_LAYOUT;
       else if (words_g) flags |= kNodeCompare;
-      if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, p0, p1, q0, q1)) flags |= FDY_NODE_DESC;
+      if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, p0, p1, q0, q1, same_ctx)) flags |= FDY_NODE_DESC;
     } else {
       flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
     }
@@ -660,13 +698,15 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
     if (is_t) a.live_src[gi] = g;
   }
 
+  // Raw CRC of the chunk's records: record i's raw CRC times x^(8*16*(255-i)),
+  // XOR-joined (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).
   uint64_t zt = 0, zk = 0;
   if (valid) {
-    zt = crc_slice8(slice, crc_slice8(slice, 0, tw0), tw1);
-    zk = crc_slice8(slice, crc_slice8(slice, 0, kw0), kw1);
+    const uint64_t m = a.cc->pos16[tid];
+    zt = gf2_mulmod(m, crc_slice8(slice, crc_slice8(slice, 0, tw0), tw1));
+    zk = gf2_mulmod(m, crc_slice8(slice, crc_slice8(slice, 0, kw0), kw1));
   }
-  zt = block_crc_combine(zt, s_nib, s_wave);
-  zk = block_crc_combine(zk, s_nib, s_wave);
+  block_xor2(zt, zk, s_wave);
   uint32_t sum_g = words_g, sum_t = words_t;
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
