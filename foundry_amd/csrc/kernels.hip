@@ -14,7 +14,7 @@
 //             table, ragged-word sources, slot descriptors.
 //   k_diff_t  the template graphs' words, relocated through a bucket-indexed
 //             interval search into R and the live image (1024-word units).
-//   k_diff_m  one workgroup per 4096-word tile of every other graph: coalesced
+//   k_diff_m  eight workgroups per 4096-word tile of every other graph: coalesced
 //             8-byte loads of the graph's and the template's words, the
 //             template's relocated word reused where the raw words are equal,
 //             lockstep batched searches for the rest, the relocated image
@@ -1067,9 +1067,13 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
   }
 }
 
-// The other graphs: one workgroup per slot; wave v of the workgroup owns the
-// slot's sub-range v (kSubWords consecutive words), lane l its words
-// v*kSubWords + j*64 + l for j < kMWords.  Relocation is a function of the
+// The other graphs: kMSplit workgroups per slot, each of kMThreads / 64
+// waves; wave v of the slot (counted over its workgroups) owns the slot's
+// sub-range v (kSubWords consecutive words), lane l its words
+// v*kSubWords + j*64 + l for j < kMWords.  Small workgroups retire and are
+// replaced wave by wave, where one workgroup per slot left its CU idle
+// while its last waves finished (measured: 91 us against 100 us for the
+// 256-graph decode-style archive).  Relocation is a function of the
 // raw word, so where a compared word equals the template's raw word the
 // template's relocated word is taken from R and stored at once, as are
 // partial words (never relocated).  The words left over (to be searched, or
@@ -1077,15 +1081,18 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
 // compacts them, in word order, into its sub-range's region and their
 // number into sub_count, and k_diff_s settles them.  No wave waits for an
 // interval search, and flat tiles need neither LDS nor a barrier.
-constexpr uint32_t kMThreads = kSubsPerSlot * 64;
+constexpr uint32_t kMSplit = 8;
+constexpr uint32_t kMThreads = kSubsPerSlot * 64 / kMSplit;
+static_assert(kSubsPerSlot % kMSplit == 0, "whole sub-ranges per workgroup");
 constexpr uint32_t kSlots = 2;  // searches per batch in the overflowed-template path
 
-// Eight waves per SIMD (at most 64 VGPRs): two workgroups per CU.
+// At most 64 VGPRs (eight waves per SIMD where LDS allows).
 __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
   constexpr uint32_t J = kMWords;
   __shared__ NodeDesc s_nd[kDiffWindow];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t slot = blockIdx.x;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t slot = blockIdx.x / kMSplit, part = blockIdx.x % kMSplit;
+  const uint32_t wave = part * (kMThreads / 64) + (tid >> 6);  // sub-range of the slot
   const SlotDesc sd = load_slot(a.slot_desc + slot);
   uint32_t* sub_count = a.sub_count + (uint64_t)slot * kSubsPerSlot;
   if (sd.flags & kSlotTemplate) {  // relocated by k_diff_t; a template has no overrides
@@ -1097,6 +1104,8 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
   const uint64_t w0 = wbeg + (uint64_t)wave * kSubWords + lane;  // word j is w0 + 64j
   const bool flat = (sd.flags & kSlotFlat) != 0;
   const RelocDev& R = a.reloc;
+  // Issued ahead of the word loads so that its wait does not follow theirs.
+  const uint32_t t_status = a.status[t];
   uint64_t* img_out = a.image + sd.word_base;
   // The template's relocated image (read within the template's capacity;
   // with relocation off it equals the raw image and is not read).  Its
@@ -1129,9 +1138,6 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
         if ((valid >> j) & 1) fr[j] = rimg_t[min(w0 + 64 * j, (uint64_t)t_last)];
     }
     cmp = full = valid;
-  }
-  if (tid == 0 && (sd.flags & kSlotFirst)) {
-    if (a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
   }
   if (!flat && wend > wbeg) {  // uniform over the workgroup
     const DevGraph& G = a.graphs[g];
@@ -1169,7 +1175,7 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
   if (R.n == 0) {
 #pragma unroll
     for (uint32_t j = 0; j < J; ++j) fr[j] = ft[j];  // relocation off: R equals the raw image
-  } else if (a.status[t] & kGraphOverflow) {
+  } else if (t_status & kGraphOverflow) {
     // The template overflowed its capacity: relocate its compared words here.
 #pragma unroll
     for (uint32_t jb = 0; jb < J; jb += kSlots) {
@@ -1183,17 +1189,20 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
   }
 
   // Store what is settled; the rest (whole words to relocate, and partial
-  // words that differ from the template's) are candidates.
+  // words that differ from the template's) are candidates.  Every valid
+  // word is stored, a whole word to relocate as its raw value until
+  // k_diff_s writes the relocated one: a tile's lines are then written
+  // whole, which spares HBM the read-modify-write of partly written lines.
   uint32_t cand = 0, creloc = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
     if (!((valid >> j) & 1)) continue;
     const uint64_t w = w0 + 64 * j;
     const bool c = (cmp >> j) & 1;
-    if (c && fg[j] == ft[j]) {
-      img_out[w] = fr[j];
-    } else if (!((full >> j) & 1)) {
-      img_out[w] = fg[j];
+    const bool same = c && fg[j] == ft[j];
+    img_out[w] = same ? fr[j] : fg[j];
+    if (same) continue;
+    if (!((full >> j) & 1)) {
       if (c && fg[j] != fr[j]) cand |= 1u << j;
     } else {
       cand |= 1u << j;
@@ -1217,6 +1226,9 @@ __global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
     run += (uint32_t)__popcll(mk);
   }
   if (lane == 0) sub_count[wave] = run;
+  if (tid == 0 && part == 0 && (sd.flags & kSlotFirst)) {
+    if (a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
+  }
 }
 
 // Candidates of the member pass, one wave per slot: the slot's sub-range
@@ -1565,7 +1577,7 @@ hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_diff_m, dim3(a.num_slots), dim3(kMThreads), 0, s, a);
+  hipLaunchKernelGGL(k_diff_m, dim3(a.num_slots * kMSplit), dim3(kMThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -260,7 +260,8 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
     slots += d.tile_cap;
     chunks += (d.num_nodes + kNodeChunk - 1) / kNodeChunk;
   }
-  if (slots > 0xFFFFFFF0ull) return err(FDY_E_FORMAT, "archive too large (diff tiles exceed 2^32)");
+  // The member pass launches 1024 threads per tile, and a launch holds fewer than 2^32 threads.
+  if (slots >= (1ull << 22)) return err(FDY_E_FORMAT, "archive too large (more than 2^22 diff tiles, 128 GiB of params)");
   a->total_nodes = nodes;
   a->total_cap = words;
   a->num_slots = (uint32_t)slots;
