@@ -1086,8 +1086,8 @@ constexpr uint32_t kMThreads = kSubsPerSlot * 64 / kMSplit;
 static_assert(kSubsPerSlot % kMSplit == 0, "whole sub-ranges per workgroup");
 constexpr uint32_t kSlots = 2;  // searches per batch in the overflowed-template path
 
-// At most 64 VGPRs (eight waves per SIMD where LDS allows).
-__global__ __launch_bounds__(kMThreads, 8) void k_diff_m(RestoreArgs a) {
+// Five waves per SIMD: the node window in LDS allows no more.
+__global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
   constexpr uint32_t J = kMWords;
   __shared__ NodeDesc s_nd[kDiffWindow];
   const uint32_t tid = threadIdx.x, lane = tid & 63;

@@ -21,6 +21,7 @@
 #include "cugraph.h"
 #include "json_min.h"
 #include "kernels.h"
+#include "writer.h"
 
 namespace fdy {
 
@@ -409,17 +410,52 @@ const char* fdy_version(void) { return "foundry-mi355x restore 0.1 (gfx950)"; }
 int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads, fdy_archive** out) {
   if (!paths || !out || n == 0) return err(FDY_E_INVALID, "need at least one path and an output pointer");
   *out = nullptr;
+  const uint32_t threads = std::min(num_threads ? num_threads : 4u, n);
   std::vector<std::string> names(n);
   std::vector<uint64_t> sizes(n), off(n);
-  uint64_t at = 0;
-  for (uint32_t i = 0; i < n; ++i) {
-    std::string p = paths[i] ? paths[i] : "";
+  std::vector<std::vector<uint8_t>> converted(n);  // graphs read from their JSON document
+  std::vector<std::string> errs(n);
+  std::vector<int> codes(n, FDY_OK);
+  // Which file holds each graph: the .cugraph if it opens with a v1 header
+  // (csrc/BinaryGraphIO.cpp:710-737), else the JSON document at the path
+  // (csrc/CUDAGraphParallel.cpp:1606-1617), converted as save_binary would.
+  parallel_for(n, threads, [&](uint32_t i) {
+    const std::string path = paths[i] ? paths[i] : "";
+    std::string p = path;
     if (p.size() >= 5 && p.compare(p.size() - 5, 5, ".json") == 0) p = p.substr(0, p.size() - 5) + ".cugraph";
     struct stat st;
-    if (p.empty() || stat(p.c_str(), &st) != 0 || !S_ISREG(st.st_mode))
-      return err(FDY_E_IO, "cannot open " + (p.empty() ? std::string("<null path>") : p));
-    names[i] = p;
-    sizes[i] = (uint64_t)st.st_size;
+    if (!p.empty() && stat(p.c_str(), &st) == 0 && S_ISREG(st.st_mode) && (uint64_t)st.st_size >= sizeof(fdy_file_header)) {
+      fdy_file_header h;
+      FILE* f = std::fopen(p.c_str(), "rb");
+      const bool ok = f && std::fread(&h, 1, sizeof h, f) == sizeof h && std::memcmp(h.magic, "CUGRAPH", 8) == 0 &&
+                      h.version == FDY_FORMAT_VERSION;
+      if (f) std::fclose(f);
+      if (ok) {
+        names[i] = p;
+        sizes[i] = (uint64_t)st.st_size;
+        return;
+      }
+    }
+    names[i] = path;
+    std::string text;
+    FILE* f = path.empty() ? nullptr : std::fopen(path.c_str(), "rb");
+    if (!f) {
+      codes[i] = FDY_E_IO;
+      errs[i] = "cannot open " + (p.empty() ? std::string("<null path>") : p) + (p == path ? "" : " or " + path);
+      return;
+    }
+    char buf[1 << 16];
+    size_t got;
+    while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, got);
+    std::fclose(f);
+    codes[i] = fdy::cugraph_from_json(text.data(), text.size(), converted[i], errs[i]);
+    if (codes[i] == FDY_OK) sizes[i] = converted[i].size();
+    else errs[i] = path + ": " + errs[i];
+  });
+  for (uint32_t i = 0; i < n; ++i)
+    if (codes[i] != FDY_OK) return err(codes[i], errs[i]);
+  uint64_t at = 0;
+  for (uint32_t i = 0; i < n; ++i) {
     off[i] = at;
     at = align_up(at + sizes[i], 256);
   }
@@ -430,9 +466,13 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
   HostStage stage;
   int rc = stage.alloc(at ? at : 256);
   if (rc) return rc;
-  std::vector<std::string> errs(n);
   // Phase 1a: parallel reads (csrc/CUDAGraphParallel.cpp:1583-1620), straight into the staging buffer.
-  parallel_for(n, std::min(num_threads ? num_threads : 4u, n), [&](uint32_t i) {
+  parallel_for(n, threads, [&](uint32_t i) {
+    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
+    if (!converted[i].empty() || sizes[i] == 0) {
+      if (sizes[i]) std::memcpy(stage.p + off[i], converted[i].data(), sizes[i]);
+      return;
+    }
     FILE* f = std::fopen(names[i].c_str(), "rb");
     if (!f) {
       errs[i] = "cannot open";
@@ -441,7 +481,6 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
     size_t got = std::fread(stage.p + off[i], 1, sizes[i], f);
     std::fclose(f);
     if (got != sizes[i]) errs[i] = "short read";
-    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
   });
   for (uint32_t i = 0; i < n; ++i)
     if (!errs[i].empty()) return err(FDY_E_IO, names[i] + ": " + errs[i]);
@@ -536,6 +575,34 @@ int fdy_archive_set_groups(fdy_archive* a, const uint32_t* template_of) {
   FDY_HIP(hipSetDevice(a->device));
   FDY_HIP(hipMemcpy(a->explicit_tmpl.p, template_of, 4ull * a->G, hipMemcpyHostToDevice));
   a->use_explicit = true;
+  return FDY_OK;
+}
+
+int fdy_cugraph_from_json(const char* json, uint64_t len, uint8_t* out, uint64_t cap, uint64_t* size_out) {
+  if (!json && len) return err(FDY_E_INVALID, "null document");
+  if (!size_out) return err(FDY_E_INVALID, "need size_out");
+  std::vector<uint8_t> img;
+  std::string why;
+  const int rc = fdy::cugraph_from_json(json ? json : "", len, img, why);
+  if (rc) return err(rc, why);
+  *size_out = img.size();
+  if (!out || cap < img.size())
+    return err(FDY_E_CAPACITY, "archive needs " + std::to_string(img.size()) + " bytes, buffer holds " + std::to_string(out ? cap : 0));
+  std::memcpy(out, img.data(), img.size());
+  return FDY_OK;
+}
+
+int fdy_cugraph_save_binary(const char* bin_path, const char* json, uint64_t len) {
+  if (!bin_path) return err(FDY_E_INVALID, "null path");
+  if (!json && len) return err(FDY_E_INVALID, "null document");
+  std::vector<uint8_t> img;
+  std::string why;
+  const int rc = fdy::cugraph_from_json(json ? json : "", len, img, why);
+  if (rc) return err(rc, why);
+  FILE* f = std::fopen(bin_path, "wb");
+  if (!f) return err(FDY_E_IO, std::string("Failed to write binary graph: ") + bin_path);
+  const bool ok = std::fwrite(img.data(), 1, img.size(), f) == img.size();
+  if (std::fclose(f) != 0 || !ok) return err(FDY_E_IO, std::string("Failed to write binary graph: ") + bin_path);
   return FDY_OK;
 }
 

@@ -7,6 +7,7 @@ hipStream_t integer, or None for the null stream.
 from __future__ import annotations
 
 import ctypes as C
+import sys
 from typing import Sequence
 
 import numpy as np
@@ -260,6 +261,38 @@ class RelocPlan:
 
 def version() -> str:
     return restore_lib().fdy_version().decode()
+
+
+def cugraph_from_json(text) -> bytes:
+    """The .cugraph archive CUDAGraph::save_binary writes for one graph's JSON
+    document (csrc/BinaryGraphIO.cpp:15-371); no device needed."""
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    n = C.c_uint64()
+    rc = restore_lib().fdy_cugraph_from_json(data, len(data), None, 0, C.byref(n))
+    if rc != -8:  # FDY_E_CAPACITY: the size is known
+        check(rc)
+    buf = (C.c_uint8 * max(1, n.value))()
+    check(restore_lib().fdy_cugraph_from_json(data, len(data), buf, n.value, C.byref(n)))
+    return bytes(buf)[: n.value]
+
+
+def cugraph_path(json_path: str) -> str:
+    """The archive path CUDAGraph::save writes beside a graph's JSON
+    (csrc/CUDAGraph.cpp:1494-1500): ".json" replaced, else ".cugraph" appended."""
+    return json_path[:-5] + ".cugraph" if json_path.endswith(".json") else json_path + ".cugraph"
+
+
+def save_binary(bin_path: str, text) -> None:
+    """CUDAGraph::save_binary (csrc/BinaryGraphIO.cpp:15-371): write the archive
+    of one graph's JSON document to bin_path.  As there, a file that cannot
+    be written prints a warning and returns; a document that cannot be
+    serialised raises."""
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    rc = restore_lib().fdy_cugraph_save_binary(bin_path.encode(), data, len(data))
+    if rc == -2:  # FDY_E_IO
+        print(f"[foundry] WARNING: Failed to write binary graph: {bin_path}", file=sys.stderr)
+        return
+    check(rc)
 
 
 def manifest_groups(text, names: Sequence[str]):

@@ -96,10 +96,31 @@ const char* fdy_last_error(void);
 const char* fdy_version(void);
 
 /* Open `n` archives given by path.  A path ending in ".json" names the
- * sibling ".cugraph" (csrc/CUDAGraphParallel.cpp:1591-1594).  Files are read
- * on min(num_threads, n) host threads (csrc/CUDAGraphParallel.cpp:1553,1584),
- * validated, and copied to HBM in one transfer.  Replaces Phase 1a. */
+ * sibling ".cugraph" (csrc/CUDAGraphParallel.cpp:1591-1594).  Where that
+ * file is missing, shorter than a header or not a v1 header, the graph is
+ * read from the JSON document at the path itself, as the reference then
+ * parses it (1606-1617), converted with fdy_cugraph_from_json.  Files are
+ * read on min(num_threads, n) host threads (csrc/CUDAGraphParallel.cpp:
+ * 1553,1584), validated, and copied to HBM in one transfer.  Replaces
+ * Phase 1a. */
 int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads, fdy_archive** out);
+
+/* The .cugraph v1 archive of one graph's JSON document (the object
+ * CUDAGraph::save builds, csrc/CUDAGraph.cpp:1389-1491), byte for byte as
+ * CUDAGraph::save_binary writes it (csrc/BinaryGraphIO.cpp:15-371).
+ * *size_out receives the archive size; with out NULL or cap below that size
+ * the call returns FDY_E_CAPACITY and writes nothing.  A document the
+ * reference cannot serialise (a required member missing, a value of the
+ * wrong type or out of its field's range, an unreadable value_hex pair) is
+ * FDY_E_FORMAT, as are duplicate keys; a non-integer number inside
+ * allocator_events or output_tensors is FDY_E_UNSUPPORTED.  No device
+ * needed. */
+int fdy_cugraph_from_json(const char* json, uint64_t len, uint8_t* out, uint64_t cap, uint64_t* size_out);
+/* fdy_cugraph_from_json into the file bin_path (CUDAGraph::save_binary;
+ * CUDAGraph::save names it after the .json path, csrc/CUDAGraph.cpp:
+ * 1494-1501).  FDY_E_IO when the file cannot be written, where the
+ * reference prints a warning and returns. */
+int fdy_cugraph_save_binary(const char* bin_path, const char* json, uint64_t len);
 
 /* Same, from archive images already in host memory. */
 int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes, uint32_t n,

@@ -33,6 +33,8 @@ class Kernel:
     shmem: int = 0
     cluster: tuple | None = None                 # per-node cluster dims
     cooperative: int | None = None
+    func_attrs: tuple = (0, -1, 0, 0, 0, 0)      # max dyn shmem, carveout, sched pref, required cluster w/h/d
+    kna_ints: tuple | None = None                # (sched, cooperative, priority, mem sync domain) as stored
     type = 0
 
 
@@ -93,10 +95,10 @@ def _kernel_arm(k: Kernel, name_off: int, pio: int) -> bytes:
     arm = struct.pack("<7I", *k.block, *k.grid, k.shmem)
     arm += struct.pack("<Q", k.binary_hash)
     arm += struct.pack("<II", name_off, len(k.name))
-    arm += struct.pack("<6i", 0, -1, 0, 0, 0, 0)                 # func attrs, no required cluster
+    arm += struct.pack("<6i", *k.func_attrs)
     arm += struct.pack("<4I", kna, *cl)
     arm += struct.pack("<3I", 0, 0, 0)
-    arm += struct.pack("<4i", -1, coop, -1, -1)
+    arm += struct.pack("<4i", *(k.kna_ints if k.kna_ints is not None else (-1, coop, -1, -1)))
     arm += struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
     return arm, npar, aoff, asize
 
@@ -115,7 +117,7 @@ FLAG_ALLOC_EVENTS, FLAG_OUTPUT_TENSORS = 4, 8
 
 
 def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: bytes = b"",
-          output_tensors: bytes = b"") -> bytes:
+          output_tensors: bytes = b"", common_ints=(-1, -1, -1, -1)) -> bytes:
     """Archive bytes for `nodes` (Kernel/Memset/...); deps are (from_id, to_id).
     alloc_events / output_tensors are the JSON texts of those sections."""
     ids = list(node_ids) if node_ids is not None else list(range(len(nodes)))
@@ -159,7 +161,7 @@ def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: byte
     common = b""
     if common_cluster is not None:
         common = struct.pack("<4I", KNA_CLUSTER_DIM, *common_cluster) + struct.pack("<3I", 0, 0, 0)
-        common += struct.pack("<4i", -1, -1, -1, -1) + struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
+        common += struct.pack("<4i", *common_ints) + struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
     secs = [strings, b"".join(entries), b"".join(struct.pack("<II", *d) for d in deps),
             b"".join(struct.pack("<II", *p) for p in pidx), pdata, arg_data, common, b"", alloc_events,
             output_tensors, saved_key(nodes)]
