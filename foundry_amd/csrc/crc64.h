@@ -108,32 +108,28 @@ __host__ __device__ inline uint64_t nibble_mul(const uint64_t (*tab)[16], uint64
   return r;
 }
 
-// Levels of the block combine tree: level k joins runs of 2^k records, so
-// its multiplier is x^(8 * S * 2^k); levels 0-5 run inside a wave, 6-9
-// across the waves of a 1024-thread block, and level 10 joins 1024-record
-// chunks.
-constexpr int kTreeLevels = 11;
-
 // Records per node-pass chunk, and the multiplier of record i's raw CRC in
 // its chunk's CRC: x^(8 * 16 * (kPosRecords - 1 - i)) mod P.
 constexpr int kPosRecords = 256;
 
+// Lanes of a byte-stream chunk (64 bytes each), and the multiplier of lane
+// i's raw CRC in its chunk's CRC: x^(8 * 64 * (kPosLanes - 1 - i)) mod P.
+constexpr int kPosLanes = 1024;
+
 struct CrcConsts {
   SliceTables slice;
-  NibbleTable rec16[kTreeLevels];  // S = 16-byte records (node records)
-  NibbleTable rec64[kTreeLevels];  // S = 64-byte records (byte streams, 8 words per lane)
+  NibbleTable chunk64;             // x^(8 * 64 * kPosLanes): joins 64 KB byte-stream chunks
   X2nTable x2n;
   uint64_t pos16[kPosRecords];
+  uint64_t pos64[kPosLanes];
 };
 
 inline void make_crc_consts(CrcConsts* c) {
   c->slice = make_slice_tables();
   c->x2n = make_x2n_table();
-  for (int k = 0; k < kTreeLevels; ++k) {
-    c->rec16[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)16 << k, 3));
-    c->rec64[k] = make_nibble_table(x2n_mod(c->x2n.v, (uint64_t)64 << k, 3));
-  }
+  c->chunk64 = make_nibble_table(x2n_mod(c->x2n.v, 64ull * kPosLanes, 3));
   for (int i = 0; i < kPosRecords; ++i) c->pos16[i] = x2n_mod(c->x2n.v, 16ull * (kPosRecords - 1 - i), 3);
+  for (int i = 0; i < kPosLanes; ++i) c->pos64[i] = x2n_mod(c->x2n.v, 64ull * (kPosLanes - 1 - i), 3);
 }
 
 // Finish a raw CRC of an L-byte stream: crc = raw ^ (~0 * x^(8L)) ^ ~0.

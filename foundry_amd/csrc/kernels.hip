@@ -35,9 +35,8 @@ namespace {
 
 constexpr uint32_t kHashThreads = 1024;
 constexpr uint32_t kNodeThreads = 1024;
-constexpr int kChunkLevel = 10;  // combine level joining 1024-record chunks (log2 of the block size)
-static_assert((1u << kChunkLevel) == kHashThreads && kHashThreads == kNodeThreads, "chunk level");
-constexpr uint32_t kGroupThreads = 1024;
+constexpr uint32_t kGroupWaves = 4;  // graphs per workgroup in k_group
+constexpr uint32_t kGroupSteps = 8;  // 64-candidate steps whose loads are issued together
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
 constexpr uint32_t kRelocBatch = 4;  // words searched in lockstep (8 and 2 measured no faster)
@@ -51,43 +50,6 @@ __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
 }
 
 __device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
-
-// Copy the slice tables and one family of combine multipliers into LDS.
-// `levels` combine levels are staged (log2 of the block size suffices
-// unless chunks of a block's records are joined too).
-__device__ void stage_crc_tables(const CrcConsts* cc, bool rec16, uint64_t (*slice)[256],
-                                 uint64_t (*nib)[16][16], uint32_t levels = kTreeLevels) {
-  stage_words(&slice[0][0], &cc->slice.t[0][0], 8 * 256);
-  stage_words(&nib[0][0][0], rec16 ? &cc->rec16[0].t[0][0] : &cc->rec64[0].t[0][0], levels * 256);
-  __syncthreads();
-}
-
-// Join the raw CRCs of blockDim.x consecutive records (one per thread, in
-// thread order; blockDim.x a power of two) into the raw CRC of the whole
-// run: a shuffle tree inside each wave, then one across the waves.  Valid
-// in thread 0.
-__device__ uint64_t block_crc_combine(uint64_t z, const uint64_t (*nib)[16][16], uint64_t* s_wave) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-#pragma unroll
-  for (int k = 0; k < 6; ++k) {
-    uint64_t o = shfl_down64(z, 1 << k);
-    uint64_t m = nibble_mul(nib[k], z) ^ o;
-    if ((lane & ((2u << k) - 1)) == 0) z = m;
-  }
-  if (lane == 0) s_wave[wave] = z;
-  __syncthreads();
-  uint64_t r = 0;
-  if (wave == 0) {
-    r = lane < nw ? s_wave[lane] : 0;
-    for (uint32_t k = 0; (1u << k) < nw; ++k) {
-      uint64_t o = shfl_down64(r, 1 << k);
-      uint64_t m = nibble_mul(nib[6 + k], r) ^ o;
-      if ((lane & ((2u << k) - 1)) == 0) r = m;
-    }
-  }
-  __syncthreads();
-  return r;
-}
 
 // XOR of two values over the block (blockDim.x a multiple of 64); valid in
 // thread 0.
@@ -127,17 +89,36 @@ __device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b
   return (w0 >> (8 * sh)) | (word(q + 1) << (64 - 8 * sh));
 }
 
+// XOR of one value over the block (blockDim.x a multiple of 64); valid in
+// thread 0.
+__device__ uint64_t block_xor(uint64_t x, uint64_t* s_wave) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
+  if (lane == 0) s_wave[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (uint32_t w = 1; w < nw; ++w) x ^= s_wave[w];
+  __syncthreads();
+  return x;
+}
+
 // CRC-64/XZ of an L-byte stream.  Each lane absorbs 64 consecutive bytes
-// (eight slicing steps), lanes are joined by the combine tree for 64-byte
-// records, and the stream is front-padded with zeros to whole 64 KB chunks
+// (eight slicing steps); lane i's raw CRC times x^(8*64*(1023-i)) is its
+// share of the 64 KB chunk's raw CRC (crc(A || B) = crc(A) * x^(8|B|) xor
+// crc(B)), XOR-joined over the block; chunks are joined by the 64 KB
+// multiplier.  The stream is front-padded with zeros to whole chunks
 // (leading zeros leave a zero-initialised register at zero; `fin`, the
 // stream's finishing term, adds the effect of the all-ones initial value).
 __device__ uint64_t block_crc_bytes(const uint8_t* p, uint64_t L, const uint64_t (*slice)[256],
-                                    const uint64_t (*nib)[16][16], uint64_t fin, uint64_t* s_wave) {
+                                    const uint64_t (*chunk_mul)[16], const uint64_t* pos64, uint64_t fin,
+                                    uint64_t* s_wave) {
   constexpr uint64_t kLane = 64;
   constexpr uint64_t kChunk = kHashThreads * kLane;
+  static_assert(kHashThreads == kPosLanes, "one position multiplier per lane");
   const uint64_t pad = (kChunk - L % kChunk) % kChunk;
   const uint64_t nchunks = (L + pad) / kChunk;
+  const uint64_t m = pos64[threadIdx.x];
   uint64_t acc = 0;
   for (uint64_t c = 0; c < nchunks; ++c) {
     const int64_t b0 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad;
@@ -147,76 +128,61 @@ __device__ uint64_t block_crc_bytes(const uint8_t* p, uint64_t L, const uint64_t
     uint64_t z = 0;
 #pragma unroll
     for (uint32_t q = 0; q < kLane / 8; ++q) z = crc_slice8(slice, z, v[q]);
-    z = block_crc_combine(z, nib, s_wave);
-    if (threadIdx.x == 0) acc = nibble_mul(nib[kChunkLevel], acc) ^ z;
+    z = block_xor(z ? gf2_mulmod(m, z) : 0, s_wave);
+    if (threadIdx.x == 0) acc = nibble_mul(chunk_mul, acc) ^ z;
   }
   return threadIdx.x == 0 ? acc ^ fin : 0;
 }
 
 __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
   __shared__ uint64_t s_slice[8][256];
-  __shared__ uint64_t s_nib[kTreeLevels][16][16];
+  __shared__ uint64_t s_chunk[16][16];  // multiplier x^(8 * 64 KB): joins chunks
   __shared__ uint64_t s_wave[kHashThreads / 64];
-  stage_crc_tables(a.cc, false, s_slice, s_nib);
+  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  stage_words(&s_chunk[0][0], &a.cc->chunk64.t[0][0], 256);
+  __syncthreads();
   const uint32_t g = blockIdx.x;
   const DevGraph& G = a.graphs[g];
   uint64_t dk = block_crc_bytes(a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY],
-                                s_slice, s_nib, G.crc_fin[0], s_wave);
-  uint64_t de = block_crc_bytes(a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, s_slice, s_nib,
-                                G.crc_fin[1], s_wave);
+                                s_slice, s_chunk, a.cc->pos64, G.crc_fin[0], s_wave);
+  uint64_t de = block_crc_bytes(a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, s_slice, s_chunk,
+                                a.cc->pos64, G.crc_fin[1], s_wave);
   if (threadIdx.x == 0) {
     a.digests[4ull * g + 0] = dk;
     a.digests[4ull * g + 1] = de;
   }
 }
 
-__global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
-  const uint32_t G = a.num_graphs;
-  if (threadIdx.x == 0) *a.tslot_count = 0;  // the node pass lists template slots here
+// template_of[i] = the lowest j <= i whose saved key has the same digest
+// and length (the byte-exact check follows in the node pass): one wave per
+// graph, its lanes testing 64 candidates per step and eight steps' loads in
+// flight at once.
+__global__ __launch_bounds__(64 * kGroupWaves) void k_group(RestoreArgs a) {
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t i = blockIdx.x * kGroupWaves + (threadIdx.x >> 6);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *a.tslot_count = 0;  // the node pass lists template slots here
+  if (i >= a.num_graphs) return;
   if (a.explicit_template) {
-    for (uint32_t i = threadIdx.x; i < G; i += kGroupThreads) a.template_of[i] = a.explicit_template[i];
+    if (lane == 0) a.template_of[i] = a.explicit_template[i];
     return;
   }
-  constexpr uint32_t kChunk = 2048;
-  __shared__ uint64_t s_d[kChunk];
-  __shared__ uint64_t s_l[kChunk];
-  for (uint32_t i0 = 0; i0 < G; i0 += kGroupThreads) {
-    const uint32_t i = i0 + threadIdx.x;
-    const uint32_t lim = min(i0 + kGroupThreads, G);
-    uint64_t di = 0, li = 0;
-    if (i < G) {
-      di = a.digests[4ull * i];
-      li = a.graphs[i].sec_size[FDY_SEC_TOPOLOGY_KEY];
-    }
-    uint32_t found = 0xFFFFFFFFu;
-    for (uint32_t base = 0; base < lim; base += kChunk) {
-      __syncthreads();
-      const uint32_t end = min(base + kChunk, lim);
-      for (uint32_t j = base + threadIdx.x; j < end; j += kGroupThreads) {
-        s_d[j - base] = a.digests[4ull * j];
-        s_l[j - base] = a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY];
-      }
-      __syncthreads();
-      if (i < G && found == 0xFFFFFFFFu) {
-        // Eight candidates per step with independent LDS loads (indices
-        // clamped inside the chunk), first match wins.
-        const uint32_t stop = min(end, i + 1);
-        for (uint32_t j = base; j < stop && found == 0xFFFFFFFFu; j += 8) {
-          uint64_t d[8], l[8];
+  const uint64_t di = a.digests[4ull * i];
+  const uint64_t li = a.graphs[i].sec_size[FDY_SEC_TOPOLOGY_KEY];
+  uint32_t found = i;
+  for (uint32_t base = 0; base < i && found == i; base += 64 * kGroupSteps) {
+    bool m[kGroupSteps];
 #pragma unroll
-          for (uint32_t q = 0; q < 8; ++q) {
-            const uint32_t jj = min(j + q, stop - 1) - base;
-            d[q] = s_d[jj];
-            l[q] = s_l[jj];
-          }
-#pragma unroll
-          for (uint32_t q = 0; q < 8; ++q)
-            if (found == 0xFFFFFFFFu && j + q < stop && d[q] == di && l[q] == li) found = j + q;
-        }
-      }
+    for (uint32_t k = 0; k < kGroupSteps; ++k) {
+      const uint32_t j = base + 64 * k + lane;
+      m[k] = j < i && a.digests[4ull * j] == di && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == li;
     }
-    if (i < G) a.template_of[i] = found;
+#pragma unroll
+    for (uint32_t k = 0; k < kGroupSteps; ++k) {
+      const uint64_t mk = __ballot(m[k]);
+      if (found == i && mk) found = base + 64 * k + (uint32_t)__ffsll((long long)mk) - 1;
+    }
   }
+  if (lane == 0) a.template_of[i] = found;
 }
 
 // ---- node pass ----------------------------------------------------------
@@ -1555,7 +1521,8 @@ hipError_t launch_hash(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(kGroupThreads), 0, s, a);
+  hipLaunchKernelGGL(k_group, dim3(std::max(1u, (a.num_graphs + kGroupWaves - 1) / kGroupWaves)), dim3(64 * kGroupWaves),
+                     0, s, a);
   return hipGetLastError();
 }
 
