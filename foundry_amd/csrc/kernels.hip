@@ -21,8 +21,8 @@
 //             store, and per-wave ballot compaction of the differing words
 //             into override record regions.
 //   k_count   override records per graph.
-//   k_scan    prefix of the per-graph record counts -> override offsets.
-//   k_compact record regions -> the dense override array in canonical order,
+//   k_compact record regions -> the dense override array in canonical order
+//             (offsets from the per-graph record counts),
 //             completing each record's node and template word index.
 //   k_switch  override scatter for one graph switch.
 //   k_mirror  dirty nodes' live words -> a group graph's host mirror.
@@ -1281,7 +1281,7 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
 }
 
 // Records per graph: the sum of its slots' sub-range counts (one workgroup
-// per graph).
+// per graph; a global atomic per slot instead measured slower).
 constexpr uint32_t kCountThreads = 256;
 
 __global__ __launch_bounds__(kCountThreads) void k_count(RestoreArgs a) {
@@ -1302,46 +1302,17 @@ __global__ __launch_bounds__(kCountThreads) void k_count(RestoreArgs a) {
   }
 }
 
-// Exclusive prefix of the per-graph record counts (one workgroup): the
-// per-graph override offsets.
-__global__ __launch_bounds__(1024) void k_scan(RestoreArgs a) {
-  __shared__ uint64_t s_w[16];
-  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t n = a.num_graphs;
-  const uint32_t per = (n + 1023) / 1024;
-  const uint32_t lo = min(n, tid * per), hi = min(n, lo + per);
-  uint64_t sum = 0;
-  for (uint32_t i = lo; i < hi; ++i) sum += a.graph_count[i];
-  uint64_t x = sum;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint32_t ylo = __shfl_up((uint32_t)x, (unsigned)d, 64), yhi = __shfl_up((uint32_t)(x >> 32), (unsigned)d, 64);
-    if (lane >= (uint32_t)d) x += ((uint64_t)yhi << 32) | ylo;
-  }
-  if (lane == 63) s_w[wave] = x;
-  __syncthreads();
-  uint64_t before = 0, total = 0;
-  for (uint32_t w = 0; w < 16; ++w) {
-    if (w < wave) before += s_w[w];
-    total += s_w[w];
-  }
-  uint64_t run = before + x - sum;
-  for (uint32_t i = lo; i < hi; ++i) {
-    a.ovr_off[i] = run;
-    run += a.graph_count[i];
-  }
-  if (tid == 1023) a.ovr_off[n] = total;
-}
-
 // Move each slot's records to their place in the dense array, completing
 // them: the node holding the word (searched in the slot's node window) and
-// the word's index in the template's image.  A slot's records follow those
-// of the graph's earlier slots; one pass covers all its sub-ranges.
+// the word's index in the template's image.  A slot's records follow every
+// earlier graph's and its graph's earlier slots'; one pass covers all its
+// sub-ranges.  A graph's first slot also writes the graph's override offset
+// (and the last graph's, the total).
 constexpr uint32_t kCompactThreads = 256;
 
 __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   __shared__ NodeDesc s_nd[kDiffWindow];
-  __shared__ uint32_t s_part[kCompactThreads / 64];
+  __shared__ uint64_t s_part[kCompactThreads / 64];
   __shared__ uint32_t s_sub[kSubsPerSlot + 1];  // exclusive prefix of the slot's sub-range counts
   const uint32_t slot = blockIdx.x, tid = threadIdx.x;
   const uint32_t* cnt = a.sub_count + (uint64_t)slot * kSubsPerSlot;
@@ -1355,20 +1326,28 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   }
   __syncthreads();
   const uint32_t total = s_sub[kSubsPerSlot];
-  if (total == 0) return;  // uniform over the workgroup
   const SlotDesc sd = load_slot(a.slot_desc + slot);
   const DevGraph& G = a.graphs[sd.graph];
-  uint32_t part = 0;
+  const bool first = slot == G.tile_base;
+  if (total == 0 && !first) return;  // uniform over the workgroup
+  uint64_t part = 0;
+  for (uint32_t j = tid; j < sd.graph; j += kCompactThreads) part += a.graph_count[j];
   for (uint64_t i = (uint64_t)G.tile_base * kSubsPerSlot + tid; i < (uint64_t)slot * kSubsPerSlot; i += kCompactThreads)
     part += a.sub_count[i];
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) part += __shfl_down(part, (unsigned)d, 64);
+  for (int d = 32; d >= 1; d >>= 1) part += shfl_down64(part, d);
   if ((tid & 63) == 0) s_part[tid >> 6] = part;
-  const NodeWindow nw = stage_window(a, G, slot, s_nd);
   __syncthreads();
-  uint64_t base = a.ovr_off[sd.graph];
+  uint64_t base = 0;
 #pragma unroll
   for (uint32_t w = 0; w < kCompactThreads / 64; ++w) base += s_part[w];
+  if (first && tid == 0) {
+    a.ovr_off[sd.graph] = base;
+    if (sd.graph + 1 == a.num_graphs) a.ovr_off[a.num_graphs] = base + a.graph_count[sd.graph];
+  }
+  if (total == 0) return;
+  const NodeWindow nw = stage_window(a, G, slot, s_nd);
+  __syncthreads();
   const Candidate* regions = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
   for (uint32_t i = tid; i < total; i += kCompactThreads) {
     uint32_t q = 0;  // the sub-range holding record i
@@ -1556,10 +1535,7 @@ hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
 
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_count, dim3(a.num_graphs), dim3(kCountThreads), 0, s, a);
-  hipError_t e0 = hipGetLastError();
-  if (e0 != hipSuccess) return e0;
-  hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, a);
-  hipError_t e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(kCompactThreads), 0, s, a);
   return hipGetLastError();
