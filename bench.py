@@ -397,6 +397,13 @@ def main():
             "sample": f"{what}: oracle restore (digests, grouping, param extraction, relocation, diff), "
                       f"median of {len(times)} runs ({1e3 * med:.1f} ms per restore)",
         }
+        # The same restore on one thread (the oracle's scalar form).
+        t1 = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.Restore(images, iv, threads=1)
+            t1.append(time.perf_counter() - t0)
+        cpu["oracle_T1_ms"] = round(1e3 * statistics.median(t1), 1)
         if n_cpu == G:
             with tempfile.TemporaryDirectory() as d:
                 paths = s.write_dir(d)

@@ -1157,8 +1157,8 @@ __global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
   // Store what is settled; the rest (whole words to relocate, and partial
   // words that differ from the template's) are candidates.  Every valid
   // word is stored, a whole word to relocate as its raw value until
-  // k_diff_s writes the relocated one: a tile's lines are then written
-  // whole, which spares HBM the read-modify-write of partly written lines.
+  // k_diff_s writes the relocated one, so each word takes one
+  // unconditional store.
   uint32_t cand = 0, creloc = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
