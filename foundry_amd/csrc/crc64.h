@@ -116,12 +116,19 @@ constexpr int kPosRecords = 256;
 // i's raw CRC in its chunk's CRC: x^(8 * 64 * (kPosLanes - 1 - i)) mod P.
 constexpr int kPosLanes = 1024;
 
+// Node-pass chunks a graph's chunk CRCs can be shifted past by table: for
+// k < kChunkShifts, chunk_shift[k][i] = x^(8 * 16 * kPosRecords * k) * x^i
+// mod P, so one wave forms a chunk's shifted CRC with one multiple per lane
+// (lane i takes it when bit x^i of the CRC is set) and an XOR reduction.
+constexpr int kChunkShifts = 256;
+
 struct CrcConsts {
   SliceTables slice;
   NibbleTable chunk64;             // x^(8 * 64 * kPosLanes): joins 64 KB byte-stream chunks
   X2nTable x2n;
   uint64_t pos16[kPosRecords];
   uint64_t pos64[kPosLanes];
+  uint64_t chunk_shift[kChunkShifts][64];
 };
 
 inline void make_crc_consts(CrcConsts* c) {
@@ -130,6 +137,13 @@ inline void make_crc_consts(CrcConsts* c) {
   c->chunk64 = make_nibble_table(x2n_mod(c->x2n.v, 64ull * kPosLanes, 3));
   for (int i = 0; i < kPosRecords; ++i) c->pos16[i] = x2n_mod(c->x2n.v, 16ull * (kPosRecords - 1 - i), 3);
   for (int i = 0; i < kPosLanes; ++i) c->pos64[i] = x2n_mod(c->x2n.v, 64ull * (kPosLanes - 1 - i), 3);
+  for (int k = 0; k < kChunkShifts; ++k) {
+    uint64_t m = x2n_mod(c->x2n.v, 16ull * kPosRecords * k, 3);
+    for (int i = 0; i < 64; ++i) {
+      c->chunk_shift[k][i] = m;
+      m = (m >> 1) ^ (kCrcPolyRefl & (0 - (m & 1)));  // times x
+    }
+  }
 }
 
 // Finish a raw CRC of an L-byte stream: crc = raw ^ (~0 * x^(8L)) ^ ~0.

@@ -741,17 +741,29 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   }
 
   // Chunk results: each chunk's raw CRC times x^(8 * bytes after it),
-  // XOR-joined; param bytes and status bits.
+  // XOR-joined; param bytes and status bits.  One wave per chunk: lane i
+  // holds the multiplier times x^i and keeps it where the CRC has x^i
+  // (bit 63 - i); the wave's XOR is the product.
+  static_assert(kNodeChunk == kPosRecords, "chunk shift tables are built for kPosRecords records per chunk");
   const uint32_t nch = (N + kNodeChunk - 1) / kNodeChunk;
   uint64_t xt = 0, xk = 0, pb = 0;
   uint32_t st = 0;
-  for (uint32_t c = threadIdx.x; c < nch; c += kNodeThreads) {
+  for (uint32_t c = wave; c < nch; c += kNodeThreads / 64) {
     const NodeChunk ch = a.chunks[Gg.chunk_base + c];
-    const uint64_t m = x2n_mod(a.cc->x2n.v, 16ull * kNodeChunk * (nch - 1 - c), 3);
-    xt ^= gf2_mulmod(m, ch.crc_type);
-    xk ^= gf2_mulmod(m, ch.crc_kent);
-    pb += ch.pbytes;
-    st |= ch.status;
+    const uint32_t k = nch - 1 - c;
+    if (k < (uint32_t)kChunkShifts) {
+      const uint64_t mi = a.cc->chunk_shift[k][lane];
+      if ((ch.crc_type >> (63 - lane)) & 1) xt ^= mi;
+      if ((ch.crc_kent >> (63 - lane)) & 1) xk ^= mi;
+    } else if (lane == 0) {
+      const uint64_t m = x2n_mod(a.cc->x2n.v, 16ull * kNodeChunk * k, 3);
+      xt ^= gf2_mulmod(m, ch.crc_type);
+      xk ^= gf2_mulmod(m, ch.crc_kent);
+    }
+    if (lane == 0) {
+      pb += ch.pbytes;
+      st |= ch.status;
+    }
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {

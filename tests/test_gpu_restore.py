@@ -108,3 +108,13 @@ def test_switch_sequence(cuda):
         tw, gw = ref.node_words(t), ref.node_words(cur)
         for n in np.nonzero((flags & NODE_LAYOUT) == 0)[0]:
             np.testing.assert_array_equal(words[tw[n]:tw[n + 1]], img[gw[n]:gw[n + 1]])
+
+
+def test_graph_longer_than_the_chunk_shift_table(cuda):
+    # 66,000 nodes = 258 chunks of 256: the first two chunks of each graph are
+    # shifted past the node-type and kernel-entry streams without the table.
+    p = synth.preset(1, num_graphs=3, nodes_per_graph=66000)
+    _print_case("long-graphs", p)
+    s = synth.SynthArchive(p)
+    arch, ref = gpu_and_oracle(s)
+    assert_restore_parity(arch, ref)
