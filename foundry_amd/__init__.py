@@ -23,6 +23,7 @@ _API_NAMES = {
     "free_preallocated_region",
     "get_current_alloc_offset",
     "graph",
+    "install_as_foundry",
     "load_cuda_modules_and_libraries",
     "parse_size",
     "preallocate_region",

@@ -204,6 +204,8 @@ _GRAPH_SIGS = {
     "fdy_group_graph_reset_all": (C.c_int, [_vp, _vp, C.POINTER(SelectStats)]),
     "fdy_group_graph_launch": (C.c_int, [_vp, _vp]),
     "fdy_group_graph_info_get": (C.c_int, [_vp, C.POINTER(GroupGraphInfo)]),
+    "fdy_group_graph_handles": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),
+    "fdy_group_graph_debug_dot": (C.c_int, [_vp, C.c_char_p]),
 }
 _SIGS.update(_GRAPH_SIGS)
 

@@ -145,12 +145,56 @@ def save_graph_manifest(archive_dir: str) -> None:
           f"{on_demand} on-demand, {stripped} stripped)", file=sys.stderr)
 
 
+def install_as_foundry() -> None:
+    """Register this build under the reference's module names, so code that
+    imports `foundry`, `foundry.graph`, `foundry.ops` or
+    `foundry.allocation_region` (the vLLM and SGLang integrations do:
+    python/foundry/integration/vllm/graph_ops.py:36) runs on it unchanged.
+
+    `foundry` is assembled as python/foundry/__init__.py:3-17 assembles it:
+    the allocation-region helpers, then CUDAGraph / graph /
+    save_graph_manifest from `foundry.graph`, then every name of `foundry.ops`
+    -- which, coming last, leaves `foundry.CUDAGraph` naming the ops class
+    while `foundry.graph.CUDAGraph` is the subclass whose load() returns the
+    graph alone when it has no outputs.  Refused if another `foundry` is
+    already imported."""
+    import types
+
+    current = sys.modules.get("foundry")
+    if current is not None and not getattr(current, "__foundry_amd__", False):
+        raise RuntimeError("a different `foundry` package is already imported")
+    region = types.ModuleType("foundry.allocation_region")
+    for name in ("allocation_region", "free_preallocated_region", "get_current_alloc_offset", "parse_size",
+                 "preallocate_region", "resume_allocation_region", "set_current_alloc_offset",
+                 "set_allocation_region", "stop_allocation_region"):
+        setattr(region, name, globals()[name])
+    gmod = types.ModuleType("foundry.graph")
+    for name in ("CUDAGraph", "graph", "save_graph_manifest"):
+        setattr(gmod, name, globals()[name])
+    pkg = types.ModuleType("foundry", "The reference's `foundry` package names, on the MI355X restore path.")
+    pkg.__path__ = []
+    pkg.__foundry_amd__ = True
+    for mod in (region, gmod):
+        for name, value in vars(mod).items():
+            if not name.startswith("_"):
+                setattr(pkg, name, value)
+    for name in ops.__all__:
+        setattr(pkg, name, getattr(ops, name))
+    pkg.__all__ = ["CUDAGraph", "allocation_region", "free_preallocated_region", "get_current_alloc_offset",
+                   "graph", "parse_size", "preallocate_region", "resume_allocation_region", "save_graph_manifest",
+                   "set_current_alloc_offset"]
+    pkg.ops = ops
+    sys.modules.update({"foundry": pkg, "foundry.graph": gmod, "foundry.ops": ops,
+                        "foundry.allocation_region": region})
+
+
 __all__ = [
     "CUDAGraph",
     "allocation_region",
     "free_preallocated_region",
     "get_current_alloc_offset",
     "graph",
+    "install_as_foundry",
     "load_cuda_modules_and_libraries",
     "parse_size",
     "preallocate_region",

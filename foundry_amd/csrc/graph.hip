@@ -893,6 +893,20 @@ int fdy_group_graph_launch(fdy_group_graph* gg, void* stream) {
   return FDY_OK;
 }
 
+int fdy_group_graph_handles(fdy_group_graph* gg, void** graph, void** exec) {
+  if (!gg) return err(FDY_E_INVALID, "null group graph");
+  if (graph) *graph = gg->graph;
+  if (exec) *exec = gg->exec;
+  return FDY_OK;
+}
+
+int fdy_group_graph_debug_dot(fdy_group_graph* gg, const char* path) {
+  if (!gg || !path) return err(FDY_E_INVALID, "need a group graph and a path");
+  FDY_HIP(hipSetDevice(gg->a->device));
+  FDY_HIP(hipGraphDebugDotPrint(gg->graph, path, hipGraphDebugDotFlagsVerbose));
+  return FDY_OK;
+}
+
 int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out) {
   if (!gg || !out) return err(FDY_E_INVALID, "need a group graph and an output pointer");
   *out = gg->info;

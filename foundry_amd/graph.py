@@ -90,6 +90,16 @@ class GroupGraph:
         self.launch(stream)
         return st
 
+    def handles(self) -> tuple[int, int]:
+        """(hipGraph_t, hipGraphExec_t) as integers; owned by this group graph."""
+        g, e = C.c_void_p(), C.c_void_p()
+        check(restore_lib().fdy_group_graph_handles(self._h, C.byref(g), C.byref(e)))
+        return g.value or 0, e.value or 0
+
+    def debug_dot(self, path: str) -> None:
+        """hipGraphDebugDotPrint (verbose) of the group's graph to `path`."""
+        check(restore_lib().fdy_group_graph_debug_dot(self._h, path.encode()))
+
     def info(self) -> dict:
         i = GroupGraphInfo()
         check(restore_lib().fdy_group_graph_info_get(self._h, C.byref(i)))

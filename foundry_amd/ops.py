@@ -8,8 +8,11 @@ reference binds in csrc/binding.cpp:13-338 for the LOAD side:
                       get_ / set_current_alloc_offset        (csrc/binding.cpp:16-69)
   code objects        load_cuda_modules_and_libraries(dir)   (csrc/binding.cpp:81-86)
   graphs              CUDAGraph.load / start_graph_builds / finish_graph_loads /
-                      finish_one_graph_load, CUDAGraph.replay / reset
-                                                             (csrc/binding.cpp:118-338)
+                      finish_one_graph_load, CUDAGraph.replay / reset / pool /
+                      debug_dump / raw_cuda_graph(_exec)     (csrc/binding.cpp:118-338)
+  the rest            graph_pool_handle, get_graph_ptr, preallocate_cublas_workspaces,
+                      and the fatbin / NVSHMEM switches, which have nothing to act
+                      on for gfx950 code objects              (csrc/binding.cpp:14-90)
 
 Underneath: the archives are opened and restored on the GPU in one pass
 (`Archive`), each topology group gets one hipGraph exec (`GroupGraph`), and a
@@ -27,6 +30,7 @@ import ctypes as C
 import json
 import os
 import threading
+import warnings
 from typing import Sequence
 
 import numpy as np
@@ -133,6 +137,51 @@ def region_free(ptr: int) -> None:
 
 def graph_pool_handle():
     return torch.cuda.graph_pool_handle()
+
+
+def get_graph_ptr(graph) -> int:
+    """csrc/binding.cpp:16-19: an integer naming the graph object for hook
+    integration (here the Python object's identity)."""
+    return id(graph)
+
+
+# ---- switches of the reference's fatbin / NVSHMEM machinery ------------------
+# csrc/binding.cpp:54-81.  They configure NVIDIA fatbin packing and NVSHMEM
+# module initialisation, neither of which exists for gfx950 code objects:
+# the setters record the value and change nothing, initialisation finds no
+# modules to initialise, and packing (a SAVE-side step) is refused.
+
+_flags = {"pack_fatbins_on_exit": False, "skip_fatbin_processing": False, "nvshmem_auto_init": True}
+
+
+def set_pack_fatbins_on_exit(enabled: bool) -> None:
+    _flags["pack_fatbins_on_exit"] = bool(enabled)
+
+
+def set_skip_fatbin_processing(enabled: bool) -> None:
+    _flags["skip_fatbin_processing"] = bool(enabled)
+
+
+def set_nvshmem_auto_init(enabled: bool) -> None:
+    _flags["nvshmem_auto_init"] = bool(enabled)
+
+
+def init_nvshmem_for_loaded_modules() -> int:
+    """Modules initialised for NVSHMEM: none among gfx950 code objects."""
+    return 0
+
+
+def pack_fatbins_to_folder(folder_path: str) -> None:
+    raise NotImplementedError("packing the captured code objects is part of SAVE, which this build does not provide")
+
+
+def preallocate_cublas_workspaces() -> None:
+    """csrc/binding.cpp:88-90: create the BLAS handle and workspace of the
+    current stream before graphs that use them are loaded (hipBLAS/hipBLASLt
+    through torch: one small product on the current stream)."""
+    torch.cuda.current_blas_handle()
+    a = torch.ones((8, 8), device="cuda", dtype=torch.bfloat16)
+    (a @ a).sum().item()
 
 
 # ---- code objects -----------------------------------------------------------
@@ -274,7 +323,8 @@ class PendingGraphLoads:
     """The split-load state (include/CUDAGraphInternal.h:13-28): the restored
     archive, one group graph per topology group, and one CUDAGraph per graph."""
 
-    def __init__(self, json_paths: Sequence[str], num_threads: int, stream):
+    def __init__(self, json_paths: Sequence[str], num_threads: int, stream, pool=None):
+        self.pool = pool if pool is not None else (0, 0)
         self.json_paths = list(json_paths)
         self.names = [os.path.basename(p) for p in self.json_paths]
         self.archive = Archive.open(self.json_paths, max(1, int(num_threads)))
@@ -349,8 +399,48 @@ class CUDAGraph:
         self._pending = None
         self._index = -1
 
+    def register_generator_state(self, generator) -> None:
+        raise NotImplementedError("graph capture is not part of this build (LOAD path only)")
+
+    def _group(self) -> GroupGraph:
+        if self._pending is None:
+            raise RuntimeError("this CUDAGraph holds no restored graph")
+        return self._pending.group_graph(self._index)
+
+    def pool(self):
+        """csrc/CUDAGraph.cpp:611-614: the graph's memory pool id.  Restored
+        graphs allocate nothing through a pool of their own, so this is the
+        pool the load was given (or the default (0, 0))."""
+        if self._pending is None:
+            raise RuntimeError("Called CUDAGraph::pool() without a preceding successful capture.")
+        return self._pending.pool
+
+    def enable_debug_mode(self) -> None:
+        self._debug = True
+
+    def debug_dump(self, debug_path: str) -> None:
+        """csrc/CUDAGraph.cpp:515-532: write the graph as DOT (the group's
+        hipGraph, which this graph's params are selected into first) when
+        debug mode or keep_graph is on; otherwise warn, as the reference does."""
+        if not (getattr(self, "_debug", False) or self.keep_graph):
+            warnings.warn("CUDA Graphs debug not enabled, set with [graph].enable_debug_mode()")
+            return
+        gg = self._group()
+        gg.select(self._index, torch.cuda.current_stream())
+        gg.debug_dot(debug_path)
+
+    def raw_cuda_graph(self) -> int:
+        """csrc/CUDAGraph.cpp:537-544: the hipGraph_t (the topology group's, shared
+        by its members) as an integer; like the reference, only with keep_graph."""
+        if not self.keep_graph:
+            raise RuntimeError("You cannot access the raw cudaGraph_t instance unless CUDAGraph was initialized "
+                               "with keep_graph=true")
+        return self._group().handles()[0]
+
     def raw_cuda_graph_exec(self) -> int:
-        raise NotImplementedError("the exec belongs to the topology group (GroupGraph)")
+        """csrc/CUDAGraph.cpp:546-551: the hipGraphExec_t (the topology group's,
+        shared by its members; replay() selects this graph's params into it)."""
+        return self._group().handles()[1]
 
     @property
     def index(self) -> int:
@@ -367,7 +457,7 @@ class CUDAGraph:
         if not json_paths:
             raise RuntimeError("start_graph_builds: no graphs given")
         torch.cuda.synchronize()
-        return PendingGraphLoads(json_paths, num_threads, torch.cuda.current_stream())
+        return PendingGraphLoads(json_paths, num_threads, torch.cuda.current_stream(), pool)
 
     @staticmethod
     def finish_one_graph_load(pending: PendingGraphLoads, index: int):
@@ -397,3 +487,26 @@ class CUDAGraph:
         """One graph: (graph, outputs or None) (csrc/CUDAGraph.cpp:1520-1560)."""
         pending = CUDAGraph.start_graph_builds([json_path], pool, 1)
         return CUDAGraph.finish_one_graph_load(pending, 0)
+
+
+# The names csrc/binding.cpp binds (a star import of this module gives these).
+__all__ = [
+    "CUDAGraph",
+    "PendingGraphLoads",
+    "free_preallocated_region",
+    "get_current_alloc_offset",
+    "get_graph_ptr",
+    "graph_pool_handle",
+    "init_nvshmem_for_loaded_modules",
+    "load_cuda_modules_and_libraries",
+    "pack_fatbins_to_folder",
+    "preallocate_cublas_workspaces",
+    "preallocate_region",
+    "resume_allocation_region",
+    "set_allocation_region",
+    "set_current_alloc_offset",
+    "set_nvshmem_auto_init",
+    "set_pack_fatbins_on_exit",
+    "set_skip_fatbin_processing",
+    "stop_allocation_region",
+]

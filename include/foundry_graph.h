@@ -117,6 +117,13 @@ int fdy_group_graph_reset_all(fdy_group_graph* gg, void* stream, fdy_select_stat
 /* Launch the exec on `stream` (csrc/CUDAGraph.cpp:476-477). */
 int fdy_group_graph_launch(fdy_group_graph* gg, void* stream);
 int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out);
+/* The group graph's hipGraph_t and hipGraphExec_t (either pointer may be
+ * NULL), owned by the group graph: CUDAGraph::raw_cuda_graph and
+ * raw_cuda_graph_exec (csrc/CUDAGraph.cpp:537-551) of every member. */
+int fdy_group_graph_handles(fdy_group_graph* gg, void** graph, void** exec);
+/* hipGraphDebugDotPrint of the group graph, verbose, to `path`
+ * (CUDAGraph::debug_dump, csrc/CUDAGraph.cpp:515-532). */
+int fdy_group_graph_debug_dot(fdy_group_graph* gg, const char* path);
 
 #ifdef __cplusplus
 } /* extern "C" */

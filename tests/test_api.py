@@ -77,3 +77,68 @@ def test_save_graph_manifest_needs_every_key(tmp_path):
     (tmp_path / "graph_0.json").write_text(json.dumps({"topology_key": ""}))
     api.save_graph_manifest(str(tmp_path))
     assert not os.path.exists(tmp_path / "graph_manifest.json")
+
+
+# python/foundry/__init__.py names, and those tests/test_imports.py:41-54 pins.
+REFERENCE_PUBLIC_NAMES = ["CUDAGraph", "allocation_region", "free_preallocated_region", "get_current_alloc_offset",
+                          "graph", "parse_size", "preallocate_region", "resume_allocation_region",
+                          "save_graph_manifest", "set_current_alloc_offset", "set_allocation_region",
+                          "stop_allocation_region"]
+# csrc/binding.cpp:14-90 module functions.
+REFERENCE_OPS_FUNCTIONS = ["graph_pool_handle", "get_graph_ptr", "set_allocation_region", "stop_allocation_region",
+                           "resume_allocation_region", "preallocate_region", "free_preallocated_region",
+                           "get_current_alloc_offset", "set_current_alloc_offset", "set_pack_fatbins_on_exit",
+                           "set_skip_fatbin_processing", "set_nvshmem_auto_init", "init_nvshmem_for_loaded_modules",
+                           "pack_fatbins_to_folder", "load_cuda_modules_and_libraries",
+                           "preallocate_cublas_workspaces"]
+REFERENCE_CUDAGRAPH_METHODS = ["capture_begin", "capture_end", "register_generator_state", "replay", "reset", "pool",
+                               "debug_dump", "enable_debug_mode", "raw_cuda_graph", "raw_cuda_graph_exec", "save",
+                               "load", "start_graph_builds", "finish_graph_loads", "finish_one_graph_load"]
+
+
+def test_ops_surface_complete():
+    from foundry_amd import ops
+
+    assert sorted(set(REFERENCE_OPS_FUNCTIONS) - set(ops.__all__)) == []
+    for name in REFERENCE_OPS_FUNCTIONS:
+        assert callable(getattr(ops, name)), name
+    for name in REFERENCE_CUDAGRAPH_METHODS:
+        assert callable(getattr(ops.CUDAGraph, name)), name
+    assert ops.init_nvshmem_for_loaded_modules() == 0
+    ops.set_skip_fatbin_processing(True)
+    ops.set_pack_fatbins_on_exit(False)
+    ops.set_nvshmem_auto_init(False)
+    with pytest.raises(NotImplementedError):
+        ops.pack_fatbins_to_folder("/nonexistent")
+    g = ops.CUDAGraph()
+    with pytest.raises(RuntimeError, match="keep_graph"):
+        g.raw_cuda_graph()
+    with pytest.raises(RuntimeError):
+        g.pool()
+
+
+def test_install_as_foundry():
+    import importlib
+    import sys
+
+    from foundry_amd import api, ops
+
+    saved = {k: sys.modules.pop(k) for k in list(sys.modules) if k == "foundry" or k.startswith("foundry.")}
+    try:
+        api.install_as_foundry()
+        foundry = importlib.import_module("foundry")
+        assert [n for n in REFERENCE_PUBLIC_NAMES if not hasattr(foundry, n)] == []
+        from foundry.graph import CUDAGraph as GraphCUDAGraph
+        from foundry.ops import set_skip_fatbin_processing
+
+        assert GraphCUDAGraph is api.CUDAGraph
+        assert foundry.CUDAGraph is ops.CUDAGraph  # the star import of foundry.ops comes last
+        assert set_skip_fatbin_processing is ops.set_skip_fatbin_processing
+        assert foundry.graph is api.graph  # the class shadows the submodule, as in the reference
+        region = importlib.import_module("foundry.allocation_region")
+        assert region.parse_size("16MB") == 16 << 20
+        api.install_as_foundry()  # idempotent
+    finally:
+        for k in [k for k in sys.modules if k == "foundry" or k.startswith("foundry.")]:
+            del sys.modules[k]
+        sys.modules.update(saved)

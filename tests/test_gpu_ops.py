@@ -105,3 +105,22 @@ def test_finish_one_out_of_range(loaded):
     pending, _ = loaded
     with pytest.raises(IndexError):
         api.CUDAGraph.finish_one_graph_load(pending, 4)
+
+
+def test_debug_dump_and_raw_handles(loaded, tmp_path):
+    pending, _ = loaded
+    results = api.CUDAGraph.finish_graph_loads(pending)
+    g1 = results[1][0]
+    with pytest.warns(UserWarning, match="debug not enabled"):
+        g1.debug_dump(str(tmp_path / "no.dot"))
+    assert not (tmp_path / "no.dot").exists()
+    g1.enable_debug_mode()
+    g1.debug_dump(str(tmp_path / "g1.dot"))
+    dot = (tmp_path / "g1.dot").read_text()
+    assert "digraph" in dot
+    exec_handle = g1.raw_cuda_graph_exec()
+    assert exec_handle != 0 and exec_handle == results[2][0].raw_cuda_graph_exec()  # one exec per group
+    with pytest.raises(RuntimeError, match="keep_graph"):
+        g1.raw_cuda_graph()
+    assert g1.pool() == (0, 0)
+    assert ops.get_graph_ptr(g1) == ops.get_graph_ptr(g1) != ops.get_graph_ptr(results[2][0])
