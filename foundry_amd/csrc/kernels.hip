@@ -1067,6 +1067,8 @@ constexpr uint32_t kSlots = 2;  // searches per batch in the overflowed-template
 // Five waves per SIMD: the node window in LDS allows no more.
 __global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
   constexpr uint32_t J = kMWords;
+  static_assert((kMThreads / 64) * kSubWords * sizeof(Candidate) <= kDiffWindow * sizeof(NodeDesc),
+                "each wave's candidates fit its part of the node window");
   __shared__ NodeDesc s_nd[kDiffWindow];
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t slot = blockIdx.x / kMSplit, part = blockIdx.x % kMSplit;
@@ -1187,8 +1189,15 @@ __global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
       creloc |= 1u << j;
     }
   }
+  // The candidates are compacted into the wave's part of the node window's
+  // LDS (free once the loads are done), then copied out as whole 8-byte
+  // words: one or two wide stores per wave where storing each word's
+  // candidate directly took two narrow stores per word (measured: 91 -> 86 us
+  // for the 256-graph decode-style archive).
   Candidate* out = a.cand + ((uint64_t)slot * kSubsPerSlot + wave) * kSubWords;
   const uint64_t lt = (1ull << lane) - 1;
+  if (!flat) __syncthreads();  // every wave of the workgroup is done with the node window
+  Candidate* stage = reinterpret_cast<Candidate*>(s_nd) + (tid >> 6) * kSubWords;
   uint32_t run = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
@@ -1199,9 +1208,16 @@ __global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
       c.flags = (((creloc >> j) & 1) ? kCandReloc : 0u) | (((cmp >> j) & 1) ? kCandCompare : 0u);
       c.raw = fg[j];
       c.tval = fr[j];
-      out[run + (uint32_t)__popcll(mk & lt)] = c;
+      stage[run + (uint32_t)__popcll(mk & lt)] = c;
     }
     run += (uint32_t)__popcll(mk);
+  }
+  {
+    static_assert(sizeof(Candidate) % 8 == 0, "candidates copy as 8-byte words");
+    constexpr uint32_t kCandWords = sizeof(Candidate) / 8;
+    const uint64_t* src = reinterpret_cast<const uint64_t*>(stage);
+    uint64_t* dst = reinterpret_cast<uint64_t*>(out);
+    for (uint32_t i = lane; i < run * kCandWords; i += 64) dst[i] = src[i];
   }
   if (lane == 0) sub_count[wave] = run;
   if (tid == 0 && part == 0 && (sd.flags & kSlotFirst)) {
