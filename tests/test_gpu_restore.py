@@ -8,6 +8,10 @@ every output.
 import numpy as np
 import pytest
 
+import oracle
+from foundry_amd._lib import FoundryError
+from foundry_amd.restore import Archive
+
 from foundry_amd import synth
 from foundry_amd._lib import NODE_DESC, NODE_LAYOUT, RELOC_INCLUSIVE
 from tests.parity import assert_live_matches, assert_restore_parity, gpu_and_oracle
@@ -118,3 +122,64 @@ def test_graph_longer_than_the_chunk_shift_table(cuda):
     s = synth.SynthArchive(p)
     arch, ref = gpu_and_oracle(s)
     assert_restore_parity(arch, ref)
+
+
+def _two_node_graph(values, overlap: bool) -> bytes:
+    """Node 0: four 64-byte params; node 1: ten 64-byte params.  With
+    `overlap`, node 1's ten entries all cover the same 64 bytes (the
+    param-data section holds only those), so the param image (112 words)
+    exceeds the capacity the sections allow (56 words) and the graph is
+    flagged OVERFLOW; node 0's 32 words lie within the capacity."""
+    import struct
+
+    import cugraph_writer as W
+
+    p0 = [b"".join(W.le(v) for v in values[8 * i:8 * i + 8]) for i in range(4)]
+    p1 = [b"".join(W.le(v) for v in values[32 + 8 * i:40 + 8 * i]) for i in range(10)]
+    if overlap:
+        p1 = [p1[0]] + [b""] * 9
+    img = bytearray(W.write([W.Kernel("k0", 0x1234, params=p0), W.Kernel("k1", 0x1234, params=p1)]))
+    if overlap:
+        pidx_off = struct.unpack_from("<Q", img, 64 + 24 * 3 + 8)[0]
+        for j in range(10):
+            struct.pack_into("<II", img, pidx_off + 8 * (4 + j), 256, 64)
+    return bytes(img)
+
+
+def test_members_of_an_overflowed_template(cuda):
+    # The template's image overflows its capacity (OVERFLOW): it keeps no
+    # image, its node past the capacity is not compared (its members keep no
+    # records there, and switches to them are refused), and its node within
+    # the capacity is compared against template words the member pass
+    # relocates itself -- those records must equal the oracle's.
+    print("[case] overflowed template with two members", flush=True)
+    base, size = 0x7F0000000000, 1 << 32
+    rng = np.random.default_rng(7)
+    tvals = [int(base + 16 * rng.integers(0, size // 16)) if i % 3 == 0 else int(rng.integers(0, 1 << 62))
+             for i in range(112)]
+    images = [_two_node_graph(tvals, True)]
+    for m in range(2):
+        vals = list(tvals[:32]) + list(tvals[32:40]) * 10  # what the template's params read
+        for i in range(0, 112, 5 + m):  # some words differ, some of them pointers
+            vals[i] = int(base + 16 * rng.integers(0, size // 16)) if i % 2 else int(rng.integers(0, 1 << 62))
+        images.append(_two_node_graph(vals, False))
+    lo = np.array([base, base + (1 << 31)], dtype=np.uint64)
+    hi = np.array([base + (1 << 31), base + size], dtype=np.uint64)
+    nlo = np.array([0x7E0000000000, 0x7D0000000000], dtype=np.uint64)
+    arch = Archive.from_images(images)
+    arch.set_relocation(lo, hi, nlo)
+    arch.restore()
+    ref = oracle.Restore(images, (lo, hi, nlo))
+    status = arch.status()
+    assert status[0] & 0x20 and status[0] & 0x02, status  # OVERFLOW, reported as BAD_PARAMS
+    assert not (status[1] & 0x22) and not (status[2] & 0x22), status
+    assert arch.groups().tolist() == [0, 0, 0]
+    assert arch.param_image(0).size == 0
+    for g in (1, 2):
+        np.testing.assert_array_equal(arch.param_image(g), ref.param_image(g), err_msg=f"param image g={g}")
+        a, b = arch.overrides(g), ref.overrides(g)
+        b0 = b[b["node"] == 0]
+        assert len(b0) > 0 and len(b) > len(b0)
+        np.testing.assert_array_equal(a, b0, err_msg=f"node-0 overrides g={g}")
+        with pytest.raises(FoundryError):
+            arch.switch(g)
