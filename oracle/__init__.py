@@ -194,8 +194,9 @@ class Restore:
         self.n = len(images)
 
     def __del__(self):
-        if getattr(self, "_h", None):
-            lib().orc_free(self._h)
+        # At interpreter exit the module's globals may already be gone.
+        if getattr(self, "_h", None) and _lib is not None:
+            _lib.orc_free(self._h)
             self._h = None
 
     def digests(self) -> np.ndarray:
