@@ -1288,9 +1288,12 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
       }
     }
     reloc_batch<K>(a.reloc, raw, res, m);
+    // The member pass stored each candidate's raw word; only the words the
+    // relocation moved are stored again (a scattered 8-byte store costs a
+    // partly written line).
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k)
-      if ((m >> k) & 1) img_out[word[k]] = res[k];
+      if (((m >> k) & 1) && res[k] != raw[k]) img_out[word[k]] = res[k];
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
       const bool d = (fl[k] & kCandCompare) && res[k] != tval[k];
