@@ -42,6 +42,7 @@ struct RestoreArgs {
   Candidate* cand;            // per (slot, sub-range): kSubWords candidates, then as many records
   uint32_t* sub_count;        // records per (slot, sub-range)
   uint32_t* graph_count;      // records per graph
+  uint32_t* slot_off;         // per slot: its records' offset among its graph's
   RelocDev reloc;
 };
 

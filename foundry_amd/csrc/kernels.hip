@@ -51,27 +51,6 @@ __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
 
 __device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
 
-// XOR of two values over the block (blockDim.x a multiple of 64); valid in
-// thread 0.
-__device__ void block_xor2(uint64_t& x, uint64_t& y, uint64_t (*s_wave)[2]) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    x ^= shfl_down64(x, d);
-    y ^= shfl_down64(y, d);
-  }
-  if (lane == 0) {
-    s_wave[wave][0] = x;
-    s_wave[wave][1] = y;
-  }
-  __syncthreads();
-  if (threadIdx.x == 0)
-    for (uint32_t w = 1; w < nw; ++w) {
-      x ^= s_wave[w][0];
-      y ^= s_wave[w][1];
-    }
-}
-
 // The 8 bytes [b0, b0+8) of the L-byte stream at p (8-aligned), with bytes
 // outside [0, L) read as zero.
 __device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b0) {
@@ -525,7 +504,9 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
   __shared__ uint64_t s_slice[8][256];
   __shared__ uint64_t s_str[2][kStrStage / 8];
   __shared__ uint64_t s_common[2][7];
-  __shared__ uint64_t s_wave[kNodeChunk / 64][2];
+  // The chunk's node-type and kernel-entry records, eight to a row; the odd
+  // row length keeps a half-wave's reads of eight rows apart in the banks.
+  __shared__ uint64_t s_rec[2][kNodeChunk / 8][17];
   __shared__ uint32_t s_diff;
   __shared__ uint32_t s_sum[2][kNodeChunk / 64];
   __shared__ uint64_t s_pb[kNodeChunk / 64];
@@ -664,15 +645,12 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
     if (is_t) a.live_src[gi] = g;
   }
 
-  // Raw CRC of the chunk's records: record i's raw CRC times x^(8*16*(255-i)),
-  // XOR-joined (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).
-  uint64_t zt = 0, zk = 0;
-  if (valid) {
-    const uint64_t m = a.cc->pos16[tid];
-    zt = gf2_mulmod(m, crc_slice8(slice, crc_slice8(slice, 0, tw0), tw1));
-    zk = gf2_mulmod(m, crc_slice8(slice, crc_slice8(slice, 0, kw0), kw1));
-  }
-  block_xor2(zt, zk, s_wave);
+  // The records go to LDS (zero for the front padding: leading zero records
+  // leave a zero-initialised CRC at zero).
+  s_rec[0][tid >> 3][2 * (tid & 7)] = tw0;
+  s_rec[0][tid >> 3][2 * (tid & 7) + 1] = tw1;
+  s_rec[1][tid >> 3][2 * (tid & 7)] = kw0;
+  s_rec[1][tid >> 3][2 * (tid & 7) + 1] = kw1;
   uint32_t sum_g = words_g, sum_t = words_t;
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
@@ -686,9 +664,27 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
     s_pb[tid >> 6] = pbytes;
   }
   __syncthreads();
+  if (tid >= 64) return;
+  // Raw CRCs of the two record streams, by the first wave: lane l folds the
+  // eight records 8q..8q+7 (q = l % 32) of stream l / 32 into one raw CRC
+  // and moves it into place, times x^(8*16*(255-(8q+7))); each half-wave
+  // XOR-joins its 32 shares (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).
+  // One position multiply per lane of one wave, where a multiply per record
+  // would cost every wave two.
+  static_assert(kNodeChunk == 8 * 32, "eight records per lane, 32 lanes per stream");
+  uint64_t z = 0;
+  {
+    const uint32_t st = tid >> 5, q = tid & 31;
+#pragma unroll
+    for (uint32_t r = 0; r < 16; ++r) z = crc_slice8(slice, z, s_rec[st][q][r]);
+    z = z ? gf2_mulmod(a.cc->pos16[8 * q + 7], z) : 0;
+#pragma unroll
+    for (int d = 16; d >= 1; d >>= 1) z ^= shfl_down64(z, d);  // lanes 0 and 32 hold their half's XOR
+  }
+  const uint64_t zk = ((uint64_t)__shfl((uint32_t)(z >> 32), 32, 64) << 32) | __shfl((uint32_t)z, 32, 64);
   if (tid == 0) {
     NodeChunk c;
-    c.crc_type = zt;
+    c.crc_type = z;
     c.crc_kent = zk;
     c.pbytes = 0;
     uint64_t wg = 0, wt = 0;
@@ -1315,35 +1311,85 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
 // per graph; a global atomic per slot instead measured slower).
 constexpr uint32_t kCountThreads = 256;
 
+// Exclusive prefix sum of u64 values over the block (blockDim.x a multiple
+// of 64, at most 4096); *total gets the sum.
+__device__ uint64_t block_excl_scan64(uint64_t v, uint64_t* s_tmp, uint64_t* total) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint64_t y = ((uint64_t)shfl_up32((uint32_t)(x >> 32), d) << 32) | shfl_up32((uint32_t)x, d);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_tmp[wave] = x;
+  __syncthreads();
+  uint64_t before = 0, sum = 0;
+  for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
+    const uint64_t t = s_tmp[w];
+    if (w < wave) before += t;
+    sum += t;
+  }
+  __syncthreads();
+  *total = sum;
+  return before + x - v;
+}
+
+// Records per graph and each slot's offset among its graph's records (an
+// exclusive scan over the graph's slots, one slot per thread), so that the
+// compaction reads its base instead of summing every earlier slot's count.
 __global__ __launch_bounds__(kCountThreads) void k_count(RestoreArgs a) {
-  __shared__ uint32_t s_part[kCountThreads / 64];
+  static_assert(kCountThreads == 256, "block_excl_scan covers 256 values");
+  static_assert(kSubsPerSlot % 4 == 0, "a slot's counts are read 16 bytes at a time");
+  __shared__ uint32_t s_tmp[kCountThreads / 64];
   const uint32_t g = blockIdx.x, tid = threadIdx.x;
   const DevGraph& G = a.graphs[g];
-  const uint64_t lo = (uint64_t)G.tile_base * kSubsPerSlot, hi = lo + (uint64_t)G.tile_cap * kSubsPerSlot;
-  uint32_t part = 0;
-  for (uint64_t i = lo + tid; i < hi; i += kCountThreads) part += a.sub_count[i];
+  uint32_t carry = 0;
+  for (uint32_t k0 = 0; k0 < G.tile_cap; k0 += kCountThreads) {
+    const uint32_t k = k0 + tid;
+    uint32_t n = 0;
+    if (k < G.tile_cap) {
+      const uint4* c = reinterpret_cast<const uint4*>(a.sub_count + (uint64_t)(G.tile_base + k) * kSubsPerSlot);
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) part += __shfl_down(part, (unsigned)d, 64);
-  if ((tid & 63) == 0) s_part[tid >> 6] = part;
-  __syncthreads();
-  if (tid == 0) {
-    uint32_t total = 0;
-    for (uint32_t w = 0; w < kCountThreads / 64; ++w) total += s_part[w];
-    a.graph_count[g] = total;
+      for (uint32_t q = 0; q < kSubsPerSlot / 4; ++q) {
+        const uint4 v = c[q];
+        n += v.x + v.y + v.z + v.w;
+      }
+    }
+    uint32_t tot;
+    const uint32_t ex = block_excl_scan(n, s_tmp, &tot);
+    if (k < G.tile_cap) a.slot_off[G.tile_base + k] = carry + ex;
+    carry += tot;
   }
+  if (tid == 0) a.graph_count[g] = carry;
+}
+
+// The override offsets: an exclusive scan of the graph counts by one
+// workgroup (a separate launch: a last-workgroup scan inside the count pass
+// needs device-wide fences, whose L2 write-backs measured slower).
+constexpr uint32_t kScanThreads = 1024;
+
+__global__ __launch_bounds__(kScanThreads) void k_scan(RestoreArgs a) {
+  __shared__ uint64_t s_tmp[kScanThreads / 64];
+  uint64_t base = 0;
+  for (uint32_t j0 = 0; j0 < a.num_graphs; j0 += kScanThreads) {
+    const uint32_t j = j0 + threadIdx.x;
+    uint64_t tot;
+    const uint64_t ex = block_excl_scan64(j < a.num_graphs ? a.graph_count[j] : 0, s_tmp, &tot);
+    if (j < a.num_graphs) a.ovr_off[j] = base + ex;
+    base += tot;
+  }
+  if (threadIdx.x == 0) a.ovr_off[a.num_graphs] = base;
 }
 
 // Move each slot's records to their place in the dense array, completing
 // them: the node holding the word (searched in the slot's node window) and
-// the word's index in the template's image.  A slot's records follow every
-// earlier graph's and its graph's earlier slots'; one pass covers all its
-// sub-ranges.  A graph's first slot also writes the graph's override offset
-// (and the last graph's, the total).
+// the word's index in the template's image.  A slot's records start at its
+// graph's override offset plus the slot's offset among the graph's records;
+// one pass covers all its sub-ranges.
 constexpr uint32_t kCompactThreads = 256;
 
 __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   __shared__ NodeDesc s_nd[kDiffWindow];
-  __shared__ uint64_t s_part[kCompactThreads / 64];
   __shared__ uint32_t s_sub[kSubsPerSlot + 1];  // exclusive prefix of the slot's sub-range counts
   const uint32_t slot = blockIdx.x, tid = threadIdx.x;
   const uint32_t* cnt = a.sub_count + (uint64_t)slot * kSubsPerSlot;
@@ -1357,26 +1403,10 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   }
   __syncthreads();
   const uint32_t total = s_sub[kSubsPerSlot];
+  if (total == 0) return;  // uniform over the workgroup
   const SlotDesc sd = load_slot(a.slot_desc + slot);
   const DevGraph& G = a.graphs[sd.graph];
-  const bool first = slot == G.tile_base;
-  if (total == 0 && !first) return;  // uniform over the workgroup
-  uint64_t part = 0;
-  for (uint32_t j = tid; j < sd.graph; j += kCompactThreads) part += a.graph_count[j];
-  for (uint64_t i = (uint64_t)G.tile_base * kSubsPerSlot + tid; i < (uint64_t)slot * kSubsPerSlot; i += kCompactThreads)
-    part += a.sub_count[i];
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) part += shfl_down64(part, d);
-  if ((tid & 63) == 0) s_part[tid >> 6] = part;
-  __syncthreads();
-  uint64_t base = 0;
-#pragma unroll
-  for (uint32_t w = 0; w < kCompactThreads / 64; ++w) base += s_part[w];
-  if (first && tid == 0) {
-    a.ovr_off[sd.graph] = base;
-    if (sd.graph + 1 == a.num_graphs) a.ovr_off[a.num_graphs] = base + a.graph_count[sd.graph];
-  }
-  if (total == 0) return;
+  const uint64_t base = a.ovr_off[sd.graph] + a.slot_off[slot];
   const NodeWindow nw = stage_window(a, G, slot, s_nd);
   __syncthreads();
   const Candidate* regions = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
@@ -1566,7 +1596,10 @@ hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
 
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_count, dim3(a.num_graphs), dim3(kCountThreads), 0, s, a);
-  const hipError_t e = hipGetLastError();
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, s, a);
+  e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(kCompactThreads), 0, s, a);
   return hipGetLastError();

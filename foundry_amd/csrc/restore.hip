@@ -298,6 +298,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->tslots, 4 * (slots + 1), "template slot list");
   alloc(a->sub_count, 4 * slots * kSubsPerSlot, "record counts");
   alloc(a->graph_count, 4ull * G, "graph record counts");
+  alloc(a->slot_off, 4 * slots, "slot record offsets");
   alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * slots, "candidate and record regions");
   alloc(a->aux, 8 * words, "ragged word sources");
   alloc(a->image, 8 * words, "param images");
@@ -697,6 +698,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.cand = a->cand.as<Candidate>();
   r.sub_count = a->sub_count.as<uint32_t>();
   r.graph_count = a->graph_count.as<uint32_t>();
+  r.slot_off = a->slot_off.as<uint32_t>();
   r.reloc = a->reloc.dev;
   if (a->timing) {
     for (hipEvent_t& e : a->ev)
