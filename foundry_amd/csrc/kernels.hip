@@ -1383,47 +1383,77 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(RestoreArgs a) {
 
 // Move each slot's records to their place in the dense array, completing
 // them: the node holding the word (searched in the slot's node window) and
-// the word's index in the template's image.  A slot's records start at its
-// graph's override offset plus the slot's offset among the graph's records;
-// one pass covers all its sub-ranges.
+// the word's index in the template's image.  The search pass leaves a slot's
+// records at the start of its region in word order, their number in the
+// slot's first sub-range count (the others are zero).  A slot's records
+// start at its graph's override offset plus the slot's offset among the
+// graph's records.  Everything that depends on the slot alone (the count,
+// the first records, the window's bounds) is loaded before what depends on
+// its graph, to keep the chain of dependent loads short.
 constexpr uint32_t kCompactThreads = 256;
+constexpr uint32_t kCompactPre = 2;  // records per thread loaded up front
 
 __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
-  __shared__ NodeDesc s_nd[kDiffWindow];
-  __shared__ uint32_t s_sub[kSubsPerSlot + 1];  // exclusive prefix of the slot's sub-range counts
+  __shared__ uint2 s_gt[kDiffWindow];  // {first graph word, first template word} of the window's nodes
   const uint32_t slot = blockIdx.x, tid = threadIdx.x;
-  const uint32_t* cnt = a.sub_count + (uint64_t)slot * kSubsPerSlot;
-  if (tid == 0) {
-    uint32_t r = 0;
-    for (uint32_t q = 0; q < kSubsPerSlot; ++q) {
-      s_sub[q] = r;
-      r += cnt[q];
-    }
-    s_sub[kSubsPerSlot] = r;
+  const uint32_t total = a.sub_count[(uint64_t)slot * kSubsPerSlot];
+  if (total == 0) return;  // uniform over the workgroup
+  const fdy_override* recs = reinterpret_cast<const fdy_override*>(a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords);
+  fdy_override pre[kCompactPre];
+#pragma unroll
+  for (uint32_t p = 0; p < kCompactPre; ++p) {
+    const uint32_t i = tid + p * kCompactThreads;
+    if (i < total) pre[p] = recs[i];
+  }
+  const SlotDesc sd = load_slot(a.slot_desc + slot);
+  const uint32_t n0 = a.tile_node[slot];
+  const uint32_t off = a.slot_off[slot];
+  const DevGraph& G = a.graphs[sd.graph];
+  const uint32_t k = slot - G.tile_base;
+  const uint32_t N = G.num_nodes;
+  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
+  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
+  const uint32_t nwin = min(kDiffWindow, n_last - n0 + 1);
+  const NodeDesc* nd = a.node_desc + G.node_base;
+  const uint64_t base = a.ovr_off[sd.graph] + off;
+  for (uint32_t i = tid; i < nwin; i += kCompactThreads) {
+    const uint4 v = *reinterpret_cast<const uint4*>(nd + n0 + i);  // gword, nwords, tword, flags
+    s_gt[i] = make_uint2(v.x, v.z);
   }
   __syncthreads();
-  const uint32_t total = s_sub[kSubsPerSlot];
-  if (total == 0) return;  // uniform over the workgroup
-  const SlotDesc sd = load_slot(a.slot_desc + slot);
-  const DevGraph& G = a.graphs[sd.graph];
-  const uint64_t base = a.ovr_off[sd.graph] + a.slot_off[slot];
-  const NodeWindow nw = stage_window(a, G, slot, s_nd);
-  __syncthreads();
-  const Candidate* regions = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
-  for (uint32_t i = tid; i < total; i += kCompactThreads) {
-    uint32_t q = 0;  // the sub-range holding record i
-#pragma unroll
-    for (uint32_t b = kSubsPerSlot / 2; b >= 1; b >>= 1)
-      if (s_sub[q + b] <= i) q += b;
-    fdy_override o = reinterpret_cast<const fdy_override*>(regions + (uint64_t)q * kSubWords)[i - s_sub[q]];
+  auto finish = [&](fdy_override o, uint32_t i) {
     const uint64_t w = o.word;
-    uint32_t node;
-    find_nodes<1>(s_nd, nw, &w, &node);
-    const NodeDesc d = window_desc(s_nd, nw, node);
-    o.word = d.tword + (uint32_t)(w - d.gword);
+    // The last node whose first word is <= w (nodes without words never
+    // match: the node holding w follows them); past a full window the
+    // search continues in global memory.
+    uint32_t lo = 0;
+    for (uint32_t len = nwin; len > 1;) {
+      const uint32_t half = len >> 1;
+      if (s_gt[lo + half].x <= w) lo += half;
+      len -= half;
+    }
+    uint32_t node = n0 + lo, gw = s_gt[lo].x, tw = s_gt[lo].y;
+    if (nwin == kDiffWindow && lo == kDiffWindow - 1 && w >= (uint64_t)nd[node].gword + nd[node].nwords) {
+      uint32_t l2 = node, h2 = N;
+      while (h2 - l2 > 1) {
+        const uint32_t mid = (l2 + h2) >> 1;
+        if (nd[mid].gword <= w) l2 = mid;
+        else h2 = mid;
+      }
+      node = l2;
+      gw = nd[node].gword;
+      tw = nd[node].tword;
+    }
+    o.word = tw + (uint32_t)(w - gw);
     o.node = node;
     a.ovr[base + i] = o;
+  };
+#pragma unroll
+  for (uint32_t p = 0; p < kCompactPre; ++p) {
+    const uint32_t i = tid + p * kCompactThreads;
+    if (i < total) finish(pre[p], i);
   }
+  for (uint32_t i = tid + kCompactPre * kCompactThreads; i < total; i += kCompactThreads) finish(recs[i], i);
 }
 
 // ---- switch --------------------------------------------------------------
