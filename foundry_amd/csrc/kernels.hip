@@ -68,64 +68,93 @@ __device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b
   return (w0 >> (8 * sh)) | (word(q + 1) << (64 - 8 * sh));
 }
 
-// XOR of one value over the block (blockDim.x a multiple of 64); valid in
-// thread 0.
-__device__ uint64_t block_xor(uint64_t x, uint64_t* s_wave) {
+// XOR of two values over the block (blockDim.x a multiple of 64); valid in
+// thread 0.  s_wave is free again when it returns.
+__device__ void block_xor2(uint64_t& x, uint64_t& y, uint64_t (*s_wave)[2]) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
-  if (lane == 0) s_wave[wave] = x;
+  for (int d = 32; d >= 1; d >>= 1) {
+    x ^= shfl_down64(x, d);
+    y ^= shfl_down64(y, d);
+  }
+  if (lane == 0) {
+    s_wave[wave][0] = x;
+    s_wave[wave][1] = y;
+  }
   __syncthreads();
   if (threadIdx.x == 0)
-    for (uint32_t w = 1; w < nw; ++w) x ^= s_wave[w];
+    for (uint32_t w = 1; w < nw; ++w) {
+      x ^= s_wave[w][0];
+      y ^= s_wave[w][1];
+    }
   __syncthreads();
-  return x;
 }
 
-// CRC-64/XZ of an L-byte stream.  Each lane absorbs 64 consecutive bytes
+// One of the two byte streams hashed together by block_crc_bytes2.
+struct HashStream {
+  const uint8_t* p;
+  uint64_t L;
+  uint64_t fin;  // the stream's finishing term
+};
+
+// CRC-64/XZ of two byte streams at once (their loads in flight together, one
+// reduction for both).  Each lane absorbs 64 consecutive bytes of a stream
 // (eight slicing steps); lane i's raw CRC times x^(8*64*(1023-i)) is its
 // share of the 64 KB chunk's raw CRC (crc(A || B) = crc(A) * x^(8|B|) xor
 // crc(B)), XOR-joined over the block; chunks are joined by the 64 KB
-// multiplier.  The stream is front-padded with zeros to whole chunks
-// (leading zeros leave a zero-initialised register at zero; `fin`, the
-// stream's finishing term, adds the effect of the all-ones initial value).
-__device__ uint64_t block_crc_bytes(const uint8_t* p, uint64_t L, const uint64_t (*slice)[256],
-                                    const uint64_t (*chunk_mul)[16], const uint64_t* pos64, uint64_t fin,
-                                    uint64_t* s_wave) {
+// multiplier.  Each stream is front-padded with zeros to whole chunks
+// (leading zeros leave a zero-initialised register at zero; `fin` adds the
+// effect of the all-ones initial value).  Results in thread 0.
+__device__ void block_crc_bytes2(const HashStream& s0, const HashStream& s1, const uint64_t (*slice)[256],
+                                 const uint64_t (*chunk_mul)[16], const uint64_t* pos64, uint64_t (*s_wave)[2],
+                                 uint64_t* out0, uint64_t* out1) {
   constexpr uint64_t kLane = 64;
   constexpr uint64_t kChunk = kHashThreads * kLane;
   static_assert(kHashThreads == kPosLanes, "one position multiplier per lane");
-  const uint64_t pad = (kChunk - L % kChunk) % kChunk;
-  const uint64_t nchunks = (L + pad) / kChunk;
+  const uint64_t pad0 = (kChunk - s0.L % kChunk) % kChunk, pad1 = (kChunk - s1.L % kChunk) % kChunk;
+  const uint64_t n0 = (s0.L + pad0) / kChunk, n1 = (s1.L + pad1) / kChunk;
   const uint64_t m = pos64[threadIdx.x];
-  uint64_t acc = 0;
-  for (uint64_t c = 0; c < nchunks; ++c) {
-    const int64_t b0 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad;
-    uint64_t v[kLane / 8];
+  uint64_t acc0 = 0, acc1 = 0;
+  for (uint64_t c = 0; c < n0 || c < n1; ++c) {
+    const int64_t b0 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad0;
+    const int64_t b1 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad1;
+    uint64_t v0[kLane / 8], v1[kLane / 8];
 #pragma unroll
-    for (uint32_t q = 0; q < kLane / 8; ++q) v[q] = stream_window(p, L, b0 + 8 * q);
-    uint64_t z = 0;
+    for (uint32_t q = 0; q < kLane / 8; ++q) {
+      v0[q] = c < n0 ? stream_window(s0.p, s0.L, b0 + 8 * q) : 0;
+      v1[q] = c < n1 ? stream_window(s1.p, s1.L, b1 + 8 * q) : 0;
+    }
+    uint64_t z0 = 0, z1 = 0;
 #pragma unroll
-    for (uint32_t q = 0; q < kLane / 8; ++q) z = crc_slice8(slice, z, v[q]);
-    z = block_xor(z ? gf2_mulmod(m, z) : 0, s_wave);
-    if (threadIdx.x == 0) acc = nibble_mul(chunk_mul, acc) ^ z;
+    for (uint32_t q = 0; q < kLane / 8; ++q) {
+      z0 = crc_slice8(slice, z0, v0[q]);
+      z1 = crc_slice8(slice, z1, v1[q]);
+    }
+    z0 = z0 ? gf2_mulmod(m, z0) : 0;
+    z1 = z1 ? gf2_mulmod(m, z1) : 0;
+    block_xor2(z0, z1, s_wave);
+    if (threadIdx.x == 0) {
+      if (c < n0) acc0 = nibble_mul(chunk_mul, acc0) ^ z0;
+      if (c < n1) acc1 = nibble_mul(chunk_mul, acc1) ^ z1;
+    }
   }
-  return threadIdx.x == 0 ? acc ^ fin : 0;
+  *out0 = acc0 ^ s0.fin;
+  *out1 = acc1 ^ s1.fin;
 }
 
 __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
   __shared__ uint64_t s_slice[8][256];
   __shared__ uint64_t s_chunk[16][16];  // multiplier x^(8 * 64 KB): joins chunks
-  __shared__ uint64_t s_wave[kHashThreads / 64];
+  __shared__ uint64_t s_wave[kHashThreads / 64][2];
   stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
   stage_words(&s_chunk[0][0], &a.cc->chunk64.t[0][0], 256);
   __syncthreads();
   const uint32_t g = blockIdx.x;
   const DevGraph& G = a.graphs[g];
-  uint64_t dk = block_crc_bytes(a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY],
-                                s_slice, s_chunk, a.cc->pos64, G.crc_fin[0], s_wave);
-  uint64_t de = block_crc_bytes(a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, s_slice, s_chunk,
-                                a.cc->pos64, G.crc_fin[1], s_wave);
+  const HashStream key{a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY], G.crc_fin[0]};
+  const HashStream deps{a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, G.crc_fin[1]};
+  uint64_t dk, de;
+  block_crc_bytes2(key, deps, s_slice, s_chunk, a.cc->pos64, s_wave, &dk, &de);
   if (threadIdx.x == 0) {
     a.digests[4ull * g + 0] = dk;
     a.digests[4ull * g + 1] = de;
@@ -1232,7 +1261,7 @@ __global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
 // its own sub-range region, hence past them; a batch reads all its
 // candidates before writing any record.
 constexpr uint32_t kSThreads = 256;  // four slots per workgroup
-constexpr uint32_t kSBatch = 256;
+constexpr uint32_t kSBatch = 128;  // two per lane: 256 measured slower (fewer waves in flight)
 
 __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
