@@ -124,6 +124,17 @@ def test_graph_longer_than_the_chunk_shift_table(cuda):
     assert_restore_parity(arch, ref)
 
 
+def test_more_graphs_than_a_scan_block(cuda):
+    # 1100 graphs: the override offsets are scanned 1024 graphs at a time, the
+    # second batch continuing from the first one's total.
+    p = synth.preset(1, num_graphs=1100, nodes_per_graph=6, num_groups=5)
+    _print_case("many-graphs", p)
+    s = synth.SynthArchive(p)
+    arch, ref = gpu_and_oracle(s)
+    assert_restore_parity(arch, ref)
+    assert int(np.asarray(arch.override_offsets())[-1]) > 0
+
+
 def _two_node_graph(values, overlap: bool) -> bytes:
     """Node 0: four 64-byte params; node 1: ten 64-byte params.  With
     `overlap`, node 1's ten entries all cover the same 64 bytes (the
