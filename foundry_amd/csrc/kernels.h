@@ -43,9 +43,12 @@ struct RestoreArgs {
   uint32_t* sub_count;        // records per (slot, sub-range)
   uint32_t* graph_count;      // records per graph
   uint32_t* slot_off;         // per slot: its records' offset among its graph's
+  const uint32_t* planes;     // field-major node table: per 256-node chunk, 42 planes of 256 dwords
   RelocDev reloc;
 };
 
+hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
+                         uint32_t* planes, hipStream_t s);
 hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);

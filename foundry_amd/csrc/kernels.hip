@@ -206,14 +206,43 @@ struct Side {
   const uint8_t* pidx; // param entries (per-param style)
 };
 
+// A node entry's fields (byte offsets, multiples of 4).  RawEntry reads the
+// 168 saved bytes in place; PlaneEntry reads the field-major copy of the
+// node table (dword k of every node of a 256-node chunk in one plane), where
+// a wave's read of one field is one coalesced access instead of 64 lines.
+
+struct RawEntry {
+  const uint8_t* e;
+  __device__ uint32_t u32(uint32_t off) const { return f32(e, off); }
+  __device__ uint64_t u64(uint32_t off) const { return f64(e, off); }
+  __device__ uint8_t type() const { return e[FDY_NODE_OFF_TYPE]; }
+};
+
+struct PlaneEntry {
+  const uint32_t* p;  // dword 0 of the node
+  __device__ uint32_t u32(uint32_t off) const { return p[(off >> 2) * kNodeChunk]; }
+  __device__ uint64_t u64(uint32_t off) const { return (uint64_t)u32(off) | ((uint64_t)u32(off + 4) << 32); }
+  __device__ uint8_t type() const { return (uint8_t)(u32(FDY_NODE_OFF_TYPE & ~3u) >> (8 * (FDY_NODE_OFF_TYPE & 3))); }
+};
+
+// Node n of graph G in the field-major table: chunks hold 256 nodes, a
+// graph's first chunk padded at the front.
+__device__ inline PlaneEntry plane_entry(const uint32_t* planes, const DevGraph& G, uint32_t n) {
+  const uint32_t pad = (kNodeChunk - G.num_nodes % kNodeChunk) % kNodeChunk;
+  const uint32_t pos = pad + n;
+  return PlaneEntry{planes + ((uint64_t)(G.chunk_base + pos / kNodeChunk) * kEntryDwords) * kNodeChunk +
+                    pos % kNodeChunk};
+}
+
 // The param references of kernel node entry e: the name, param-index and
 // arg-buffer bounds; an extra-style node's blob.  Per-param nodes are
 // completed by scan_params.
-__device__ __forceinline__ void side_header(const uint8_t* img, const DevGraph& G, const uint8_t* e, Side& s) {
+template <class E>
+__device__ __forceinline__ void side_header(const uint8_t* img, const DevGraph& G, const E& e, Side& s) {
   s = Side{};
-  const uint32_t pio = f32(e, FDY_KOFF_PARAM_INDEX), np = f32(e, FDY_KOFF_NUM_PARAMS);
-  const uint32_t ao = f32(e, FDY_KOFF_ARG_OFFSET), as = f32(e, FDY_KOFF_ARG_SIZE);
-  const uint32_t no = f32(e, FDY_KOFF_NAME_OFFSET), nl = f32(e, FDY_KOFF_NAME_LENGTH);
+  const uint32_t pio = e.u32(FDY_KOFF_PARAM_INDEX), np = e.u32(FDY_KOFF_NUM_PARAMS);
+  const uint32_t ao = e.u32(FDY_KOFF_ARG_OFFSET), as = e.u32(FDY_KOFF_ARG_SIZE);
+  const uint32_t no = e.u32(FDY_KOFF_NAME_OFFSET), nl = e.u32(FDY_KOFF_NAME_LENGTH);
   s.bad = (uint64_t)no + nl > G.sec_size[FDY_SEC_STRINGS] ||
           (uint64_t)pio + 8ull * np > G.sec_size[FDY_SEC_PARAM_INDEX];
   s.extra = ao != FDY_NO_ARG_BUFFER;
@@ -319,24 +348,25 @@ struct Attrs {
       has_carve, carve;
 };
 
-__device__ inline void attrs_from(const uint8_t* b, Attrs& a, bool merge) {
-  const uint32_t f = f32(b, 0);
+template <class E>
+__device__ inline void attrs_from(const E& b, uint32_t base, Attrs& a, bool merge) {
+  const uint32_t f = b.u32(base);
   if (f & FDY_KNA_CLUSTER_DIM) {
     a.has_cluster = 1;
-    a.cx = (int32_t)f32(b, 4);
-    a.cy = (int32_t)f32(b, 8);
-    a.cz = (int32_t)f32(b, 12);
+    a.cx = (int32_t)b.u32(base + 4);
+    a.cy = (int32_t)b.u32(base + 8);
+    a.cz = (int32_t)b.u32(base + 12);
   }
   if (f & FDY_KNA_PREFERRED_CLUSTER_DIM) {
     a.has_pref = 1;
-    a.px = (int32_t)f32(b, 16);
-    a.py = (int32_t)f32(b, 20);
-    a.pz = (int32_t)f32(b, 24);
+    a.px = (int32_t)b.u32(base + 16);
+    a.py = (int32_t)b.u32(base + 20);
+    a.pz = (int32_t)b.u32(base + 24);
   }
   // When merging per-node attrs over common ones, a negative value does not override.
   auto take = [&](uint32_t flag, uint32_t off, int32_t& dst) {
     if (!(f & flag)) return;
-    int32_t v = (int32_t)f32(b, off);
+    int32_t v = (int32_t)b.u32(base + off);
     if (!merge || v >= 0) dst = v;
   };
   take(FDY_KNA_CLUSTER_SCHEDULING, 28, a.sched);
@@ -345,21 +375,22 @@ __device__ inline void attrs_from(const uint8_t* b, Attrs& a, bool merge) {
   take(FDY_KNA_MEM_SYNC_DOMAIN, 40, a.msd);
   if (f & FDY_KNA_MEM_SYNC_DOMAIN_MAP) {
     a.has_map = 1;
-    a.map_def = b[44];
-    a.map_remote = b[45];
+    a.map_def = b.u32(base + 44) & 0xFF;
+    a.map_remote = (b.u32(base + 44) >> 8) & 0xFF;
   }
   if (f & FDY_KNA_SHARED_MEM_CARVEOUT) {
     a.has_carve = 1;
-    a.carve = (int32_t)f32(b, 48);
+    a.carve = (int32_t)b.u32(base + 48);
   }
 }
 
 // `common`: the graph's common kernel attrs, or null.
-__device__ __forceinline__ Attrs effective_attrs(const uint8_t* common, const uint8_t* e) {
+template <class E>
+__device__ __forceinline__ Attrs effective_attrs(const uint8_t* common, const E& e) {
   Attrs a{0, 0, 0, 0, 0, 0, 0, 0, -1, -1, -1, -1, 0, 0, 0, 0, 0};
-  if (common) attrs_from(common, a, false);
-  if (f32(e, FDY_KOFF_KNA_FLAGS) != 0) attrs_from(e + FDY_KOFF_KNA_FLAGS, a, true);
-  const int32_t w = (int32_t)f32(e, 64), h = (int32_t)f32(e, 68), d = (int32_t)f32(e, 72);
+  if (common) attrs_from(RawEntry{common}, 0, a, false);
+  if (e.u32(FDY_KOFF_KNA_FLAGS) != 0) attrs_from(e, FDY_KOFF_KNA_FLAGS, a, true);
+  const int32_t w = (int32_t)e.u32(64), h = (int32_t)e.u32(68), d = (int32_t)e.u32(72);
   if (w > 0 || h > 0 || d > 0) {
     a.has_cluster = 1;
     a.cx = w > 0 ? w : 1;
@@ -384,9 +415,10 @@ struct Strings {
 };
 
 // Equal kernel names, compared through 8-byte windows.
-__device__ __forceinline__ bool names_equal(const Strings& A, const uint8_t* ea, const Strings& B, const uint8_t* eb) {
-  const uint32_t ao = f32(ea, FDY_KOFF_NAME_OFFSET), al = f32(ea, FDY_KOFF_NAME_LENGTH);
-  const uint32_t bo = f32(eb, FDY_KOFF_NAME_OFFSET), bl = f32(eb, FDY_KOFF_NAME_LENGTH);
+template <class E>
+__device__ __forceinline__ bool names_equal(const Strings& A, const E& ea, const Strings& B, const E& eb) {
+  const uint32_t ao = ea.u32(FDY_KOFF_NAME_OFFSET), al = ea.u32(FDY_KOFF_NAME_LENGTH);
+  const uint32_t bo = eb.u32(FDY_KOFF_NAME_OFFSET), bl = eb.u32(FDY_KOFF_NAME_LENGTH);
   if (al != bl) return false;
   if ((uint64_t)ao + al > A.size || (uint64_t)bo + bl > B.size) return false;
   bool eq = true;
@@ -399,8 +431,9 @@ __device__ __forceinline__ bool names_equal(const Strings& A, const uint8_t* ea,
 }
 
 // CRC-64/XZ of a kernel's name.
-__device__ __forceinline__ uint64_t name_crc(const Strings& S, const uint8_t* e, const uint64_t (*slice)[256]) {
-  const uint32_t no = f32(e, FDY_KOFF_NAME_OFFSET), nl = f32(e, FDY_KOFF_NAME_LENGTH);
+template <class E>
+__device__ __forceinline__ uint64_t name_crc(const Strings& S, const E& e, const uint64_t (*slice)[256]) {
+  const uint32_t no = e.u32(FDY_KOFF_NAME_OFFSET), nl = e.u32(FDY_KOFF_NAME_LENGTH);
   if ((uint64_t)no + nl > S.size) return 0;
   uint64_t c = ~0ull;
   uint32_t i = 0;
@@ -413,23 +446,25 @@ __device__ __forceinline__ uint64_t name_crc(const Strings& S, const uint8_t* e,
 }
 
 // Relocated memset dst / memcpy dst, src of node entry e (0 when not a pointer node).
-__device__ __forceinline__ void node_pointers(const uint8_t* e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
-  const uint8_t type = e[FDY_NODE_OFF_TYPE];
+template <class E>
+__device__ __forceinline__ void node_pointers(const E& e, const RelocDev& r, uint64_t* p0, uint64_t* p1) {
+  const uint8_t type = e.type();
   *p0 = 0;
   *p1 = 0;
   if (type == FDY_NODE_MEMSET) {
-    *p0 = reloc_word(r, f64(e, FDY_MSOFF_DST));
+    *p0 = reloc_word(r, e.u64(FDY_MSOFF_DST));
   } else if (type == FDY_NODE_MEMCPY) {
-    const uint64_t dst = f64(e, FDY_MCOFF_DST), src = f64(e, FDY_MCOFF_SRC);
-    const int32_t dt = (int32_t)f32(e, FDY_MCOFF_DST_MEMTYPE), st = (int32_t)f32(e, FDY_MCOFF_SRC_MEMTYPE);
+    const uint64_t dst = e.u64(FDY_MCOFF_DST), src = e.u64(FDY_MCOFF_SRC);
+    const int32_t dt = (int32_t)e.u32(FDY_MCOFF_DST_MEMTYPE), st = (int32_t)e.u32(FDY_MCOFF_SRC_MEMTYPE);
     *p0 = (dt == FDY_MEMTYPE_DEVICE || dt == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, dst) : dst;
     *p1 = (st == FDY_MEMTYPE_DEVICE || st == FDY_MEMTYPE_UNIFIED) ? reloc_word(r, src) : src;
   }
 }
 
-__device__ __forceinline__ bool u64_range_differs(const uint8_t* a, const uint8_t* b, uint32_t off, uint32_t n) {
+template <class E>
+__device__ __forceinline__ bool u64_range_differs(const E& a, const E& b, uint32_t off, uint32_t n) {
   bool d = false;
-  for (uint32_t i = 0; i < n; i += 8) d |= f64(a, off + i) != f64(b, off + i);
+  for (uint32_t i = 0; i < n; i += 8) d |= a.u64(off + i) != b.u64(off + i);
   return d;
 }
 
@@ -438,31 +473,32 @@ __device__ __forceinline__ bool u64_range_differs(const uint8_t* a, const uint8_
 // same_ctx: both graphs have byte-identical string sections and common
 // attrs, so equal entry bytes [8, 128) (launch config, function hash, name
 // offset and length, function attrs, per-node attrs) mean equal descriptors.
-__device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const uint8_t* ea, const Strings& B,
-                             const uint8_t* cb, const uint8_t* eb, uint64_t pa0, uint64_t pa1, uint64_t pb0,
+template <class E>
+__device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const E& ea, const Strings& B,
+                             const uint8_t* cb, const E& eb, uint64_t pa0, uint64_t pa1, uint64_t pb0,
                              uint64_t pb1, bool same_ctx) {
-  const uint8_t ta = ea[FDY_NODE_OFF_TYPE], tb = eb[FDY_NODE_OFF_TYPE];
+  const uint8_t ta = ea.type(), tb = eb.type();
   if (ta != tb) return true;
   switch (ta) {
     case FDY_NODE_KERNEL: {
       if (same_ctx && !u64_range_differs(ea, eb, 8, 120)) return false;
       bool d = false;
-      for (uint32_t off = 8; off < 44; off += 4) d |= f32(ea, off) != f32(eb, off);
-      for (uint32_t off = 52; off < 76; off += 4) d |= f32(ea, off) != f32(eb, off);
+      for (uint32_t off = 8; off < 44; off += 4) d |= ea.u32(off) != eb.u32(off);
+      for (uint32_t off = 52; off < 76; off += 4) d |= ea.u32(off) != eb.u32(off);
       if (d) return true;
       if (!names_equal(A, ea, B, eb)) return true;
       return !attrs_equal(effective_attrs(ca, ea), effective_attrs(cb, eb));
     }
     case FDY_NODE_MEMSET:
-      return pa0 != pb0 || f32(ea, 16) != f32(eb, 16) || u64_range_differs(ea, eb, 24, 16) ||
-             f32(ea, 40) != f32(eb, 40) || f64(ea, 48) != f64(eb, 48);
+      return pa0 != pb0 || ea.u32(16) != eb.u32(16) || u64_range_differs(ea, eb, 24, 16) ||
+             ea.u32(40) != eb.u32(40) || ea.u64(48) != eb.u64(48);
     case FDY_NODE_MEMCPY:
       return pa0 != pb0 || pa1 != pb1 || u64_range_differs(ea, eb, 8, 24) || u64_range_differs(ea, eb, 40, 48) ||
-             f32(ea, 88) != f32(eb, 88) || u64_range_differs(ea, eb, 104, 48) ||
-             f32(ea, 152) != f32(eb, 152);
+             ea.u32(88) != eb.u32(88) || u64_range_differs(ea, eb, 104, 48) ||
+             ea.u32(152) != eb.u32(152);
     case FDY_NODE_EVENT_RECORD:
     case FDY_NODE_EVENT_WAIT:
-      return f32(ea, FDY_EVOFF_ID) != f32(eb, FDY_EVOFF_ID);
+      return ea.u32(FDY_EVOFF_ID) != eb.u32(FDY_EVOFF_ID);
     default:
       return false;
   }
@@ -510,6 +546,30 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
   (void)e;
 }
 
+// The field-major node table: thread l of chunk c copies the 42 dwords of
+// node (c - chunk_base) * 256 + l - pad of its graph into plane k at
+// planes[(c * 42 + k) * 256 + l]; padding lanes write zeros.
+__global__ __launch_bounds__(kNodeChunk) void k_planes(const uint8_t* img, const DevGraph* graphs,
+                                                       const uint32_t* chunk_graph, uint32_t* planes) {
+  const uint32_t c = blockIdx.x, l = threadIdx.x;
+  const DevGraph& G = graphs[chunk_graph[c]];
+  const uint32_t N = G.num_nodes;
+  const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
+  const int64_t n = (int64_t)(c - G.chunk_base) * kNodeChunk + l - pad;
+  uint32_t v[kEntryDwords];
+  if (n >= 0 && n < (int64_t)N) {
+    const uint32_t* e = reinterpret_cast<const uint32_t*>(img + G.sec_off[FDY_SEC_NODES] + 168ull * (uint64_t)n);
+#pragma unroll
+    for (uint32_t k = 0; k < kEntryDwords; ++k) v[k] = e[k];
+  } else {
+#pragma unroll
+    for (uint32_t k = 0; k < kEntryDwords; ++k) v[k] = 0;
+  }
+  uint32_t* out = planes + (uint64_t)c * kEntryDwords * kNodeChunk + l;
+#pragma unroll
+  for (uint32_t k = 0; k < kEntryDwords; ++k) out[k * kNodeChunk] = v[k];
+}
+
 // The node pass runs in two parts.
 //
 // Part A, k_node_a: one workgroup of kNodeChunk threads per chunk of a
@@ -527,7 +587,9 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
 // tile -> first-node table, ragged-word sources, flatness, status, digests
 // and the slot descriptors of the diff pass.
 
-__global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
+// Five waves per SIMD: held to 96 VGPRs it spills 12 bytes per lane and
+// still beats four waves per SIMD at 99 VGPRs (73 -> 68 us, decode-style).
+__global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   constexpr uint32_t kStrStage = 2048; // string sections up to this size are staged in LDS
   static_assert(kNodeChunk == kPosRecords, "one position multiplier per record of a chunk");
   __shared__ uint64_t s_slice[8][256];
@@ -595,22 +657,22 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
   uint32_t words_g = 0, words_t = 0, flags = 0;
   uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0, pbytes = 0;
   uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
-  const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
-  const uint8_t* et = img + Gt.sec_off[FDY_SEC_NODES] + 168ull * (n < NT ? n : 0);
+  const PlaneEntry eg{a.planes + ((uint64_t)chunk * kEntryDwords) * kNodeChunk + tid};
+  const PlaneEntry et = plane_entry(a.planes, Gt, n < NT ? n : 0);
   if (valid) {
-    const uint8_t type = eg[FDY_NODE_OFF_TYPE];
+    const uint8_t type = eg.type();
     const bool has_t = !is_t && n < NT;
-    const uint8_t ttype = has_t ? et[FDY_NODE_OFF_TYPE] : 0xFF;
+    const uint8_t ttype = has_t ? et.type() : 0xFF;
     tw0 = type;
     Side sg{}, st{};
     bool same_sizes = false;
     if (type == FDY_NODE_KERNEL) {
       // Cluster dims of the recomputed key (csrc/CUDAGraphParallel.cpp:1807-1833).
       uint32_t cx = 0, cy = 0, cz = 0;
-      if (f32(eg, FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
-        cx = f32(eg, 80);
-        cy = f32(eg, 84);
-        cz = f32(eg, 88);
+      if (eg.u32(FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
+        cx = eg.u32(80);
+        cy = eg.u32(84);
+        cz = eg.u32(88);
       }
       if (cx == 0 && common_g && (f32(common_g, 0) & FDY_KNA_CLUSTER_DIM)) {
         cx = f32(common_g, 4);
@@ -618,13 +680,13 @@ __global__ __launch_bounds__(kNodeChunk) void k_node_a(RestoreArgs a) {
         cz = f32(common_g, 12);
       }
       if (cx == 0) {
-        cx = f32(eg, 64);
-        cy = f32(eg, 68);
-        cz = f32(eg, 72);
+        cx = eg.u32(64);
+        cy = eg.u32(68);
+        cz = eg.u32(72);
       }
       tw0 |= (uint64_t)cx << 32;
       tw1 = cy | ((uint64_t)cz << 32);
-      kw0 = f64(eg, FDY_KOFF_BINARY_HASH);
+      kw0 = eg.u64(FDY_KOFF_BINARY_HASH);
       kw1 = name_crc(sg_str, eg, slice);
       side_header(img, Gg, eg, sg);
     }
@@ -841,7 +903,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
           const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
           Side sd_{}, none_{};
           bool same_;
-          side_header(img, Gg, eg, sd_);
+          side_header(img, Gg, RawEntry{eg}, sd_);
           scan_params(Gg, sd_, true, Gg, none_, false, &same_);
           write_aux(img, Gg, eg, sd_, a.aux, gword);
         }
@@ -1653,6 +1715,12 @@ hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s) {
 hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
   const uint32_t sgrid = (a.num_slots + kSThreads / 64 - 1) / (kSThreads / 64);
   hipLaunchKernelGGL(k_diff_s, dim3(sgrid), dim3(kSThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
+                         uint32_t* planes, hipStream_t s) {
+  hipLaunchKernelGGL(k_planes, dim3(num_chunks), dim3(kNodeChunk), 0, s, img, graphs, chunk_graph, planes);
   return hipGetLastError();
 }
 
