@@ -813,9 +813,10 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     s_flat = 1;
   }
   __syncthreads();
-  if (!is_t) {
-    // The template must carry the very same key bytes (digest collisions are
-    // reported, never silently merged).
+  if (!is_t && a.explicit_template == nullptr) {
+    // A template found by key digest must carry the very same key bytes
+    // (digest collisions are reported, never silently merged).  Explicit
+    // groups (a manifest) pair graphs whatever their keys.
     const uint64_t L = Gg.sec_size[FDY_SEC_TOPOLOGY_KEY];
     if (L != Gt.sec_size[FDY_SEC_TOPOLOGY_KEY]) {
       if (threadIdx.x == 0) s_key_differs = 1;

@@ -78,6 +78,25 @@ def test_explicit_groups(cuda):
     assert_restore_parity(arch, ref)
 
 
+def test_explicit_template_of_another_length(cuda):
+    # Graphs of 300 and 520 nodes grouped across lengths: a template's node n
+    # sits at another lane of the field-major node table than the member's
+    # node n, and a member longer than its template has nodes without one.
+    a = synth.SynthArchive(synth.preset(1, num_graphs=2, nodes_per_graph=300, seed=11))
+    b = synth.SynthArchive(synth.preset(1, num_graphs=2, nodes_per_graph=520, seed=12))
+    images = a.images() + b.images()
+    iv = a.intervals()
+    tmpl = np.array([0, 2, 2, 0], dtype=np.uint32)
+    print("[case] cross-length groups 300/520 nodes", flush=True)
+    arch = Archive.from_images(images)
+    arch.set_relocation(*iv)
+    arch.set_groups(tmpl)
+    arch.restore()
+    ref = oracle.Restore(images, iv, template_of=tmpl)
+    assert_restore_parity(arch, ref)
+    arch.close()
+
+
 def test_restore_twice_is_identical(cuda):
     p = synth.preset(2, num_graphs=8, nodes_per_graph=200, num_groups=2)
     s = synth.SynthArchive(p)
