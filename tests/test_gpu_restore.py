@@ -97,6 +97,25 @@ def test_explicit_template_of_another_length(cuda):
     arch.close()
 
 
+def test_explicit_template_with_other_kernels(cuda):
+    # Same length, different kernels (other seeds): grouped explicitly, every
+    # node is compared against a template node of another name, function
+    # hash and params.
+    a = synth.SynthArchive(synth.preset(2, num_graphs=2, nodes_per_graph=400, num_groups=1, seed=21))
+    b = synth.SynthArchive(synth.preset(2, num_graphs=2, nodes_per_graph=400, num_groups=1, seed=22))
+    images = a.images() + b.images()
+    iv = a.intervals()
+    tmpl = np.array([0, 2, 2, 0], dtype=np.uint32)
+    print("[case] explicit groups across kernels, 400 nodes", flush=True)
+    arch = Archive.from_images(images)
+    arch.set_relocation(*iv)
+    arch.set_groups(tmpl)
+    arch.restore()
+    ref = oracle.Restore(images, iv, template_of=tmpl)
+    assert_restore_parity(arch, ref)
+    arch.close()
+
+
 def test_restore_twice_is_identical(cuda):
     p = synth.preset(2, num_graphs=8, nodes_per_graph=200, num_groups=2)
     s = synth.SynthArchive(p)
