@@ -72,7 +72,7 @@ struct fdy_archive {
 
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
   fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
-  fdy::DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count, slot_off, planes;
+  fdy::DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count, slot_off, planes, pplanes;
 
   fdy::RelocPlan reloc;
   bool use_explicit = false;

@@ -44,11 +44,12 @@ struct RestoreArgs {
   uint32_t* graph_count;      // records per graph
   uint32_t* slot_off;         // per slot: its records' offset among its graph's
   const uint32_t* planes;     // field-major node table: per 256-node chunk, 42 planes of 256 dwords
+  const uint64_t* pplanes;    // per 256-node chunk, 16 planes of 256 param entries (the first 16 of each node)
   RelocDev reloc;
 };
 
 hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
-                         uint32_t* planes, hipStream_t s);
+                         uint32_t* planes, uint64_t* pplanes, hipStream_t s);
 hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);

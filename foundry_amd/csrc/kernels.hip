@@ -204,6 +204,7 @@ struct Side {
   uint64_t src;        // absolute byte offset of the blob
   uint64_t pbytes;     // param bytes (0 when bad)
   const uint8_t* pidx; // param entries (per-param style)
+  const uint64_t* pp;  // the first kPlaneParams of them, field-major (stride kNodeChunk), or null
 };
 
 // A node entry's fields (byte offsets, multiples of 4).  RawEntry reads the
@@ -225,13 +226,17 @@ struct PlaneEntry {
   __device__ uint8_t type() const { return (uint8_t)(u32(FDY_NODE_OFF_TYPE & ~3u) >> (8 * (FDY_NODE_OFF_TYPE & 3))); }
 };
 
-// Node n of graph G in the field-major table: chunks hold 256 nodes, a
+// Node n of graph G in the field-major tables: chunks hold 256 nodes, a
 // graph's first chunk padded at the front.
-__device__ inline PlaneEntry plane_entry(const uint32_t* planes, const DevGraph& G, uint32_t n) {
+struct PlanePos {
+  uint64_t chunk;
+  uint32_t lane;
+};
+
+__device__ inline PlanePos plane_pos(const DevGraph& G, uint32_t n) {
   const uint32_t pad = (kNodeChunk - G.num_nodes % kNodeChunk) % kNodeChunk;
   const uint32_t pos = pad + n;
-  return PlaneEntry{planes + ((uint64_t)(G.chunk_base + pos / kNodeChunk) * kEntryDwords) * kNodeChunk +
-                    pos % kNodeChunk};
+  return PlanePos{G.chunk_base + pos / kNodeChunk, pos % kNodeChunk};
 }
 
 // The param references of kernel node entry e: the name, param-index and
@@ -303,15 +308,19 @@ __device__ __forceinline__ void scan_params(const DevGraph& Gg, Side& g, bool wi
 #pragma unroll
       for (uint32_t k = 0; k < kParamBatch; ++k) {
         const uint32_t j = jb + k;
-        eg[k] = j < ng ? *reinterpret_cast<const uint64_t*>(g.pidx + 8ull * j) : 0;
-        et[k] = j < nt ? *reinterpret_cast<const uint64_t*>(t.pidx + 8ull * j) : 0;
+        eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk]
+                                                   : *reinterpret_cast<const uint64_t*>(g.pidx + 8ull * j))
+                       : 0;
+        et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk]
+                                                   : *reinterpret_cast<const uint64_t*>(t.pidx + 8ull * j))
+                       : 0;
       }
     } else {
 #pragma unroll
       for (uint32_t k = 0; k < kParamBatch; ++k) {
         const uint32_t j = jb + k;
-        eg[k] = j < ng ? ld_u64(g.pidx + 8ull * j) : 0;
-        et[k] = j < nt ? ld_u64(t.pidx + 8ull * j) : 0;
+        eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk] : ld_u64(g.pidx + 8ull * j)) : 0;
+        et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk] : ld_u64(t.pidx + 8ull * j)) : 0;
       }
     }
 #pragma unroll
@@ -550,7 +559,8 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
 // node (c - chunk_base) * 256 + l - pad of its graph into plane k at
 // planes[(c * 42 + k) * 256 + l]; padding lanes write zeros.
 __global__ __launch_bounds__(kNodeChunk) void k_planes(const uint8_t* img, const DevGraph* graphs,
-                                                       const uint32_t* chunk_graph, uint32_t* planes) {
+                                                       const uint32_t* chunk_graph, uint32_t* planes,
+                                                       uint64_t* pplanes) {
   const uint32_t c = blockIdx.x, l = threadIdx.x;
   const DevGraph& G = graphs[chunk_graph[c]];
   const uint32_t N = G.num_nodes;
@@ -568,6 +578,20 @@ __global__ __launch_bounds__(kNodeChunk) void k_planes(const uint8_t* img, const
   uint32_t* out = planes + (uint64_t)c * kEntryDwords * kNodeChunk + l;
 #pragma unroll
   for (uint32_t k = 0; k < kEntryDwords; ++k) out[k * kNodeChunk] = v[k];
+  // The first kPlaneParams param entries of a per-param kernel node whose
+  // entries lie inside the param-index section (others are never read).
+  uint32_t np = 0;
+  const uint8_t* pidx = nullptr;
+  if (n >= 0 && n < (int64_t)N && (v[FDY_NODE_OFF_TYPE / 4] >> (8 * (FDY_NODE_OFF_TYPE % 4)) & 0xFF) == FDY_NODE_KERNEL) {
+    const uint32_t pio = v[FDY_KOFF_PARAM_INDEX / 4], num = v[FDY_KOFF_NUM_PARAMS / 4];
+    if (v[FDY_KOFF_ARG_OFFSET / 4] == FDY_NO_ARG_BUFFER && (uint64_t)pio + 8ull * num <= G.sec_size[FDY_SEC_PARAM_INDEX]) {
+      np = min(num, kPlaneParams);
+      pidx = img + G.sec_off[FDY_SEC_PARAM_INDEX] + pio;
+    }
+  }
+  uint64_t* pout = pplanes + (uint64_t)c * kPlaneParams * kNodeChunk + l;
+#pragma unroll
+  for (uint32_t j = 0; j < kPlaneParams; ++j) pout[j * kNodeChunk] = j < np ? ld_u64(pidx + 8ull * j) : 0;
 }
 
 // The node pass runs in two parts.
@@ -658,7 +682,8 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0, pbytes = 0;
   uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
   const PlaneEntry eg{a.planes + ((uint64_t)chunk * kEntryDwords) * kNodeChunk + tid};
-  const PlaneEntry et = plane_entry(a.planes, Gt, n < NT ? n : 0);
+  const PlanePos tpos = plane_pos(Gt, n < NT ? n : 0);
+  const PlaneEntry et{a.planes + (tpos.chunk * kEntryDwords) * kNodeChunk + tpos.lane};
   if (valid) {
     const uint8_t type = eg.type();
     const bool has_t = !is_t && n < NT;
@@ -692,6 +717,8 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     }
     const bool t_kernel = has_t && ttype == FDY_NODE_KERNEL;
     if (t_kernel) side_header(img, Gt, et, st);
+    sg.pp = a.pplanes + ((uint64_t)chunk * kPlaneParams) * kNodeChunk + tid;
+    st.pp = a.pplanes + (tpos.chunk * kPlaneParams) * kNodeChunk + tpos.lane;
     scan_params(Gg, sg, type == FDY_NODE_KERNEL, Gt, st, t_kernel, &same_sizes);
     if (type == FDY_NODE_KERNEL) {
       words_g = sg.words;
@@ -1720,8 +1747,8 @@ hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
-                         uint32_t* planes, hipStream_t s) {
-  hipLaunchKernelGGL(k_planes, dim3(num_chunks), dim3(kNodeChunk), 0, s, img, graphs, chunk_graph, planes);
+                         uint32_t* planes, uint64_t* pplanes, hipStream_t s) {
+  hipLaunchKernelGGL(k_planes, dim3(num_chunks), dim3(kNodeChunk), 0, s, img, graphs, chunk_graph, planes, pplanes);
   return hipGetLastError();
 }
 

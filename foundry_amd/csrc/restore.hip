@@ -294,6 +294,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->tile_node, 4 * slots, "tile table");
   alloc(a->chunk_graph, 4 * chunks, "node chunk table");
   alloc(a->planes, 4ull * kEntryDwords * kNodeChunk * chunks, "field-major node table");
+  alloc(a->pplanes, 8ull * kPlaneParams * kNodeChunk * chunks, "field-major param entries");
   alloc(a->chunks, sizeof(NodeChunk) * chunks, "node chunk results");
   alloc(a->slot_desc, sizeof(SlotDesc) * slots, "slot descriptors");
   alloc(a->tslots, 4 * (slots + 1), "template slot list");
@@ -319,7 +320,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   // them with coalesced loads (the image itself never changes).
   if (chunks) {
     FDY_HIP(launch_planes(a->img.as<uint8_t>(), a->dgraphs.as<DevGraph>(), a->chunk_graph.as<uint32_t>(),
-                          (uint32_t)chunks, a->planes.as<uint32_t>(), nullptr));
+                          (uint32_t)chunks, a->planes.as<uint32_t>(), a->pplanes.as<uint64_t>(), nullptr));
     FDY_HIP(hipStreamSynchronize(nullptr));
   }
   return FDY_OK;
@@ -708,6 +709,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.graph_count = a->graph_count.as<uint32_t>();
   r.slot_off = a->slot_off.as<uint32_t>();
   r.planes = a->planes.as<uint32_t>();
+  r.pplanes = a->pplanes.as<uint64_t>();
   r.reloc = a->reloc.dev;
   if (a->timing) {
     for (hipEvent_t& e : a->ev)

@@ -49,6 +49,7 @@ struct DevGraph {
 // Nodes per chunk of the node pass, and what a chunk reports to its graph.
 constexpr uint32_t kNodeChunk = 256;
 constexpr uint32_t kEntryDwords = 168 / 4;  // dwords of a node entry (planes of the field-major table)
+constexpr uint32_t kPlaneParams = 16;       // param entries of a node kept field-major beside its entry
 struct NodeChunk {
   uint64_t crc_type, crc_kent;  // raw CRCs (zero initial value) of the chunk's node-type and kernel-entry records
   uint64_t pbytes;              // param bytes of the chunk's kernel nodes
