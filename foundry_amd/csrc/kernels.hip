@@ -299,29 +299,15 @@ __device__ __forceinline__ void scan_params(const DevGraph& Gg, Side& g, bool wi
   const uint32_t ng = wg ? g.num_params : 0, nt = wt ? t.num_params : 0;
   uint64_t prev_g = 0, prev_t = 0, words_g = 0, words_t = 0;
   bool same = ng == nt;
-  // Entries of a side sit at one alignment: the common 8-byte-aligned case
-  // loads them directly, the rest through byte-safe loads.
-  const bool aligned = ((reinterpret_cast<uintptr_t>(g.pidx) | reinterpret_cast<uintptr_t>(t.pidx)) & 7) == 0;
+  // The first kPlaneParams entries come from the field-major copy, the rest
+  // in place (byte-safe loads: a side's entries may sit at any alignment).
   for (uint32_t jb = 0; jb < max(ng, nt); jb += kParamBatch) {
     uint64_t eg[kParamBatch], et[kParamBatch];
-    if (aligned) {
 #pragma unroll
-      for (uint32_t k = 0; k < kParamBatch; ++k) {
-        const uint32_t j = jb + k;
-        eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk]
-                                                   : *reinterpret_cast<const uint64_t*>(g.pidx + 8ull * j))
-                       : 0;
-        et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk]
-                                                   : *reinterpret_cast<const uint64_t*>(t.pidx + 8ull * j))
-                       : 0;
-      }
-    } else {
-#pragma unroll
-      for (uint32_t k = 0; k < kParamBatch; ++k) {
-        const uint32_t j = jb + k;
-        eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk] : ld_u64(g.pidx + 8ull * j)) : 0;
-        et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk] : ld_u64(t.pidx + 8ull * j)) : 0;
-      }
+    for (uint32_t k = 0; k < kParamBatch; ++k) {
+      const uint32_t j = jb + k;
+      eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk] : ld_u64(g.pidx + 8ull * j)) : 0;
+      et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk] : ld_u64(t.pidx + 8ull * j)) : 0;
     }
 #pragma unroll
     for (uint32_t k = 0; k < kParamBatch; ++k) {
