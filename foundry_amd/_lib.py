@@ -180,6 +180,9 @@ _SIGS = {
     "fdy_get_node_pointers": (C.c_int, [_vp, _vp, C.c_uint32, u64p, C.c_uint64, u64p]),
     "fdy_get_section": (C.c_int, [_vp, C.c_uint32, C.c_uint32, u8p, C.c_uint64, u64p]),
     "fdy_cugraph_from_json": (C.c_int, [C.c_char_p, C.c_uint64, u8p, C.c_uint64, u64p]),
+    "fdy_load_topology_key": (C.c_int, [C.c_char_p, C.c_uint64, C.c_char_p, C.c_uint64, u64p]),
+    "fdy_dlpack_view": (_vp, [C.c_uint64, C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_int64),
+                              C.POINTER(C.c_int64), C.c_uint8, C.c_uint8]),
     "fdy_cugraph_save_binary": (C.c_int, [C.c_char_p, C.c_char_p, C.c_uint64]),
     "fdy_switch": (C.c_int, [_vp, C.c_uint32, _vp]),
     "fdy_get_live": (C.c_int, [_vp, _vp, C.c_uint32, u64p, C.c_uint64, u32p, C.c_uint64, u32p]),

@@ -4,12 +4,13 @@
 //             of the dependency table, as a block-wide segmented CRC (each
 //             lane absorbs 64 bytes, lanes are joined by a combine tree whose
 //             multipliers are constants applied through nibble tables in LDS).
-//   k_group   template_of[g] = lowest graph with the same key digest and length.
+//   k_group   template_of[g] = lowest graph with the same key bytes (found by
+//             key digest and length, then compared byte for byte).
 //   k_node_a  one workgroup per 256-node chunk of a graph: per node, the
 //             param layout, the compare against the template's node,
 //             memset/memcpy pointer relocation, the node-type and kernel-entry
 //             records (raw CRC per chunk) and the node descriptor.
-//   k_node_b  one workgroup per graph: key check, chunk CRCs joined into the
+//   k_node_b  one workgroup per graph: chunk CRCs joined into the
 //             digests, word offsets by block scans, the diff-tile -> first-node
 //             table, ragged-word sources, slot descriptors.
 //   k_diff_t  the template graphs' words, relocated through a bucket-indexed
@@ -35,7 +36,6 @@ namespace {
 
 constexpr uint32_t kHashThreads = 1024;
 constexpr uint32_t kNodeThreads = 1024;
-constexpr uint32_t kGroupWaves = 4;  // graphs per workgroup in k_group
 constexpr uint32_t kGroupSteps = 8;  // 64-candidate steps whose loads are issued together
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
@@ -161,36 +161,73 @@ __global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
   }
 }
 
-// template_of[i] = the lowest j <= i whose saved key has the same digest
-// and length (the byte-exact check follows in the node pass): one wave per
-// graph, its lanes testing 64 candidates per step and eight steps' loads in
-// flight at once.
-__global__ __launch_bounds__(64 * kGroupWaves) void k_group(RestoreArgs a) {
-  const uint32_t lane = threadIdx.x & 63;
-  const uint32_t i = blockIdx.x * kGroupWaves + (threadIdx.x >> 6);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *a.tslot_count = 0;  // the node pass lists template slots here
-  if (i >= a.num_graphs) return;
+// template_of[i] = the lowest j <= i whose saved key has the same bytes
+// (the reference partitions by exact key string, csrc/CUDAGraphParallel.cpp:
+// 1788-1851): one workgroup per graph.  Its first wave finds the lowest
+// candidate with an equal key digest and length (64 candidates per step,
+// eight steps' loads in flight at once); the workgroup then compares the
+// two keys' bytes, and on a digest collision (equal digest and length,
+// other bytes) flags the graph and goes on scanning past the candidate.
+constexpr uint32_t kGroupThreads = 256;
+
+__global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
+  __shared__ uint32_t s_found, s_differs;
+  const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
   if (a.explicit_template) {
-    if (lane == 0) a.template_of[i] = a.explicit_template[i];
+    if (tid == 0) {
+      a.template_of[i] = a.explicit_template[i];
+      a.status[i] = 0;
+    }
     return;
   }
+  const DevGraph& Gi = a.graphs[i];
   const uint64_t di = a.digests[4ull * i];
-  const uint64_t li = a.graphs[i].sec_size[FDY_SEC_TOPOLOGY_KEY];
-  uint32_t found = i;
-  for (uint32_t base = 0; base < i && found == i; base += 64 * kGroupSteps) {
-    bool m[kGroupSteps];
+  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
+  const uint8_t* pi = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
+  uint32_t from = 0, status = 0, tmpl = i;
+  for (;;) {
+    if (tid < 64) {
+      uint32_t found = i;
+      for (uint32_t base = from; base < i && found == i; base += 64 * kGroupSteps) {
+        bool m[kGroupSteps];
 #pragma unroll
-    for (uint32_t k = 0; k < kGroupSteps; ++k) {
-      const uint32_t j = base + 64 * k + lane;
-      m[k] = j < i && a.digests[4ull * j] == di && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == li;
-    }
+        for (uint32_t k = 0; k < kGroupSteps; ++k) {
+          const uint32_t j = base + 64 * k + lane;
+          m[k] = j < i && a.digests[4ull * j] == di && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == L;
+        }
 #pragma unroll
-    for (uint32_t k = 0; k < kGroupSteps; ++k) {
-      const uint64_t mk = __ballot(m[k]);
-      if (found == i && mk) found = base + 64 * k + (uint32_t)__ffsll((long long)mk) - 1;
+        for (uint32_t k = 0; k < kGroupSteps; ++k) {
+          const uint64_t mk = __ballot(m[k]);
+          if (found == i && mk) found = base + 64 * k + (uint32_t)__ffsll((long long)mk) - 1;
+        }
+      }
+      if (tid == 0) {
+        s_found = found;
+        s_differs = 0;
+      }
     }
+    __syncthreads();
+    const uint32_t j = s_found;
+    if (j == i) break;  // uniform over the workgroup
+    const uint8_t* pj = a.img + a.graphs[j].sec_off[FDY_SEC_TOPOLOGY_KEY];
+    bool d = false;
+    for (uint64_t q = tid; q * 8 < L; q += kGroupThreads)
+      d |= stream_window(pi, L, (int64_t)q * 8) != stream_window(pj, L, (int64_t)q * 8);
+    if (d) s_differs = 1;
+    __syncthreads();
+    if (!s_differs) {
+      tmpl = j;
+      break;
+    }
+    status = FDY_GRAPH_COLLISION;
+    from = j + 1;
+    __syncthreads();  // every thread has read s_found and s_differs
   }
-  if (lane == 0) a.template_of[i] = found;
+  if (tid == 0) {
+    a.template_of[i] = tmpl;
+    a.status[i] = status;  // completed by the node pass
+  }
 }
 
 // ---- node pass ----------------------------------------------------------
@@ -809,7 +846,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   __shared__ uint32_t s_tmp[kNodeThreads / 64];
   __shared__ uint64_t s_x[2][kNodeThreads / 64];
   __shared__ unsigned long long s_pb;
-  __shared__ uint32_t s_status, s_key_differs, s_words, s_flat, s_tbase;
+  __shared__ uint32_t s_status, s_words, s_flat, s_tbase;
 
   const uint32_t g = blockIdx.x;
   const uint32_t t = a.template_of[g];
@@ -820,26 +857,11 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   const uint8_t* img = a.img;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (threadIdx.x == 0) {
-    s_status = 0;
-    s_key_differs = 0;
+    s_status = a.status[g];  // the grouping pass's collision bit
     s_pb = 0;
     s_flat = 1;
   }
   __syncthreads();
-  if (!is_t && a.explicit_template == nullptr) {
-    // A template found by key digest must carry the very same key bytes
-    // (digest collisions are reported, never silently merged).  Explicit
-    // groups (a manifest) pair graphs whatever their keys.
-    const uint64_t L = Gg.sec_size[FDY_SEC_TOPOLOGY_KEY];
-    if (L != Gt.sec_size[FDY_SEC_TOPOLOGY_KEY]) {
-      if (threadIdx.x == 0) s_key_differs = 1;
-    } else {
-      const uint8_t* pg = img + Gg.sec_off[FDY_SEC_TOPOLOGY_KEY];
-      const uint8_t* pt = img + Gt.sec_off[FDY_SEC_TOPOLOGY_KEY];
-      for (uint64_t q = threadIdx.x; q * 8 < L; q += kNodeThreads)
-        if (stream_window(pg, L, (int64_t)q * 8) != stream_window(pt, L, (int64_t)q * 8)) s_key_differs = 1;
-    }
-  }
 
   // Chunk results: each chunk's raw CRC times x^(8 * bytes after it),
   // XOR-joined; param bytes and status bits.  One wave per chunk: lane i
@@ -936,7 +958,6 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     const bool overflow = gcarry > Gg.word_cap;
     s_words = overflow ? 0 : gcarry;
     uint32_t stat = s_status;
-    if (s_key_differs) stat |= FDY_GRAPH_COLLISION;
     if (!is_t && N != NT) stat |= kGraphNodeCount;
     if (overflow) stat |= FDY_GRAPH_BAD_PARAMS | kGraphOverflow;
     a.status[g] = stat;
@@ -1648,8 +1669,10 @@ __global__ __launch_bounds__(kFillThreads) void k_fill(FillArgs a) {
 
 // ---- standalone relocation ---------------------------------------------
 
-__global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint64_t* __restrict__ in,
-                                                         uint64_t* __restrict__ out, uint64_t n, int vec) {
+// `in` and `out` may be the same array: each word is read and then written
+// by one thread, so in-place relocation needs no ordering between threads.
+__global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint64_t* in, uint64_t* out, uint64_t n,
+                                                         int vec) {
   // Each thread owns kRelocPairs 16-byte pairs per chunk (coalesced across
   // the workgroup): all loads first, then the searches, then the stores, so
   // the searches of 2 * kRelocPairs words overlap.
@@ -1699,8 +1722,7 @@ hipError_t launch_hash(const RestoreArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_group, dim3(std::max(1u, (a.num_graphs + kGroupWaves - 1) / kGroupWaves)), dim3(64 * kGroupWaves),
-                     0, s, a);
+  hipLaunchKernelGGL(k_group, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -458,7 +458,7 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
     size_t got;
     while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, got);
     std::fclose(f);
-    codes[i] = fdy::cugraph_from_json(text.data(), text.size(), converted[i], errs[i]);
+    codes[i] = fdy::cugraph_for_load(text.data(), text.size(), converted[i], errs[i]);
     if (codes[i] == FDY_OK) sizes[i] = converted[i].size();
     else errs[i] = path + ": " + errs[i];
   });
@@ -602,6 +602,20 @@ int fdy_cugraph_from_json(const char* json, uint64_t len, uint8_t* out, uint64_t
   return FDY_OK;
 }
 
+int fdy_load_topology_key(const char* json, uint64_t len, char* out, uint64_t cap, uint64_t* size_out) {
+  if (!json && len) return err(FDY_E_INVALID, "null document");
+  if (!size_out) return err(FDY_E_INVALID, "need size_out");
+  std::string key, why;
+  const int rc = fdy::load_topology_key(json ? json : "", len, key, why);
+  if (rc) return err(rc, why);
+  *size_out = key.size();
+  if (!out || cap < key.size())
+    return err(FDY_E_CAPACITY, "key needs " + std::to_string(key.size()) + " bytes, buffer holds " +
+                                   std::to_string(out ? cap : 0));
+  std::memcpy(out, key.data(), key.size());
+  return FDY_OK;
+}
+
 int fdy_cugraph_save_binary(const char* bin_path, const char* json, uint64_t len) {
   if (!bin_path) return err(FDY_E_INVALID, "null path");
   if (!json && len) return err(FDY_E_INVALID, "null document");
@@ -624,7 +638,7 @@ int fdy_manifest_groups(const char* text, uint64_t len, const char* const* names
   std::unordered_map<std::string, uint32_t> index;
   for (uint32_t i = 0; i < n; ++i) {
     if (!names[i]) return err(FDY_E_INVALID, "null name " + std::to_string(i));
-    index.emplace(names[i], i);  // a repeated name resolves to its first graph
+    index[names[i]] = i;  // a repeated name resolves to its last graph (filename_to_idx[fname] = i, 1728-1732)
   }
   json::Value doc;
   std::string perr;
@@ -878,6 +892,62 @@ int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint
   if (rc) return rc;
   if (current) *current = a->h_current[t];
   return FDY_OK;
+}
+
+// DLPack's managed tensor (dlpack.h v0.8 layout): a non-owning view whose
+// deleter frees only this block.
+namespace {
+struct DLDevice_ {
+  int32_t device_type, device_id;
+};
+struct DLDataType_ {
+  uint8_t code, bits;
+  uint16_t lanes;
+};
+struct DLTensor_ {
+  void* data;
+  DLDevice_ device;
+  int32_t ndim;
+  DLDataType_ dtype;
+  int64_t* shape;
+  int64_t* strides;
+  uint64_t byte_offset;
+};
+struct DLManagedTensor_ {
+  DLTensor_ dl_tensor;
+  void* manager_ctx;
+  void (*deleter)(DLManagedTensor_*);
+};
+void free_view(DLManagedTensor_* t) { std::free(t); }
+}  // namespace
+
+void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int32_t ndim, const int64_t* shape,
+                      const int64_t* strides, uint8_t code, uint8_t bits) {
+  if (ndim < 0 || ndim > 64 || (ndim && (!shape || !strides))) {
+    err(FDY_E_INVALID, "fdy_dlpack_view: bad shape");
+    return nullptr;
+  }
+  const size_t bytes = sizeof(DLManagedTensor_) + 2 * sizeof(int64_t) * (size_t)ndim;
+  auto* t = static_cast<DLManagedTensor_*>(std::malloc(bytes));
+  if (!t) {
+    err(FDY_E_NOMEM, "fdy_dlpack_view: out of host memory");
+    return nullptr;
+  }
+  int64_t* dims = reinterpret_cast<int64_t*>(t + 1);
+  for (int32_t i = 0; i < ndim; ++i) {
+    dims[i] = shape[i];
+    dims[ndim + i] = strides[i];
+  }
+  t->dl_tensor.data = reinterpret_cast<void*>(ptr);
+  t->dl_tensor.device = DLDevice_{device_type, device_id};
+  t->dl_tensor.ndim = ndim;
+  t->dl_tensor.dtype = DLDataType_{code, bits, 1};
+  t->dl_tensor.shape = dims;
+  t->dl_tensor.strides = dims + ndim;
+  t->dl_tensor.byte_offset = 0;
+  t->manager_ctx = nullptr;
+  t->deleter = free_view;
+  return t;
 }
 
 int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,

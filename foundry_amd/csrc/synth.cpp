@@ -439,7 +439,8 @@ int fdy_synth_preset(uint32_t preset, fdy_synth_params* o) {
       break;
     case 3:
       o->num_graphs = 256; o->num_groups = 16; o->nodes_per_graph = 3000;
-      o->min_blob_bytes = 32; o->max_blob_bytes = 4096; o->max_params = 16;
+      // Up to 40 params per kernel (grouped-GEMM descriptor arrays take many).
+      o->min_blob_bytes = 32; o->max_blob_bytes = 4096; o->max_params = 40;
       o->memset_pct = 10; o->memcpy_pct = 5; o->grid_bs_pct = 20;
       o->pointer_frac = 0.25; o->diff_lo = o->diff_hi = 0.10;
       o->run_min_bytes = 64; o->run_max_bytes = 256;

@@ -238,7 +238,67 @@ void put(std::vector<uint8_t>& out, const T& x) {
   out.insert(out.end(), p, p + sizeof(T));
 }
 
-void build(const Value& root, std::vector<uint8_t>& out) {
+// The key the LOAD path groups a graph read from its JSON document by
+// (csrc/CUDAGraphParallel.cpp:1791-1841): its topology_key when that is a
+// non-empty string, else the key recomputed from its nodes -- each node's
+// type string, and for a KernelNode ":C<x>_<y>_<z>" (or ":0" when all are 0)
+// with the cluster dims taken from the node's kernel_node_attrs when they
+// hold clusterDimX, else from common_kernel_node_attrs when x is still 0,
+// else, when x is still 0, from whichever required_cluster_* fields the
+// node's func_attrs hold.  Values are read as unsigned 32-bit integers.
+std::string load_key(const Value& root) {
+  if (root.kind != Value::Object) fail("the graph document is not an object");
+  if (has(root, "topology_key")) {
+    const std::string& k = as_string(at(root, "topology_key", "graph"), "topology_key");
+    if (!k.empty()) return k;
+  }
+  const auto& nodes = as_array(at(root, "nodes", "graph"), "nodes");
+  std::string key;
+  key.reserve(nodes.size() * 14);
+  auto dims = [](const Value& o, uint32_t c[3]) {
+    c[0] = to_num<uint32_t>(at(o, "clusterDimX", "attrs"), "clusterDimX");
+    c[1] = to_num<uint32_t>(at(o, "clusterDimY", "attrs"), "clusterDimY");
+    c[2] = to_num<uint32_t>(at(o, "clusterDimZ", "attrs"), "clusterDimZ");
+  };
+  for (size_t n = 0; n < nodes.size(); ++n) {
+    if (n) key += ',';
+    const Value& no = nodes[n];
+    const std::string& type = as_string(at(no, "type", "node"), "node type");
+    key += type;
+    if (type != "KernelNode") continue;
+    uint32_t c[3] = {0, 0, 0};
+    const Value& p = at(no, "params", "node");
+    if (p.kind != Value::Object) fail("kernel params are not an object");
+    if (has(p, "kernel_node_attrs")) {
+      const Value& kna = at(p, "kernel_node_attrs", "params");
+      if (kna.kind != Value::Object) fail("kernel_node_attrs is not an object");
+      if (has(kna, "clusterDimX")) dims(kna, c);
+    }
+    if (c[0] == 0 && has(root, "common_kernel_node_attrs")) {
+      const Value& ck = at(root, "common_kernel_node_attrs", "graph");
+      if (ck.kind != Value::Object) fail("common_kernel_node_attrs is not an object");
+      if (has(ck, "clusterDimX")) dims(ck, c);
+    }
+    if (c[0] == 0 && has(p, "func_attrs")) {
+      const Value& fa = at(p, "func_attrs", "params");
+      if (fa.kind != Value::Object) fail("func_attrs is not an object");
+      if (has(fa, "required_cluster_width"))
+        c[0] = to_num<uint32_t>(at(fa, "required_cluster_width", "func_attrs"), "required_cluster_width");
+      if (has(fa, "required_cluster_height"))
+        c[1] = to_num<uint32_t>(at(fa, "required_cluster_height", "func_attrs"), "required_cluster_height");
+      if (has(fa, "required_cluster_depth"))
+        c[2] = to_num<uint32_t>(at(fa, "required_cluster_depth", "func_attrs"), "required_cluster_depth");
+    }
+    if (c[0] || c[1] || c[2])
+      key += ":C" + std::to_string(c[0]) + "_" + std::to_string(c[1]) + "_" + std::to_string(c[2]);
+    else
+      key += ":0";
+  }
+  return key;
+}
+
+// key_override: the TOPOLOGY_KEY section's bytes instead of topology_key.
+void build(const Value& root, std::vector<uint8_t>& out, const std::string* key_override) {
   if (root.kind != Value::Object) fail("the graph document is not an object");
   check_unique_keys(root);
   const auto& nodes = as_array(at(root, "nodes", "graph"), "nodes");
@@ -257,7 +317,9 @@ void build(const Value& root, std::vector<uint8_t>& out) {
     interned.emplace(s, off);
     return off;
   };
-  const std::string key = has(root, "topology_key") ? as_string(at(root, "topology_key", "graph"), "topology_key") : "";
+  const std::string key = key_override ? *key_override
+                         : has(root, "topology_key") ? as_string(at(root, "topology_key", "graph"), "topology_key")
+                                                     : "";
 
   const bool has_common = has(root, "common_kernel_node_attrs");
   fdy_common_attrs common{};
@@ -448,7 +510,11 @@ void build(const Value& root, std::vector<uint8_t>& out) {
 
 }  // namespace
 
-int cugraph_from_json(const char* text, size_t len, std::vector<uint8_t>& out, std::string& error) {
+namespace {
+
+// Parse `text` and run f(root); errors as FDY_E_* codes.
+template <typename F>
+int with_document(const char* text, size_t len, std::string& error, F&& fn) {
   json::Value root;
   json::Reader rd(text, len);
   if (!rd.parse(root, error)) {
@@ -456,7 +522,7 @@ int cugraph_from_json(const char* text, size_t len, std::vector<uint8_t>& out, s
     return FDY_E_FORMAT;
   }
   try {
-    build(root, out);
+    fn(root);
   } catch (const Fail& f) {
     error = "graph document: " + f.what;
     return f.code;
@@ -465,6 +531,23 @@ int cugraph_from_json(const char* text, size_t len, std::vector<uint8_t>& out, s
     return FDY_E_NOMEM;
   }
   return 0;
+}
+
+}  // namespace
+
+int cugraph_from_json(const char* text, size_t len, std::vector<uint8_t>& out, std::string& error) {
+  return with_document(text, len, error, [&](const Value& root) { build(root, out, nullptr); });
+}
+
+int load_topology_key(const char* text, size_t len, std::string& key, std::string& error) {
+  return with_document(text, len, error, [&](const Value& root) { key = load_key(root); });
+}
+
+int cugraph_for_load(const char* text, size_t len, std::vector<uint8_t>& out, std::string& error) {
+  return with_document(text, len, error, [&](const Value& root) {
+    const std::string key = load_key(root);
+    build(root, out, &key);
+  });
 }
 
 }  // namespace fdy

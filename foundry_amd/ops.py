@@ -42,7 +42,7 @@ from .region import Region
 from .restore import Archive
 
 MiB = 1 << 20
-SEC_ALLOC_EVENTS, SEC_OUTPUT_TENSORS = 8, 9
+SEC_GENERATORS, SEC_ALLOC_EVENTS, SEC_OUTPUT_TENSORS = 7, 8, 9
 
 # ---- allocation region (per thread, as the reference's TLS state, csrc/hook.cpp:218-251) ----
 
@@ -221,33 +221,6 @@ _SCALAR_TYPES = {
 }
 
 
-class _DLDevice(C.Structure):
-    _fields_ = [("device_type", C.c_int32), ("device_id", C.c_int32)]
-
-
-class _DLDataType(C.Structure):
-    _fields_ = [("code", C.c_uint8), ("bits", C.c_uint8), ("lanes", C.c_uint16)]
-
-
-class _DLTensor(C.Structure):
-    _fields_ = [("data", C.c_void_p), ("device", _DLDevice), ("ndim", C.c_int32), ("dtype", _DLDataType),
-                ("shape", C.POINTER(C.c_int64)), ("strides", C.POINTER(C.c_int64)), ("byte_offset", C.c_uint64)]
-
-
-class _DLManagedTensor(C.Structure):
-    pass
-
-
-_DELETER = C.CFUNCTYPE(None, C.POINTER(_DLManagedTensor))
-_DLManagedTensor._fields_ = [("dl_tensor", _DLTensor), ("manager_ctx", C.c_void_p), ("deleter", _DELETER)]
-_live_views: dict[int, tuple] = {}
-
-
-@_DELETER
-def _release_view(p):
-    _live_views.pop(C.addressof(p.contents), None)
-
-
 _PyCapsule_New = C.pythonapi.PyCapsule_New
 _PyCapsule_New.restype = C.py_object
 _PyCapsule_New.argtypes = [C.c_void_p, C.c_char_p, C.c_void_p]
@@ -257,25 +230,17 @@ _kDLROCM = 10
 def tensor_at(ptr: int, sizes: Sequence[int], strides: Sequence[int], dtype: torch.dtype, device_index: int = 0,
               requires_grad: bool = False) -> torch.Tensor:
     """A non-owning view of device memory at `ptr` (at::from_blob,
-    csrc/CUDAGraph.cpp:996): built through DLPack as unsigned integers of the
-    element size, then viewed as `dtype`."""
+    csrc/CUDAGraph.cpp:996): a DLPack view made by the library (whose deleter
+    frees only its own block, no Python involved), imported as unsigned
+    integers of the element size and viewed as `dtype`."""
     esize = torch.empty((), dtype=dtype).element_size()
     nd = len(sizes)
     shape = (C.c_int64 * max(1, nd))(*sizes)
     strd = (C.c_int64 * max(1, nd))(*strides)
-    m = _DLManagedTensor()
-    m.dl_tensor.data = ptr
-    m.dl_tensor.device = _DLDevice(_kDLROCM, device_index)
-    m.dl_tensor.ndim = nd
-    m.dl_tensor.dtype = _DLDataType(1, 8 * esize, 1)
-    m.dl_tensor.shape = C.cast(shape, C.POINTER(C.c_int64))
-    m.dl_tensor.strides = C.cast(strd, C.POINTER(C.c_int64))
-    m.dl_tensor.byte_offset = 0
-    m.manager_ctx = None
-    m.deleter = _release_view
-    _live_views[C.addressof(m)] = (m, shape, strd)
-    cap = _PyCapsule_New(C.addressof(m), b"dltensor", None)
-    t = torch.from_dlpack(cap).view(dtype)
+    view = _lib.restore_lib().fdy_dlpack_view(int(ptr), _kDLROCM, int(device_index), nd, shape, strd, 1, 8 * esize)
+    if not view:
+        raise RuntimeError(_lib.restore_lib().fdy_last_error().decode(errors="replace"))
+    t = torch.from_dlpack(_PyCapsule_New(view, b"dltensor", None)).view(dtype)
     if requires_grad:
         t.requires_grad_(True)
     return t
@@ -314,6 +279,100 @@ def _outputs_from(text: bytes, intervals):
         ts = [one(m) for m in metas]
         return tuple(ts) if kind == 3 else ts
     return None
+
+
+# ---- generator state (csrc/CUDAGraph.cpp:35-97, 133-160, 185-194) -----------
+
+_I64 = 1 << 63
+
+
+def _as_i64(v: int) -> int:
+    """int64_t(v) for a uint64 value, as the reference's fill_ receives it."""
+    v &= (1 << 64) - 1
+    return v - (1 << 64) if v >= _I64 else v
+
+
+class GeneratorState:
+    """The state a captured graph's random-number kernels read: the graph-safe
+    Philox seed and offset words (at::CUDAGeneratorState as the reference
+    overrides it, csrc/CUDAGraph.cpp:35-97).
+
+    The two words are allocated when the first graph registers (register_graph,
+    35-46): as two one-element int64 tensors, which torch's caching allocator
+    places 512 bytes apart in a fresh small-block segment of 2 MiB.  With an
+    allocation region enabled on this thread the segment is one region
+    allocation of 2 MiB at the cursor (what the reference's cuMemAlloc_v2
+    interposer does with that segment), seed at +0 and offset at +512; the
+    reference registers before replaying the graph's allocator events, so the
+    words land where they were at SAVE.  Without a region, a torch tensor of
+    the same layout.  replay_prologue (79-86) writes both words on the
+    current stream and advances the offset by the graph's increment rounded
+    up to a multiple of 4 (increase, 60-77)."""
+
+    SEGMENT = 2 * MiB
+    OFFSET_AT = 512
+
+    def __init__(self, seed: int, philox_offset_per_thread: int = 0):
+        self.seed = int(seed) & ((1 << 64) - 1)
+        self.philox_offset_per_thread = int(philox_offset_per_thread)
+        self._graphs: set[int] = set()
+        self._buf = None      # torch tensor keeping the words alive (no region)
+        self._region_ptr = 0  # region allocation holding them
+        self.seed_ptr = 0
+        self.offset_ptr = 0
+
+    def register_graph(self, graph) -> None:
+        if not self._graphs:
+            r = _region()
+            if r is not None and allocation_region_enabled():
+                self._region_ptr = r.alloc(self.SEGMENT)
+                self.seed_ptr = self._region_ptr
+            else:
+                self._buf = torch.empty(self.SEGMENT // 8, dtype=torch.int64, device="cuda")
+                self.seed_ptr = self._buf.data_ptr()
+            self.offset_ptr = self.seed_ptr + self.OFFSET_AT
+            dev = torch.cuda.current_device()
+            self._seed = tensor_at(self.seed_ptr, [1], [1], torch.int64, dev)
+            self._offset = tensor_at(self.offset_ptr, [1], [1], torch.int64, dev)
+        self._graphs.add(id(graph))
+
+    def unregister_graph(self, graph) -> None:
+        self._graphs.discard(id(graph))
+
+    def replay_prologue(self, wholegraph_increment: int) -> None:
+        if wholegraph_increment:
+            self._seed.fill_(_as_i64(self.seed))
+            self._offset.fill_(_as_i64(self.philox_offset_per_thread))
+            self.philox_offset_per_thread += (int(wholegraph_increment) + 3) // 4 * 4
+
+
+class GeneratorStateRegistry:
+    """Generator states by the id a graph saved them under; a new id makes a
+    state of the saved seed and offset 0 (get_state_from_id,
+    csrc/CUDAGraph.cpp:147-160)."""
+
+    def __init__(self):
+        self._states: dict[int, GeneratorState] = {}
+        self._lock = threading.Lock()
+
+    def get_state_from_id(self, state_id: int, seed: int) -> GeneratorState:
+        with self._lock:
+            st = self._states.get(int(state_id))
+            if st is None:
+                st = GeneratorState(seed, 0)
+                self._states[int(state_id)] = st
+            return st
+
+
+global_generator_state_registry = GeneratorStateRegistry()
+
+
+def generators_of(section: bytes) -> list[tuple[int, int, int]]:
+    """(id, seed, wholegraph_increment) rows of a GENERATORS section
+    (BinGenerator, include/BinaryGraphFormat.h:214-219)."""
+    n = len(section) // 24
+    a = np.frombuffer(section[: 24 * n], dtype="<u8").reshape(n, 3)
+    return [(int(r[0]), int(r[1]), int(r[2])) for r in a]
 
 
 # ---- graphs -----------------------------------------------------------------
@@ -366,6 +425,8 @@ class CUDAGraph:
         self.keep_graph = keep_graph
         self._pending: PendingGraphLoads | None = None
         self._index = -1
+        # generator state -> wholegraph increment (captured_generator_states_)
+        self._generators: dict[GeneratorState, int] = {}
 
     @classmethod
     def _restored(cls, pending: PendingGraphLoads, index: int) -> "CUDAGraph":
@@ -393,14 +454,26 @@ class CUDAGraph:
         gg = self._pending.group_graph(self._index)
         stream = torch.cuda.current_stream()
         gg.select(self._index, stream)
+        for state, increment in self._generators.items():  # 469-472
+            state.replay_prologue(increment)
         gg.launch(stream)
 
     def reset(self) -> None:
+        for state in self._generators:
+            state.unregister_graph(self)
+        self._generators = {}
         self._pending = None
         self._index = -1
 
-    def register_generator_state(self, generator) -> None:
-        raise NotImplementedError("graph capture is not part of this build (LOAD path only)")
+    def register_generator_state(self, state, wholegraph_increment: int = 0) -> None:
+        """csrc/CUDAGraph.cpp:185-194: run `state`'s replay prologue with this
+        increment before every replay.  A torch.Generator (the capture-side
+        overload) is refused: capture is not part of this build."""
+        if not isinstance(state, GeneratorState):
+            raise NotImplementedError("registering a torch generator is part of capture, which this build "
+                                      "does not provide (LOAD path only)")
+        state.register_graph(self)
+        self._generators[state] = int(wholegraph_increment)
 
     def _group(self) -> GroupGraph:
         if self._pending is None:
@@ -461,14 +534,21 @@ class CUDAGraph:
 
     @staticmethod
     def finish_one_graph_load(pending: PendingGraphLoads, index: int):
-        """csrc/CUDAGraphParallel.cpp:2034-2069: replay graph `index`'s
-        allocator events into the region (in SAVE order), then rebuild its
-        output tensors.  Raises IndexError out of range, as the reference's
-        std::out_of_range does through pybind."""
+        """csrc/CUDAGraphParallel.cpp:2034-2069: register graph `index`'s
+        saved generator states, replay its allocator events into the region
+        (in SAVE order), then rebuild its output tensors.  Raises IndexError
+        out of range, as the reference's std::out_of_range does through
+        pybind."""
         if index < 0 or index >= len(pending.graphs):
             raise IndexError(f"finish_one_graph_load: index {index} out of range "
                              f"(num_graphs={len(pending.graphs)})")
         if not pending.finished[index]:
+            # Deferred generators first, so that their words land where SAVE
+            # put them (2048-2059).
+            graph = pending.graphs[index]
+            for state_id, seed, increment in generators_of(pending.archive.section(index, SEC_GENERATORS)):
+                graph.register_generator_state(global_generator_state_registry.get_state_from_id(state_id, seed),
+                                               increment)
             events = pending.archive.section(index, SEC_ALLOC_EVENTS)
             r = _region()
             if events and r is not None:
@@ -492,6 +572,8 @@ class CUDAGraph:
 # The names csrc/binding.cpp binds (a star import of this module gives these).
 __all__ = [
     "CUDAGraph",
+    "GeneratorState",
+    "GeneratorStateRegistry",
     "PendingGraphLoads",
     "free_preallocated_region",
     "get_current_alloc_offset",

@@ -276,6 +276,19 @@ def cugraph_from_json(text) -> bytes:
     return bytes(buf)[: n.value]
 
 
+def load_topology_key(text) -> bytes:
+    """The key the LOAD path groups a graph read from its JSON document by
+    (csrc/CUDAGraphParallel.cpp:1791-1841); no device needed."""
+    data = text.encode() if isinstance(text, str) else bytes(text)
+    n = C.c_uint64()
+    rc = restore_lib().fdy_load_topology_key(data, len(data), None, 0, C.byref(n))
+    if rc != -8:  # FDY_E_CAPACITY: the size is known
+        check(rc)
+    buf = C.create_string_buffer(max(1, n.value))
+    check(restore_lib().fdy_load_topology_key(data, len(data), buf, n.value, C.byref(n)))
+    return buf.raw[: n.value]
+
+
 def cugraph_path(json_path: str) -> str:
     """The archive path CUDAGraph::save writes beside a graph's JSON
     (csrc/CUDAGraph.cpp:1494-1500): ".json" replaced, else ".cugraph" appended."""

@@ -16,7 +16,7 @@
  *      4 groups, blobs 32-1024 B in 1-16 params, 25% pointers into a 64 GiB
  *      region of 40k intervals, 3% of words differ.
  *   3  256 graphs x ~3000 nodes (85% kernel, 10% memset, 5% memcpy), 16 groups,
- *      blobs up to 4 KiB, 10% of words differ in 64-256 B runs.
+ *      blobs up to 4 KiB in 1-40 params, 10% of words differ in 64-256 B runs.
  *   4  words only: 1 GiB of packed words, 40% pointers, 2M intervals tiling
  *      200 GiB, 1% boundary pointers (lo, hi-1, hi, lo-1).
  *   5  1024 graphs x 5000 nodes in 32 groups, 1-8% of words differ per graph.

@@ -67,7 +67,8 @@ extern "C" {
 /* ---- per-graph status bits (fdy_get_graph_status) ---------------------- */
 #define FDY_GRAPH_TYPE_MISMATCH 0x01u /* recomputed node-type digest differs from the template's */
 #define FDY_GRAPH_BAD_PARAMS 0x02u    /* a param/arg/name range lies outside its section */
-#define FDY_GRAPH_COLLISION 0x08u     /* equal key digest but different key bytes */
+#define FDY_GRAPH_COLLISION 0x08u     /* a lower graph's key has an equal digest and length but other bytes
+                                         (grouped apart all the same: groups follow the exact key bytes) */
 #define FDY_GRAPH_NODE_COUNT 0x10u    /* node count differs from the template (switch refused) */
 #define FDY_GRAPH_OVERFLOW 0x20u      /* param image larger than the capacity the sections allow */
 
@@ -99,7 +100,10 @@ const char* fdy_version(void);
  * sibling ".cugraph" (csrc/CUDAGraphParallel.cpp:1591-1594).  Where that
  * file is missing, shorter than a header or not a v1 header, the graph is
  * read from the JSON document at the path itself, as the reference then
- * parses it (1606-1617), converted with fdy_cugraph_from_json.  Files are
+ * parses it (1606-1617), converted with fdy_cugraph_from_json except that
+ * its TOPOLOGY_KEY section holds the key the reference groups such a graph
+ * by (fdy_load_topology_key: recomputed from the nodes when the document's
+ * topology_key is missing or empty, 1796-1840).  Files are
  * read on min(num_threads, n) host threads (csrc/CUDAGraphParallel.cpp:
  * 1553,1584), validated, and copied to HBM in one transfer.  Replaces
  * Phase 1a. */
@@ -116,6 +120,18 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
  * allocator_events or output_tensors is FDY_E_UNSUPPORTED.  No device
  * needed. */
 int fdy_cugraph_from_json(const char* json, uint64_t len, uint8_t* out, uint64_t cap, uint64_t* size_out);
+/* The key start_graph_builds groups a graph read from its JSON document by
+ * (csrc/CUDAGraphParallel.cpp:1791-1841): the document's topology_key when
+ * it is a non-empty string, else the key recomputed from its nodes (node
+ * type strings joined by ','; a KernelNode gets ":C<x>_<y>_<z>" from its
+ * kernel_node_attrs cluster dims, else the common attrs', else its
+ * func_attrs' required_cluster_* fields, or ":0" when all are zero).  A
+ * graph read from a .cugraph is grouped by its saved key as it stands.
+ * The key's bytes (no NUL) go to out; *size_out receives its length, and
+ * with out NULL or cap below it the call returns FDY_E_CAPACITY.  No device
+ * needed. */
+int fdy_load_topology_key(const char* json, uint64_t len, char* out, uint64_t cap, uint64_t* size_out);
+
 /* fdy_cugraph_from_json into the file bin_path (CUDAGraph::save_binary;
  * CUDAGraph::save names it after the .json path, csrc/CUDAGraph.cpp:
  * 1494-1501).  FDY_E_IO when the file cannot be written, where the
@@ -166,7 +182,9 @@ int fdy_archive_set_manifest(fdy_archive* a, const char* text, uint64_t len, con
  *   1. digests per graph (CRC-64/XZ): saved topology key, dependency table,
  *      recomputed node-type stream, kernel-entry stream;
  *   2. template_of[g] = lowest index with an identical saved topology key
- *      (csrc/CUDAGraphParallel.cpp:1788-1851), verified byte-exactly;
+ *      (csrc/CUDAGraphParallel.cpp:1788-1851): found by key digest and
+ *      length, then compared byte for byte (a digest collision never merges
+ *      two keys);
  *   3. per node: layout/descriptor compare against the template, param-image
  *      layout, memset/memcpy pointer relocation;
  *   4. fused diff + relocate over every param word: writes the relocated
@@ -223,6 +241,15 @@ int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t
 int fdy_reloc_plan_destroy(fdy_reloc_plan* p);
 int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
                        void* stream);
+
+/* A non-owning DLPack view (a DLManagedTensor*, dlpack.h v0.8 layout) of
+ * `ndim`-dimensional device memory at ptr: what the reference's output
+ * tensors are (at::from_blob at the saved data_ptr, csrc/CUDAGraph.cpp:
+ * 971-999), for a framework to import (torch.from_dlpack through a
+ * "dltensor" capsule).  Its deleter frees only the view's own host block,
+ * never the memory it describes.  NULL on bad arguments. */
+void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int32_t ndim, const int64_t* shape,
+                      const int64_t* strides, uint8_t code, uint8_t bits);
 
 /* Timing of the last fdy_restore, from HIP events recorded on its stream
  * around each kernel (milliseconds).  Synchronizes. */

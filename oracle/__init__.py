@@ -43,6 +43,8 @@ def lib() -> C.CDLL:
             "orc_group_by_keys": (C.c_int, [C.POINTER(C.c_char_p), u64p, C.c_uint32, u32p]),
             "orc_group_manifest": (C.c_int, [C.c_char_p, C.c_uint64, C.POINTER(C.c_char_p), C.c_uint32, u32p]),
             "orc_extract_node_params": (C.c_int64, [C.c_char_p, C.c_uint64, C.c_uint32, u8p, C.c_uint64]),
+            "orc_effective_attrs": (C.c_int, [C.c_char_p, C.c_uint64, C.c_uint32, C.POINTER(C.c_int32)]),
+            "orc_set_mutation": (None, [C.c_int]),
             "orc_restore": (
                 C.c_int,
                 [C.POINTER(u8p), u64p, C.c_uint32, u64p, u64p, u64p, C.c_uint64, C.c_uint32, u32p, C.c_uint32,
@@ -137,6 +139,19 @@ def extract_node_params(image: bytes, node: int, cap: int = 1 << 20) -> bytes:
     if n < 0:
         raise ValueError("bounds error")
     return bytes(buf[:n])
+
+
+def effective_attrs(image: bytes, node: int) -> list[int]:
+    """The 17 merged launch-attribute fields of kernel node `node`."""
+    out = (C.c_int32 * 17)()
+    if lib().orc_effective_attrs(image, len(image), node, out):
+        raise ValueError("not a kernel node")
+    return list(out)
+
+
+def set_mutation(m: int) -> None:
+    """Plant mistake m in the oracle's attribute merge (0 removes it); test use only."""
+    lib().orc_set_mutation(m)
 
 
 def relocate_word(w: int, lo, hi, new_lo, policy: int = 0) -> int:

@@ -197,26 +197,56 @@ Attrs attrs_from_block(const uint8_t* b) {
   return a;
 }
 
+// A planted mistake in the merge below (orc_set_mutation; 0 = none).  Test
+// infrastructure for showing that the attribute fixtures pin the merge:
+// each mutation must change an effective attribute or a DESC flag they hold.
+int g_mutation = 0;
+
+// Per-node attrs p merged over a (csrc/CUDAGraphParallel.cpp:1345-1373):
+// dims and the map/carveout when flagged, scalars when not negative.
+void merge_over(Attrs& a, const Attrs& p) {
+  if (p.has_cluster) { a.has_cluster = 1; a.cx = p.cx; a.cy = p.cy; a.cz = p.cz; }
+  if (p.has_pref) { a.has_pref = 1; a.px = p.px; a.py = p.py; a.pz = p.pz; }
+  if (p.sched >= 0) a.sched = p.sched;
+  if (p.coop >= 0) a.coop = p.coop;
+  if (p.prio >= 0) a.prio = p.prio;
+  if (p.msd >= 0) a.msd = p.msd;
+  if (p.has_map) { a.has_map = 1; a.map_def = p.map_def; a.map_remote = p.map_remote; }
+  if (p.has_carve) { a.has_carve = 1; a.carve = p.carve; }
+}
+
 Attrs effective_attrs(const View& v, const uint8_t* e) {
   Attrs a;
-  if (v.flags & HDR_COMMON && v.sz[S_COMMON] >= 52) a = attrs_from_block(v.d + v.off[S_COMMON]);
+  const bool has_common = v.flags & HDR_COMMON && v.sz[S_COMMON] >= 52 && g_mutation != 5;  // 5: common ignored
+  if (has_common) a = attrs_from_block(v.d + v.off[S_COMMON]);
   if (rd<uint32_t>(e, 76) != 0) {
     Attrs p = attrs_from_block(e + 76);
-    if (p.has_cluster) { a.has_cluster = 1; a.cx = p.cx; a.cy = p.cy; a.cz = p.cz; }
-    if (p.has_pref) { a.has_pref = 1; a.px = p.px; a.py = p.py; a.pz = p.pz; }
-    if (p.sched >= 0) a.sched = p.sched;
-    if (p.coop >= 0) a.coop = p.coop;
-    if (p.prio >= 0) a.prio = p.prio;
-    if (p.msd >= 0) a.msd = p.msd;
-    if (p.has_map) { a.has_map = 1; a.map_def = p.map_def; a.map_remote = p.map_remote; }
-    if (p.has_carve) { a.has_carve = 1; a.carve = p.carve; }
+    if (g_mutation == 1 && has_common) {  // 1: common attrs win over per-node ones
+      Attrs c = a;
+      a = Attrs();
+      merge_over(a, p);
+      merge_over(a, c);
+    } else if (g_mutation == 4) {  // 4: per-node attrs replace the common ones wholesale
+      a = p;
+    } else {
+      merge_over(a, p);
+      if (g_mutation == 2) {  // 2: flagged per-node scalars override even when negative
+        const uint32_t f = rd<uint32_t>(e, 76);
+        if (f & KNA_SCHED) a.sched = p.sched;
+        if (f & KNA_COOP) a.coop = p.coop;
+        if (f & KNA_PRIO) a.prio = p.prio;
+        if (f & KNA_MSD) a.msd = p.msd;
+      }
+    }
   }
+  // Required cluster dims win over both (1376-1385); zero dims become 1.
   int32_t w = rd<int32_t>(e, 64), h = rd<int32_t>(e, 68), dd = rd<int32_t>(e, 72);
-  if (w > 0 || h > 0 || dd > 0) {
+  if ((w > 0 || h > 0 || dd > 0) && g_mutation != 3) {  // 3: required cluster ignored
     a.has_cluster = 1;
-    a.cx = w > 0 ? w : 1;
-    a.cy = h > 0 ? h : 1;
-    a.cz = dd > 0 ? dd : 1;
+    const int32_t one = g_mutation == 6 ? 0 : 1;  // 6: zero dims stay 0
+    a.cx = w > 0 ? w : one;
+    a.cy = h > 0 ? h : one;
+    a.cz = dd > 0 ? dd : one;
   }
   return a;
 }
@@ -341,7 +371,7 @@ struct Graph {
 };
 
 constexpr uint8_t F_LAYOUT = 1, F_DESC = 2, F_RAGGED = 4, F_TEMPLATE = 8;
-constexpr uint32_t ST_TYPE = 1, ST_BAD = 2, ST_COUNT = 0x10;
+constexpr uint32_t ST_TYPE = 1, ST_BAD = 2, ST_COLLISION = 8, ST_COUNT = 0x10;
 
 // Pass 1 of a graph: layout, relocated image, pointers, digests.
 void build_graph(Graph& g, const Table& tab) {
@@ -678,6 +708,19 @@ int orc_group_manifest(const char* text, uint64_t len, const char* const* names,
   return 0;
 }
 
+void orc_set_mutation(int m) { g_mutation = m; }
+
+int orc_effective_attrs(const uint8_t* image, uint64_t size, uint32_t node, int32_t* out) {
+  View v;
+  if (!open_view(image, size, &v) || node >= v.num_nodes) return -1;
+  const uint8_t* e = node_at(v, node);
+  if (e[4] != N_KERNEL) return -1;
+  const Attrs a = effective_attrs(v, e);
+  static_assert(sizeof(Attrs) == 17 * sizeof(int32_t), "17 attribute fields");
+  std::memcpy(out, &a, sizeof(Attrs));
+  return 0;
+}
+
 int64_t orc_extract_node_params(const uint8_t* image, uint64_t size, uint32_t node, uint8_t* out, uint64_t cap) {
   View v;
   if (!open_view(image, size, &v) || node >= v.num_nodes) return -1;
@@ -717,6 +760,13 @@ int orc_restore(const uint8_t* const* images, const uint64_t* sizes, uint32_t n,
       kl[i] = keys[i].size();
     }
     orc_group_by_keys(kp.data(), kl.data(), n, r->tmpl.data());
+    // Collision bit (a build-defined report, the grouping above is by exact
+    // key strings): a graph below i's template whose key has the same
+    // CRC-64/XZ and length as i's but other bytes.
+    for (uint32_t i = 0; i < n; ++i)
+      for (uint32_t j = 0; j < r->tmpl[i]; ++j)
+        if (r->g[j].dig[0] == r->g[i].dig[0] && keys[j].size() == keys[i].size() && keys[j] != keys[i])
+          r->g[i].status |= ST_COLLISION;
   }
   for (uint32_t i = 0; i < n; ++i) {
     if (r->tmpl[i] >= n) {

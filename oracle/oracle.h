@@ -54,6 +54,20 @@ int orc_group_by_keys(const char* const* keys, const uint64_t* lens, uint32_t n,
 int orc_group_manifest(const char* manifest, uint64_t len, const char* const* names, uint32_t n,
                        uint32_t* out);
 
+/* Effective launch attributes of kernel node `node`, merged as
+ * prepare_on_demand_graph_binary does (csrc/CUDAGraphParallel.cpp:1211-1389):
+ * out[17] = has_cluster, cx, cy, cz, has_pref, px, py, pz, sched, coop, prio,
+ * msd, has_map, map_default, map_remote, has_carveout, carveout.  -1 if the
+ * node is not a kernel node or the image is bad. */
+int orc_effective_attrs(const uint8_t* image, uint64_t size, uint32_t node, int32_t* out);
+
+/* Test hook: plant mistake m (1..6) in the attribute merge, 0 to remove it.
+ * 1 common wins over per-node, 2 negative per-node scalars override,
+ * 3 required cluster ignored, 4 per-node attrs replace common wholesale,
+ * 5 common attrs ignored, 6 required zero dims stay 0.  Not thread-safe;
+ * for the tests that show the attribute fixtures pin the merge. */
+void orc_set_mutation(int m);
+
 /* Per-param byte extraction of one kernel node (csrc/CUDAGraphParallel.cpp:1391-1409):
  * writes the node's params back-to-back into out (or the arg buffer for
  * extra-style nodes).  Returns bytes written, -1 on bounds error. */

@@ -235,7 +235,9 @@ def _serialise(v) -> str:
     return json.dumps(v, ensure_ascii=False, separators=(",", ":"))
 
 
-def save_binary(text: bytes | str) -> bytes:
+def save_binary(text: bytes | str, key_override: bytes | None = None) -> bytes:
+    """The archive bytes; key_override, if given, is written as the topology
+    key instead of the document's."""
     root = parse(text)
     if not isinstance(root, dict):
         raise WriterError("document is not an object")
@@ -252,6 +254,8 @@ def save_binary(text: bytes | str) -> bytes:
         return interned[s]
 
     key = _str(root["topology_key"]) if "topology_key" in root else b""
+    if key_override is not None:
+        key = key_override
     has_common = "common_kernel_node_attrs" in root
     common = _kna_bytes(_kna(root["common_kernel_node_attrs"])) if has_common else b""
 
@@ -343,3 +347,61 @@ def save_binary(text: bytes | str) -> bytes:
     header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, flags, len(entries), len(deps), len(gens), NUM_SECTIONS,
                          len(interned))
     return header + table + body
+
+
+def load_topology_key(text: bytes | str) -> bytes:
+    """The key start_graph_builds groups a graph read from its JSON document
+    by (csrc/CUDAGraphParallel.cpp:1791-1841), restated line by line:
+    topology_key when present and non-empty (1796-1797); otherwise, per node,
+    the type string (1802-1806), and for a KernelNode the cluster dims from
+    kernel_node_attrs when it contains clusterDimX (1809-1816), else from
+    common_kernel_node_attrs when x is still 0 (1817-1824), else each
+    required_cluster_* field func_attrs contains, when x is still 0
+    (1825-1832); ":C<x>_<y>_<z>" if any is nonzero, ":0" otherwise
+    (1833-1838).  Numbers as to_number<unsigned int>."""
+    root = parse(text)
+    if not isinstance(root, dict):
+        raise WriterError("document is not an object")
+    if "topology_key" in root and _str(root["topology_key"]) != b"":
+        return _str(root["topology_key"])
+    parts = []
+    for no in _arr(_get(root, "nodes")):
+        t = _str(_get(no, "type"))
+        if t != b"KernelNode":
+            parts.append(t)
+            continue
+        cdx = cdy = cdz = 0
+        p = _get(no, "params")
+        if not isinstance(p, dict):
+            raise WriterError("params not an object")
+        if "kernel_node_attrs" in p:
+            kna = p["kernel_node_attrs"]
+            if not isinstance(kna, dict):
+                raise WriterError("kernel_node_attrs not an object")
+            if "clusterDimX" in kna:
+                cdx, cdy, cdz = (u32(_get(kna, k)) for k in ("clusterDimX", "clusterDimY", "clusterDimZ"))
+        if cdx == 0 and "common_kernel_node_attrs" in root:
+            ck = root["common_kernel_node_attrs"]
+            if not isinstance(ck, dict):
+                raise WriterError("common_kernel_node_attrs not an object")
+            if "clusterDimX" in ck:
+                cdx, cdy, cdz = (u32(_get(ck, k)) for k in ("clusterDimX", "clusterDimY", "clusterDimZ"))
+        if cdx == 0 and "func_attrs" in p:
+            fa = p["func_attrs"]
+            if not isinstance(fa, dict):
+                raise WriterError("func_attrs not an object")
+            if "required_cluster_width" in fa:
+                cdx = u32(fa["required_cluster_width"])
+            if "required_cluster_height" in fa:
+                cdy = u32(fa["required_cluster_height"])
+            if "required_cluster_depth" in fa:
+                cdz = u32(fa["required_cluster_depth"])
+        parts.append(t + (b":C%d_%d_%d" % (cdx, cdy, cdz) if (cdx or cdy or cdz) else b":0"))
+    return b",".join(parts)
+
+
+def load_archive(text: bytes | str) -> bytes:
+    """The archive the product restores a graph read from its JSON document
+    from: save_binary's, with load_topology_key's key as the topology key
+    (the reference keeps that key beside the parsed document)."""
+    return save_binary(text, key_override=load_topology_key(text))

@@ -113,13 +113,17 @@ def saved_key(nodes) -> bytes:
     return ",".join(parts).encode()
 
 
-FLAG_ALLOC_EVENTS, FLAG_OUTPUT_TENSORS = 4, 8
+FLAG_ALLOC_EVENTS, FLAG_OUTPUT_TENSORS, FLAG_GENERATORS = 4, 8, 16
 
 
 def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: bytes = b"",
-          output_tensors: bytes = b"", common_ints=(-1, -1, -1, -1)) -> bytes:
+          output_tensors: bytes = b"", common_ints=(-1, -1, -1, -1), key: bytes | None = None,
+          generators=()) -> bytes:
     """Archive bytes for `nodes` (Kernel/Memset/...); deps are (from_id, to_id).
-    alloc_events / output_tensors are the JSON texts of those sections."""
+    alloc_events / output_tensors are the JSON texts of those sections.
+    `key` replaces the saved topology key CUDAGraph::save would write;
+    `generators` are (id, seed, wholegraph_increment) rows of the GENERATORS
+    section (BinGenerator, include/BinaryGraphFormat.h:214-219)."""
     ids = list(node_ids) if node_ids is not None else list(range(len(nodes)))
     strings = b""
     name_at = {}
@@ -162,9 +166,10 @@ def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: byte
     if common_cluster is not None:
         common = struct.pack("<4I", KNA_CLUSTER_DIM, *common_cluster) + struct.pack("<3I", 0, 0, 0)
         common += struct.pack("<4i", *common_ints) + struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
+    gens = b"".join(struct.pack("<3Q", *g) for g in generators)
     secs = [strings, b"".join(entries), b"".join(struct.pack("<II", *d) for d in deps),
-            b"".join(struct.pack("<II", *p) for p in pidx), pdata, arg_data, common, b"", alloc_events,
-            output_tensors, saved_key(nodes)]
+            b"".join(struct.pack("<II", *p) for p in pidx), pdata, arg_data, common, gens, alloc_events,
+            output_tensors, saved_key(nodes) if key is None else key]
     off = 64 + 11 * 24
     table, body = b"", b""
     for i, s in enumerate(secs):
@@ -174,7 +179,9 @@ def write(nodes, deps=(), node_ids=None, common_cluster=None, alloc_events: byte
         off += len(s) + pad
     flags = (FLAG_COMMON if common else 0) | (FLAG_DEPS if deps else 0)
     flags |= (FLAG_ALLOC_EVENTS if alloc_events else 0) | (FLAG_OUTPUT_TENSORS if output_tensors else 0)
-    header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, flags, len(nodes), len(deps), 0, 11, len(name_at))
+    flags |= FLAG_GENERATORS if generators else 0
+    header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, flags, len(nodes), len(deps), len(generators), 11,
+                         len(name_at))
     return header + table + body
 
 

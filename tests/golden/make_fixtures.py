@@ -29,17 +29,30 @@ FLAG_COMMON, FLAG_DEPS = 1, 2
 NONE = 0xFFFFFFFF
 
 
+# Launch-attribute flag bits (BinaryGraphFormat.h KNA_*) and the 52-byte
+# attribute block shared by a kernel entry (entry bytes 76..128) and the
+# common-attrs section (BinKernelNode 110-142, BinCommonKernelAttrs 197-212).
+KNA_PREF, KNA_SCHED, KNA_COOP, KNA_PRIO, KNA_MSD, KNA_MAP, KNA_CARVE = 2, 4, 8, 16, 32, 64, 128
+KNA_ALL = 255
+
+
+def kna(flags=0, cluster=(0, 0, 0), pref=(0, 0, 0), sched=-1, coop=-1, prio=-1, msd=-1, mp=(0, 0), carve=0):
+    b = struct.pack("<4I", flags, *cluster)                     # flags, clusterDim
+    b += struct.pack("<3I", *pref)                              # preferredClusterDim
+    b += struct.pack("<4i", sched, coop, prio, msd)             # scheduling, cooperative, priority, memSyncDomain
+    b += struct.pack("<4B", mp[0], mp[1], 0, 0)                 # map default/remote, attrQueryAvailable, pad
+    b += struct.pack("<I", carve)                               # preferredSharedMemCarveout
+    assert len(b) == 52
+    return b
+
+
 def kernel_entry(node_id, block, grid, bhash, name_off, name_len, req=(0, 0, 0), kna_flags=0, cluster=(0, 0, 0),
-                 pio=0, npar=0, aoff=NONE, asize=0):
+                 pio=0, npar=0, aoff=NONE, asize=0, attrs=None):
     arm = struct.pack("<7I", *block, *grid, 0)                 # block, grid, sharedMemBytes
     arm += struct.pack("<Q", bhash)                             # binary_hash (entry offset 36)
     arm += struct.pack("<II", name_off, name_len)
     arm += struct.pack("<6i", 0, -1, 0, *req)                   # func_attrs
-    arm += struct.pack("<4I", kna_flags, *cluster)              # kna_flags, clusterDim
-    arm += struct.pack("<3I", 0, 0, 0)                          # preferredClusterDim
-    arm += struct.pack("<4i", -1, -1, -1, -1)                   # scheduling, cooperative, priority, memSyncDomain
-    arm += struct.pack("<4B", 0, 0, 0, 0)                       # map default/remote, attrQueryAvailable, pad
-    arm += struct.pack("<I", 0)                                 # preferredSharedMemCarveout
+    arm += attrs if attrs is not None else kna(kna_flags, cluster)
     arm += struct.pack("<4I", pio, npar, aoff, asize)
     assert len(arm) == 136
     return entry(node_id, 0, arm)
@@ -67,10 +80,7 @@ def event_entry(node_id, ntype, event_id):
 
 
 def common_attrs(cluster):
-    b = struct.pack("<4I", KNA_CLUSTER_DIM, *cluster) + struct.pack("<3I", 0, 0, 0)
-    b += struct.pack("<4i", -1, -1, -1, -1) + struct.pack("<4B", 0, 0, 0, 0) + struct.pack("<I", 0)
-    assert len(b) == 52
-    return b
+    return kna(KNA_CLUSTER_DIM, cluster)
 
 
 def archive(strings, nodes, deps, pidx, pdata, arg, common, key, num_strings):
@@ -86,6 +96,20 @@ def archive(strings, nodes, deps, pidx, pdata, arg, common, key, num_strings):
     flags = (FLAG_COMMON if common else 0) | (FLAG_DEPS if deps else 0)
     header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, flags, len(nodes), len(deps), 0, 11, num_strings)
     assert len(header) == 64
+    return header + table + body
+
+
+def archive_raw_pidx(strings, nodes, pidx_bytes, pdata, key, num_strings):
+    """archive() with the param-index section given as raw bytes."""
+    secs = [strings, b"".join(nodes), b"", pidx_bytes, pdata, b"", b"", b"", b"", b"", key]
+    off = 64 + 11 * 24
+    table, body = b"", b""
+    for i, s in enumerate(secs):
+        table += struct.pack("<IIQQ", i, 0, off, len(s))
+        pad = (8 - len(s) % 8) % 8
+        body += s + b"\0" * pad
+        off += len(s) + pad
+    header = struct.pack("<8s7I28x", b"CUGRAPH\0", 1, 0, len(nodes), 0, 0, 11, num_strings)
     return header + table + body
 
 
@@ -135,7 +159,135 @@ def main():
     d_nodes = [kernel_entry(0, (32, 1, 1), (1, 1, 1), 0x9999AAAABBBBCCCC, 8, 9, req=(0, 2, 0), pio=0, npar=1)]
     d = archive(strings, d_nodes, [], [(0, 8)], le(0xDEADBEEF), b"", None, b"", 2)
 
-    for name, img in (("tiny_a", a), ("tiny_b", b), ("tiny_c", c), ("tiny_d", d)):
+    # attr_t / attr_m: one template and one member whose launch attributes come
+    # from conflicting sources.  attr_t's common attrs set every attribute;
+    # its nodes override some of them per node (negative scalar values do
+    # not override, csrc/CUDAGraphParallel.cpp:1362-1369) and node 1 has a
+    # required cluster (0, 3, 0), which wins over both (1376-1385; zero dims
+    # become 1).  attr_m has no common attrs and spells every attribute out
+    # per node, so each of its nodes' effective attributes is the value
+    # written.  The effective attributes below are derived by hand from
+    # those rules; a node's DESC flag is set exactly where they differ
+    # (everything else about the two nodes is equal).
+    ct = dict(cluster=(4, 1, 1), pref=(8, 1, 1), sched=1, coop=1, prio=2, msd=1, mp=(1, 2), carve=50)
+
+    def full(**kw):  # every attribute explicit: attr_t's common values, some replaced
+        v = dict(ct)
+        v.update(kw)
+        return kna(KNA_ALL, **v)
+
+    attr_cases = [  # (attr_t node's per-node block, its required cluster, attr_m node's block)
+        (kna(KNA_CLUSTER_DIM, (2, 1, 1)), (0, 0, 0), full(cluster=(2, 1, 1))),
+        (kna(KNA_CLUSTER_DIM, (2, 1, 1)), (0, 3, 0), full(cluster=(1, 3, 1))),
+        (kna(KNA_SCHED | KNA_COOP | KNA_PRIO | KNA_MSD, sched=-1, coop=0, prio=-1, msd=3), (0, 0, 0),
+         full(coop=0, msd=3)),
+        (kna(KNA_PRIO, prio=5), (0, 0, 0), full(prio=5)),
+        (kna(0, cluster=(9, 9, 9), prio=9), (0, 0, 0), full()),   # values without flags are not read
+        (kna(0), (0, 0, 0), full(cluster=(2, 1, 1))),             # a real difference
+        (kna(KNA_PREF | KNA_CARVE, pref=(3, 1, 1), carve=20), (0, 0, 0), full(pref=(3, 1, 1), carve=20)),
+        (kna(KNA_PRIO, prio=7), (0, 0, 0), full(prio=2)),         # a real difference
+        (kna(KNA_MAP, mp=(3, 0)), (0, 0, 0), full(mp=(3, 0))),
+        (kna(KNA_COOP, coop=-5), (0, 0, 0), full()),
+    ]
+    # Effective attributes, in the order has_cluster, cx, cy, cz, has_pref,
+    # px, py, pz, sched, coop, prio, msd, has_map, map_default, map_remote,
+    # has_carveout, carveout.
+    common_eff = [1, 4, 1, 1, 1, 8, 1, 1, 1, 1, 2, 1, 1, 1, 2, 1, 50]
+
+    def eff(**kw):
+        v = list(common_eff)
+        for k, x in kw.items():
+            at = {"c": 1, "p": 5, "sched": 8, "coop": 9, "prio": 10, "msd": 11, "map": 13, "carve": 16}[k]
+            x = list(x) if isinstance(x, tuple) else [x]
+            v[at:at + len(x)] = x
+        return v
+
+    eff_t = [eff(c=(2, 1, 1)), eff(c=(1, 3, 1)), eff(coop=0, msd=3), eff(prio=5), eff(), eff(),
+             eff(p=(3, 1, 1), carve=20), eff(prio=7), eff(map=(3, 0)), eff()]
+    eff_m = [eff(c=(2, 1, 1)), eff(c=(1, 3, 1)), eff(coop=0, msd=3), eff(prio=5), eff(), eff(c=(2, 1, 1)),
+             eff(p=(3, 1, 1), carve=20), eff(prio=2), eff(map=(3, 0)), eff()]
+    desc_m = [0, 0, 0, 0, 0, 1, 0, 1, 0, 0]
+    # Cluster dims of the recomputed key: per-node, else common, else required.
+    key_t = ",".join("KernelNode:C%d_%d_%d" % c for c in
+                     [(2, 1, 1), (2, 1, 1)] + [(4, 1, 1)] * 8)
+    key_m = ",".join("KernelNode:C%d_%d_%d" % c for c in
+                     [(2, 1, 1), (1, 3, 1), (4, 1, 1), (4, 1, 1), (4, 1, 1), (2, 1, 1)] + [(4, 1, 1)] * 4)
+    params_t = [0x100 * n + 1 for n in range(len(attr_cases))]
+    params_m = list(params_t)
+    params_m[7] = 0x7FF
+
+    def attr_archive(side, common, params):
+        nodes = []
+        for n, case in enumerate(attr_cases):
+            block, req = (case[0], case[1]) if side == "t" else (case[2], case[1])
+            nodes.append(kernel_entry(n, (128, 1, 1), (32, 1, 1), 0x1111222233334444, 0, 7, req=req, pio=8 * n,
+                                      npar=1, attrs=block))
+        pidx = [(8 * n, 8) for n in range(len(nodes))]
+        pdata = b"".join(le(v) for v in params)
+        # Both carry attr_t's key, so they group together whatever they recompute.
+        return archive(strings, nodes, [], pidx, pdata, b"", common, key_t.encode(), 2)
+
+    attr_t = attr_archive("t", kna(KNA_ALL, **ct), params_t)
+    attr_m = attr_archive("m", None, params_m)
+    expected["attrs"] = {
+        "effective_t": eff_t,
+        "effective_m": eff_m,
+        "desc_m": desc_m,
+        "recomputed_key_t": key_t,
+        "recomputed_key_m": key_m,
+        "template_of": [0, 0],
+        "status": [0, 1],                 # attr_m's recomputed node types differ: TYPE_MISMATCH
+        "words_t": params_t,
+        "words_m": params_m,
+        "overrides_m": [[7, 7, 0x7FF]],
+    }
+
+    # tiny_e / tiny_f: param-index offsets that are not multiples of 8 (the
+    # reference reads BinParamEntry at any byte offset, pack(1),
+    # csrc/CUDAGraphParallel.cpp:1391-1394) and a node with 18 params.  The
+    # param-index section is written byte by byte:
+    #   [0, 4)     unreferenced bytes
+    #   [4, 20)    node 0 (pio 4): (0, 8), (8, 12)
+    #   [20, 21)   unreferenced
+    #   [21, 29)   node 1 (pio 21): (24, 16)
+    #   [29, 173)  node 3 (pio 29): (40 + 8j, 8) for j < 18
+    # node 2 has no params.
+    def build_ef(word1, p17):
+        pidx = b"\xAA" * 4 + struct.pack("<II", 0, 8) + struct.pack("<II", 8, 12) + b"\xBB"
+        pidx += struct.pack("<II", 24, 16)
+        pidx += b"".join(struct.pack("<II", 40 + 8 * j, 8) for j in range(18))
+        assert len(pidx) == 173
+        pdata = le(0x7F0000001000) + le(word1) + le(0x2B, 4) + le(0xCCCCCCCC, 4) + le(0x7F0000002000) + le(0x77)
+        pdata += b"".join(le(p17 if j == 17 else 0x100 + j) for j in range(18))
+        assert len(pdata) == 184
+        nodes = [
+            kernel_entry(0, (64, 1, 1), (2, 1, 1), 0x1111222233334444, 0, 7, pio=4, npar=2),
+            kernel_entry(1, (64, 1, 1), (2, 1, 1), 0x1111222233334444, 0, 7, pio=21, npar=1),
+            kernel_entry(2, (64, 1, 1), (2, 1, 1), 0x1111222233334444, 0, 7, pio=0, npar=0),
+            kernel_entry(3, (64, 1, 1), (2, 1, 1), 0x5555666677778888, 8, 9, pio=29, npar=18),
+        ]
+        key = b"KernelNode:0,KernelNode:0,KernelNode:0,KernelNode:0"
+        return archive_raw_pidx(strings, nodes, pidx, pdata, key, 2)
+
+    e_img = build_ef(0x2A, 0x111)
+    f_img = build_ef(0x2C, 0x999)
+    words_e = [0x7F0000001000, 0x2A, 0x2B, 0x7F0000002000, 0x77] + [0x100 + j for j in range(18)]
+    words_e[-1] = 0x111
+    words_f = list(words_e)
+    words_f[1], words_f[22] = 0x2C, 0x999
+    expected["unaligned_pidx"] = {
+        "node_words": [3, 2, 0, 18],
+        "ragged_nodes": [0],
+        "words_e": words_e,
+        "words_f": words_f,
+        "template_of": [0, 0],
+        "overrides_f": [[1, 0, 0x2C], [22, 3, 0x999]],
+        # relocated by the same interval as the other fixtures
+        "words_e_relocated": [0x7E0000001000, 0x2A, 0x2B, 0x7E0000002000, 0x77] + words_e[5:],
+    }
+
+    for name, img in (("tiny_a", a), ("tiny_b", b), ("tiny_c", c), ("tiny_d", d), ("attr_t", attr_t),
+                      ("attr_m", attr_m), ("tiny_e", e_img), ("tiny_f", f_img)):
         with open(os.path.join(HERE, name + ".cugraph"), "wb") as f:
             f.write(img)
 

@@ -49,6 +49,16 @@ extern "C" __global__ void probe_count(uint64_t* out, uint32_t idx, uint32_t cap
   atomicAdd(reinterpret_cast<unsigned long long*>(out + idx), (unsigned long long)v);
 }
 
+// What a kernel drawing random numbers in a captured graph reads of its
+// generator (the graph-safe Philox state): out[idx] = *seed,
+// out[idx + 1] = *offset + intragraph (the offset the capture recorded).
+extern "C" __global__ void probe_rng(uint64_t* out, uint32_t idx, uint32_t cap, const int64_t* seed,
+                                     const int64_t* offset, uint32_t intragraph) {
+  if (!first_thread() || idx + 1 >= cap) return;
+  out[idx] = (uint64_t)*seed;
+  out[idx + 1] = (uint64_t)*offset + intragraph;
+}
+
 // Pointer-free variant for the extra-style (packed arg buffer) path: the
 // result goes to this code object's own array, indexed below its size.
 constexpr uint32_t kProbeSlots = 256;

@@ -142,3 +142,49 @@ def test_install_as_foundry():
         for k in [k for k in sys.modules if k == "foundry" or k.startswith("foundry.")]:
             del sys.modules[k]
         sys.modules.update(saved)
+
+
+def test_generator_registry_and_section_rows():
+    """get_state_from_id makes a state of the saved seed and offset 0 once per
+    id (csrc/CUDAGraph.cpp:147-160); GENERATORS rows are (id, seed,
+    wholegraph_increment) u64 triples (include/BinaryGraphFormat.h:214-219)."""
+    import struct
+
+    from foundry_amd import ops
+
+    reg = ops.GeneratorStateRegistry()
+    a = reg.get_state_from_id(3, 0xFFFF_FFFF_FFFF_FFF0)
+    assert a.seed == 0xFFFF_FFFF_FFFF_FFF0 and a.philox_offset_per_thread == 0
+    assert reg.get_state_from_id(3, 1) is a and a.seed == 0xFFFF_FFFF_FFFF_FFF0
+    assert reg.get_state_from_id(4, 1) is not a
+    rows = ops.generators_of(struct.pack("<6Q", 1, 2, 3, 4, 5, 6))
+    assert rows == [(1, 2, 3), (4, 5, 6)]
+    assert ops.generators_of(b"") == []
+    assert ops._as_i64(0xFFFF_FFFF_FFFF_FFF0) == -16 and ops._as_i64(5) == 5
+
+
+def test_dlpack_view_of_host_memory():
+    """fdy_dlpack_view's struct layout and deleter, checked on host memory
+    (DLPack device type 1, kDLCPU) with torch's importer: shape, strides,
+    dtype and aliasing, and views that die before and after the memory's
+    owner is read again."""
+    import ctypes as C
+
+    import numpy as np
+    import torch
+
+    from foundry_amd import _lib, ops
+
+    a = np.arange(24, dtype=np.int64)
+    shape = (C.c_int64 * 2)(4, 3)
+    strides = (C.c_int64 * 2)(6, 2)
+    view = _lib.restore_lib().fdy_dlpack_view(a.ctypes.data, 1, 0, 2, shape, strides, 1, 64)
+    t = torch.from_dlpack(ops._PyCapsule_New(view, b"dltensor", None)).view(torch.int64)
+    assert t.shape == (4, 3) and t.stride() == (6, 2)
+    assert t.tolist() == [[0, 2, 4], [6, 8, 10], [12, 14, 16], [18, 20, 22]]
+    t[1, 1] = -5
+    assert a[8] == -5
+    del t
+    for _ in range(100):  # many views made and freed
+        v = _lib.restore_lib().fdy_dlpack_view(a.ctypes.data, 1, 0, 1, (C.c_int64 * 1)(24), (C.c_int64 * 1)(1), 1, 64)
+        assert int(torch.from_dlpack(ops._PyCapsule_New(v, b"dltensor", None)).sum()) == int(a.sum())

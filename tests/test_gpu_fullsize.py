@@ -36,14 +36,23 @@ def test_full_size_parity(cuda, preset):
     arch.close()
 
 
-def test_1024_graph_archive_sampled(cuda):
+@pytest.fixture(scope="module")
+def c5(cuda):
+    """The 1024-graph archive, restored whole on the GPU (shared by the
+    sampled restore check and the switch sequence)."""
     p = synth.preset(5)
-    _case("preset5-full, sampled", p)
+    _case("preset5-full", p)
     s = synth.SynthArchive(p)
     lo, hi, new_lo = s.intervals()
     arch = Archive.from_synth(s)
     arch.set_relocation(lo, hi, new_lo)
     arch.restore()
+    yield p, s, arch, (lo, hi, new_lo)
+    arch.close()
+
+
+def test_1024_graph_archive_sampled(c5):
+    p, s, arch, (lo, hi, new_lo) = c5
     groups = arch.groups()
     assert len(set(groups.tolist())) == p.num_groups
     rng = np.random.default_rng(5)
@@ -65,4 +74,31 @@ def test_1024_graph_archive_sampled(cuda):
         np.testing.assert_array_equal(arch.node_pointers(g), ref.node_pointers(i), err_msg=f"node pointers g={g}")
         np.testing.assert_array_equal(arch.overrides(g), ref.overrides(i), err_msg=f"overrides g={g}")
     np.testing.assert_array_equal(arch.digests()[sample], ref.digests(), err_msg="digests")
-    arch.close()
+
+
+def test_1024_graph_archive_switch_sequence(c5):
+    """The 10,000 seeded switches of the 1024-graph workload, then every
+    group's live state against the oracle's: the live image depends only on
+    the last graph switched to in the group (the switch end state of
+    csrc/CUDAGraph.cpp:340-461), so the oracle restores each template with
+    that graph alone and switches once."""
+    p, s, arch, (lo, hi, new_lo) = c5
+    groups = arch.groups()
+    seq = synth.switch_sequence(p.seed, s.num_graphs, 10_000)
+    print(f"[case] preset5-full: {len(seq)} seeded switches", flush=True)
+    for g in seq:
+        arch.switch(int(g))
+    last = {int(t): int(t) for t in set(groups.tolist())}
+    for g in seq:
+        last[int(groups[g])] = int(g)
+    assert len(last) == p.num_groups
+    for t, g in sorted(last.items()):
+        w, src, cur = arch.live(t)
+        assert cur == g, f"group {t}"
+        pair = [t] if g == t else [t, g]
+        ref = Restore([s.image(x) for x in pair], (lo, hi, new_lo), template_of=[0] * len(pair), threads=16)
+        if g != t:
+            ref.switch(1)
+        w2, src2, cur2 = ref.live(0)
+        np.testing.assert_array_equal(w, w2, err_msg=f"live words of group {t} (last graph {g})")
+        np.testing.assert_array_equal(src, np.array(pair, dtype=np.uint32)[src2], err_msg=f"node sources of group {t}")

@@ -43,6 +43,26 @@ def test_relocate_unaligned_and_odd_length(cuda):
     np.testing.assert_array_equal(got, oracle.relocate_words(words, lo, hi, nlo, 0))
 
 
+@pytest.mark.parametrize("n,offset", [(1 << 20, 0), (100_001, 1)])
+def test_relocate_in_place(cuda, n, offset):
+    """in == out (the header allows it), on a 16-byte-aligned even array and
+    on an 8-byte-aligned odd one."""
+    p = synth.preset(4, num_words=n, num_intervals=5000, seed=11 + n)
+    print(f"[case] relocate in place words={n} offset={offset}", flush=True)
+    s = synth.SynthArchive(p)
+    words = np.array(s.words(), copy=True)
+    lo, hi, nlo = s.intervals()
+    plan = RelocPlan(lo, hi, nlo, 0)
+    d = cuda.zeros(n + offset, dtype=cuda.int64, device="cuda")
+    d[offset:] = cuda.from_numpy(words.view(np.int64)).to("cuda")
+    ptr = d.data_ptr() + 8 * offset
+    plan.relocate(ptr, ptr, n)
+    cuda.cuda.synchronize()
+    got = d.cpu().numpy().view(np.uint64)[offset:]
+    plan.close()
+    np.testing.assert_array_equal(got, oracle.relocate_words(words, lo, hi, nlo, 0, threads=8))
+
+
 def test_relocate_full_size_round_trip(cuda):
     # 1 GiB of words against 2M intervals: relocating with the inverse table
     # restores every word that was relocated (size-independent check).

@@ -17,6 +17,7 @@ from tests.parity import assert_live_matches, assert_restore_parity, gpu_and_ora
 pytestmark = pytest.mark.gpu
 
 CASES = 40
+WIDE = 12  # more cases whose kernel nodes take 17-48 params (past the 16 kept field-major)
 
 
 def _params(seed: int):
@@ -46,10 +47,14 @@ def _params(seed: int):
     )
     if rng.random() < 0.3:
         p.run_min_bytes, p.run_max_bytes = 64, 256
-    return p, rng.randrange(2)
+    policy = rng.randrange(2)
+    if seed >= CASES:
+        p.max_params = 17 + (7 * seed) % 32
+        p.max_blob_bytes = max(p.max_blob_bytes, 16 * p.max_params)
+    return p, policy
 
 
-@pytest.mark.parametrize("seed", range(CASES))
+@pytest.mark.parametrize("seed", range(CASES + WIDE))
 def test_random_shape(cuda, seed):
     p, policy = _params(seed)
     print(f"[case] sweep seed={seed}: base preset {p.preset}, graphs={p.num_graphs} groups={p.num_groups} "

@@ -53,9 +53,46 @@ def test_json_only_graphs_restore(tmp_path):
     from_bin = Archive.open([str(bdir / f"graph_{i}.json") for i in range(len(texts))])
     from_json.restore()
     from_bin.restore()
-    ref = Restore([OW.save_binary(t) for t in texts], None)
+    ref = Restore([OW.load_archive(t) for t in texts], None)
     assert_restore_parity(from_json, ref)
     for g in range(len(texts)):
         np.testing.assert_array_equal(from_json.param_image(g), from_bin.param_image(g))
         np.testing.assert_array_equal(from_json.overrides(g), from_bin.overrides(g))
     assert from_json.section(0, 8) == b'{"start_base_addr":0,"events":[]}'
+
+
+def test_keyless_json_graphs_group_by_recomputed_keys(tmp_path):
+    """JSON documents without a topology_key (or with an empty one) group by
+    the key recomputed from their nodes (csrc/CUDAGraphParallel.cpp:
+    1796-1840), not all under one empty key."""
+    rng = random.Random(11)
+    base = sample_nodes(rng, 30)
+    alt = list(base)
+    k = next(i for i, n in enumerate(alt) if n.type == 0)
+    n0 = alt[k]
+    alt[k] = W.Kernel(n0.name, n0.binary_hash, n0.grid, n0.block, n0.params, n0.arg, n0.shmem, (4, 1, 1),
+                      n0.cooperative, n0.func_attrs, n0.kna_ints)
+    short = sample_nodes(rng, 20)
+    order = [base, alt, base, short, alt, base, short]
+    texts = []
+    for g, nodes in enumerate(order):
+        d = doc_of(nodes, [], {"start_base_addr": 0, "events": []})
+        if g % 2:
+            d["topology_key"] = ""
+        else:
+            del d["topology_key"]
+        texts.append(json.dumps(d))
+    for i, t in enumerate(texts):
+        (tmp_path / f"graph_{i}.json").write_text(t)
+    keys = [OW.load_topology_key(t) for t in texts]
+    assert len(set(keys)) == 3 and b"" not in keys
+    print("key-less json archive: 7 graphs, 3 recomputed keys", flush=True)
+    arch = Archive.open([str(tmp_path / f"graph_{i}.json") for i in range(len(texts))])
+    try:
+        arch.restore()
+        assert arch.groups().tolist() == [0, 1, 0, 3, 1, 0, 3]
+        for g in range(len(texts)):
+            assert arch.section(g, 10) == keys[g]
+        assert_restore_parity(arch, Restore([OW.load_archive(t) for t in texts], None))
+    finally:
+        arch.close()

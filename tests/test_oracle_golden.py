@@ -103,3 +103,83 @@ def test_digests_are_crcs_of_the_defined_streams():
     d = r.digests()
     for i, data in enumerate(images):
         assert d[i].tolist() == _digests_from_reader(data), NAMES[i]
+
+
+# ---- launch-attribute merge (attr_t / attr_m) ---------------------------
+
+ATTR = EXP["attrs"]
+
+
+def _attr_fixture_disagreements():
+    """Which hand-derived attribute values the oracle (as currently built or
+    mutated) does not reproduce: effective attributes, DESC flags, status."""
+    t, m = img("attr_t"), img("attr_m")
+    bad = []
+    for n, want in enumerate(ATTR["effective_t"]):
+        if oracle.effective_attrs(t, n) != want:
+            bad.append(("effective_t", n))
+    for n, want in enumerate(ATTR["effective_m"]):
+        if oracle.effective_attrs(m, n) != want:
+            bad.append(("effective_m", n))
+    r = oracle.Restore([t, m])
+    desc = ((r.node_flags(1) & DESC) != 0).astype(int).tolist()
+    if desc != ATTR["desc_m"]:
+        bad.append(("desc_m", desc))
+    return bad, r
+
+
+def test_attribute_merge_matches_the_hand_derived_values():
+    bad, r = _attr_fixture_disagreements()
+    assert bad == []
+    assert r.groups().tolist() == ATTR["template_of"]
+    assert r.status().tolist() == ATTR["status"]
+    assert r.param_image(0).tolist() == ATTR["words_t"]
+    assert r.param_image(1).tolist() == ATTR["words_m"]
+    o = r.overrides(1)
+    assert [[int(x["word"]), int(x["node"]), int(x["value"])] for x in o] == ATTR["overrides_m"]
+    assert oracle.topology_key_recomputed(img("attr_t")).decode() == ATTR["recomputed_key_t"]
+    assert oracle.topology_key_recomputed(img("attr_m")).decode() == ATTR["recomputed_key_m"]
+
+
+@pytest.mark.parametrize("mutation", [1, 2, 3, 4, 5, 6])
+def test_every_planted_merge_mistake_is_caught(mutation):
+    """A mistake planted in the oracle's merge (common over per-node,
+    negative values overriding, the required cluster ignored, per-node attrs
+    replacing common ones, common attrs ignored, zero required dims kept)
+    disagrees with the hand-derived values on at least one node."""
+    oracle.set_mutation(mutation)
+    try:
+        bad, _ = _attr_fixture_disagreements()
+    finally:
+        oracle.set_mutation(0)
+    assert bad, f"mutation {mutation} went unnoticed"
+
+
+def test_planted_swap_changes_a_desc_flag():
+    """The swapped merge order (common attrs over per-node ones) shows up in
+    the DESC flags themselves, the output the GPU test compares."""
+    oracle.set_mutation(1)
+    try:
+        bad, _ = _attr_fixture_disagreements()
+    finally:
+        oracle.set_mutation(0)
+    assert any(k == "desc_m" for k, _ in bad)
+
+
+# ---- unaligned param-index offsets, a node past 16 params (tiny_e / tiny_f) ----
+
+UNAL = EXP["unaligned_pidx"]
+
+
+def test_unaligned_param_index_offsets():
+    r = oracle.Restore([img("tiny_e"), img("tiny_f")])
+    assert r.groups().tolist() == UNAL["template_of"]
+    assert np.diff(r.node_words(0)).tolist() == UNAL["node_words"]
+    assert r.param_image(0).tolist() == UNAL["words_e"]
+    assert r.param_image(1).tolist() == UNAL["words_f"]
+    o = r.overrides(1)
+    assert [[int(x["word"]), int(x["node"]), int(x["value"])] for x in o] == UNAL["overrides_f"]
+    fe = r.node_flags(0)
+    assert [n for n in range(4) if fe[n] & RAGGED] == UNAL["ragged_nodes"]
+    r2 = oracle.Restore([img("tiny_e"), img("tiny_f")], intervals())
+    assert r2.param_image(0).tolist() == UNAL["words_e_relocated"]

@@ -77,3 +77,15 @@ def test_manifest_unknown_template_is_skipped_before_its_members_are_read():
     m = manifest([{"template": "graph_9.json", "members": 7},
                   {"template": "graph_0.json", "members": ["graph_3.json"]}])
     assert oracle.group_manifest(m, NAMES).tolist() == [NONE, NONE, NONE, 0, NONE, NONE]
+
+
+def test_digest_collisions_group_by_exact_bytes():
+    """Two keys with equal CRC-64/XZ and length but other bytes stay apart,
+    and the graph that met a colliding lower key is flagged (0x08)."""
+    import collision_cases as CC
+
+    r = oracle.Restore(CC.images())
+    assert r.groups().tolist() == CC.TEMPLATE_OF
+    assert r.status().tolist() == CC.STATUS
+    d = r.digests()
+    assert d[0, 0] == d[1, 0]  # the forged key really collides
