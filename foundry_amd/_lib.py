@@ -189,6 +189,7 @@ _SIGS = {
     "fdy_reloc_plan_create": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, C.POINTER(_vp)]),
     "fdy_reloc_plan_destroy": (C.c_int, [_vp]),
     "fdy_relocate_words": (C.c_int, [_vp, _vp, _vp, C.c_uint64, _vp]),
+    "fdy_relocate_words_static": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, _vp, _vp, C.c_uint64, _vp]),
     "fdy_restore_timing_get": (C.c_int, [_vp, C.POINTER(RestoreTiming)]),
     "fdy_set_timing": (C.c_int, [_vp, C.c_int]),
 }
@@ -268,6 +269,15 @@ def _bind(path: str, sigs: dict) -> C.CDLL:
 def restore_lib() -> C.CDLL:
     global _restore
     if _restore is None:
+        # One HIP runtime per process: torch bundles its own libamdhip64 under
+        # the same soname as the system's, and whichever loads first serves
+        # both.  Loading torch first makes it torch's, so device memory and
+        # streams from torch and the library's calls meet in one runtime (the
+        # library loaded first ran a second runtime that found no device).
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         _restore = _bind(RESTORE_LIB, _SIGS)
     return _restore
 

@@ -11,6 +11,7 @@
 #include <cstdio>
 #include <cstring>
 #include <memory>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <unordered_map>
@@ -79,8 +80,19 @@ struct HostStage {
   }
 };
 
-int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
-                     RelocPlan* out) {
+// The interval search structure of a table, built on the host: the bucket
+// lines, the {hi, delta} records and the lo keys, with the search
+// parameters (dev's pointers are set when the arrays are placed on the
+// device).
+struct HostIndex {
+  std::vector<RelocBucket> bucket;
+  std::vector<RelocRec> rec;
+  const uint64_t* lo = nullptr;
+  RelocDev dev{};
+};
+
+int build_reloc_index(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
+                      HostIndex* out) {
   std::memset(&out->dev, 0, sizeof(out->dev));
   if (policy > FDY_RELOC_INCLUSIVE) return err(FDY_E_INVALID, "unknown relocation policy");
   if (n == 0) return FDY_OK;
@@ -95,7 +107,8 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
   if (n > 0xFFFFFFF0ull) return err(FDY_E_INVALID, "more than 2^32 intervals");
   const uint64_t span = hi[n - 1] - lo[0];
   if (span >> 54) return err(FDY_E_INVALID, "intervals span more than 2^54 bytes");
-  std::vector<RelocRec> rec(n);
+  std::vector<RelocRec>& rec = out->rec;
+  rec.resize(n);
   for (uint64_t i = 0; i < n; ++i) rec[i] = RelocRec{hi[i], nlo[i] - lo[i]};
   // Bucket width: the smallest power of two giving at most ~n/2 buckets over
   // [lo_min, hi_max], and at most 2^32 so in-bucket offsets fit in 32 bits.
@@ -109,7 +122,8 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
     const uint64_t off = b << shift;  // b <= nb, so no overflow below 2^55
     return off > UINT64_MAX - lo[0] ? UINT64_MAX : lo[0] + off;
   };
-  std::vector<RelocBucket> bucket(nb);
+  std::vector<RelocBucket>& bucket = out->bucket;
+  bucket.assign(nb, RelocBucket{});
   auto leaf = [&](RelocBucket& e, uint64_t s0, uint64_t i, uint64_t j) {
     e.first = (uint32_t)i;
     e.count = (uint32_t)(j - i);
@@ -180,21 +194,31 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
       if (cj - ci > kBucketOffsets) todo.push_back({base + c, s0, ci, cj, cw, p.depth + 1});
     }
   }
-  int rc = dev_alloc(out->bucket, bucket.size() * sizeof(RelocBucket), "interval buckets");
-  if (!rc) rc = dev_alloc(out->rec, n * sizeof(RelocRec), "interval records");
-  if (!rc) rc = dev_alloc(out->lo, n * 8, "interval starts");
-  if (rc) return rc;
-  FDY_HIP(hipMemcpy(out->bucket.p, bucket.data(), bucket.size() * sizeof(RelocBucket), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(out->rec.p, rec.data(), n * sizeof(RelocRec), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(out->lo.p, lo, n * 8, hipMemcpyHostToDevice));
-  out->dev.bucket = out->bucket.as<RelocBucket>();
-  out->dev.rec = out->rec.as<RelocRec>();
-  out->dev.lo = out->lo.as<uint64_t>();
+  out->lo = lo;
   out->dev.n = n;
   out->dev.lo_min = lo[0];
   out->dev.hi_max = hi[n - 1];
   out->dev.shift = shift;
   out->dev.policy = policy;
+  return FDY_OK;
+}
+
+int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
+                     RelocPlan* out) {
+  HostIndex x;
+  int rc = build_reloc_index(lo, hi, nlo, n, policy, &x);
+  out->dev = x.dev;
+  if (rc || n == 0) return rc;
+  rc = dev_alloc(out->bucket, x.bucket.size() * sizeof(RelocBucket), "interval buckets");
+  if (!rc) rc = dev_alloc(out->rec, n * sizeof(RelocRec), "interval records");
+  if (!rc) rc = dev_alloc(out->lo, n * 8, "interval starts");
+  if (rc) return rc;
+  FDY_HIP(hipMemcpy(out->bucket.p, x.bucket.data(), x.bucket.size() * sizeof(RelocBucket), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->rec.p, x.rec.data(), n * sizeof(RelocRec), hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(out->lo.p, lo, n * 8, hipMemcpyHostToDevice));
+  out->dev.bucket = out->bucket.as<RelocBucket>();
+  out->dev.rec = out->rec.as<RelocRec>();
+  out->dev.lo = out->lo.as<uint64_t>();
   return FDY_OK;
 }
 
@@ -948,6 +972,75 @@ void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int3
   t->manager_ctx = nullptr;
   t->deleter = free_view;
   return t;
+}
+
+// ---- relocation without device allocation --------------------------------
+
+namespace {
+
+// The interval index of fdy_relocate_words_static.  Each GPU the library
+// runs on holds its own copy until the process ends.  In host code the
+// array's name is not a device address: it is only ever passed to
+// hipGetSymbolAddress, and the address that returns is what kernels,
+// copies and fills receive.
+static __device__ __align__(256) uint8_t scratch[FDY_STATIC_INDEX_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The device address of `scratch` on device `dev` (current), looked up on
+// the first call on that device.
+int scratch_on(int dev, uint8_t** out) {
+  if (dev < 0 || dev >= kMaxDevices) return err(FDY_E_RANGE, "device " + std::to_string(dev) + " out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return err(FDY_E_HIP, std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = static_cast<uint8_t*>(g_scratch[dev]);
+  return FDY_OK;
+}
+
+}  // namespace
+
+int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n_iv,
+                              uint32_t policy, const uint64_t* in, uint64_t* out, uint64_t n, void* stream) {
+  if ((!in && n) || (!out && n)) return err(FDY_E_INVALID, "null word array");
+  if (((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 7) != 0)
+    return err(FDY_E_INVALID, "word arrays must be 8-byte aligned");
+  HostIndex x;
+  int rc = build_reloc_index(lo, hi, nlo, n_iv, policy, &x);
+  if (rc) return rc;
+  const uint64_t b_bytes = x.bucket.size() * sizeof(RelocBucket), r_bytes = n_iv * sizeof(RelocRec);
+  const uint64_t at_rec = align_up(b_bytes, 256), at_lo = align_up(at_rec + r_bytes, 256);
+  const uint64_t total = at_lo + 8 * n_iv;
+  if (total > FDY_STATIC_INDEX_BYTES)
+    return err(FDY_E_CAPACITY, "the index of " + std::to_string(n_iv) + " intervals takes " + std::to_string(total) +
+                                   " bytes; the static index holds " + std::to_string(FDY_STATIC_INDEX_BYTES));
+  int dev = 0;
+  FDY_HIP(hipGetDevice(&dev));
+  uint8_t* base = nullptr;
+  rc = scratch_on(dev, &base);
+  if (rc) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  RelocDev d = x.dev;
+  if (n_iv) {
+    // In stream order, so after any earlier call's kernel on this stream;
+    // then wait for the copies, after which the host arrays may go.
+    FDY_HIP(hipMemcpyAsync(base, x.bucket.data(), b_bytes, hipMemcpyHostToDevice, s));
+    FDY_HIP(hipMemcpyAsync(base + at_rec, x.rec.data(), r_bytes, hipMemcpyHostToDevice, s));
+    FDY_HIP(hipMemcpyAsync(base + at_lo, lo, 8 * n_iv, hipMemcpyHostToDevice, s));
+    FDY_HIP(hipStreamSynchronize(s));
+    d.bucket = reinterpret_cast<const RelocBucket*>(base);
+    d.rec = reinterpret_cast<const RelocRec*>(base + at_rec);
+    d.lo = reinterpret_cast<const uint64_t*>(base + at_lo);
+  }
+  FDY_HIP(launch_reloc_words(d, in, out, n, s));
+  return FDY_OK;
 }
 
 int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,

@@ -259,6 +259,19 @@ class RelocPlan:
             pass
 
 
+def relocate_words_static(lo, hi, new_lo, d_in: int, d_out: int, n_words: int, policy: int = _lib.RELOC_HALF_OPEN,
+                          stream=None) -> None:
+    """fdy_relocate_words_static: relocate device words by the table (lo, hi,
+    new_lo) with no device allocation (the index lives in the library's
+    static per-GPU array)."""
+    lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+    if not (len(lo) == len(hi) == len(new_lo)):
+        raise ValueError("lo, hi and new_lo must have one entry per interval")
+    check(restore_lib().fdy_relocate_words_static(lo.ctypes.data_as(_lib.u64p), hi.ctypes.data_as(_lib.u64p),
+                                                  new_lo.ctypes.data_as(_lib.u64p), len(lo), policy, d_in, d_out,
+                                                  n_words, _stream(stream)))
+
+
 def version() -> str:
     return restore_lib().fdy_version().decode()
 

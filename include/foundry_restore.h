@@ -242,6 +242,26 @@ int fdy_reloc_plan_destroy(fdy_reloc_plan* p);
 int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
                        void* stream);
 
+/* fdy_relocate_words without any device allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (serving
+ * loops and harnesses that forbid hipMalloc).  It takes the table of
+ * fdy_reloc_plan_create (validated the same way) and relocates n_words
+ * words at d_in into d_out (which may alias) exactly as a plan of that table
+ * would, but builds the interval index on the host and keeps it in a static
+ * device array of FDY_STATIC_INDEX_BYTES bytes that each GPU holds until the
+ * process ends: no hipMalloc, hipFree or other device or pinned allocation.
+ * An index larger than the array (past about 120 thousand intervals spread
+ * like the relocation-heavy workload's; the index grows with crowded
+ * buckets) is FDY_E_CAPACITY before anything is enqueued.  The index is copied in `stream`'s order and the call waits for
+ * those copies, then enqueues the relocation.  Every call on one GPU shares
+ * the array: calls on different streams that overlap race (the later index
+ * can replace the earlier one under its running kernel); calls in one
+ * stream's order do not. */
+#define FDY_STATIC_INDEX_BYTES (8u << 20)
+int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
+                              uint32_t policy, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
+                              void* stream);
+
 /* A non-owning DLPack view (a DLManagedTensor*, dlpack.h v0.8 layout) of
  * `ndim`-dimensional device memory at ptr: what the reference's output
  * tensors are (at::from_blob at the saved data_ptr, csrc/CUDAGraph.cpp:
