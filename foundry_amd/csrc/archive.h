@@ -72,7 +72,7 @@ struct fdy_archive {
 
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
   fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
-  fdy::DevBuf aux, image, live, ovr, ovr_off, cand, sub_count, graph_count, slot_off, planes, pplanes;
+  fdy::DevBuf aux, image, live, ovr, cand, sub_count, graph_count, node_pbytes, key_hash;
 
   fdy::RelocPlan reloc;
   bool use_explicit = false;
@@ -82,7 +82,7 @@ struct fdy_archive {
   // Host copies taken after a restore (one synchronisation, then reused).
   bool cached = false;
   std::vector<uint32_t> h_tmpl, h_status, h_gwords;
-  std::vector<uint64_t> h_ovr_off, h_pbytes;
+  std::vector<uint64_t> h_ovr_off, h_pbytes;  // h_ovr_off: prefix of the per-graph record counts
   std::vector<uint32_t> h_current;
 
   // Group graph bound to each template (null if none); while any is bound the
@@ -93,11 +93,19 @@ struct fdy_archive {
 
   bool timing = false;
   bool timed = false;
-  hipEvent_t ev[8] = {};
+  hipEvent_t ev[10] = {};  // 0..7 on the restore stream, 8..9 around the digest kernel
+
+  // The digest kernel's stream (default priority) and the events that fork
+  // it from, and join it back into, the restore stream.
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)
       if (e) (void)hipEventDestroy(e);
+    if (fork) (void)hipEventDestroy(fork);
+    if (join) (void)hipEventDestroy(join);
+    if (side) (void)hipStreamDestroy(side);
   }
 };
 

@@ -21,6 +21,7 @@ struct RestoreArgs {
   NodeChunk* chunks;          // per node chunk
   uint64_t* digests;          // 4 per graph
   const uint32_t* explicit_template;  // or null
+  uint64_t* key_hash;                 // per graph: the grouping pass's key hash
   uint32_t* template_of;
   uint32_t* status;
   uint32_t* gwords;
@@ -37,20 +38,15 @@ struct RestoreArgs {
   uint64_t* live;             // live images (template graphs)
   uint32_t* live_src;         // per node
   uint32_t* live_cur;         // per graph
-  fdy_override* ovr;          // dense override records, canonical order
-  uint64_t* ovr_off;          // G+1
+  fdy_override* ovr;          // override records: graph g's in canonical order from index word_base(g)
   Candidate* cand;            // per (slot, sub-range): kSubWords candidates, then as many records
   uint32_t* sub_count;        // records per (slot, sub-range)
   uint32_t* graph_count;      // records per graph
-  uint32_t* slot_off;         // per slot: its records' offset among its graph's
-  const uint32_t* planes;     // field-major node table: per 256-node chunk, 42 planes of 256 dwords
-  const uint64_t* pplanes;    // per 256-node chunk, 16 planes of 256 param entries (the first 16 of each node)
+  uint64_t* node_pbytes;      // param bytes per node (nodes the first node pass handles itself)
   RelocDev reloc;
 };
 
-hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
-                         uint32_t* planes, uint64_t* pplanes, hipStream_t s);
-hipError_t launch_hash(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_digests(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);

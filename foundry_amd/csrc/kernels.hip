@@ -1,30 +1,34 @@
 // kernels.hip -- the restore kernels for gfx950 (wave64, 160 KB LDS per CU).
 //
-//   k_hash    one workgroup per graph: CRC-64/XZ of the saved topology key and
-//             of the dependency table, as a block-wide segmented CRC (each
-//             lane absorbs 64 bytes, lanes are joined by a combine tree whose
-//             multipliers are constants applied through nibble tables in LDS).
-//   k_group   template_of[g] = lowest graph with the same key bytes (found by
-//             key digest and length, then compared byte for byte).
-//   k_node_a  one workgroup per 256-node chunk of a graph: per node, the
-//             param layout, the compare against the template's node,
-//             memset/memcpy pointer relocation, the node-type and kernel-entry
-//             records (raw CRC per chunk) and the node descriptor.
-//   k_node_b  one workgroup per graph: chunk CRCs joined into the
-//             digests, word offsets by block scans, the diff-tile -> first-node
-//             table, ragged-word sources, slot descriptors.
+//   k_khash   a word hash of every graph's saved key.
+//   k_digest  the CRC-64/XZ digests of every graph's saved key and
+//             dependency table (on a second stream, beside the passes
+//             below, joined before the compaction, which reads them).
+//   k_group   template_of[g] = lowest graph with the same key bytes (by the
+//             word hash, then a byte compare).
+//   k_node_a  one workgroup per 256-node chunk of a graph: for a
+//             member, a coalesced compare of the chunk's node entries and
+//             param entries with its template's; the per-node path (param
+//             layout, compare against the template's node, memset/memcpy
+//             pointer relocation, node-type and kernel-entry records) for
+//             every node that differs or has nothing to compare with.
+//   k_node_b  one workgroup per graph: clean nodes completed from the
+//             template's results, chunk CRCs joined into the four digests,
+//             word offsets by block scans, the diff-tile -> first-node table,
+//             ragged-word sources, slot descriptors.
 //   k_diff_t  the template graphs' words, relocated through a bucket-indexed
 //             interval search into R and the live image (1024-word units).
 //   k_diff_m  eight workgroups per 4096-word tile of every other graph: coalesced
 //             8-byte loads of the graph's and the template's words, the
 //             template's relocated word reused where the raw words are equal,
-//             lockstep batched searches for the rest, the relocated image
-//             store, and per-wave ballot compaction of the differing words
-//             into override record regions.
-//   k_count   override records per graph.
-//   k_compact record regions -> the dense override array in canonical order
-//             (offsets from the per-graph record counts),
-//             completing each record's node and template word index.
+//             the relocated image store, and per-wave ballot compaction of
+//             the words left to search or compare into candidate regions.
+//   k_diff_s  one wave per tile: the candidates' interval searches, and the
+//             differing words as override records.
+//   k_compact record regions -> each graph's dense override array (at the
+//             graph's word base) in canonical order, completing each
+//             record's node and template word index; per-graph counts and
+//             the collision report.
 //   k_switch  override scatter for one graph switch.
 //   k_mirror  dirty nodes' live words -> a group graph's host mirror.
 //   k_fill    memset node of a restored graph, as a kernel node.
@@ -34,9 +38,7 @@
 namespace fdy {
 namespace {
 
-constexpr uint32_t kHashThreads = 1024;
 constexpr uint32_t kNodeThreads = 1024;
-constexpr uint32_t kGroupSteps = 8;  // 64-candidate steps whose loads are issued together
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
 constexpr uint32_t kRelocBatch = 4;  // words searched in lockstep (8 and 2 measured no faster)
@@ -51,156 +53,179 @@ __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
 
 __device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
 
+// Word qi (bytes [8 qi, 8 qi + 8)) of the L-byte stream at p (8-aligned,
+// inside the archive-image buffer), with bytes outside [0, L) read as zero.
+// The load is unconditional, from the nearest word of the stream (word 0
+// of an empty stream: the buffer ends in 4 KB of zero padding, so that load
+// stays inside it), so a run of calls issues its loads together instead of
+// one branch and wait per word.
+__device__ __forceinline__ uint64_t stream_word(const uint8_t* p, uint64_t L, int64_t qi) {
+  const int64_t last = L ? (int64_t)((L - 1) >> 3) : 0;
+  const int64_t qc = qi < 0 ? 0 : (qi > last ? last : qi);
+  uint64_t v = *reinterpret_cast<const uint64_t*>(p + 8 * qc);
+  const uint64_t rem = L - 8 * (uint64_t)qc;
+  if (rem < 8) v &= (1ull << (8 * rem)) - 1;
+  return qi == qc ? v : 0;
+}
+
 // The 8 bytes [b0, b0+8) of the L-byte stream at p (8-aligned), with bytes
 // outside [0, L) read as zero.
-__device__ inline uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b0) {
+__device__ __forceinline__ uint64_t stream_window(const uint8_t* p, uint64_t L, int64_t b0) {
   const int64_t q = b0 >> 3;
   const uint32_t sh = (uint32_t)(b0 & 7);
-  auto word = [&](int64_t qi) -> uint64_t {
-    if (qi < 0 || (uint64_t)qi * 8 >= L) return 0;
-    uint64_t v = *reinterpret_cast<const uint64_t*>(p + qi * 8);
-    uint64_t rem = L - (uint64_t)qi * 8;
-    if (rem < 8) v &= (1ull << (8 * rem)) - 1;
-    return v;
-  };
-  uint64_t w0 = word(q);
-  if (sh == 0) return w0;
-  return (w0 >> (8 * sh)) | (word(q + 1) << (64 - 8 * sh));
+  const uint64_t w0 = stream_word(p, L, q), w1 = stream_word(p, L, q + 1);
+  return sh ? (w0 >> (8 * sh)) | (w1 << (64 - 8 * sh)) : w0;
 }
 
-// XOR of two values over the block (blockDim.x a multiple of 64); valid in
-// thread 0.  s_wave is free again when it returns.
-__device__ void block_xor2(uint64_t& x, uint64_t& y, uint64_t (*s_wave)[2]) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+// A 4 KB unit: a chunk's records, or a slice of a key or dependency table.
+constexpr uint32_t kSliceBytes = 4096;
+static_assert(kSliceBytes == 16 * kPosRecords, "a slice is as long as a chunk's records");
+
+// Shift a raw CRC z past k 4 KB units (a chunk's records, or a stream
+// slice): lane i holds x^(8 * 4096 * k) * x^i and keeps it where z has x^i
+// (bit 63 - i); the caller XORs over the wave.  Past the table, one lane
+// multiplies.
+__device__ __forceinline__ uint64_t shift_share(const CrcConsts* cc, uint64_t z, uint32_t k, uint32_t lane) {
+  if (k < (uint32_t)kChunkShifts) return ((z >> (63 - lane)) & 1) ? cc->chunk_shift[k][lane] : 0ull;
+  return lane == 0 ? gf2_mulmod(x2n_mod(cc->x2n.v, (uint64_t)kSliceBytes * k, 3), z) : 0ull;
+}
+
+// A 64-bit hash of a key for finding grouping candidates (not a digest the
+// restore reports): the XOR over the key's 8-byte words w_k (the last one
+// zero-padded) of the SplitMix64 finaliser (Steele, Lea and Flood 2014) of
+// w_k + (k + 1) * golden ratio.  Word terms are independent, so every lane
+// hashes its own words; equal keys hash equal, and a hash match is always
+// confirmed byte for byte.
+__device__ __forceinline__ uint64_t key_term(uint64_t w, uint64_t k) {
+  uint64_t z = w + (k + 1) * 0x9E3779B97F4A7C15ull;
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+// Raw CRC (zero initial value) of one 4 KB slice of an L-byte stream (p
+// 8-byte aligned), by one wave: the slice ends `back` bytes before the
+// stream's end, and bytes before 0 read as zero.  Lane l absorbs the 64
+// bytes [end - 64 (64 - l), end - 64 (63 - l)) through the slicing tables
+// and moves its CRC into place, times x^(8 * 64 * (63 - l)) (an entry of the
+// 64-byte position table); the wave XORs the shares
+// (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).  The result is valid in
+// every lane.
+__device__ __forceinline__ uint64_t wave_slice_crc(const uint8_t* p, uint64_t L, uint64_t back,
+                                                   const uint64_t (*slice)[256], const CrcConsts* cc, uint32_t lane) {
+  const int64_t b0 = (int64_t)L - (int64_t)back - 64 * (64 - (int64_t)lane);
+  uint64_t z = 0;
+  if (b0 + 64 > 0) {
+    // b0 = 8 q0 + sh with sh = L mod 8 for every lane (the slice and lane
+    // offsets are multiples of 8), so the shift is uniform.
+    const int64_t q0 = b0 >> 3;
+    const uint32_t sh = (uint32_t)(L & 7);
+    uint64_t w[9];
+#pragma unroll
+    for (uint32_t k = 0; k < 9; ++k) w[k] = stream_word(p, L, q0 + k);
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) z = crc_slice8(slice, z, sh ? (w[k] >> (8 * sh)) | (w[k + 1] << (64 - 8 * sh)) : w[k]);
+    z = z ? gf2_mulmod(cc->pos64[kPosLanes - 64 + lane], z) : 0;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) z ^= shfl_down64(z, d);
+  return ((uint64_t)__shfl((uint32_t)(z >> 32), 0, 64) << 32) | __shfl((uint32_t)z, 0, 64);
+}
+
+constexpr uint32_t kGroupThreads = 256;
+
+// The grouping hash of every graph's saved key, one workgroup per graph.
+__global__ __launch_bounds__(kGroupThreads) void k_khash(RestoreArgs a) {
+  __shared__ uint64_t s_x[kGroupThreads / 64];
+  const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
+  const DevGraph& Gi = a.graphs[i];
+  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
+  const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
+  uint64_t x = 0;
+  for (uint64_t k = tid; 8 * k < L; k += kGroupThreads) x ^= key_term(stream_word(p, L, (int64_t)k), k);
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
+  if (lane == 0) s_x[wave] = x;
+  __syncthreads();
+  if (tid == 0) {
+    for (uint32_t w = 1; w < kGroupThreads / 64; ++w) x ^= s_x[w];
+    a.key_hash[i] = x;
+  }
+}
+
+// The CRC-64/XZ digests of every graph's saved key and dependency table,
+// one workgroup per graph: the two streams' 4 KB slices (counted from each
+// stream's end) go round the waves; each wave shifts a slice's CRC past the
+// slices after it.  Depends on the archive image only, so it runs beside
+// the grouping and node passes.
+__global__ __launch_bounds__(kGroupThreads) void k_digest(RestoreArgs a) {
+  __shared__ uint64_t s_x[2][kGroupThreads / 64];
+  __shared__ uint64_t s_slice[8][256];
+  const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  const DevGraph& Gi = a.graphs[i];
+  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY], Ld = 8ull * Gi.num_deps;
+  const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
+  const uint8_t* pd = a.img + Gi.sec_off[FDY_SEC_DEPS];
+  __syncthreads();
+  const uint64_t nk = (L + kSliceBytes - 1) / kSliceBytes, nd = (Ld + kSliceBytes - 1) / kSliceBytes;
+  uint64_t ck = 0, cd = 0;  // lane shares of the shifted slice CRCs
+  for (uint64_t u = wave; u < nk + nd; u += kGroupThreads / 64) {
+    const bool key = u < nk;
+    const uint64_t back = key ? u : u - nk;
+    const uint64_t z = key ? wave_slice_crc(p, L, kSliceBytes * back, s_slice, a.cc, lane)
+                           : wave_slice_crc(pd, Ld, kSliceBytes * back, s_slice, a.cc, lane);
+    const uint64_t sh = back ? shift_share(a.cc, z, (uint32_t)back, lane) : (lane == 0 ? z : 0);
+    if (key) ck ^= sh;
+    else cd ^= sh;
+  }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
-    x ^= shfl_down64(x, d);
-    y ^= shfl_down64(y, d);
+    ck ^= shfl_down64(ck, d);
+    cd ^= shfl_down64(cd, d);
   }
   if (lane == 0) {
-    s_wave[wave][0] = x;
-    s_wave[wave][1] = y;
+    s_x[0][wave] = ck;
+    s_x[1][wave] = cd;
   }
   __syncthreads();
-  if (threadIdx.x == 0)
-    for (uint32_t w = 1; w < nw; ++w) {
-      x ^= s_wave[w][0];
-      y ^= s_wave[w][1];
+  if (tid == 0) {
+    for (uint32_t w = 1; w < kGroupThreads / 64; ++w) {
+      ck ^= s_x[0][w];
+      cd ^= s_x[1][w];
     }
-  __syncthreads();
-}
-
-// One of the two byte streams hashed together by block_crc_bytes2.
-struct HashStream {
-  const uint8_t* p;
-  uint64_t L;
-  uint64_t fin;  // the stream's finishing term
-};
-
-// CRC-64/XZ of two byte streams at once (their loads in flight together, one
-// reduction for both).  Each lane absorbs 64 consecutive bytes of a stream
-// (eight slicing steps); lane i's raw CRC times x^(8*64*(1023-i)) is its
-// share of the 64 KB chunk's raw CRC (crc(A || B) = crc(A) * x^(8|B|) xor
-// crc(B)), XOR-joined over the block; chunks are joined by the 64 KB
-// multiplier.  Each stream is front-padded with zeros to whole chunks
-// (leading zeros leave a zero-initialised register at zero; `fin` adds the
-// effect of the all-ones initial value).  Results in thread 0.
-__device__ void block_crc_bytes2(const HashStream& s0, const HashStream& s1, const uint64_t (*slice)[256],
-                                 const uint64_t (*chunk_mul)[16], const uint64_t* pos64, uint64_t (*s_wave)[2],
-                                 uint64_t* out0, uint64_t* out1) {
-  constexpr uint64_t kLane = 64;
-  constexpr uint64_t kChunk = kHashThreads * kLane;
-  static_assert(kHashThreads == kPosLanes, "one position multiplier per lane");
-  const uint64_t pad0 = (kChunk - s0.L % kChunk) % kChunk, pad1 = (kChunk - s1.L % kChunk) % kChunk;
-  const uint64_t n0 = (s0.L + pad0) / kChunk, n1 = (s1.L + pad1) / kChunk;
-  const uint64_t m = pos64[threadIdx.x];
-  uint64_t acc0 = 0, acc1 = 0;
-  for (uint64_t c = 0; c < n0 || c < n1; ++c) {
-    const int64_t b0 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad0;
-    const int64_t b1 = (int64_t)(c * kChunk + kLane * threadIdx.x) - (int64_t)pad1;
-    uint64_t v0[kLane / 8], v1[kLane / 8];
-#pragma unroll
-    for (uint32_t q = 0; q < kLane / 8; ++q) {
-      v0[q] = c < n0 ? stream_window(s0.p, s0.L, b0 + 8 * q) : 0;
-      v1[q] = c < n1 ? stream_window(s1.p, s1.L, b1 + 8 * q) : 0;
-    }
-    uint64_t z0 = 0, z1 = 0;
-#pragma unroll
-    for (uint32_t q = 0; q < kLane / 8; ++q) {
-      z0 = crc_slice8(slice, z0, v0[q]);
-      z1 = crc_slice8(slice, z1, v1[q]);
-    }
-    z0 = z0 ? gf2_mulmod(m, z0) : 0;
-    z1 = z1 ? gf2_mulmod(m, z1) : 0;
-    block_xor2(z0, z1, s_wave);
-    if (threadIdx.x == 0) {
-      if (c < n0) acc0 = nibble_mul(chunk_mul, acc0) ^ z0;
-      if (c < n1) acc1 = nibble_mul(chunk_mul, acc1) ^ z1;
-    }
-  }
-  *out0 = acc0 ^ s0.fin;
-  *out1 = acc1 ^ s1.fin;
-}
-
-__global__ __launch_bounds__(kHashThreads) void k_hash(RestoreArgs a) {
-  __shared__ uint64_t s_slice[8][256];
-  __shared__ uint64_t s_chunk[16][16];  // multiplier x^(8 * 64 KB): joins chunks
-  __shared__ uint64_t s_wave[kHashThreads / 64][2];
-  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
-  stage_words(&s_chunk[0][0], &a.cc->chunk64.t[0][0], 256);
-  __syncthreads();
-  const uint32_t g = blockIdx.x;
-  const DevGraph& G = a.graphs[g];
-  const HashStream key{a.img + G.sec_off[FDY_SEC_TOPOLOGY_KEY], G.sec_size[FDY_SEC_TOPOLOGY_KEY], G.crc_fin[0]};
-  const HashStream deps{a.img + G.sec_off[FDY_SEC_DEPS], 8ull * G.num_deps, G.crc_fin[1]};
-  uint64_t dk, de;
-  block_crc_bytes2(key, deps, s_slice, s_chunk, a.cc->pos64, s_wave, &dk, &de);
-  if (threadIdx.x == 0) {
-    a.digests[4ull * g + 0] = dk;
-    a.digests[4ull * g + 1] = de;
+    a.digests[4ull * i + 0] = ck ^ Gi.crc_fin[0];
+    a.digests[4ull * i + 1] = cd ^ Gi.crc_fin[1];
   }
 }
 
 // template_of[i] = the lowest j <= i whose saved key has the same bytes
-// (the reference partitions by exact key string, csrc/CUDAGraphParallel.cpp:
-// 1788-1851): one workgroup per graph.  Its first wave finds the lowest
-// candidate with an equal key digest and length (64 candidates per step,
-// eight steps' loads in flight at once); the workgroup then compares the
-// two keys' bytes, and on a digest collision (equal digest and length,
-// other bytes) flags the graph and goes on scanning past the candidate.
-constexpr uint32_t kGroupThreads = 256;
-
+// (the reference partitions graphs by exact key string,
+// csrc/CUDAGraphParallel.cpp:1788-1851), one workgroup per graph: its first
+// wave finds the lowest j with i's key hash and length, 64 candidates per
+// step; the workgroup compares the two keys byte for byte, and on a
+// difference goes on scanning past j.
 __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
   __shared__ uint32_t s_found, s_differs;
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
-  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
   if (a.explicit_template) {
-    if (tid == 0) {
-      a.template_of[i] = a.explicit_template[i];
-      a.status[i] = 0;
-    }
+    if (tid == 0) a.template_of[i] = a.explicit_template[i];
     return;
   }
   const DevGraph& Gi = a.graphs[i];
-  const uint64_t di = a.digests[4ull * i];
   const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
   const uint8_t* pi = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
-  uint32_t from = 0, status = 0, tmpl = i;
+  const uint64_t hi = a.key_hash[i];
+  uint32_t from = 0, tmpl = i;
   for (;;) {
     if (tid < 64) {
       uint32_t found = i;
-      for (uint32_t base = from; base < i && found == i; base += 64 * kGroupSteps) {
-        bool m[kGroupSteps];
-#pragma unroll
-        for (uint32_t k = 0; k < kGroupSteps; ++k) {
-          const uint32_t j = base + 64 * k + lane;
-          m[k] = j < i && a.digests[4ull * j] == di && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == L;
-        }
-#pragma unroll
-        for (uint32_t k = 0; k < kGroupSteps; ++k) {
-          const uint64_t mk = __ballot(m[k]);
-          if (found == i && mk) found = base + 64 * k + (uint32_t)__ffsll((long long)mk) - 1;
-        }
+      for (uint32_t base = from; base < i && found == i; base += 64) {
+        const uint32_t j = base + lane;
+        const bool m = j < i && a.key_hash[j] == hi && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == L;
+        const uint64_t mk = __ballot(m);
+        if (mk) found = base + (uint32_t)__ffsll((long long)mk) - 1;
       }
       if (tid == 0) {
         s_found = found;
@@ -220,14 +245,10 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
       tmpl = j;
       break;
     }
-    status = FDY_GRAPH_COLLISION;
     from = j + 1;
     __syncthreads();  // every thread has read s_found and s_differs
   }
-  if (tid == 0) {
-    a.template_of[i] = tmpl;
-    a.status[i] = status;  // completed by the node pass
-  }
+  if (tid == 0) a.template_of[i] = tmpl;
 }
 
 // ---- node pass ----------------------------------------------------------
@@ -241,40 +262,16 @@ struct Side {
   uint64_t src;        // absolute byte offset of the blob
   uint64_t pbytes;     // param bytes (0 when bad)
   const uint8_t* pidx; // param entries (per-param style)
-  const uint64_t* pp;  // the first kPlaneParams of them, field-major (stride kNodeChunk), or null
 };
 
-// A node entry's fields (byte offsets, multiples of 4).  RawEntry reads the
-// 168 saved bytes in place; PlaneEntry reads the field-major copy of the
-// node table (dword k of every node of a 256-node chunk in one plane), where
-// a wave's read of one field is one coalesced access instead of 64 lines.
-
+// A node entry's fields (byte offsets, multiples of 4), read in place (the
+// image in global memory; every field of an entry is 4-byte aligned).
 struct RawEntry {
   const uint8_t* e;
   __device__ uint32_t u32(uint32_t off) const { return f32(e, off); }
   __device__ uint64_t u64(uint32_t off) const { return f64(e, off); }
   __device__ uint8_t type() const { return e[FDY_NODE_OFF_TYPE]; }
 };
-
-struct PlaneEntry {
-  const uint32_t* p;  // dword 0 of the node
-  __device__ uint32_t u32(uint32_t off) const { return p[(off >> 2) * kNodeChunk]; }
-  __device__ uint64_t u64(uint32_t off) const { return (uint64_t)u32(off) | ((uint64_t)u32(off + 4) << 32); }
-  __device__ uint8_t type() const { return (uint8_t)(u32(FDY_NODE_OFF_TYPE & ~3u) >> (8 * (FDY_NODE_OFF_TYPE & 3))); }
-};
-
-// Node n of graph G in the field-major tables: chunks hold 256 nodes, a
-// graph's first chunk padded at the front.
-struct PlanePos {
-  uint64_t chunk;
-  uint32_t lane;
-};
-
-__device__ inline PlanePos plane_pos(const DevGraph& G, uint32_t n) {
-  const uint32_t pad = (kNodeChunk - G.num_nodes % kNodeChunk) % kNodeChunk;
-  const uint32_t pos = pad + n;
-  return PlanePos{G.chunk_base + pos / kNodeChunk, pos % kNodeChunk};
-}
 
 // The param references of kernel node entry e: the name, param-index and
 // arg-buffer bounds; an extra-style node's blob.  Per-param nodes are
@@ -336,15 +333,14 @@ __device__ __forceinline__ void scan_params(const DevGraph& Gg, Side& g, bool wi
   const uint32_t ng = wg ? g.num_params : 0, nt = wt ? t.num_params : 0;
   uint64_t prev_g = 0, prev_t = 0, words_g = 0, words_t = 0;
   bool same = ng == nt;
-  // The first kPlaneParams entries come from the field-major copy, the rest
-  // in place (byte-safe loads: a side's entries may sit at any alignment).
+  // Byte-safe loads: a side's entries may sit at any alignment.
   for (uint32_t jb = 0; jb < max(ng, nt); jb += kParamBatch) {
     uint64_t eg[kParamBatch], et[kParamBatch];
 #pragma unroll
     for (uint32_t k = 0; k < kParamBatch; ++k) {
       const uint32_t j = jb + k;
-      eg[k] = j < ng ? (g.pp && j < kPlaneParams ? g.pp[(uint64_t)j * kNodeChunk] : ld_u64(g.pidx + 8ull * j)) : 0;
-      et[k] = j < nt ? (t.pp && j < kPlaneParams ? t.pp[(uint64_t)j * kNodeChunk] : ld_u64(t.pidx + 8ull * j)) : 0;
+      eg[k] = j < ng ? ld_u64(g.pidx + 8ull * j) : 0;
+      et[k] = j < nt ? ld_u64(t.pidx + 8ull * j) : 0;
     }
 #pragma unroll
     for (uint32_t k = 0; k < kParamBatch; ++k) {
@@ -578,87 +574,187 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
   (void)e;
 }
 
-// The field-major node table: thread l of chunk c copies the 42 dwords of
-// node (c - chunk_base) * 256 + l - pad of its graph into plane k at
-// planes[(c * 42 + k) * 256 + l]; padding lanes write zeros.
-__global__ __launch_bounds__(kNodeChunk) void k_planes(const uint8_t* img, const DevGraph* graphs,
-                                                       const uint32_t* chunk_graph, uint32_t* planes,
-                                                       uint64_t* pplanes) {
-  const uint32_t c = blockIdx.x, l = threadIdx.x;
-  const DevGraph& G = graphs[chunk_graph[c]];
-  const uint32_t N = G.num_nodes;
-  const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
-  const int64_t n = (int64_t)(c - G.chunk_base) * kNodeChunk + l - pad;
-  uint32_t v[kEntryDwords];
-  if (n >= 0 && n < (int64_t)N) {
-    const uint32_t* e = reinterpret_cast<const uint32_t*>(img + G.sec_off[FDY_SEC_NODES] + 168ull * (uint64_t)n);
-#pragma unroll
-    for (uint32_t k = 0; k < kEntryDwords; ++k) v[k] = e[k];
-  } else {
-#pragma unroll
-    for (uint32_t k = 0; k < kEntryDwords; ++k) v[k] = 0;
-  }
-  uint32_t* out = planes + (uint64_t)c * kEntryDwords * kNodeChunk + l;
-#pragma unroll
-  for (uint32_t k = 0; k < kEntryDwords; ++k) out[k * kNodeChunk] = v[k];
-  // The first kPlaneParams param entries of a per-param kernel node whose
-  // entries lie inside the param-index section (others are never read).
-  uint32_t np = 0;
-  const uint8_t* pidx = nullptr;
-  if (n >= 0 && n < (int64_t)N && (v[FDY_NODE_OFF_TYPE / 4] >> (8 * (FDY_NODE_OFF_TYPE % 4)) & 0xFF) == FDY_NODE_KERNEL) {
-    const uint32_t pio = v[FDY_KOFF_PARAM_INDEX / 4], num = v[FDY_KOFF_NUM_PARAMS / 4];
-    if (v[FDY_KOFF_ARG_OFFSET / 4] == FDY_NO_ARG_BUFFER && (uint64_t)pio + 8ull * num <= G.sec_size[FDY_SEC_PARAM_INDEX]) {
-      np = min(num, kPlaneParams);
-      pidx = img + G.sec_off[FDY_SEC_PARAM_INDEX] + pio;
-    }
-  }
-  uint64_t* pout = pplanes + (uint64_t)c * kPlaneParams * kNodeChunk + l;
-#pragma unroll
-  for (uint32_t j = 0; j < kPlaneParams; ++j) pout[j * kNodeChunk] = j < np ? ld_u64(pidx + 8ull * j) : 0;
-}
-
 // The node pass runs in two parts.
 //
 // Part A, k_node_a: one workgroup of kNodeChunk threads per chunk of a
-// graph's nodes, one node per thread.  A graph's chunks end at its last
-// node, so its first chunk is padded at the front (leading zero records
-// leave a zero-initialised CRC at zero).  Per node: type, params and their
-// bounds, layout and descriptor against the template's node, relocated
-// memset/memcpy pointers, the node-type and kernel-entry records; written
-// to the node descriptor with the node's word counts in place of its word
-// offsets.  Per chunk: the raw CRCs of the two record streams, word and
-// param-byte totals, status bits.
-//
-// Part B, k_node_b: one workgroup per graph: the template's key bytes, the
-// chunk CRCs shifted to their place, word offsets by block scans, the
-// tile -> first-node table, ragged-word sources, flatness, status, digests
-// and the slot descriptors of the diff pass.
+// graph's nodes (a graph's chunks end at its last node, so its first chunk
+// is padded at the front; a graph without nodes has one empty chunk).
+//   - A member whose node count, section sizes and common attrs match its
+//     template's compares the chunk's node entries with the template's
+//     (8-byte words, coalesced) and the union of its clean kernel nodes'
+//     param entries likewise.  Nodes whose bytes all agree are "clean":
+//     every output of theirs equals the template node's (the string
+//     sections and common attrs being identical), so part B copies them.
+//     The chunk's records are then the XOR of the graph's and the
+//     template's (zero at clean nodes; CRCs are linear, so part B adds the
+//     template chunk's CRC).
+//   - Every other node (all of a template's, and those that differ) takes
+//     the per-node path, compacted into the first lanes: type, params and
+//     their bounds, layout and descriptor against the template's node,
+//     relocated memset/memcpy pointers, the node-type and kernel-entry
+//     records.
+// Part B, k_node_b: one workgroup per graph: clean nodes completed from the
+// template's results, the chunk CRCs shifted to their place, word offsets
+// by block scans, the tile -> first-node table, ragged-word sources,
+// flatness, status, digests and the slot descriptors of the diff pass.
 
-// Five waves per SIMD: held to 96 VGPRs it spills 12 bytes per lane and
-// still beats four waves per SIMD at 99 VGPRs (73 -> 68 us, decode-style).
+constexpr uint32_t kEntryWords = 168 / 8;  // 8-byte words of a node entry
+constexpr uint32_t kCompareBatch = 7;      // entry words per side whose loads are issued together
+static_assert(kEntryWords % kCompareBatch == 0, "whole batches");
+constexpr uint32_t kStrStage = 2048;       // string sections up to this size are staged in LDS
+constexpr uint32_t kChunkCtxDiff = 1, kChunkPidxDiff = 2;
+
+__device__ __forceinline__ uint32_t node_chunks(uint32_t N) { return max(1u, (N + kNodeChunk - 1) / kNodeChunk); }
+
+// The node-type record (type, then the key's cluster dims for a kernel
+// node, csrc/CUDAGraphParallel.cpp:1807-1833) and the kernel-entry record
+// (binary hash, CRC-64/XZ of the name) of node entry e.
+__device__ __forceinline__ void node_records(const RawEntry& e, const uint8_t* common, const Strings& str,
+                                             const uint64_t (*slice)[256], uint64_t r[4]) {
+  const uint8_t type = e.type();
+  r[0] = type;
+  r[1] = r[2] = r[3] = 0;
+  if (type != FDY_NODE_KERNEL) return;
+  uint32_t cx = 0, cy = 0, cz = 0;
+  if (e.u32(FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
+    cx = e.u32(80);
+    cy = e.u32(84);
+    cz = e.u32(88);
+  }
+  if (cx == 0 && common && (f32(common, 0) & FDY_KNA_CLUSTER_DIM)) {
+    cx = f32(common, 4);
+    cy = f32(common, 8);
+    cz = f32(common, 12);
+  }
+  if (cx == 0) {
+    cx = e.u32(64);
+    cy = e.u32(68);
+    cz = e.u32(72);
+  }
+  r[0] |= (uint64_t)cx << 32;
+  r[1] = cy | ((uint64_t)cz << 32);
+  r[2] = e.u64(FDY_KOFF_BINARY_HASH);
+  r[3] = name_crc(str, e, slice);
+}
+
+// The per-node path for node n of graph g (template t, is_t when g is its
+// own template): everything the node pass reports for the node.
+struct NodeOut {
+  NodeDesc d;
+  uint64_t p0, p1;
+  uint64_t pbytes;
+  uint64_t rec[4];  // node-type record (2 words), kernel-entry record (2 words)
+};
+
+__device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& Gg, const DevGraph& Gt, bool is_t,
+                                          uint32_t n, const Strings& sg_str, const Strings& st_str,
+                                          const uint8_t* common_g, const uint8_t* common_t, bool same_ctx,
+                                          bool xor_t, const uint64_t (*slice)[256], NodeOut& o) {
+  const uint8_t* img = a.img;
+  const uint32_t NT = Gt.num_nodes;
+  const RawEntry eg{img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n};
+  const bool has_t = !is_t && n < NT;
+  const RawEntry et{img + Gt.sec_off[FDY_SEC_NODES] + 168ull * (has_t ? n : 0)};
+  uint32_t words_g = 0, words_t = 0, flags = 0;
+  uint64_t src_g = 0, src_t = 0, pbytes = 0;
+  const uint8_t type = eg.type();
+  const uint8_t ttype = has_t ? et.type() : 0xFF;
+  node_records(eg, common_g, sg_str, slice, o.rec);
+  Side sg{}, st{};
+  bool same_sizes = false;
+  if (type == FDY_NODE_KERNEL) side_header(img, Gg, eg, sg);
+  const bool t_kernel = has_t && ttype == FDY_NODE_KERNEL;
+  if (t_kernel) side_header(img, Gt, et, st);
+  scan_params(Gg, sg, type == FDY_NODE_KERNEL, Gt, st, t_kernel, &same_sizes);
+  if (type == FDY_NODE_KERNEL) {
+    words_g = sg.words;
+    pbytes = sg.pbytes;
+    src_g = sg.src;
+    if (sg.ragged) flags |= FDY_NODE_RAGGED;
+    if (sg.bad) flags |= kNodeBad;
+    if (sg.extra) flags |= kNodeExtra;
+  }
+  node_pointers(eg, a.reloc, &o.p0, &o.p1);
+  if (is_t) {
+    flags |= FDY_NODE_TEMPLATE;
+  } else if (has_t) {
+    uint64_t q0, q1;
+    node_pointers(et, a.reloc, &q0, &q1);
+    bool layout = ttype != type;
+    if (t_kernel) {
+      words_t = st.words;
+      src_t = st.src;
+      if (st.ragged) flags |= kNodeRaggedT;
+      if (type == FDY_NODE_KERNEL) layout = !same_layout(sg, st, same_sizes);
+    }
+    if (layout) flags |= FDY_NODE_LAYOUT;
+    else if (words_g) flags |= kNodeCompare;
+    if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, o.p0, o.p1, q0, q1, same_ctx)) flags |= FDY_NODE_DESC;
+    if (xor_t) {
+      uint64_t rt[4];
+      node_records(et, common_t, st_str, slice, rt);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) o.rec[k] ^= rt[k];
+    }
+  } else {
+    flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
+  }
+  o.d.gword = 0;        // word offsets are filled in by k_node_b
+  o.d.nwords = words_g;
+  o.d.tword = words_t;  // the template node's word count until then
+  o.d.flags = flags;
+  o.d.src_g = src_g;
+  o.d.src_t = src_t;
+  o.pbytes = pbytes;
+}
+
+// Five waves per SIMD (registers held to 96 for that; LDS under 32 KB).
 __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
-  constexpr uint32_t kStrStage = 2048; // string sections up to this size are staged in LDS
   static_assert(kNodeChunk == kPosRecords, "one position multiplier per record of a chunk");
   __shared__ uint64_t s_slice[8][256];
   __shared__ uint64_t s_str[2][kStrStage / 8];
   __shared__ uint64_t s_common[2][7];
   // The chunk's node-type and kernel-entry records, eight to a row; the odd
   // row length keeps a half-wave's reads of eight rows apart in the banks.
+  // Before the records, the same rows hold each node's param-index offset
+  // and count for the param-entry check.
   __shared__ uint64_t s_rec[2][kNodeChunk / 8][17];
-  __shared__ uint32_t s_diff;
-  __shared__ uint32_t s_sum[2][kNodeChunk / 64];
+  static_assert(sizeof(s_rec) >= 2 * kNodeChunk * sizeof(uint32_t), "param-entry fields fit the record rows");
+  uint32_t* const s_pio = reinterpret_cast<uint32_t*>(&s_rec[0][0][0]);
+  uint32_t* const s_np = s_pio + kNodeChunk;
+  __shared__ uint8_t s_type[kNodeChunk], s_perparam[kNodeChunk], s_dirty[kNodeChunk], s_launch[kNodeChunk];
+  __shared__ uint16_t s_list[kNodeChunk];
+  __shared__ uint32_t s_wave_n[kNodeChunk / 64];
   __shared__ uint64_t s_pb[kNodeChunk / 64];
-  __shared__ uint32_t s_status;
+  __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax;
 
-  const uint32_t chunk = blockIdx.x, tid = threadIdx.x;
+  const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint32_t g = a.chunk_graph[chunk];
   const uint32_t t = a.template_of[g];
   const bool is_t = t == g;
   const DevGraph& Gg = a.graphs[g];
   const DevGraph& Gt = a.graphs[t];
-  const uint32_t N = Gg.num_nodes, NT = Gt.num_nodes;
+  const uint32_t N = Gg.num_nodes;
+  const uint32_t c = chunk - Gg.chunk_base;
   const uint8_t* img = a.img;
-  if (tid == 0) s_status = 0;
+  const bool common_g_on = (Gg.flags & FDY_HAS_COMMON_ATTRS) && Gg.sec_size[FDY_SEC_COMMON_ATTRS] >= 52;
+  const bool common_t_on = (Gt.flags & FDY_HAS_COMMON_ATTRS) && Gt.sec_size[FDY_SEC_COMMON_ATTRS] >= 52;
+  // Equal node counts, section sizes (bounds then agree node for node) and
+  // common-attr presence: the byte compare may decide nodes.
+  const bool fast = !is_t && N == Gt.num_nodes && common_g_on == common_t_on &&
+                    Gg.sec_size[FDY_SEC_STRINGS] == Gt.sec_size[FDY_SEC_STRINGS] &&
+                    Gg.sec_size[FDY_SEC_PARAM_INDEX] == Gt.sec_size[FDY_SEC_PARAM_INDEX] &&
+                    Gg.sec_size[FDY_SEC_PARAM_DATA] == Gt.sec_size[FDY_SEC_PARAM_DATA] &&
+                    Gg.sec_size[FDY_SEC_ARG_DATA] == Gt.sec_size[FDY_SEC_ARG_DATA];
+
+  if (tid == 0) {
+    s_flags = 0;
+    s_status = 0;
+    s_pmin = 0xFFFFFFFFu;
+    s_pmax = 0;
+  }
+  s_dirty[tid] = 0;
+  s_launch[tid] = 0;
 
   // CRC tables, the (small) string sections and the common attrs in LDS;
   // sections start 8-byte aligned.
@@ -670,181 +766,197 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     }
     return S;
   };
-  auto stage_common = [&](const DevGraph& G, uint64_t* buf) -> const uint8_t* {
-    if (!(G.flags & FDY_HAS_COMMON_ATTRS) || G.sec_size[FDY_SEC_COMMON_ATTRS] < 52) return nullptr;
+  auto stage_common = [&](bool on, const DevGraph& G, uint64_t* buf) -> const uint8_t* {
+    if (!on) return nullptr;
     if (tid < 7) buf[tid] = reinterpret_cast<const uint64_t*>(img + G.sec_off[FDY_SEC_COMMON_ATTRS])[tid];
     return reinterpret_cast<const uint8_t*>(buf);
   };
   const Strings sg_str = stage_strings(Gg, s_str[0]);
   const Strings st_str = is_t ? sg_str : stage_strings(Gt, s_str[1]);
-  const uint8_t* common_g = stage_common(Gg, s_common[0]);
-  const uint8_t* common_t = is_t ? common_g : stage_common(Gt, s_common[1]);
-  if (tid == 0) s_diff = 0;
+  const uint8_t* common_g = stage_common(common_g_on, Gg, s_common[0]);
+  const uint8_t* common_t = is_t ? common_g : stage_common(common_t_on, Gt, s_common[1]);
   stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
-  __syncthreads();
-  const uint64_t (*slice)[256] = s_slice;
-  // Identical string sections and common attrs (both staged in LDS) let the
-  // descriptor compare use the entry bytes alone.
-  bool same_ctx = false;
-  if (!is_t && sg_str.size == st_str.size && sg_str.size <= kStrStage && (common_g == nullptr) == (common_t == nullptr)) {
-    const uint32_t nw = (uint32_t)((sg_str.size + 7) / 8);
-    uint32_t d = 0;
-    for (uint32_t w = tid; w < nw; w += kNodeChunk) d |= s_str[0][w] != s_str[1][w];
-    if (common_g && tid < 7) d |= s_common[0][tid] != s_common[1][tid];
-    if (d) atomicOr(&s_diff, 1u);
-    __syncthreads();
-    same_ctx = s_diff == 0;
-  }
 
   const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
-  const int64_t first = (int64_t)(chunk - Gg.chunk_base) * kNodeChunk - pad;  // node of thread 0
+  const int64_t first = (int64_t)c * kNodeChunk - pad;  // node of thread 0
+  if (fast) {
+    // The chunk's entries against the template's: word w of the chunk is
+    // word w % 21 of its node w / 21 (168 = 21 * 8), read coalesced.
+    const uint8_t* eg0 = img + Gg.sec_off[FDY_SEC_NODES];
+    const uint8_t* et0 = img + Gt.sec_off[FDY_SEC_NODES];
+    const int64_t b0 = first * 168, bend = 168 * (int64_t)N;
+#pragma unroll
+    for (uint32_t mb = 0; mb < kEntryWords; mb += kCompareBatch) {
+      uint64_t vg[kCompareBatch], vt[kCompareBatch];
+#pragma unroll
+      for (uint32_t m = 0; m < kCompareBatch; ++m) {
+        const int64_t off = b0 + 8 * (int64_t)(tid + kNodeChunk * (mb + m));
+        const bool ok = off >= 0 && off < bend;
+        vg[m] = ok ? *reinterpret_cast<const uint64_t*>(eg0 + off) : 0;
+        vt[m] = ok ? *reinterpret_cast<const uint64_t*>(et0 + off) : 0;
+      }
+#pragma unroll
+      for (uint32_t m = 0; m < kCompareBatch; ++m) {
+        const uint32_t w = tid + kNodeChunk * (mb + m), node = w / kEntryWords, k = w % kEntryWords;
+        // Words 1-3 and the low half of word 4 of a kernel entry are its
+        // launch dimensions and shared memory (bytes 8-36): a difference
+        // there alone changes the node's descriptor and nothing else.
+        const uint64_t x = vg[m] ^ vt[m];
+        if (x) {
+          if ((k >= 1 && k <= 3) || (k == 4 && (x >> 32) == 0)) s_launch[node] = 1;
+          else s_dirty[node] = 1;
+        }
+        // Fields the param-entry check needs: type (word 0), param index
+        // offset and count (word 16), arg buffer offset (word 17).
+        if (k == 0) s_type[node] = (uint8_t)(vg[m] >> 32);
+        if (k == FDY_KOFF_PARAM_INDEX / 8) {
+          s_pio[node] = (uint32_t)vg[m];
+          s_np[node] = (uint32_t)(vg[m] >> 32);
+        }
+        if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg[m] == FDY_NO_ARG_BUFFER;
+      }
+    }
+  }
+  __syncthreads();
+
   const int64_t ns = first + tid;
   const bool valid = ns >= 0 && ns < (int64_t)N;
   const uint32_t n = valid ? (uint32_t)ns : 0;
-  uint32_t words_g = 0, words_t = 0, flags = 0;
-  uint64_t src_g = 0, src_t = 0, p0 = 0, p1 = 0, pbytes = 0;
-  uint64_t tw0 = 0, tw1 = 0, kw0 = 0, kw1 = 0;
-  const PlaneEntry eg{a.planes + ((uint64_t)chunk * kEntryDwords) * kNodeChunk + tid};
-  const PlanePos tpos = plane_pos(Gt, n < NT ? n : 0);
-  const PlaneEntry et{a.planes + (tpos.chunk * kEntryDwords) * kNodeChunk + tpos.lane};
-  if (valid) {
-    const uint8_t type = eg.type();
-    const bool has_t = !is_t && n < NT;
-    const uint8_t ttype = has_t ? et.type() : 0xFF;
-    tw0 = type;
-    Side sg{}, st{};
-    bool same_sizes = false;
-    if (type == FDY_NODE_KERNEL) {
-      // Cluster dims of the recomputed key (csrc/CUDAGraphParallel.cpp:1807-1833).
-      uint32_t cx = 0, cy = 0, cz = 0;
-      if (eg.u32(FDY_KOFF_KNA_FLAGS) & FDY_KNA_CLUSTER_DIM) {
-        cx = eg.u32(80);
-        cy = eg.u32(84);
-        cz = eg.u32(88);
+  if (fast) {
+    // Identical string sections and common attrs.
+    bool d = false;
+    if (tid < 7 && common_g) d |= s_common[0][tid] != s_common[1][tid];
+    const uint32_t nw = (uint32_t)((sg_str.size + 7) / 8);
+    const uint64_t* ps = reinterpret_cast<const uint64_t*>(sg_str.p);
+    const uint64_t* pt = reinterpret_cast<const uint64_t*>(st_str.p);
+    for (uint32_t w = tid; w < nw; w += kNodeChunk) d |= ps[w] != pt[w];
+    // Launch-dimension differences are such only in kernel entries (the
+    // same bytes hold other fields of other node types).
+    if (valid && s_launch[tid] && s_type[tid] != FDY_NODE_KERNEL) s_dirty[tid] = 1;
+    // The clean per-param kernel nodes' param entries span [pmin, pmax).
+    uint32_t pmin = 0xFFFFFFFFu, pmax = 0;
+    if (valid && !s_dirty[tid] && s_type[tid] == FDY_NODE_KERNEL && s_perparam[tid] && s_np[tid]) {
+      const uint64_t end = (uint64_t)s_pio[tid] + 8ull * s_np[tid];
+      if (end > Gg.sec_size[FDY_SEC_PARAM_INDEX]) {
+        s_dirty[tid] = 1;  // out of bounds: the per-node path reports it
+      } else {
+        pmin = s_pio[tid];
+        pmax = (uint32_t)end;
       }
-      if (cx == 0 && common_g && (f32(common_g, 0) & FDY_KNA_CLUSTER_DIM)) {
-        cx = f32(common_g, 4);
-        cy = f32(common_g, 8);
-        cz = f32(common_g, 12);
-      }
-      if (cx == 0) {
-        cx = eg.u32(64);
-        cy = eg.u32(68);
-        cz = eg.u32(72);
-      }
-      tw0 |= (uint64_t)cx << 32;
-      tw1 = cy | ((uint64_t)cz << 32);
-      kw0 = eg.u64(FDY_KOFF_BINARY_HASH);
-      kw1 = name_crc(sg_str, eg, slice);
-      side_header(img, Gg, eg, sg);
     }
-    const bool t_kernel = has_t && ttype == FDY_NODE_KERNEL;
-    if (t_kernel) side_header(img, Gt, et, st);
-    sg.pp = a.pplanes + ((uint64_t)chunk * kPlaneParams) * kNodeChunk + tid;
-    st.pp = a.pplanes + (tpos.chunk * kPlaneParams) * kNodeChunk + tpos.lane;
-    scan_params(Gg, sg, type == FDY_NODE_KERNEL, Gt, st, t_kernel, &same_sizes);
-    if (type == FDY_NODE_KERNEL) {
-      words_g = sg.words;
-      pbytes = sg.pbytes;
-      src_g = sg.src;
-      if (sg.ragged) flags |= FDY_NODE_RAGGED;
-      if (sg.bad) flags |= kNodeBad;
-    }
-    node_pointers(eg, a.reloc, &p0, &p1);
-    if (is_t) {
-      flags |= FDY_NODE_TEMPLATE;
-    } else if (has_t) {
-      uint64_t q0, q1;
-      node_pointers(et, a.reloc, &q0, &q1);
-      bool layout = ttype != type;
-      if (t_kernel) {
-        words_t = st.words;
-        src_t = st.src;
-        if (st.ragged) flags |= kNodeRaggedT;
-        if (type == FDY_NODE_KERNEL) layout = !same_layout(sg, st, same_sizes);
-      }
-      if (layout) flags |= FDY_NODE_LAYOUT;
-      else if (words_g) flags |= kNodeCompare;
-      if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, p0, p1, q0, q1, same_ctx)) flags |= FDY_NODE_DESC;
-    } else {
-      flags |= FDY_NODE_LAYOUT | FDY_NODE_DESC;
-    }
-    if (flags & kNodeBad) atomicOr(&s_status, FDY_GRAPH_BAD_PARAMS);
-
-    const uint64_t gi = Gg.node_base + n;
-    NodeDesc d;
-    d.gword = 0;          // word offsets are filled in by k_node_b
-    d.nwords = words_g;
-    d.tword = words_t;    // the template node's word count until then
-    d.flags = flags;
-    d.src_g = src_g;
-    d.src_t = src_t;
-    a.node_desc[gi] = d;
-    a.node_flags[gi] = (uint8_t)(flags & 0x0F);
-    a.node_ptrs[2 * gi] = p0;
-    a.node_ptrs[2 * gi + 1] = p1;
-    if (is_t) a.live_src[gi] = g;
-  }
-
-  // The records go to LDS (zero for the front padding: leading zero records
-  // leave a zero-initialised CRC at zero).
-  s_rec[0][tid >> 3][2 * (tid & 7)] = tw0;
-  s_rec[0][tid >> 3][2 * (tid & 7) + 1] = tw1;
-  s_rec[1][tid >> 3][2 * (tid & 7)] = kw0;
-  s_rec[1][tid >> 3][2 * (tid & 7) + 1] = kw1;
-  uint32_t sum_g = words_g, sum_t = words_t;
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    sum_g += __shfl_down(sum_g, (unsigned)d, 64);
-    sum_t += __shfl_down(sum_t, (unsigned)d, 64);
-    pbytes += shfl_down64(pbytes, d);
-  }
-  if ((tid & 63) == 0) {
-    s_sum[0][tid >> 6] = sum_g;
-    s_sum[1][tid >> 6] = sum_t;
-    s_pb[tid >> 6] = pbytes;
+    for (int dd = 32; dd >= 1; dd >>= 1) {
+      pmin = min(pmin, (uint32_t)__shfl_down(pmin, (unsigned)dd, 64));
+      pmax = max(pmax, (uint32_t)__shfl_down(pmax, (unsigned)dd, 64));
+    }
+    if (lane == 0 && pmax) {
+      atomicMin(&s_pmin, pmin);
+      atomicMax(&s_pmax, pmax);
+    }
+    if (__ballot(d) && lane == 0) atomicOr(&s_flags, kChunkCtxDiff);
   }
   __syncthreads();
+  if (fast && s_pmax > s_pmin) {
+    // The section sizes are equal and 8-byte aligned, so the words that
+    // cover [pmin, pmax) lie inside both.
+    const uint64_t* pg = reinterpret_cast<const uint64_t*>(img + Gg.sec_off[FDY_SEC_PARAM_INDEX]);
+    const uint64_t* pt = reinterpret_cast<const uint64_t*>(img + Gt.sec_off[FDY_SEC_PARAM_INDEX]);
+    bool d = false;
+    for (uint32_t q = s_pmin / 8 + tid; q < (s_pmax + 7) / 8; q += kNodeChunk) d |= pg[q] != pt[q];
+    if (d) atomicOr(&s_flags, kChunkPidxDiff);
+  }
+  __syncthreads();
+  // The record rows are free again: zero them (clean and padding nodes
+  // keep zero records).
+  s_rec[0][tid >> 3][2 * (tid & 7)] = s_rec[0][tid >> 3][2 * (tid & 7) + 1] = 0;
+  s_rec[1][tid >> 3][2 * (tid & 7)] = s_rec[1][tid >> 3][2 * (tid & 7) + 1] = 0;
+  const bool same_ctx = fast && !(s_flags & kChunkCtxDiff);
+  const bool diff = fast && s_flags == 0;  // records as XORs with the template's; clean nodes skipped
+  const bool mine = valid && (!diff || s_dirty[tid]);
+  const uint64_t mb = __ballot(mine);
+  if (lane == 0) s_wave_n[wave] = (uint32_t)__popcll(mb);
+  if (valid && !mine) {
+    NodeDesc d{};
+    d.flags = kNodeClean | (s_launch[tid] ? FDY_NODE_DESC : 0u);
+    a.node_desc[Gg.node_base + n] = d;
+  }
+  __syncthreads();
+  uint32_t before = 0, total = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < kNodeChunk / 64; ++w) {
+    before += w < wave ? s_wave_n[w] : 0u;
+    total += s_wave_n[w];
+  }
+  if (mine) s_list[before + (uint32_t)__popcll(mb & ((1ull << lane) - 1))] = (uint16_t)tid;
+  __syncthreads();
+
+  uint64_t pbytes = 0;
+  for (uint32_t k = tid; k < total; k += kNodeChunk) {
+    const uint32_t slot = s_list[k];
+    const uint32_t nn = (uint32_t)(first + slot);
+    NodeOut o;
+    node_full(a, Gg, Gt, is_t, nn, sg_str, st_str, common_g, common_t, same_ctx, diff, s_slice, o);
+    const uint64_t gi = Gg.node_base + nn;
+    a.node_desc[gi] = o.d;
+    a.node_flags[gi] = (uint8_t)(o.d.flags & 0x0F);
+    a.node_ptrs[2 * gi] = o.p0;
+    a.node_ptrs[2 * gi + 1] = o.p1;
+    a.node_pbytes[gi] = o.pbytes;
+    if (is_t) a.live_src[gi] = g;
+    if (o.d.flags & kNodeBad) atomicOr(&s_status, FDY_GRAPH_BAD_PARAMS);
+    pbytes += o.pbytes;
+    s_rec[0][slot >> 3][2 * (slot & 7)] = o.rec[0];
+    s_rec[0][slot >> 3][2 * (slot & 7) + 1] = o.rec[1];
+    s_rec[1][slot >> 3][2 * (slot & 7)] = o.rec[2];
+    s_rec[1][slot >> 3][2 * (slot & 7) + 1] = o.rec[3];
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) pbytes += shfl_down64(pbytes, d);
+  if (lane == 0) s_pb[wave] = pbytes;
+  __syncthreads();
   if (tid >= 64) return;
+  if (total == 0) {  // every record is zero (clean member chunk, or padding only): so are their CRCs
+    if (tid == 0) {
+      NodeChunk ch;
+      ch.crc_type = ch.crc_kent = 0;
+      ch.pbytes = 0;
+      for (uint32_t w = 0; w < kNodeChunk / 64; ++w) ch.pbytes += s_pb[w];
+      ch.status = s_status;
+      ch.mode = diff ? kChunkDiff : 0u;
+      a.chunks[chunk] = ch;
+    }
+    return;
+  }
   // Raw CRCs of the two record streams, by the first wave: lane l folds the
   // eight records 8q..8q+7 (q = l % 32) of stream l / 32 into one raw CRC
   // and moves it into place, times x^(8*16*(255-(8q+7))); each half-wave
   // XOR-joins its 32 shares (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).
-  // One position multiply per lane of one wave, where a multiply per record
-  // would cost every wave two.
   static_assert(kNodeChunk == 8 * 32, "eight records per lane, 32 lanes per stream");
   uint64_t z = 0;
   {
     const uint32_t st = tid >> 5, q = tid & 31;
 #pragma unroll
-    for (uint32_t r = 0; r < 16; ++r) z = crc_slice8(slice, z, s_rec[st][q][r]);
+    for (uint32_t r = 0; r < 16; ++r) z = crc_slice8(s_slice, z, s_rec[st][q][r]);
     z = z ? gf2_mulmod(a.cc->pos16[8 * q + 7], z) : 0;
 #pragma unroll
     for (int d = 16; d >= 1; d >>= 1) z ^= shfl_down64(z, d);  // lanes 0 and 32 hold their half's XOR
   }
   const uint64_t zk = ((uint64_t)__shfl((uint32_t)(z >> 32), 32, 64) << 32) | __shfl((uint32_t)z, 32, 64);
   if (tid == 0) {
-    NodeChunk c;
-    c.crc_type = z;
-    c.crc_kent = zk;
-    c.pbytes = 0;
-    uint64_t wg = 0, wt = 0;
-    for (uint32_t w = 0; w < kNodeChunk / 64; ++w) {
-      wg += s_sum[0][w];
-      wt += s_sum[1][w];
-      c.pbytes += s_pb[w];
-    }
-    c.words_g = wg > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)wg;
-    c.words_t = wt > 0xFFFFFFFFull ? 0xFFFFFFFFu : (uint32_t)wt;
-    c.status = s_status;
-    c.pad_ = 0;
-    a.chunks[chunk] = c;
+    NodeChunk ch;
+    ch.crc_type = z;
+    ch.crc_kent = zk;
+    ch.pbytes = 0;
+    for (uint32_t w = 0; w < kNodeChunk / 64; ++w) ch.pbytes += s_pb[w];
+    ch.status = s_status;
+    ch.mode = diff ? kChunkDiff : 0u;
+    a.chunks[chunk] = ch;
   }
 }
 
 __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   __shared__ uint32_t s_tmp[kNodeThreads / 64];
-  __shared__ uint64_t s_x[2][kNodeThreads / 64];
+  __shared__ uint64_t s_x[4][kNodeThreads / 64];
   __shared__ unsigned long long s_pb;
   __shared__ uint32_t s_status, s_words, s_flat, s_tbase;
 
@@ -857,50 +969,46 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
   const uint8_t* img = a.img;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (threadIdx.x == 0) {
-    s_status = a.status[g];  // the grouping pass's collision bit
+    s_status = 0;
     s_pb = 0;
     s_flat = 1;
   }
   __syncthreads();
 
-  // Chunk results: each chunk's raw CRC times x^(8 * bytes after it),
-  // XOR-joined; param bytes and status bits.  One wave per chunk: lane i
-  // holds the multiplier times x^i and keeps it where the CRC has x^i
-  // (bit 63 - i); the wave's XOR is the product.
+  // Chunk results, one wave per chunk: the node-type and kernel-entry CRCs
+  // (of a diff chunk: XORed with the template chunk's) shifted past the
+  // chunks after them; param bytes and status bits.
   static_assert(kNodeChunk == kPosRecords, "chunk shift tables are built for kPosRecords records per chunk");
-  const uint32_t nch = (N + kNodeChunk - 1) / kNodeChunk;
-  uint64_t xt = 0, xk = 0, pb = 0;
+  const uint32_t nch = node_chunks(N);
+  uint64_t x[4] = {0, 0, 0, 0}, pb = 0;
   uint32_t st = 0;
   for (uint32_t c = wave; c < nch; c += kNodeThreads / 64) {
     const NodeChunk ch = a.chunks[Gg.chunk_base + c];
-    const uint32_t k = nch - 1 - c;
-    if (k < (uint32_t)kChunkShifts) {
-      const uint64_t mi = a.cc->chunk_shift[k][lane];
-      if ((ch.crc_type >> (63 - lane)) & 1) xt ^= mi;
-      if ((ch.crc_kent >> (63 - lane)) & 1) xk ^= mi;
-    } else if (lane == 0) {
-      const uint64_t m = x2n_mod(a.cc->x2n.v, 16ull * kNodeChunk * k, 3);
-      xt ^= gf2_mulmod(m, ch.crc_type);
-      xk ^= gf2_mulmod(m, ch.crc_kent);
+    uint64_t rt = ch.crc_type, rk = ch.crc_kent;
+    if (ch.mode & kChunkDiff) {
+      const NodeChunk& ct = a.chunks[Gt.chunk_base + c];
+      rt ^= ct.crc_type;
+      rk ^= ct.crc_kent;
     }
+    x[2] ^= shift_share(a.cc, rt, nch - 1 - c, lane);
+    x[3] ^= shift_share(a.cc, rk, nch - 1 - c, lane);
     if (lane == 0) {
       pb += ch.pbytes;
       st |= ch.status;
     }
   }
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    xt ^= shfl_down64(xt, d);
-    xk ^= shfl_down64(xk, d);
-  }
-  if (lane == 0) {
-    s_x[0][wave] = xt;
-    s_x[1][wave] = xk;
-  }
-  if (pb) atomicAdd(&s_pb, (unsigned long long)pb);
-  if (st) atomicOr(&s_status, st);
+  for (int d = 32; d >= 1; d >>= 1)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) x[k] ^= shfl_down64(x[k], d);
+  if (lane == 0)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s_x[k][wave] = x[k];
 
-  // Word offsets of every node in the graph's and in the template's image.
+  // Word offsets of every node in the graph's and in the template's image;
+  // clean nodes first take their template node's results (its first pass
+  // is done; its second pass, running beside this one, rewrites only the
+  // template's word offsets).
   uint32_t gcarry = 0, tcarry = 0;
   for (uint32_t base = 0; base < N; base += kNodeThreads) {
     const uint32_t n = base + threadIdx.x;
@@ -908,6 +1016,31 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     const uint64_t gi = Gg.node_base + n;
     NodeDesc d{};
     if (valid) d = a.node_desc[gi];
+    if (valid && (d.flags & kNodeClean)) {
+      const uint64_t ti = Gt.node_base + n;
+      const NodeDesc* dt = a.node_desc + ti;
+      const uint32_t tw = dt->nwords, tf = dt->flags;
+      const uint64_t ts = dt->src_g;
+      const uint64_t q0 = a.node_ptrs[2 * ti], q1 = a.node_ptrs[2 * ti + 1];
+      pb += a.node_pbytes[ti];
+      uint32_t f = (tf & kNodeExtra) | (d.flags & FDY_NODE_DESC);  // launch dimensions differ: DESC
+      if (tf & kNodeBad) {
+        f |= FDY_NODE_LAYOUT | kNodeBad;
+        st |= FDY_GRAPH_BAD_PARAMS;
+      } else {
+        if (tf & FDY_NODE_RAGGED) f |= FDY_NODE_RAGGED | kNodeRaggedT;
+        if (tw) f |= kNodeCompare;
+      }
+      const int sec = (tf & kNodeExtra) ? FDY_SEC_ARG_DATA : FDY_SEC_PARAM_DATA;
+      d.nwords = tw;
+      d.tword = tw;
+      d.flags = f;
+      d.src_t = ts;
+      d.src_g = ts ? ts - Gt.sec_off[sec] + Gg.sec_off[sec] : 0;
+      a.node_flags[gi] = (uint8_t)(f & 0x0F);
+      a.node_ptrs[2 * gi] = q0;
+      a.node_ptrs[2 * gi + 1] = q1;
+    }
     const uint32_t words_g = d.nwords, words_t = d.tword;
     uint32_t flags = d.flags;
     uint32_t tot_g, tot_t;
@@ -927,10 +1060,16 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
                                   d.src_t == Gt.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword));
         if (!ok) s_flat = 0;
       }
-      d.gword = gword;
-      d.tword = tword;
-      d.flags = flags;
-      a.node_desc[gi] = d;
+      if (is_t) {
+        // Only the offsets change: members read this node's other fields.
+        a.node_desc[gi].gword = gword;
+        a.node_desc[gi].tword = tword;
+      } else {
+        d.gword = gword;
+        d.tword = tword;
+        d.flags = flags;
+        a.node_desc[gi] = d;
+      }
       if (words_g) {
         uint64_t k = ((uint64_t)gword + kTileWords - 1) / kTileWords;
         const uint64_t k_last = ((uint64_t)gword + words_g - 1) / kTileWords;
@@ -948,13 +1087,13 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     gcarry += tot_g;
     tcarry += tot_t;
   }
+  if (pb) atomicAdd(&s_pb, (unsigned long long)pb);
+  if (st) atomicOr(&s_status, st);
   __syncthreads();
   if (threadIdx.x == 0) {
-    uint64_t acc_type = 0, acc_kent = 0;
-    for (uint32_t w = 0; w < kNodeThreads / 64; ++w) {
-      acc_type ^= s_x[0][w];
-      acc_kent ^= s_x[1][w];
-    }
+    uint64_t acc[4] = {0, 0, 0, 0};
+    for (uint32_t w = 0; w < kNodeThreads / 64; ++w)
+      for (int k = 0; k < 4; ++k) acc[k] ^= s_x[k][w];
     const bool overflow = gcarry > Gg.word_cap;
     s_words = overflow ? 0 : gcarry;
     uint32_t stat = s_status;
@@ -963,8 +1102,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     a.status[g] = stat;
     a.gwords[g] = s_words;
     a.pbytes[g] = s_pb;
-    a.digests[4ull * g + 2] = acc_type ^ Gg.crc_fin[2];
-    a.digests[4ull * g + 3] = acc_kent ^ Gg.crc_fin[3];
+    for (int k = 2; k < 4; ++k) a.digests[4ull * g + k] = acc[k] ^ Gg.crc_fin[k];  // key and deps: k_digest's
     if (is_t) {
       a.live_cur[g] = g;
       // List the template's slots that hold words for k_diff_t.
@@ -1433,92 +1571,20 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   if (lane < kSubsPerSlot) counts[lane] = lane == 0 ? run : 0u;
 }
 
-// Records per graph: the sum of its slots' sub-range counts (one workgroup
-// per graph; a global atomic per slot instead measured slower).
-constexpr uint32_t kCountThreads = 256;
-
-// Exclusive prefix sum of u64 values over the block (blockDim.x a multiple
-// of 64, at most 4096); *total gets the sum.
-__device__ uint64_t block_excl_scan64(uint64_t v, uint64_t* s_tmp, uint64_t* total) {
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint64_t x = v;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const uint64_t y = ((uint64_t)shfl_up32((uint32_t)(x >> 32), d) << 32) | shfl_up32((uint32_t)x, d);
-    if (lane >= (uint32_t)d) x += y;
-  }
-  if (lane == 63) s_tmp[wave] = x;
-  __syncthreads();
-  uint64_t before = 0, sum = 0;
-  for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
-    const uint64_t t = s_tmp[w];
-    if (w < wave) before += t;
-    sum += t;
-  }
-  __syncthreads();
-  *total = sum;
-  return before + x - v;
-}
-
-// Records per graph and each slot's offset among its graph's records (an
-// exclusive scan over the graph's slots, one slot per thread), so that the
-// compaction reads its base instead of summing every earlier slot's count.
-__global__ __launch_bounds__(kCountThreads) void k_count(RestoreArgs a) {
-  static_assert(kCountThreads == 256, "block_excl_scan covers 256 values");
-  static_assert(kSubsPerSlot % 4 == 0, "a slot's counts are read 16 bytes at a time");
-  __shared__ uint32_t s_tmp[kCountThreads / 64];
-  const uint32_t g = blockIdx.x, tid = threadIdx.x;
-  const DevGraph& G = a.graphs[g];
-  uint32_t carry = 0;
-  for (uint32_t k0 = 0; k0 < G.tile_cap; k0 += kCountThreads) {
-    const uint32_t k = k0 + tid;
-    uint32_t n = 0;
-    if (k < G.tile_cap) {
-      const uint4* c = reinterpret_cast<const uint4*>(a.sub_count + (uint64_t)(G.tile_base + k) * kSubsPerSlot);
-#pragma unroll
-      for (uint32_t q = 0; q < kSubsPerSlot / 4; ++q) {
-        const uint4 v = c[q];
-        n += v.x + v.y + v.z + v.w;
-      }
-    }
-    uint32_t tot;
-    const uint32_t ex = block_excl_scan(n, s_tmp, &tot);
-    if (k < G.tile_cap) a.slot_off[G.tile_base + k] = carry + ex;
-    carry += tot;
-  }
-  if (tid == 0) a.graph_count[g] = carry;
-}
-
-// The override offsets: an exclusive scan of the graph counts by one
-// workgroup (a separate launch: a last-workgroup scan inside the count pass
-// needs device-wide fences, whose L2 write-backs measured slower).
-constexpr uint32_t kScanThreads = 1024;
-
-__global__ __launch_bounds__(kScanThreads) void k_scan(RestoreArgs a) {
-  __shared__ uint64_t s_tmp[kScanThreads / 64];
-  uint64_t base = 0;
-  for (uint32_t j0 = 0; j0 < a.num_graphs; j0 += kScanThreads) {
-    const uint32_t j = j0 + threadIdx.x;
-    uint64_t tot;
-    const uint64_t ex = block_excl_scan64(j < a.num_graphs ? a.graph_count[j] : 0, s_tmp, &tot);
-    if (j < a.num_graphs) a.ovr_off[j] = base + ex;
-    base += tot;
-  }
-  if (threadIdx.x == 0) a.ovr_off[a.num_graphs] = base;
-}
-
-// Move each slot's records to their place in the dense array, completing
-// them: the node holding the word (searched in the slot's node window) and
-// the word's index in the template's image.  The search pass leaves a slot's
-// records at the start of its region in word order, their number in the
-// slot's first sub-range count (the others are zero).  A slot's records
-// start at its graph's override offset plus the slot's offset among the
-// graph's records.  Everything that depends on the slot alone (the count,
-// the first records, the window's bounds) is loaded before what depends on
-// its graph, to keep the chain of dependent loads short.
-// One wave per slot: a slot holds about a hundred records on the presets,
-// and more slots in flight per CU beat more lanes per slot (256 threads per
-// slot: 0.57 ms on the 1024-graph archive; 128: 0.41; 64: 0.36).
+// Move each slot's records to their place in the graph's dense override
+// array, completing them: the node holding the word (searched in the slot's
+// node window) and the word's index in the template's image.  The search
+// pass leaves a slot's records at the start of its region in word order,
+// their number in the slot's first sub-range count (the others are zero).
+// A graph's records start at its own word base in the override array (a
+// graph has at most one record per word), so no scan across graphs is
+// needed: a slot's place is the sum of the counts of the graph's earlier
+// slots, summed by the wave (64 counts per load), and the graph's first
+// slot also writes the graph's total.  Everything that depends on the slot
+// alone (the count, the first records, the window's bounds) is loaded
+// before what depends on its graph, to keep the chain of dependent loads
+// short.  One wave per slot: a slot holds about a hundred records on the
+// presets, and more slots in flight per CU beat more lanes per slot.
 constexpr uint32_t kCompactThreads = 64;
 constexpr uint32_t kCompactPre = 4;  // records per thread loaded up front
 
@@ -1526,7 +1592,6 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
   __shared__ uint2 s_gt[kDiffWindow];  // {first graph word, first template word} of the window's nodes
   const uint32_t slot = blockIdx.x, tid = threadIdx.x;
   const uint32_t total = a.sub_count[(uint64_t)slot * kSubsPerSlot];
-  if (total == 0) return;  // uniform over the workgroup
   const fdy_override* recs = reinterpret_cast<const fdy_override*>(a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords);
   fdy_override pre[kCompactPre];
 #pragma unroll
@@ -1535,16 +1600,45 @@ __global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
     if (i < total) pre[p] = recs[i];
   }
   const SlotDesc sd = load_slot(a.slot_desc + slot);
-  const uint32_t n0 = a.tile_node[slot];
-  const uint32_t off = a.slot_off[slot];
   const DevGraph& G = a.graphs[sd.graph];
   const uint32_t k = slot - G.tile_base;
+  // The records of the graph's slots before this one (all of them for the
+  // first slot, which also reports the graph's total).
+  const uint32_t upto = k == 0 ? G.tile_cap : k;
+  uint32_t before = 0, all = 0;
+  for (uint32_t j = tid; j < upto; j += kCompactThreads) {
+    const uint32_t c = a.sub_count[(uint64_t)(G.tile_base + j) * kSubsPerSlot];
+    all += c;
+    before += j < k ? c : 0u;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    before += __shfl_down(before, (unsigned)d, 64);
+    all += __shfl_down(all, (unsigned)d, 64);
+  }
+  before = __shfl(before, 0, 64);
+  if (k == 0) {
+    if (tid == 0) a.graph_count[sd.graph] = all;
+    // Collision report (the digests are final now): a graph below this
+    // graph's template whose key has the same CRC-64/XZ and length.  Its key
+    // bytes differ, or it would be the template (grouping is by exact bytes).
+    if (!a.explicit_template) {
+      const uint64_t dg = a.digests[4ull * sd.graph];
+      const uint64_t Lg = G.sec_size[FDY_SEC_TOPOLOGY_KEY];
+      bool coll = false;
+      for (uint32_t j = tid; j < sd.tmpl; j += kCompactThreads)
+        coll |= a.digests[4ull * j] == dg && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == Lg;
+      if (__ballot(coll) && tid == 0) atomicOr(&a.status[sd.graph], FDY_GRAPH_COLLISION);
+    }
+  }
+  if (total == 0) return;  // uniform over the workgroup
+  const uint32_t n0 = a.tile_node[slot];
   const uint32_t N = G.num_nodes;
   const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
   const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
   const uint32_t nwin = min(kDiffWindow, n_last - n0 + 1);
   const NodeDesc* nd = a.node_desc + G.node_base;
-  const uint64_t base = a.ovr_off[sd.graph] + off;
+  const uint64_t base = G.word_base + before;
   for (uint32_t i = tid; i < nwin; i += kCompactThreads) {
     const uint4 v = *reinterpret_cast<const uint4*>(nd + n0 + i);  // gword, nwords, tword, flags
     s_gt[i] = make_uint2(v.x, v.z);
@@ -1716,12 +1810,15 @@ __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint6
 
 }  // namespace
 
-hipError_t launch_hash(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_hash, dim3(a.num_graphs), dim3(kHashThreads), 0, s, a);
+hipError_t launch_digests(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_digest, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_khash, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_group, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
   return hipGetLastError();
 }
@@ -1754,19 +1851,7 @@ hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_planes(const uint8_t* img, const DevGraph* graphs, const uint32_t* chunk_graph, uint32_t num_chunks,
-                         uint32_t* planes, uint64_t* pplanes, hipStream_t s) {
-  hipLaunchKernelGGL(k_planes, dim3(num_chunks), dim3(kNodeChunk), 0, s, img, graphs, chunk_graph, planes, pplanes);
-  return hipGetLastError();
-}
-
 hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_count, dim3(a.num_graphs), dim3(kCountThreads), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_scan, dim3(1), dim3(kScanThreads), 0, s, a);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(kCompactThreads), 0, s, a);
   return hipGetLastError();
 }

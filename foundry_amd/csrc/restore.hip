@@ -283,7 +283,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
     nodes += d.num_nodes;
     words += d.word_cap;
     slots += d.tile_cap;
-    chunks += (d.num_nodes + kNodeChunk - 1) / kNodeChunk;
+    chunks += std::max<uint64_t>(1, (d.num_nodes + kNodeChunk - 1) / kNodeChunk);  // at least one per graph
   }
   // The member pass launches 1024 threads per tile, and a launch holds fewer than 2^32 threads.
   if (slots >= (1ull << 22)) return err(FDY_E_FORMAT, "archive too large (more than 2^22 diff tiles, 128 GiB of params)");
@@ -295,7 +295,9 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   std::vector<uint32_t> chunk_graph(chunks);
   for (uint32_t i = 0; i < G; ++i)
     std::fill(chunk_graph.begin() + a->graphs[i].chunk_base,
-              chunk_graph.begin() + a->graphs[i].chunk_base + (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk, i);
+              chunk_graph.begin() + a->graphs[i].chunk_base +
+                  std::max<uint64_t>(1, (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk),
+              i);
 
   int rc = 0;
   auto alloc = [&](DevBuf& b, size_t bytes, const char* what) {
@@ -317,20 +319,18 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   alloc(a->live_src, 4 * nodes, "live node sources");
   alloc(a->tile_node, 4 * slots, "tile table");
   alloc(a->chunk_graph, 4 * chunks, "node chunk table");
-  alloc(a->planes, 4ull * kEntryDwords * kNodeChunk * chunks, "field-major node table");
-  alloc(a->pplanes, 8ull * kPlaneParams * kNodeChunk * chunks, "field-major param entries");
+  alloc(a->node_pbytes, 8 * nodes, "node param bytes");
+  alloc(a->key_hash, 8ull * G, "key hashes");
   alloc(a->chunks, sizeof(NodeChunk) * chunks, "node chunk results");
   alloc(a->slot_desc, sizeof(SlotDesc) * slots, "slot descriptors");
   alloc(a->tslots, 4 * (slots + 1), "template slot list");
   alloc(a->sub_count, 4 * slots * kSubsPerSlot, "record counts");
   alloc(a->graph_count, 4ull * G, "graph record counts");
-  alloc(a->slot_off, 4 * slots, "slot record offsets");
   alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * slots, "candidate and record regions");
   alloc(a->aux, 8 * words, "ragged word sources");
   alloc(a->image, 8 * words, "param images");
   alloc(a->live, 8 * words, "live images");
   alloc(a->ovr, sizeof(fdy_override) * words, "override records");
-  alloc(a->ovr_off, 8ull * (G + 1), "override offsets");
   if (rc) return rc;
 
   FDY_HIP(hipMemcpy(a->img.p, stage.p, a->img_bytes, hipMemcpyHostToDevice));
@@ -340,13 +340,6 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(a->chunk_graph.p, chunk_graph.data(), 4 * chunks, hipMemcpyHostToDevice));
-  // The node tables, field-major, once per archive: the node pass reads
-  // them with coalesced loads (the image itself never changes).
-  if (chunks) {
-    FDY_HIP(launch_planes(a->img.as<uint8_t>(), a->dgraphs.as<DevGraph>(), a->chunk_graph.as<uint32_t>(),
-                          (uint32_t)chunks, a->planes.as<uint32_t>(), a->pplanes.as<uint64_t>(), nullptr));
-    FDY_HIP(hipStreamSynchronize(nullptr));
-  }
   return FDY_OK;
 }
 
@@ -364,11 +357,16 @@ int ensure_cache(fdy_archive* a, hipStream_t s) {
   a->h_gwords.resize(G);
   a->h_pbytes.resize(G);
   a->h_ovr_off.resize(G + 1);
+  std::vector<uint32_t> counts(G);
   FDY_HIP(hipMemcpy(a->h_tmpl.data(), a->tmpl.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_status.data(), a->status.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_gwords.data(), a->gwords.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_pbytes.data(), a->pbytes.p, 8ull * G, hipMemcpyDeviceToHost));
-  FDY_HIP(hipMemcpy(a->h_ovr_off.data(), a->ovr_off.p, 8ull * (G + 1), hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(counts.data(), a->graph_count.p, 4ull * G, hipMemcpyDeviceToHost));
+  // Offsets of each graph's records in canonical order over all graphs (the
+  // device keeps graph g's records from index word_base(g) instead).
+  a->h_ovr_off[0] = 0;
+  for (uint32_t i = 0; i < G; ++i) a->h_ovr_off[i + 1] = a->h_ovr_off[i] + counts[i];
   a->h_current.resize(G);
   for (uint32_t i = 0; i < G; ++i) a->h_current[i] = i;
   a->cached = true;
@@ -403,9 +401,9 @@ int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty) {
   if (c == g) return FDY_OK;
   FDY_HIP(hipSetDevice(a->device));
   SwitchArgs w{};
-  w.ovr_cur = a->ovr.as<fdy_override>() + a->h_ovr_off[c];
+  w.ovr_cur = a->ovr.as<fdy_override>() + a->graphs[c].word_base;
   w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
-  w.ovr_new = a->ovr.as<fdy_override>() + a->h_ovr_off[g];
+  w.ovr_new = a->ovr.as<fdy_override>() + a->graphs[g].word_base;
   w.n_new = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
   w.tmpl_image = a->image.as<uint64_t>() + a->graphs[t].word_base;
   w.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
@@ -724,6 +722,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.chunks = a->chunks.as<NodeChunk>();
   r.digests = a->digests.as<uint64_t>();
   r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
+  r.key_hash = a->key_hash.as<uint64_t>();
   r.template_of = a->tmpl.as<uint32_t>();
   r.status = a->status.as<uint32_t>();
   r.gwords = a->gwords.as<uint32_t>();
@@ -741,20 +740,29 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.live_src = a->live_src.as<uint32_t>();
   r.live_cur = a->live_cur.as<uint32_t>();
   r.ovr = a->ovr.as<fdy_override>();
-  r.ovr_off = a->ovr_off.as<uint64_t>();
   r.cand = a->cand.as<Candidate>();
   r.sub_count = a->sub_count.as<uint32_t>();
   r.graph_count = a->graph_count.as<uint32_t>();
-  r.slot_off = a->slot_off.as<uint32_t>();
-  r.planes = a->planes.as<uint32_t>();
-  r.pplanes = a->pplanes.as<uint64_t>();
+  r.node_pbytes = a->node_pbytes.as<uint64_t>();
   r.reloc = a->reloc.dev;
+  if (!a->side) {
+    FDY_HIP(hipStreamCreateWithFlags(&a->side, hipStreamNonBlocking));
+    FDY_HIP(hipEventCreateWithFlags(&a->fork, hipEventDisableTiming));
+    FDY_HIP(hipEventCreateWithFlags(&a->join, hipEventDisableTiming));
+  }
   if (a->timing) {
     for (hipEvent_t& e : a->ev)
       if (!e) FDY_HIP(hipEventCreate(&e));
     FDY_HIP(hipEventRecord(a->ev[0], s));
   }
-  FDY_HIP(launch_hash(r, s));
+  // The key and dependency digests depend on the image alone: they run on
+  // the side stream from here and join before the compaction reads them.
+  FDY_HIP(hipEventRecord(a->fork, s));
+  FDY_HIP(hipStreamWaitEvent(a->side, a->fork, 0));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[8], a->side));
+  FDY_HIP(launch_digests(r, a->side));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[9], a->side));
+  FDY_HIP(hipEventRecord(a->join, a->side));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
   FDY_HIP(launch_group(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
@@ -766,6 +774,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
   FDY_HIP(launch_diff_search(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
+  FDY_HIP(hipStreamWaitEvent(s, a->join, 0));
   FDY_HIP(launch_compact(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[7], s));
   a->timed = a->timing;
@@ -785,7 +794,7 @@ int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
   FDY_HIP(hipEventSynchronize(a->ev[7]));
-  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
+  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[8], a->ev[9]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
   FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));
@@ -842,8 +851,8 @@ int fdy_get_overrides(fdy_archive* a, void* stream, uint32_t g, fdy_override* ou
   int rc = check_graph(a, g);
   if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
   if (rc) return rc;
-  const uint64_t b = a->h_ovr_off[g], n = a->h_ovr_off[g + 1] - b;
-  return copy_out(a->ovr.as<fdy_override>() + b, n, out, cap, n_out);
+  const uint64_t n = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
+  return copy_out(a->ovr.as<fdy_override>() + a->graphs[g].word_base, n, out, cap, n_out);
 }
 
 int fdy_get_node_flags(fdy_archive* a, void* stream, uint32_t g, uint8_t* out, uint64_t cap, uint64_t* n_out) {

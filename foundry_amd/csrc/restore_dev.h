@@ -24,10 +24,13 @@ constexpr uint32_t kNoTile = 0xFFFFFFFFu;
 constexpr uint32_t kNodeRaggedT = 0x10;  // template's node n is ragged
 constexpr uint32_t kNodeCompare = 0x20;  // compare words against the template
 constexpr uint32_t kNodeBad = 0x40;      // a range of this node lies outside its section
+constexpr uint32_t kNodeExtra = 0x80;    // kernel node whose params travel in an arg buffer
+constexpr uint32_t kNodeClean = 0x100;   // entry and param entries equal the template node's: the
+                                         // second node pass completes it from the template's results
 
 // Graph status bits beyond the public FDY_GRAPH_* bits.
-constexpr uint32_t kGraphNodeCount = 0x10;  // node count differs from the template
-constexpr uint32_t kGraphOverflow = 0x20;   // param image larger than its capacity
+constexpr uint32_t kGraphNodeCount = 0x10;    // node count differs from the template
+constexpr uint32_t kGraphOverflow = 0x20;     // param image larger than its capacity
 
 // Per-graph metadata, computed on the host at open and uploaded once.
 struct DevGraph {
@@ -46,18 +49,18 @@ struct DevGraph {
   uint32_t pad_;
 };
 
-// Nodes per chunk of the node pass, and what a chunk reports to its graph.
+// Nodes per chunk of the node pass (a graph has at least one chunk), and
+// what a chunk reports to its graph.
 constexpr uint32_t kNodeChunk = 256;
-constexpr uint32_t kEntryDwords = 168 / 4;  // dwords of a node entry (planes of the field-major table)
-constexpr uint32_t kPlaneParams = 16;       // param entries of a node kept field-major beside its entry
+constexpr uint32_t kChunkDiff = 1;  // records are the XOR of the graph's and its template's
 struct NodeChunk {
-  uint64_t crc_type, crc_kent;  // raw CRCs (zero initial value) of the chunk's node-type and kernel-entry records
-  uint64_t pbytes;              // param bytes of the chunk's kernel nodes
-  uint32_t words_g, words_t;    // image words of the chunk's nodes in the graph and in its template
+  uint64_t crc_type, crc_kent;  // raw CRCs (zero initial value) of the chunk's node-type and kernel-entry
+                                // records (kChunkDiff: of the XOR of the graph's and the template's records)
+  uint64_t pbytes;              // param bytes of the chunk's nodes handled in the chunk (not the clean ones)
   uint32_t status;              // FDY_GRAPH_* bits found in the chunk
-  uint32_t pad_;
+  uint32_t mode;                // kChunkDiff or 0
 };
-static_assert(sizeof(NodeChunk) == 40, "NodeChunk is 40 B");
+static_assert(sizeof(NodeChunk) == 32, "NodeChunk is 32 B");
 
 // Per-slot work description written by the node pass for the diff pass.
 constexpr uint32_t kSlotFlat = 1;      // every word of the tile sits at kg + 8w (and kt + 8w)
