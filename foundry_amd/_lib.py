@@ -200,6 +200,9 @@ _GRAPH_SIGS = {
     "fdy_registry_destroy": (C.c_int, [_vp]),
     "fdy_registry_add": (C.c_int, [_vp, _vp, C.c_uint64, u64p]),
     "fdy_registry_add_file": (C.c_int, [_vp, C.c_char_p, u64p]),
+    "fdy_code_object_kernels": (C.c_int, [_vp, C.c_uint64, C.c_char_p, C.c_uint64, u64p]),
+    "fdy_registry_pack": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32)]),
+    "fdy_registry_load_packed": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_uint32)]),
     "fdy_registry_lookup": (C.c_int, [_vp, C.c_uint64, C.c_char_p, C.POINTER(_vp)]),
     "fdy_registry_global": (C.c_int, [_vp, C.c_uint64, C.c_char_p, C.POINTER(_vp), u64p]),
     "fdy_group_graph_create": (C.c_int, [_vp, C.c_uint32, _vp, _vp, C.POINTER(_vp)]),

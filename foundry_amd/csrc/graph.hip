@@ -11,11 +11,17 @@
 // descriptor or layout is the current or the new graph's own.
 #include <hip/hip_runtime.h>
 
+#include <elf.h>
+
 #include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <memory>
+#include <set>
+#include <sstream>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -802,6 +808,192 @@ int fdy_registry_add_file(fdy_registry* r, const char* path, uint64_t* hash_out)
   std::fclose(f);
   if (bad) return err(FDY_E_IO, std::string("read error on ") + path);
   return fdy_registry_add(r, b.data(), b.size(), hash_out);
+}
+
+namespace {
+
+// Kernel names of a code object: symbols "name.kd" (kernel descriptors)
+// of the .symtab and .dynsym of its ELF64 image, every offset
+// bounds-checked.  A clang offload bundle (what `hipcc --genco` writes:
+// magic, entry count, then {offset, size, triple length, triple} per entry)
+// is opened at its amdgcn entry.
+constexpr char kBundleMagic[] = "__CLANG_OFFLOAD_BUNDLE__";
+
+int code_object_kernels(const uint8_t* p, uint64_t n, std::vector<std::string>* out) {
+  auto bad = [](const char* why) { return err(FDY_E_FORMAT, std::string("code object: ") + why); };
+  constexpr uint64_t kMagic = sizeof(kBundleMagic) - 1;
+  if (n >= kMagic + 8 && std::memcmp(p, kBundleMagic, kMagic) == 0) {
+    uint64_t entries, at = kMagic;
+    std::memcpy(&entries, p + at, 8);
+    at += 8;
+    for (uint64_t e = 0; e < entries; ++e) {
+      if (n - at < 24) return bad("offload bundle entry out of bounds");
+      uint64_t off, size, tlen;
+      std::memcpy(&off, p + at, 8);
+      std::memcpy(&size, p + at + 8, 8);
+      std::memcpy(&tlen, p + at + 16, 8);
+      at += 24;
+      if (tlen > n - at) return bad("offload bundle triple out of bounds");
+      const std::string triple(reinterpret_cast<const char*>(p + at), tlen);
+      at += tlen;
+      if (triple.find("amdgcn") == std::string::npos) continue;
+      if (off > n || size > n - off) return bad("offload bundle image out of bounds");
+      return code_object_kernels(p + off, size, out);
+    }
+    return bad("offload bundle without an amdgcn image");
+  }
+  if (n < sizeof(Elf64_Ehdr) || std::memcmp(p, ELFMAG, SELFMAG) != 0 || p[EI_CLASS] != ELFCLASS64)
+    return bad("neither an ELF64 image nor an uncompressed offload bundle");
+  Elf64_Ehdr eh;
+  std::memcpy(&eh, p, sizeof eh);
+  if (eh.e_shentsize != sizeof(Elf64_Shdr) || eh.e_shoff > n ||
+      (uint64_t)eh.e_shnum * sizeof(Elf64_Shdr) > n - eh.e_shoff)
+    return bad("section headers out of bounds");
+  auto shdr = [&](uint32_t i) {
+    Elf64_Shdr h;
+    std::memcpy(&h, p + eh.e_shoff + (uint64_t)i * sizeof(Elf64_Shdr), sizeof h);
+    return h;
+  };
+  std::set<std::string> names;
+  for (uint32_t i = 0; i < eh.e_shnum; ++i) {
+    const Elf64_Shdr sh = shdr(i);
+    if (sh.sh_type != SHT_SYMTAB && sh.sh_type != SHT_DYNSYM) continue;
+    if (sh.sh_link >= eh.e_shnum || sh.sh_entsize != sizeof(Elf64_Sym) || sh.sh_offset > n ||
+        sh.sh_size > n - sh.sh_offset)
+      return bad("symbol table out of bounds");
+    const Elf64_Shdr st = shdr(sh.sh_link);
+    if (st.sh_offset > n || st.sh_size > n - st.sh_offset) return bad("string table out of bounds");
+    const char* strs = reinterpret_cast<const char*>(p + st.sh_offset);
+    for (uint64_t k = 0; k < sh.sh_size / sizeof(Elf64_Sym); ++k) {
+      Elf64_Sym sym;
+      std::memcpy(&sym, p + sh.sh_offset + k * sizeof(Elf64_Sym), sizeof sym);
+      if (sym.st_name >= st.sh_size) continue;
+      const size_t len = strnlen(strs + sym.st_name, st.sh_size - sym.st_name);
+      if (len == st.sh_size - sym.st_name) return bad("unterminated symbol name");
+      const std::string nm(strs + sym.st_name, len);
+      if (nm.size() > 3 && nm.compare(nm.size() - 3, 3, ".kd") == 0) names.insert(nm.substr(0, nm.size() - 3));
+    }
+  }
+  out->assign(names.begin(), names.end());
+  return FDY_OK;
+}
+
+constexpr const char* kPackedImage = "fatbin_image_packed.img";
+constexpr const char* kPackedIndex = "fatbin_entrypoint_packed.txt";
+constexpr const char* kPackedLoader = "hipModuleLoadData,binary_flags=0";
+
+}  // namespace
+
+int fdy_code_object_kernels(const void* bytes, uint64_t size, char* buf, uint64_t cap, uint64_t* len) {
+  if (!bytes || !len) return err(FDY_E_INVALID, "need a code object and a length output");
+  std::vector<std::string> names;
+  int rc = code_object_kernels(static_cast<const uint8_t*>(bytes), size, &names);
+  if (rc) return rc;
+  std::string text;
+  for (const auto& nm : names) text += nm + "\n";
+  *len = text.size();
+  if (!buf || cap < text.size()) return err(FDY_E_CAPACITY, "kernel-name buffer too small");
+  std::memcpy(buf, text.data(), text.size());
+  return FDY_OK;
+}
+
+int fdy_registry_pack(fdy_registry* r, const char* dir, uint32_t* n_out) {
+  if (!r || !dir) return err(FDY_E_INVALID, "need a registry and a directory");
+  std::error_code ec;
+  std::filesystem::create_directories(dir, ec);
+  if (ec) return err(FDY_E_IO, std::string("cannot create ") + dir + ": " + ec.message());
+  const std::filesystem::path d(dir);
+  std::ofstream img(d / kPackedImage, std::ios::binary | std::ios::trunc);
+  std::ofstream txt(d / kPackedIndex, std::ios::trunc);
+  if (!img || !txt) return err(FDY_E_IO, std::string("cannot write the packed pair in ") + dir);
+  std::lock_guard<std::mutex> lk(r->mu);
+  for (const auto& c : r->codes) {
+    std::vector<std::string> names;
+    int rc = code_object_kernels(c->bytes.data(), c->bytes.size(), &names);
+    if (rc) return rc;
+    const uint64_t hdr[2] = {c->hash, (uint64_t)c->bytes.size()};
+    img.write(reinterpret_cast<const char*>(hdr), sizeof hdr);
+    img.write(reinterpret_cast<const char*>(c->bytes.data()), (std::streamsize)c->bytes.size());
+    char hex[20];
+    std::snprintf(hex, sizeof hex, "%016llx", (unsigned long long)c->hash);
+    txt << hex << "\n" << kPackedLoader << "\n" << names.size() << "\n";
+    for (const auto& nm : names) txt << nm << "\n";
+    txt << "---\n";
+  }
+  img.flush();
+  txt.flush();
+  if (!img || !txt) return err(FDY_E_IO, std::string("write error in ") + dir);
+  if (n_out) *n_out = (uint32_t)r->codes.size();
+  return FDY_OK;
+}
+
+int fdy_registry_load_packed(fdy_registry* r, const char* dir, uint32_t* n_out) {
+  if (!r || !dir) return err(FDY_E_INVALID, "need a registry and a directory");
+  const std::filesystem::path d(dir);
+  std::ifstream img(d / kPackedImage, std::ios::binary);
+  std::ifstream txt(d / kPackedIndex);
+  if (!img || !txt)
+    return err(FDY_E_IO, std::string("packed code objects not found in ") + dir + " (" + kPackedImage + ", " +
+                             kPackedIndex + ")");
+  struct Rec {
+    uint64_t hash = 0;
+    std::vector<uint8_t> bytes;
+    std::vector<std::string> names;
+  };
+  std::vector<Rec> recs;
+  for (;;) {
+    uint64_t hdr[2];
+    img.read(reinterpret_cast<char*>(hdr), sizeof hdr);
+    if (img.gcount() == 0 && img.eof()) break;
+    if (img.gcount() != (std::streamsize)sizeof hdr) return err(FDY_E_FORMAT, "packed image: truncated record header");
+    Rec rec;
+    rec.hash = hdr[0];
+    if (hdr[1] == 0) return err(FDY_E_FORMAT, "packed image: empty record (link segments have no gfx950 form)");
+    std::error_code ec;
+    const uint64_t file_size = std::filesystem::file_size(d / kPackedImage, ec);
+    if (ec || hdr[1] > file_size) return err(FDY_E_FORMAT, "packed image: record larger than the file");
+    rec.bytes.resize(hdr[1]);
+    img.read(reinterpret_cast<char*>(rec.bytes.data()), (std::streamsize)hdr[1]);
+    if (img.gcount() != (std::streamsize)hdr[1]) return err(FDY_E_FORMAT, "packed image: truncated record");
+    if (crc64_xz(rec.bytes.data(), rec.bytes.size()) != rec.hash)
+      return err(FDY_E_FORMAT, "packed image: a record's bytes do not hash to its binary_hash");
+    recs.push_back(std::move(rec));
+  }
+  // The index: hash, loader line, name count, names, "---" per record.
+  std::string line;
+  size_t k = 0;
+  while (std::getline(txt, line)) {
+    if (k >= recs.size()) return err(FDY_E_FORMAT, "packed index lists more records than the image holds");
+    char* end = nullptr;
+    const uint64_t h = std::strtoull(line.c_str(), &end, 16);
+    if (line.size() != 16 || *end || h != recs[k].hash)
+      return err(FDY_E_FORMAT, "packed index: record " + std::to_string(k) + " names another binary_hash");
+    std::string loader, count;
+    if (!std::getline(txt, loader) || loader.rfind("hipModuleLoadData", 0) != 0)
+      return err(FDY_E_FORMAT, "packed index: record " + std::to_string(k) + " has no hipModuleLoadData line");
+    if (!std::getline(txt, count) || count.empty() || count.find_first_not_of("0123456789") != std::string::npos)
+      return err(FDY_E_FORMAT, "packed index: record " + std::to_string(k) + " has no name count");
+    const unsigned long nn = std::stoul(count);
+    for (unsigned long q = 0; q < nn; ++q) {
+      if (!std::getline(txt, line)) return err(FDY_E_FORMAT, "packed index: truncated name list");
+      recs[k].names.push_back(line);
+    }
+    if (!std::getline(txt, line) || line != "---") return err(FDY_E_FORMAT, "packed index: record without ---");
+    ++k;
+  }
+  if (k != recs.size()) return err(FDY_E_FORMAT, "packed index lists fewer records than the image holds");
+  for (const auto& rec : recs) {
+    uint64_t h = 0;
+    int rc = fdy_registry_add(r, rec.bytes.data(), rec.bytes.size(), &h);
+    if (rc) return rc;
+    for (const auto& nm : rec.names) {
+      hipFunction_t fn = nullptr;
+      rc = registry_lookup(r, h, nm.c_str(), nm.size(), &fn);
+      if (rc) return err(FDY_E_FORMAT, "packed index names kernel '" + nm + "', which its code object lacks");
+    }
+  }
+  if (n_out) *n_out = (uint32_t)recs.size();
+  return FDY_OK;
 }
 
 int fdy_registry_lookup(fdy_registry* r, uint64_t hash, const char* name, void** fn) {

@@ -21,6 +21,18 @@ def code_object_hash(data: bytes) -> int:
     return int(restore_lib().fdy_code_object_hash(data, len(data)))
 
 
+def code_object_kernels(data: bytes) -> list[str]:
+    """Kernel names of a code object (its `name.kd` symbols), sorted (no
+    device needed)."""
+    n = C.c_uint64()
+    rc = restore_lib().fdy_code_object_kernels(data, len(data), None, 0, C.byref(n))
+    if rc != -8:  # FDY_E_CAPACITY: the size query
+        check(rc)
+    buf = C.create_string_buffer(max(1, n.value))
+    check(restore_lib().fdy_code_object_kernels(data, len(data), buf, n.value, C.byref(n)))
+    return buf.raw[: n.value].decode().splitlines()
+
+
 class Registry:
     """Loaded code objects, looked up by (binary_hash, kernel name)."""
 
@@ -38,6 +50,20 @@ class Registry:
         out = C.c_uint64()
         check(restore_lib().fdy_registry_add_file(self._h, path.encode(), C.byref(out)))
         return out.value
+
+    def pack(self, directory: str) -> int:
+        """Write every registered code object into the packed pair in
+        `directory` (fdy_registry_pack); returns the number written."""
+        n = C.c_uint32()
+        check(restore_lib().fdy_registry_pack(self._h, directory.encode(), C.byref(n)))
+        return n.value
+
+    def load_packed(self, directory: str) -> int:
+        """Register the code objects of the packed pair in `directory`
+        (fdy_registry_load_packed); returns the number read."""
+        n = C.c_uint32()
+        check(restore_lib().fdy_registry_load_packed(self._h, directory.encode(), C.byref(n)))
+        return n.value
 
     def lookup(self, binary_hash: int, name: str) -> int:
         fn = C.c_void_p()
@@ -123,4 +149,4 @@ class GroupGraph:
             pass
 
 
-__all__ = ["Registry", "GroupGraph", "code_object_hash", "_lib"]
+__all__ = ["Registry", "GroupGraph", "code_object_hash", "code_object_kernels", "_lib"]

@@ -26,6 +26,7 @@ build: they raise NotImplementedError.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import json
 import os
@@ -145,16 +146,24 @@ def get_graph_ptr(graph) -> int:
     return id(graph)
 
 
-# ---- switches of the reference's fatbin / NVSHMEM machinery ------------------
-# csrc/binding.cpp:54-81.  They configure NVIDIA fatbin packing and NVSHMEM
-# module initialisation, neither of which exists for gfx950 code objects:
-# the setters record the value and change nothing, initialisation finds no
-# modules to initialise, and packing (a SAVE-side step) is refused.
+# ---- code-object packing and the reference's NVSHMEM switches --------------
+# csrc/binding.cpp:54-81.  Packing writes the process registry's gfx950 code
+# objects into the packed pair (csrc/hook.cpp:1589-1707); the fatbin
+# interception that skip_fatbin_processing turns off and the NVSHMEM module
+# initialisation have no gfx950 counterpart: those setters record the value
+# and change nothing, and initialisation finds no modules to initialise.
 
 _flags = {"pack_fatbins_on_exit": False, "skip_fatbin_processing": False, "nvshmem_auto_init": True}
+PACK_ON_EXIT_DIR = "hook_archive"  # where the reference packs at exit (csrc/hook.cpp:1702-1707)
+
+
+def _pack_on_exit() -> None:
+    if _flags["pack_fatbins_on_exit"] and _registry is not None:
+        _registry.pack(PACK_ON_EXIT_DIR)
 
 
 def set_pack_fatbins_on_exit(enabled: bool) -> None:
+    """Pack the registry into ./hook_archive when the process exits."""
     _flags["pack_fatbins_on_exit"] = bool(enabled)
 
 
@@ -172,7 +181,10 @@ def init_nvshmem_for_loaded_modules() -> int:
 
 
 def pack_fatbins_to_folder(folder_path: str) -> None:
-    raise NotImplementedError("packing the captured code objects is part of SAVE, which this build does not provide")
+    """Write every code object of the process registry into
+    folder_path/fatbin_image_packed.img + fatbin_entrypoint_packed.txt
+    (csrc/hook.cpp:1589-1700), which load_cuda_modules_and_libraries reads."""
+    registry().pack(str(folder_path))
 
 
 def preallocate_cublas_workspaces() -> None:
@@ -195,18 +207,29 @@ def registry() -> Registry:
     with _registry_lock:
         if _registry is None:
             _registry = Registry()
+            atexit.register(_pack_on_exit)
         return _registry
 
 
 def load_cuda_modules_and_libraries(directory: str) -> int:
-    """Load every gfx950 code object (*.co, *.hsaco) in `directory` into the
-    process registry; kernels resolve by CRC-64/XZ of the code object and
-    name (csrc/hook.cpp:3514-3551).  Returns the number loaded."""
+    """Register the code objects of `directory` in the process registry;
+    kernels then resolve by CRC-64/XZ of the code object and name
+    (csrc/hook.cpp:3514-3551).  The packed pair pack_fatbins_to_folder writes
+    is read when present (csrc/hook.cpp:3787-3830); otherwise every loose
+    gfx950 code object (*.co, *.hsaco).  A directory with neither is an
+    error, as the reference's missing packed files are.  Returns the number
+    of code objects registered."""
+    if all(os.path.exists(os.path.join(directory, f))
+           for f in ("fatbin_image_packed.img", "fatbin_entrypoint_packed.txt")):
+        return registry().load_packed(directory)
     n = 0
     for name in sorted(os.listdir(directory)):
         if name.endswith((".co", ".hsaco")):
             registry().add_file(os.path.join(directory, name))
             n += 1
+    if n == 0:
+        raise RuntimeError(f"no packed code objects (fatbin_image_packed.img + fatbin_entrypoint_packed.txt) "
+                           f"and no *.co / *.hsaco in {directory}")
     return n
 
 

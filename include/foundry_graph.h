@@ -71,6 +71,29 @@ int fdy_registry_lookup(fdy_registry* r, uint64_t binary_hash, const char* name,
 int fdy_registry_global(fdy_registry* r, uint64_t binary_hash, const char* name, void** device_ptr,
                         uint64_t* bytes);
 
+/* Kernel names of a code object (an ELF64 image, or an uncompressed clang
+ * offload bundle holding one): the symbols with a kernel descriptor
+ * (`name.kd`) in its symbol tables, sorted and '\n'-terminated, into buf
+ * (*len = bytes needed; with buf NULL or cap below it, FDY_E_CAPACITY and
+ * nothing written).  A malformed ELF image is FDY_E_FORMAT.  No device. */
+int fdy_code_object_kernels(const void* code_object, uint64_t size, char* buf, uint64_t cap, uint64_t* len);
+
+/* The packed code-object pair (csrc/hook.cpp:1589-1700, pack_fatbins_to_folder):
+ * every code object registered in `r`, in registration order, into
+ * dir/fatbin_image_packed.img as records {u64 binary_hash, u64 size, size
+ * bytes} and dir/fatbin_entrypoint_packed.txt as, per record, the hash in 16
+ * hex digits, the loader line "hipModuleLoadData,binary_flags=0", the number
+ * of kernel names, the names (fdy_code_object_kernels), then "---".  gfx950
+ * code objects are linked when built, so no record holds link segments.
+ * `dir` is created if missing; *n_out = records written. */
+int fdy_registry_pack(fdy_registry* r, const char* dir, uint32_t* n_out);
+/* Load a pair written by fdy_registry_pack (csrc/hook.cpp:3787-3830): both
+ * files must be present (FDY_E_IO otherwise); the two files must list the
+ * same records, and every record's bytes must hash to its binary_hash and
+ * name kernels its code object holds (FDY_E_FORMAT otherwise).  Each code
+ * object is registered as fdy_registry_add does; *n_out = records read. */
+int fdy_registry_load_packed(fdy_registry* r, const char* dir, uint32_t* n_out);
+
 /* ---- group graphs ------------------------------------------------------- */
 typedef struct fdy_group_graph_info {
   uint32_t template_graph;

@@ -8,7 +8,7 @@ import pytest
 
 import cugraph_writer as W
 import foundry_amd
-from foundry_amd import api
+from foundry_amd import _lib, api
 
 PUBLIC_NAMES_FROM_FOUNDRY = [
     "CUDAGraph", "allocation_region", "free_preallocated_region", "get_current_alloc_offset", "graph",
@@ -108,13 +108,36 @@ def test_ops_surface_complete():
     ops.set_skip_fatbin_processing(True)
     ops.set_pack_fatbins_on_exit(False)
     ops.set_nvshmem_auto_init(False)
-    with pytest.raises(NotImplementedError):
-        ops.pack_fatbins_to_folder("/nonexistent")
     g = ops.CUDAGraph()
     with pytest.raises(RuntimeError, match="keep_graph"):
         g.raw_cuda_graph()
     with pytest.raises(RuntimeError):
         g.pool()
+
+
+def test_load_modules_needs_code_objects(tmp_path):
+    """Neither the packed pair nor a loose code object: an error, as the
+    reference aborts when the packed files are missing."""
+    from foundry_amd import ops
+
+    (tmp_path / "notes.txt").write_text("no code objects here")
+    with pytest.raises(RuntimeError, match="no packed code objects"):
+        ops.load_cuda_modules_and_libraries(str(tmp_path))
+
+
+def test_code_object_kernels():
+    """Kernel names come from the code object's `.kd` symbols (no device)."""
+    import graph_cases as GC
+    from foundry_amd.graph import code_object_kernels
+
+    data = open(GC.PROBE_CO, "rb").read()
+    names = code_object_kernels(data)
+    assert {"probe_mix", "probe_chain"} <= set(names) and names == sorted(names)
+    assert all(not n.endswith(".kd") for n in names)
+    with pytest.raises(_lib.FoundryError, match="FDY_E_FORMAT"):
+        code_object_kernels(b"\x7fELF" + bytes(60))
+    with pytest.raises(_lib.FoundryError, match="FDY_E_FORMAT"):
+        code_object_kernels(data[:100])
 
 
 def test_install_as_foundry():

@@ -7,6 +7,7 @@ compared with the values graph_cases restates, so every pointer a kernel,
 fill or copy node dereferences is known to lie inside the test's buffer."""
 import ctypes
 import random
+import struct
 
 import numpy as np
 import pytest
@@ -15,7 +16,7 @@ import torch
 import graph_cases as GC
 import refcrc
 from foundry_amd import _lib
-from foundry_amd.graph import GroupGraph, Registry, code_object_hash
+from foundry_amd.graph import GroupGraph, Registry, code_object_hash, code_object_kernels
 from foundry_amd.restore import Archive
 
 pytestmark = pytest.mark.gpu
@@ -32,12 +33,16 @@ def _hip_memcpy(dst: int, src: int, n: int, kind: int) -> None:
 
 
 class Env:
-    def __init__(self):
+    def __init__(self, packed_dir: str | None = None):
         torch.cuda.set_device(0)
         self.stream = torch.cuda.current_stream()
         self.reg = Registry()
         data = open(GC.PROBE_CO, "rb").read()
-        self.bhash = self.reg.add_file(GC.PROBE_CO)
+        if packed_dir is None:
+            self.bhash = self.reg.add_file(GC.PROBE_CO)
+        else:  # the code object comes back from a packed pair
+            assert self.reg.load_packed(packed_dir) == 1
+            self.bhash = code_object_hash(data)
         assert self.bhash == refcrc.crc64_xz(data) == code_object_hash(data)
         self.slots, nbytes = self.reg.global_address(self.bhash, "probe_slots")
         assert nbytes == 256 * 8
@@ -111,6 +116,59 @@ def test_registry_lookup_and_errors(env):
         env.reg.lookup(env.bhash ^ 1, "probe_mix")
     # Adding the same bytes again keeps one module.
     assert env.reg.add(open(GC.PROBE_CO, "rb").read()) == env.bhash
+
+
+def _pack_probe(dirpath) -> tuple[int, bytes]:
+    src = Registry()
+    h = src.add_file(GC.PROBE_CO)
+    assert src.pack(str(dirpath)) == 1
+    src.close()
+    return h, open(GC.PROBE_CO, "rb").read()
+
+
+def test_packed_code_objects_reload_and_launch(tmp_path):
+    """pack_fatbins_to_folder's pair (csrc/hook.cpp:1589-1700): the image
+    holds {binary_hash, size, bytes}, the index the hash, the loader line and
+    the kernel names; a fresh registry loaded from the pair (3787-3830)
+    resolves the graphs' kernels, which then run."""
+    h, data = _pack_probe(tmp_path)
+    assert (tmp_path / "fatbin_image_packed.img").read_bytes() == struct.pack("<QQ", h, len(data)) + data
+    names = code_object_kernels(data)
+    assert (tmp_path / "fatbin_entrypoint_packed.txt").read_text().splitlines() == \
+        [f"{h:016x}", "hipModuleLoadData,binary_flags=0", str(len(names)), *names, "---"]
+    e = Env(packed_dir=str(tmp_path))
+    for n in names:
+        assert e.reg.lookup(e.bhash, n) != 0
+    with GroupGraph(e.arch, 0, e.reg, e.stream) as gg:
+        for g in [0, 3, 1]:
+            e.run(gg, g)
+
+
+def test_packed_pair_damage_is_refused(tmp_path):
+    h, data = _pack_probe(tmp_path)
+    img = tmp_path / "fatbin_image_packed.img"
+    txt = tmp_path / "fatbin_entrypoint_packed.txt"
+    good_img, good_txt = img.read_bytes(), txt.read_text()
+    cases = [
+        (good_img[:-1], good_txt, "truncated"),
+        (good_img[:100] + bytes([good_img[100] ^ 1]) + good_img[101:], good_txt, "hash to its binary_hash"),
+        (good_img, good_txt.replace(f"{h:016x}", f"{h ^ 1:016x}"), "another binary_hash"),
+        (good_img, good_txt.replace("probe_mix\n", "probe_nothing\n"), "lacks"),
+        (good_img, good_txt.replace("---\n", ""), "without ---"),
+        (good_img + good_img, good_txt, "fewer records"),
+    ]
+    for b, t, msg in cases:
+        img.write_bytes(b)
+        txt.write_text(t)
+        reg = Registry()
+        with pytest.raises(_lib.FoundryError, match=msg):
+            reg.load_packed(str(tmp_path))
+        reg.close()
+    img.unlink()
+    reg = Registry()
+    with pytest.raises(_lib.FoundryError, match="FDY_E_IO"):
+        reg.load_packed(str(tmp_path))
+    reg.close()
 
 
 def test_build_shape(env):

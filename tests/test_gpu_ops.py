@@ -101,6 +101,16 @@ def test_load_relocates_replays_and_outputs(loaded):
     del whole, outs, results
 
 
+def test_pack_and_reload_through_ops(loaded, tmp_path):
+    """pack_fatbins_to_folder writes the process registry's code objects as
+    the packed pair; load_cuda_modules_and_libraries reads the pair back."""
+    ops.pack_fatbins_to_folder(str(tmp_path))
+    assert (tmp_path / "fatbin_image_packed.img").stat().st_size > 16
+    records = (tmp_path / "fatbin_entrypoint_packed.txt").read_text().count("---\n")
+    assert records >= 1
+    assert api.load_cuda_modules_and_libraries(str(tmp_path)) == records
+
+
 def test_finish_one_out_of_range(loaded):
     pending, _ = loaded
     with pytest.raises(IndexError):
