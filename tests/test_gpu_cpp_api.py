@@ -1,0 +1,60 @@
+"""The C++ LOAD surface (include/foundry/CUDAGraph.h, the counterpart of the
+reference's include/CUDAGraph.h:43-247) driven by a compiled C++ program,
+tests/native/cudagraph_caller.cpp, in a process of its own.
+
+The archives are the ones test_gpu_ops saves: four graphs of one topology
+group, saved against an allocation region at the reference's default base,
+which the MI355X cannot map -- so the C++ load moves the region, relocates
+every saved pointer, replays the allocator events and returns output tensors
+at the relocated buffer.  The caller replays graphs in a fixed order and
+prints the buffer after each; the values are checked here."""
+import json
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import graph_cases as GC
+from cugraph_writer import le
+from foundry_amd.graph import code_object_hash
+from test_gpu_ops import SAVED_BASE, SIZE, SPECS, WEIGHTS, _save
+
+pytestmark = pytest.mark.gpu
+
+CALLER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "_build", "cudagraph_caller")
+ORDER = [0, 1, 2, 3, 0, 2, 3]
+
+
+def test_cpp_caller_loads_replays_and_outputs(tmp_path):
+    assert os.path.exists(CALLER), "build first: make -C tests/native"
+    bhash = code_object_hash(open(GC.PROBE_CO, "rb").read())
+    paths, saved_out = _save(str(tmp_path), bhash)
+    cmd = [CALLER, os.path.dirname(GC.PROBE_CO), hex(SAVED_BASE), str(SIZE), str(WEIGHTS),
+           ",".join(map(str, ORDER)), *paths]
+    print("running", " ".join(cmd[:6]), "...", flush=True)
+    p = subprocess.run(cmd, capture_output=True, text=True, timeout=90)
+    assert p.returncode == 0, p.stderr[-2000:]
+    lines = [json.loads(x) for x in p.stdout.splitlines() if x.startswith("{")]
+    meta = {k: v for d in lines if "graph" not in d for k, v in d.items()}
+    assert meta["code_objects"] >= 1
+    assert meta["used_manifest"] == 1 and meta["template_of"] == [0, 0, 0, 0]
+    assert meta["out_of_range_throws"] == 1
+    assert meta["raw_graph_needs_keep_graph"] == 1
+    assert meta["same_exec"] == 1  # one exec per topology group
+    assert meta["numel"] == 16 and meta["dtype_long"] == 1
+    base = meta["weights"]  # the region's base: the weights were its first allocation
+    assert base != SAVED_BASE
+    out = saved_out - SAVED_BASE + base
+    assert meta["out_ptr"] == out, "the output tensor is a view at the relocated buffer"
+    assert meta["done"] == 1
+    runs = [d for d in lines if "graph" in d]
+    assert [d["graph"] for d in runs] == ORDER
+    for d in runs:
+        g = d["graph"]
+        sp = SPECS[g]
+        words = np.array([int(x) for x in d["words"]], dtype=np.uint64)
+        r0 = GC.mix_expect(sp["a"], sp["b"], 2, 64)
+        assert int(words[0]) == r0 and int(words[1]) == GC.mix(r0, 1), g
+        fill = words.tobytes()[GC.FILL_OFF:GC.FILL_OFF + 128]
+        assert fill == le(sp["v"], 4) * 32, g
