@@ -59,6 +59,9 @@ class ArchiveInfo(C.Structure):
         ("total_overrides", C.c_uint64),
         ("file_bytes", C.c_uint64),
         ("num_intervals", C.c_uint64),
+        ("device_bytes", C.c_uint64),
+        ("serving_layout", C.c_uint32),
+        ("pad_", C.c_uint32),
     ]
 
 

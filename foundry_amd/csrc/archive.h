@@ -35,15 +35,27 @@ inline int err(int code, const std::string& msg) {
 struct DevBuf {
   void* p = nullptr;
   size_t bytes = 0;
+  bool owned = true;  // false: a part of another buffer (an arena), not freed here
   DevBuf() = default;
   DevBuf(const DevBuf&) = delete;
   DevBuf& operator=(const DevBuf&) = delete;
   ~DevBuf() {
-    if (p) (void)hipFree(p);
+    if (p && owned) (void)hipFree(p);
   }
   template <typename T>
   T* as() const {
     return static_cast<T*>(p);
+  }
+  void swap(DevBuf& o) {
+    std::swap(p, o.p);
+    std::swap(bytes, o.bytes);
+    std::swap(owned, o.owned);
+  }
+  void release() {
+    if (p && owned) (void)hipFree(p);
+    p = nullptr;
+    bytes = 0;
+    owned = true;
   }
 };
 
@@ -70,11 +82,22 @@ struct fdy_archive {
   uint32_t num_slots = 0;
   uint32_t num_chunks = 0;
 
+  // `arena` holds every open-time buffer other than the images, R and the
+  // restore's scratch, as parts (one allocation instead of some twenty).
+  fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
   fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
   fdy::DevBuf aux, image, live, ovr, cand, sub_count, graph_count, node_pbytes, key_hash;
 
   fdy::RelocPlan reloc;
+  // Serving layout, taken when the first group graph is bound (no restore
+  // can run until the last is destroyed): override records packed in
+  // canonical order (graph g's from h_ovr_off[g]), live images for the
+  // templates only (template t's from h_live_base[t]), each R_g packed to
+  // its words (from h_r_base[g]), and the restore's scratch (candidates,
+  // ragged-word sources) freed.  Otherwise all three start at word_base.
+  bool compact = false;
+  std::vector<uint64_t> h_live_base, h_r_base;  // h_r_base[g]: first word of R_g, packed to its words
   bool use_explicit = false;
   bool restored = false;
   hipStream_t last_stream = nullptr;
@@ -124,5 +147,25 @@ int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t);
 int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty);
 // Switch of a group that has a bound group graph (graph.hip).
 int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* stats);
+
+// First override record of graph g, first live word of template t, and
+// first word of R_g, in the current layout.
+inline uint64_t ovr_base(const fdy_archive* a, uint32_t g) {
+  return a->compact ? a->h_ovr_off[g] : a->graphs[g].word_base;
+}
+inline uint64_t live_base(const fdy_archive* a, uint32_t t) {
+  return a->compact ? a->h_live_base[t] : a->graphs[t].word_base;
+}
+inline uint64_t r_base(const fdy_archive* a, uint32_t g) {
+  return a->compact ? a->h_r_base[g] : a->graphs[g].word_base;
+}
+// Take the serving layout (after a restore, before the first group graph is
+// bound); synchronizes `s`.
+int compact_for_serving(fdy_archive* a, hipStream_t s);
+// The restore's buffers at full capacity: override records and live images
+// at word_base, candidates and ragged-word sources.
+int alloc_restore_buffers(fdy_archive* a);
+// Device bytes the archive holds.
+uint64_t held_bytes(const fdy_archive* a);
 
 }  // namespace fdy

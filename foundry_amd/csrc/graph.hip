@@ -174,7 +174,7 @@ int fetch_desc(fdy_archive* a, uint32_t g, HostGraph& h) {
 int fetch_layout(fdy_archive* a, uint32_t g, HostGraph& h) {
   const DevGraph& d = a->graphs[g];
   int rc = fetch(a->ndesc.as<NodeDesc>() + d.node_base, d.num_nodes, h.desc);
-  if (!rc) rc = fetch(a->image.as<uint64_t>() + d.word_base, a->h_gwords[g], h.words);
+  if (!rc) rc = fetch(a->image.as<uint64_t>() + r_base(a, g), a->h_gwords[g], h.words);
   if (!rc) h.layout_loaded = true;
   return rc;
 }
@@ -725,7 +725,7 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
   if (rc) return rc;
   const bool all = gg->stale;
   MirrorArgs mr{};
-  mr.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
+  mr.live = a->live.as<uint64_t>() + live_base(a, t);
   mr.desc = a->ndesc.as<NodeDesc>() + a->graphs[t].node_base;
   mr.dirty = gg->dirty.as<uint8_t>();
   mr.h_live = gg->d_live;
@@ -1036,6 +1036,9 @@ int fdy_group_graph_create(fdy_archive* a, uint32_t t, fdy_registry* r, void* st
   if (a->bound.size() != a->G) a->bound.assign(a->G, nullptr);
   if (a->bound[t]) return err(FDY_E_STATE, "template " + std::to_string(t) + " already has a group graph");
   FDY_HIP(hipSetDevice(a->device));
+  // Serving from here on: overrides packed, template live images only.
+  rc = compact_for_serving(a, s);
+  if (rc) return rc;
   // The exec starts from the template's params: move the live image back first.
   rc = enqueue_switch(a, t, s, nullptr);
   if (rc) return rc;

@@ -299,38 +299,35 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
                   std::max<uint64_t>(1, (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk),
               i);
 
-  int rc = 0;
-  auto alloc = [&](DevBuf& b, size_t bytes, const char* what) {
-    if (!rc) rc = dev_alloc(b, bytes, what);
+  // The tables: parts of one arena allocation, each 256-byte aligned.
+  const std::pair<DevBuf*, uint64_t> parts[] = {
+      {&a->dgraphs, G * sizeof(DevGraph)},  {&a->cc, sizeof(CrcConsts)},
+      {&a->digests, 32ull * G},             {&a->tmpl, 4ull * G},
+      {&a->explicit_tmpl, 4ull * G},        {&a->status, 4ull * G},
+      {&a->gwords, 4ull * G},               {&a->pbytes, 8ull * G},
+      {&a->live_cur, 4ull * G},             {&a->nflags, nodes},
+      {&a->ndesc, nodes * sizeof(NodeDesc)}, {&a->nptrs, 16 * nodes},
+      {&a->live_src, 4 * nodes},            {&a->tile_node, 4 * slots},
+      {&a->chunk_graph, 4 * chunks},        {&a->node_pbytes, 8 * nodes},
+      {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
+      {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
+      {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->graph_count, 4ull * G},
   };
-  alloc(a->img, a->img_bytes + 4096, "archive images");
-  alloc(a->dgraphs, G * sizeof(DevGraph), "graph table");
-  alloc(a->cc, sizeof(CrcConsts), "CRC tables");
-  alloc(a->digests, 32ull * G, "digests");
-  alloc(a->tmpl, 4ull * G, "template_of");
-  alloc(a->explicit_tmpl, 4ull * G, "explicit groups");
-  alloc(a->status, 4ull * G, "status");
-  alloc(a->gwords, 4ull * G, "image words");
-  alloc(a->pbytes, 8ull * G, "param bytes");
-  alloc(a->live_cur, 4ull * G, "live current");
-  alloc(a->nflags, nodes, "node flags");
-  alloc(a->ndesc, nodes * sizeof(NodeDesc), "node descriptors");
-  alloc(a->nptrs, 16 * nodes, "node pointers");
-  alloc(a->live_src, 4 * nodes, "live node sources");
-  alloc(a->tile_node, 4 * slots, "tile table");
-  alloc(a->chunk_graph, 4 * chunks, "node chunk table");
-  alloc(a->node_pbytes, 8 * nodes, "node param bytes");
-  alloc(a->key_hash, 8ull * G, "key hashes");
-  alloc(a->chunks, sizeof(NodeChunk) * chunks, "node chunk results");
-  alloc(a->slot_desc, sizeof(SlotDesc) * slots, "slot descriptors");
-  alloc(a->tslots, 4 * (slots + 1), "template slot list");
-  alloc(a->sub_count, 4 * slots * kSubsPerSlot, "record counts");
-  alloc(a->graph_count, 4ull * G, "graph record counts");
-  alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * slots, "candidate and record regions");
-  alloc(a->aux, 8 * words, "ragged word sources");
-  alloc(a->image, 8 * words, "param images");
-  alloc(a->live, 8 * words, "live images");
-  alloc(a->ovr, sizeof(fdy_override) * words, "override records");
+  uint64_t arena_bytes = 0;
+  for (const auto& pt : parts) arena_bytes += (pt.second + 255) / 256 * 256;
+  int rc = dev_alloc(a->arena, arena_bytes, "archive tables");
+  if (!rc) {
+    uint64_t at = 0;
+    for (const auto& pt : parts) {
+      pt.first->p = static_cast<uint8_t*>(a->arena.p) + at;
+      pt.first->bytes = pt.second;
+      pt.first->owned = false;
+      at += (pt.second + 255) / 256 * 256;
+    }
+  }
+  if (!rc) rc = dev_alloc(a->img, a->img_bytes + 4096, "archive images");
+  if (!rc) rc = dev_alloc(a->image, 8 * words, "param images");
+  if (!rc) rc = alloc_restore_buffers(a);
   if (rc) return rc;
 
   FDY_HIP(hipMemcpy(a->img.p, stage.p, a->img_bytes, hipMemcpyHostToDevice));
@@ -346,6 +343,69 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
 }  // namespace
 
 namespace fdy {
+
+int alloc_restore_buffers(fdy_archive* a) {
+  const uint64_t words = a->total_cap;
+  int rc = dev_alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * a->num_slots, "candidate and record regions");
+  if (!rc) rc = dev_alloc(a->aux, 8 * words, "ragged word sources");
+  if (!rc) rc = dev_alloc(a->live, 8 * words, "live images");
+  if (!rc) rc = dev_alloc(a->ovr, sizeof(fdy_override) * words, "override records");
+  if (!rc) a->compact = false;
+  return rc;
+}
+
+int compact_for_serving(fdy_archive* a, hipStream_t s) {
+  if (a->compact) return FDY_OK;
+  int rc = ensure_cache(a, s);
+  if (rc) return rc;
+  const uint32_t G = a->G;
+  std::vector<uint64_t> lbase(G, 0), rbase(G, 0);
+  uint64_t live_words = 0, r_words = 0;
+  for (uint32_t g = 0; g < G; ++g) {
+    rbase[g] = r_words;
+    r_words += a->h_gwords[g];
+    if (a->h_tmpl[g] == g) {
+      lbase[g] = live_words;
+      live_words += a->graphs[g].word_cap;
+    }
+  }
+  DevBuf ovr, live, image;
+  rc = dev_alloc(ovr, sizeof(fdy_override) * std::max<uint64_t>(1, a->h_ovr_off[G]), "packed override records");
+  if (!rc) rc = dev_alloc(live, 8 * std::max<uint64_t>(1, live_words), "template live images");
+  if (!rc) rc = dev_alloc(image, 8 * std::max<uint64_t>(1, r_words), "packed param images");
+  if (rc) return rc;
+  FDY_HIP(hipSetDevice(a->device));
+  for (uint32_t g = 0; g < G; ++g) {
+    const uint64_t n = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
+    if (n)
+      FDY_HIP(hipMemcpyAsync(ovr.as<fdy_override>() + a->h_ovr_off[g], a->ovr.as<fdy_override>() + a->graphs[g].word_base,
+                             sizeof(fdy_override) * n, hipMemcpyDeviceToDevice, s));
+    if (a->h_tmpl[g] == g && a->graphs[g].word_cap)
+      FDY_HIP(hipMemcpyAsync(live.as<uint64_t>() + lbase[g], a->live.as<uint64_t>() + a->graphs[g].word_base,
+                             8ull * a->graphs[g].word_cap, hipMemcpyDeviceToDevice, s));
+    if (a->h_gwords[g])
+      FDY_HIP(hipMemcpyAsync(image.as<uint64_t>() + rbase[g], a->image.as<uint64_t>() + a->graphs[g].word_base,
+                             8ull * a->h_gwords[g], hipMemcpyDeviceToDevice, s));
+  }
+  FDY_HIP(hipStreamSynchronize(s));
+  a->ovr.swap(ovr);
+  a->live.swap(live);
+  a->image.swap(image);
+  a->cand.release();
+  a->aux.release();
+  a->h_live_base = std::move(lbase);
+  a->h_r_base = std::move(rbase);
+  a->compact = true;
+  return FDY_OK;
+}
+
+uint64_t held_bytes(const fdy_archive* a) {
+  const DevBuf* bufs[] = {&a->arena, &a->img, &a->image, &a->aux, &a->live, &a->ovr, &a->cand,
+                          &a->reloc.bucket, &a->reloc.rec, &a->reloc.lo};
+  uint64_t n = 0;
+  for (const DevBuf* b : bufs) n += b->bytes;
+  return n;
+}
 
 int ensure_cache(fdy_archive* a, hipStream_t s) {
   if (!a->restored) return err(FDY_E_STATE, "call fdy_restore first");
@@ -401,12 +461,12 @@ int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty) {
   if (c == g) return FDY_OK;
   FDY_HIP(hipSetDevice(a->device));
   SwitchArgs w{};
-  w.ovr_cur = a->ovr.as<fdy_override>() + a->graphs[c].word_base;
+  w.ovr_cur = a->ovr.as<fdy_override>() + ovr_base(a, c);
   w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
-  w.ovr_new = a->ovr.as<fdy_override>() + a->graphs[g].word_base;
+  w.ovr_new = a->ovr.as<fdy_override>() + ovr_base(a, g);
   w.n_new = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
-  w.tmpl_image = a->image.as<uint64_t>() + a->graphs[t].word_base;
-  w.live = a->live.as<uint64_t>() + a->graphs[t].word_base;
+  w.tmpl_image = a->image.as<uint64_t>() + r_base(a, t);
+  w.live = a->live.as<uint64_t>() + live_base(a, t);
   w.flags_cur = a->nflags.as<uint8_t>() + a->graphs[c].node_base;
   w.flags_new = a->nflags.as<uint8_t>() + a->graphs[g].node_base;
   w.live_src = a->live_src.as<uint32_t>() + a->graphs[t].node_base;
@@ -568,6 +628,8 @@ int fdy_archive_info_get(fdy_archive* a, fdy_archive_info* o) {
   o->total_nodes = a->total_nodes;
   o->file_bytes = a->img_bytes;
   o->num_intervals = a->reloc.dev.n;
+  o->device_bytes = held_bytes(a);
+  o->serving_layout = a->compact ? 1u : 0u;
   if (a->restored) {
     int rc = ensure_cache(a, a->last_stream);
     if (rc) return rc;
@@ -711,6 +773,14 @@ int fdy_restore(fdy_archive* a, void* stream) {
     return err(FDY_E_STATE, "group graphs hold the restored params; destroy them before restoring again");
   hipStream_t s = static_cast<hipStream_t>(stream);
   FDY_HIP(hipSetDevice(a->device));
+  if (a->compact) {  // group graphs were bound and are gone: back to the restore's layout
+    a->ovr.release();
+    a->live.release();
+    a->image.release();
+    int rc = dev_alloc(a->image, 8 * a->total_cap, "param images");
+    if (!rc) rc = alloc_restore_buffers(a);
+    if (rc) return rc;
+  }
   RestoreArgs r{};
   r.img = a->img.as<uint8_t>();
   r.graphs = a->dgraphs.as<DevGraph>();
@@ -852,7 +922,7 @@ int fdy_get_overrides(fdy_archive* a, void* stream, uint32_t g, fdy_override* ou
   if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
   if (rc) return rc;
   const uint64_t n = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
-  return copy_out(a->ovr.as<fdy_override>() + a->graphs[g].word_base, n, out, cap, n_out);
+  return copy_out(a->ovr.as<fdy_override>() + ovr_base(a, g), n, out, cap, n_out);
 }
 
 int fdy_get_node_flags(fdy_archive* a, void* stream, uint32_t g, uint8_t* out, uint64_t cap, uint64_t* n_out) {
@@ -882,7 +952,7 @@ int fdy_get_param_image(fdy_archive* a, void* stream, uint32_t g, uint64_t* out,
   int rc = check_graph(a, g);
   if (!rc) rc = ensure_cache(a, static_cast<hipStream_t>(stream));
   if (rc) return rc;
-  return copy_out(a->image.as<uint64_t>() + a->graphs[g].word_base, a->h_gwords[g], out, cap, n_out);
+  return copy_out(a->image.as<uint64_t>() + r_base(a, g), a->h_gwords[g], out, cap, n_out);
 }
 
 int fdy_get_node_pointers(fdy_archive* a, void* stream, uint32_t g, uint64_t* out, uint64_t cap, uint64_t* n_out) {
@@ -919,7 +989,7 @@ int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint
   if (rc) return rc;
   if (a->h_tmpl[t] != t) return err(FDY_E_INVALID, "graph " + std::to_string(t) + " is not a template");
   FDY_HIP(hipStreamSynchronize(static_cast<hipStream_t>(stream)));
-  rc = copy_out(a->live.as<uint64_t>() + a->graphs[t].word_base, a->h_gwords[t], words, cap, nullptr);
+  rc = copy_out(a->live.as<uint64_t>() + live_base(a, t), a->h_gwords[t], words, cap, nullptr);
   if (!rc) rc = copy_out(a->live_src.as<uint32_t>() + a->graphs[t].node_base, a->graphs[t].num_nodes, node_src,
                          node_cap, nullptr);
   if (rc) return rc;

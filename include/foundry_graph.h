@@ -123,7 +123,14 @@ typedef struct fdy_select_stats {
  * are added in archive order with the template's relocated params, the
  * dependencies are added, and the graph is instantiated.  Synchronizes
  * `stream`.  Replaces the per-template JSON build
- * (csrc/CUDAGraphParallel.cpp:171-834, 1944-1990). */
+ * (csrc/CUDAGraphParallel.cpp:171-834, 1944-1990).
+ *
+ * The first group graph of an archive puts it in the serving layout: the
+ * override records are packed to their count, live images are kept for
+ * templates only, and the restore's scratch (candidates, ragged-word
+ * sources) is freed; fdy_archive_info's device_bytes shows what is held.
+ * fdy_restore, allowed again once the last group graph is destroyed,
+ * allocates the scratch anew. */
 int fdy_group_graph_create(fdy_archive* a, uint32_t template_graph, fdy_registry* r, void* stream,
                            fdy_group_graph** out);
 int fdy_group_graph_destroy(fdy_group_graph* gg);

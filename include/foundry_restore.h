@@ -88,6 +88,9 @@ typedef struct fdy_archive_info {
   uint64_t total_overrides;    /* valid after fdy_restore */
   uint64_t file_bytes;         /* bytes of .cugraph images resident in HBM */
   uint64_t num_intervals;
+  uint64_t device_bytes;       /* device memory the archive holds */
+  uint32_t serving_layout;     /* 1 while in the serving layout (see fdy_group_graph_create) */
+  uint32_t pad_;
 } fdy_archive_info;
 
 typedef struct fdy_archive fdy_archive;

@@ -1,0 +1,96 @@
+"""Device memory an archive holds while its group graphs serve.
+
+Binding the first group graph puts the archive in the serving layout:
+override records packed to their count, live images for templates only,
+the restore's scratch freed.  On the 256-graph x 1200-node decode-style
+archive (4 groups, 40k intervals) and the 1024-graph x 5000-node archive (32
+groups) what the process holds -- measured as the drop in hipMemGetInfo's
+free bytes from before the open to after every group is bound -- stays
+within 3x the archive's param bytes.  Results read in the serving layout
+equal those read before it, and once the group graphs are gone a new
+restore allocates its scratch again and gives the same results."""
+import numpy as np
+import pytest
+import torch
+
+import graph_cases as GC
+from foundry_amd import synth
+from foundry_amd.graph import GroupGraph, Registry
+from foundry_amd.restore import Archive
+
+pytestmark = pytest.mark.gpu
+
+SAMPLE = [0, 1, 2, 3, 5, 77, 128, 255]  # graphs whose results are compared across layouts
+
+
+def _results(arch, stream, templates):
+    out = {}
+    for g in SAMPLE:
+        out[("ovr", g)] = arch.overrides(g, stream)
+        out[("img", g)] = arch.param_image(g, stream)
+    for t in templates:
+        w, src, cur = arch.live(t)
+        out[("live", t)] = (w, src, cur)
+    return out
+
+
+def _same(a, b):
+    assert a.keys() == b.keys()
+    for k in a:
+        x, y = a[k], b[k]
+        if k[0] == "live":
+            assert x[2] == y[2] and np.array_equal(x[0], y[0]) and np.array_equal(x[1], y[1]), k
+        else:
+            assert np.array_equal(x, y), k
+
+
+@pytest.mark.parametrize("preset", [2, 5])
+def test_serving_layout_holds_at_most_three_times_the_params(preset):
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    reg = Registry()
+    params = synth.preset(preset)
+    params.sink_hash = reg.add_file(GC.PROBE_CO)
+    s = synth.SynthArchive(params)
+    iv = s.intervals()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    arch = Archive.from_synth(s)
+    arch.set_relocation(*iv)
+    arch.restore(stream)
+    groups = arch.groups(stream)
+    templates = sorted(set(int(t) for t in groups))
+    info = arch.info()
+    param_bytes = info["total_param_bytes"]
+    restore_bytes = info["device_bytes"]
+    assert info["serving_layout"] == 0
+    before = _results(arch, stream, templates)
+
+    ggs = [GroupGraph(arch, t, reg, stream) for t in templates]
+    torch.cuda.synchronize()
+    free1, _ = torch.cuda.mem_get_info()
+    info = arch.info()
+    held = info["device_bytes"]
+    print(f"preset {preset}: param bytes {param_bytes}, held while restoring {restore_bytes} "
+          f"({restore_bytes / param_bytes:.2f}x), held while serving {held} ({held / param_bytes:.2f}x), "
+          f"hipMemGetInfo drop {free0 - free1} ({(free0 - free1) / param_bytes:.2f}x)", flush=True)
+    assert info["serving_layout"] == 1
+    assert held < restore_bytes
+    assert held <= 3 * param_bytes
+    assert free0 - free1 <= 3 * param_bytes
+
+    # The serving layout reads back what the restore wrote, and switches in it.
+    _same(before, _results(arch, stream, templates))
+    for g in [1, 5, 77, 2]:
+        st = ggs[templates.index(int(groups[g]))].select(g, stream)
+        assert st["words_scattered"] >= 0
+    w, _, cur = arch.live(int(groups[77]))
+    assert cur == 77 and np.array_equal(w, arch.param_image(77, stream))
+
+    for gg in ggs:
+        gg.close()
+    arch.restore(stream)  # back to the restore's layout
+    assert arch.info()["serving_layout"] == 0
+    _same(before, _results(arch, stream, templates))
+    arch.close()
+    reg.close()
