@@ -116,19 +116,11 @@ struct fdy_archive {
 
   bool timing = false;
   bool timed = false;
-  hipEvent_t ev[10] = {};  // 0..7 on the restore stream, 8..9 around the digest kernel
-
-  // The digest kernel's stream (default priority) and the events that fork
-  // it from, and join it back into, the restore stream.
-  hipStream_t side = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
+  hipEvent_t ev[8] = {};
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)
       if (e) (void)hipEventDestroy(e);
-    if (fork) (void)hipEventDestroy(fork);
-    if (join) (void)hipEventDestroy(join);
-    if (side) (void)hipStreamDestroy(side);
   }
 };
 

@@ -1,9 +1,7 @@
 // kernels.hip -- the restore kernels for gfx950 (wave64, 160 KB LDS per CU).
 //
-//   k_khash   a word hash of every graph's saved key.
-//   k_digest  the CRC-64/XZ digests of every graph's saved key and
-//             dependency table (on a second stream, beside the passes
-//             below, joined before the compaction, which reads them).
+//   k_digest  per graph: a word hash of its saved key, and the CRC-64/XZ
+//             digests of its key and its dependency table.
 //   k_group   template_of[g] = lowest graph with the same key bytes (by the
 //             word hash, then a byte compare).
 //   k_node_a  one workgroup per 256-node chunk of a graph: for a
@@ -134,44 +132,32 @@ __device__ __forceinline__ uint64_t wave_slice_crc(const uint8_t* p, uint64_t L,
 
 constexpr uint32_t kGroupThreads = 256;
 
-// The grouping hash of every graph's saved key, one workgroup per graph.
-__global__ __launch_bounds__(kGroupThreads) void k_khash(RestoreArgs a) {
-  __shared__ uint64_t s_x[kGroupThreads / 64];
-  const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
-  const DevGraph& Gi = a.graphs[i];
-  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
-  const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
-  uint64_t x = 0;
-  for (uint64_t k = tid; 8 * k < L; k += kGroupThreads) x ^= key_term(stream_word(p, L, (int64_t)k), k);
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
-  if (lane == 0) s_x[wave] = x;
-  __syncthreads();
-  if (tid == 0) {
-    for (uint32_t w = 1; w < kGroupThreads / 64; ++w) x ^= s_x[w];
-    a.key_hash[i] = x;
-  }
-}
+// Per graph, one workgroup: the grouping hash of its saved key (key_term
+// over its words), and the CRC-64/XZ digests of its key and its dependency
+// table: the two streams' 4 KB slices (counted from each stream's end) go
+// round the waves, and each wave shifts a slice's CRC past the slices after
+// it.  (The hash in a launch of its own after this one: 210.5 against 203.3
+// us per restore of the 256 x 1200 archive.  This kernel on a second stream
+// beside the grouping and node passes: 216.6 against 208.8 us, the node
+// pass losing CUs to it and the fork and join adding latency.)
+constexpr uint32_t kDigestThreads = 512;
 
-// The CRC-64/XZ digests of every graph's saved key and dependency table,
-// one workgroup per graph: the two streams' 4 KB slices (counted from each
-// stream's end) go round the waves; each wave shifts a slice's CRC past the
-// slices after it.  Depends on the archive image only, so it runs beside
-// the grouping and node passes.
-__global__ __launch_bounds__(kGroupThreads) void k_digest(RestoreArgs a) {
-  __shared__ uint64_t s_x[2][kGroupThreads / 64];
+__global__ __launch_bounds__(kDigestThreads) void k_digest(RestoreArgs a) {
+  __shared__ uint64_t s_x[3][kDigestThreads / 64];
   __shared__ uint64_t s_slice[8][256];
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
   stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
   const DevGraph& Gi = a.graphs[i];
   const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY], Ld = 8ull * Gi.num_deps;
   const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
   const uint8_t* pd = a.img + Gi.sec_off[FDY_SEC_DEPS];
+  uint64_t x = 0;
+  for (uint64_t k = tid; 8 * k < L; k += kDigestThreads) x ^= key_term(stream_word(p, L, (int64_t)k), k);
   __syncthreads();
   const uint64_t nk = (L + kSliceBytes - 1) / kSliceBytes, nd = (Ld + kSliceBytes - 1) / kSliceBytes;
   uint64_t ck = 0, cd = 0;  // lane shares of the shifted slice CRCs
-  for (uint64_t u = wave; u < nk + nd; u += kGroupThreads / 64) {
+  for (uint64_t u = wave; u < nk + nd; u += kDigestThreads / 64) {
     const bool key = u < nk;
     const uint64_t back = key ? u : u - nk;
     const uint64_t z = key ? wave_slice_crc(p, L, kSliceBytes * back, s_slice, a.cc, lane)
@@ -182,19 +168,23 @@ __global__ __launch_bounds__(kGroupThreads) void k_digest(RestoreArgs a) {
   }
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) {
+    x ^= shfl_down64(x, d);
     ck ^= shfl_down64(ck, d);
     cd ^= shfl_down64(cd, d);
   }
   if (lane == 0) {
-    s_x[0][wave] = ck;
-    s_x[1][wave] = cd;
+    s_x[0][wave] = x;
+    s_x[1][wave] = ck;
+    s_x[2][wave] = cd;
   }
   __syncthreads();
   if (tid == 0) {
-    for (uint32_t w = 1; w < kGroupThreads / 64; ++w) {
-      ck ^= s_x[0][w];
-      cd ^= s_x[1][w];
+    for (uint32_t w = 1; w < kDigestThreads / 64; ++w) {
+      x ^= s_x[0][w];
+      ck ^= s_x[1][w];
+      cd ^= s_x[2][w];
     }
+    a.key_hash[i] = x;
     a.digests[4ull * i + 0] = ck ^ Gi.crc_fin[0];
     a.digests[4ull * i + 1] = cd ^ Gi.crc_fin[1];
   }
@@ -1811,12 +1801,11 @@ __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint6
 }  // namespace
 
 hipError_t launch_digests(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_digest, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
+  hipLaunchKernelGGL(k_digest, dim3(a.num_graphs), dim3(kDigestThreads), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_khash, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_group, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);

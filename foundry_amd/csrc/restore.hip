@@ -815,24 +815,14 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.graph_count = a->graph_count.as<uint32_t>();
   r.node_pbytes = a->node_pbytes.as<uint64_t>();
   r.reloc = a->reloc.dev;
-  if (!a->side) {
-    FDY_HIP(hipStreamCreateWithFlags(&a->side, hipStreamNonBlocking));
-    FDY_HIP(hipEventCreateWithFlags(&a->fork, hipEventDisableTiming));
-    FDY_HIP(hipEventCreateWithFlags(&a->join, hipEventDisableTiming));
-  }
   if (a->timing) {
     for (hipEvent_t& e : a->ev)
       if (!e) FDY_HIP(hipEventCreate(&e));
     FDY_HIP(hipEventRecord(a->ev[0], s));
   }
-  // The key and dependency digests depend on the image alone: they run on
-  // the side stream from here and join before the compaction reads them.
-  FDY_HIP(hipEventRecord(a->fork, s));
-  FDY_HIP(hipStreamWaitEvent(a->side, a->fork, 0));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[8], a->side));
-  FDY_HIP(launch_digests(r, a->side));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[9], a->side));
-  FDY_HIP(hipEventRecord(a->join, a->side));
+  // The key and dependency digests first: the grouping hash then reads the
+  // keys from L2.
+  FDY_HIP(launch_digests(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
   FDY_HIP(launch_group(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
@@ -844,7 +834,6 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
   FDY_HIP(launch_diff_search(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
-  FDY_HIP(hipStreamWaitEvent(s, a->join, 0));
   FDY_HIP(launch_compact(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[7], s));
   a->timed = a->timing;
@@ -864,7 +853,7 @@ int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
   FDY_HIP(hipEventSynchronize(a->ev[7]));
-  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[8], a->ev[9]));
+  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
   FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));

@@ -193,11 +193,7 @@ int fdy_archive_set_manifest(fdy_archive* a, const char* text, uint64_t len, con
  *   4. fused diff + relocate over every param word: writes the relocated
  *      param image R_g of every graph and the override set O_g of every
  *      non-template graph in canonical (node, word) order.
- * Also resets every group's live image to its template.  The digests of
- * step 1's first two streams run on a second stream the archive owns
- * (default priority), forked from `stream` by an event and joined back into
- * it before the last kernel, so to the caller every result is ordered on
- * `stream`. */
+ * Also resets every group's live image to its template. */
 int fdy_restore(fdy_archive* a, void* stream);
 
 /* Results.  Each synchronizes `stream`. */
@@ -281,11 +277,9 @@ void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int3
 /* Timing of the last fdy_restore, from HIP events recorded on its stream
  * around each kernel (milliseconds).  Synchronizes. */
 typedef struct fdy_restore_timing {
-  float hash_ms;    /* saved-key and dependency digests: a kernel on a second stream, forked from
-                       the restore stream at the start and joined before the compaction, so it
-                       overlaps the phases below (their sum can exceed total_ms less hash_ms) */
+  float hash_ms;    /* saved-key and dependency digests, and the grouping hash of every key */
   float group_ms;   /* template assignment */
-  float node_ms;    /* per-node compare, layout, and the four digests */
+  float node_ms;    /* per-node compare, layout, and the node-type and kernel-entry digests */
   float tmpl_ms;    /* relocation of the template graphs' param words */
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
   float search_ms;  /* interval searches and override records of the words left over by the diff */
