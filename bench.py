@@ -185,6 +185,8 @@ def bench_group_graphs(preset, torch, np, stream):
     if preset == 5:
         params.num_graphs = 256  # 8 of the 32 groups: bounds build time and memory
         params.num_groups = 8
+    if preset == 3:
+        params.memcpy_pct = 0  # a memcpy node is built from real device pointers; these are synthetic
     params.sink_hash = reg.add_file(PROBE_CO)
     s = synth.SynthArchive(params)
     arch = Archive.from_synth(s)
@@ -223,8 +225,9 @@ def bench_group_graphs(preset, torch, np, stream):
     arch.close()
     reg.close()
     return {
-        "sample": f"{s.num_graphs} graphs x {nodes} nodes, {len(ggs)} groups; {len(sel_us)} switches that changed "
-                  f"the exec out of {GRAPH_SWITCHES} seeded targets",
+        "sample": f"{s.num_graphs} graphs x {nodes} nodes, {len(ggs)} groups"
+                  + (" (no memcpy nodes)" if preset == 3 else "")
+                  + f"; {len(sel_us)} switches that changed the exec out of {GRAPH_SWITCHES} seeded targets",
         "build_ms_per_group": round(statistics.mean(build_ms), 3),
         "instantiate_ms_per_group": round(statistics.mean(inst_ms), 3),
         "first_select_us_p50": round(_pct(first_us, 0.5), 1),
@@ -377,7 +380,7 @@ def main():
     if args.preset == 5:
         result["switch"] = bench_switches(arch, s, stream, torch, np)
         _progress("switches timed")
-    if args.preset in (1, 2, 5) and not args.no_group_graphs:
+    if args.preset in (1, 2, 3, 5) and not args.no_group_graphs:
         result["group_graph"] = bench_group_graphs(args.preset, torch, np, stream)
         _progress("group graphs timed")
 
