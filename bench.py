@@ -377,7 +377,7 @@ def main():
     }
 
     _progress("restore timed")
-    if args.preset == 5:
+    if args.preset in (2, 5):
         result["switch"] = bench_switches(arch, s, stream, torch, np)
         _progress("switches timed")
     if args.preset in (1, 2, 3, 5) and not args.no_group_graphs:
