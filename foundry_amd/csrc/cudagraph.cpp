@@ -18,6 +18,7 @@
 #include <atomic>
 #include <cstdio>
 #include <cstring>
+#include <filesystem>
 #include <fstream>
 #include <map>
 #include <mutex>
@@ -206,26 +207,24 @@ uint64_t region_alloc(uint64_t bytes) {
 }
 
 int load_cuda_modules_and_libraries(const std::string& dir) {
+  namespace fs = std::filesystem;
   uint32_t n = 0;
-  std::string probe;
-  if (read_file(dir + "/fatbin_image_packed.img", &probe) && read_file(dir + "/fatbin_entrypoint_packed.txt", &probe)) {
+  std::error_code ec;
+  if (fs::exists(fs::path(dir) / "fatbin_image_packed.img", ec) &&
+      fs::exists(fs::path(dir) / "fatbin_entrypoint_packed.txt", ec)) {
     check(fdy_registry_load_packed(registry(), dir.c_str(), &n), "load_cuda_modules_and_libraries");
     return (int)n;
   }
   // Loose code objects, in name order.
   std::vector<std::string> names;
-  if (FILE* ls = popen(("ls -1 '" + dir + "' 2>/dev/null").c_str(), "r")) {
-    char line[4096];
-    while (std::fgets(line, sizeof line, ls)) {
-      std::string nm(line);
-      while (!nm.empty() && (nm.back() == '\n' || nm.back() == '\r')) nm.pop_back();
-      auto ends = [&](const char* suf) {
-        const size_t k = std::strlen(suf);
-        return nm.size() > k && nm.compare(nm.size() - k, k, suf) == 0;
-      };
-      if (ends(".co") || ends(".hsaco")) names.push_back(nm);
-    }
-    pclose(ls);
+  for (fs::directory_iterator it(dir, ec), end; !ec && it != end; it.increment(ec)) {
+    if (!it->is_regular_file(ec)) continue;
+    const std::string nm = it->path().filename().string();
+    auto ends = [&](const char* suf) {
+      const size_t k = std::strlen(suf);
+      return nm.size() > k && nm.compare(nm.size() - k, k, suf) == 0;
+    };
+    if (ends(".co") || ends(".hsaco")) names.push_back(nm);
   }
   std::sort(names.begin(), names.end());
   TORCH_CHECK(!names.empty(), "no packed code objects (fatbin_image_packed.img + fatbin_entrypoint_packed.txt) and no ",
