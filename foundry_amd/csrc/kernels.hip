@@ -1517,25 +1517,30 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   for (uint32_t b = 0; b < total; b += kSBatch) {
     uint64_t raw[K], tval[K], res[K];
     uint32_t word[K], fl[K], m = 0;
+    // The K candidates' loads are unconditional (a list index past the end
+    // reads the first candidate, then is masked off), so they are issued
+    // together rather than each behind its own branch and wait.
+    Candidate cand[K];
 #pragma unroll
     for (uint32_t k = 0; k < K; ++k) {
-      const uint32_t i = b + 64 * k + lane;  // list index
-      raw[k] = tval[k] = 0;
-      word[k] = fl[k] = 0;
-      if (i < total) {
-        uint32_t q = 0;
+      const uint32_t i0 = b + 64 * k + lane;  // list index
+      const uint32_t i = i0 < total ? i0 : 0u;
+      uint32_t q = 0;
 #pragma unroll
-        for (uint32_t s = 1; s < kSubsPerSlot; ++s) q += start[s] <= i;
-        uint32_t sq = start[0];
+      for (uint32_t s = 1; s < kSubsPerSlot; ++s) q += start[s] <= i;
+      uint32_t sq = start[0];
 #pragma unroll
-        for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
-        const Candidate c = base[(uint64_t)q * kSubWords + (i - sq)];
-        raw[k] = c.raw;
-        tval[k] = c.tval;
-        word[k] = c.word;
-        fl[k] = c.flags;
-        if (c.flags & kCandReloc) m |= 1u << k;
-      }
+      for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
+      cand[k] = base[(uint64_t)q * kSubWords + (i - sq)];
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < K; ++k) {
+      const bool in = b + 64 * k + lane < total;
+      raw[k] = in ? cand[k].raw : 0;
+      tval[k] = in ? cand[k].tval : 0;
+      word[k] = in ? cand[k].word : 0;
+      fl[k] = in ? cand[k].flags : 0;
+      if (fl[k] & kCandReloc) m |= 1u << k;
     }
     reloc_batch<K>(a.reloc, raw, res, m);
     // The member pass stored each candidate's raw word; only the words the

@@ -188,21 +188,33 @@ __device__ inline void stage_words(uint64_t* dst, const uint64_t* src, uint32_t 
 // step issues its K loads before waiting for any of them.
 template <int K>
 __device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_t* out, uint32_t mask) {
+  if (r.n == 0) {  // relocation off (uniform)
+#pragma unroll
+    for (int k = 0; k < K; ++k) out[k] = w[k];
+    return;
+  }
   bool ok[K];
   uint32_t x[K], width[K];
   const uint4* line[K];
   uint4 h[K];
+  // Every search's root line is loaded without a branch (bucket 0 stands in
+  // for words outside the table and is masked off): a load behind a per-word
+  // branch is followed by its own wait, and the K searches would go one
+  // after another instead of together.
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    ok[k] = ((mask >> k) & 1) && r.n != 0 && w[k] >= r.lo_min &&
-            (r.policy ? w[k] <= r.hi_max : w[k] < r.hi_max);
+    ok[k] = ((mask >> k) & 1) && w[k] >= r.lo_min && (r.policy ? w[k] <= r.hi_max : w[k] < r.hi_max);
     const uint64_t rel = w[k] - r.lo_min;
     const uint64_t b = ok[k] ? rel >> r.shift : 0;
     x[k] = (uint32_t)(rel - (b << r.shift));
     width[k] = r.shift;
     line[k] = reinterpret_cast<const uint4*>(r.bucket + b);
-    h[k] = ok[k] ? line[k][0] : make_uint4(0, 0, 0, 0);
   }
+#pragma unroll
+  for (int k = 0; k < K; ++k) h[k] = line[k][0];
+#pragma unroll
+  for (int k = 0; k < K; ++k)
+    if (!ok[k]) h[k] = make_uint4(0, 0, 0, 0);
   // Descend through split lines (crowded buckets) to the leaves.
   for (;;) {
     bool any = false;
@@ -232,12 +244,10 @@ __device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_
   if (more) {
     uint4 q1[K], q2[K], q3[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      if (h[k].y > 2) {
-        q1[k] = line[k][1];
-        q2[k] = line[k][2];
-        q3[k] = line[k][3];
-      }
+    for (int k = 0; k < K; ++k) {  // the rest of the line just read: no branch, one wait
+      q1[k] = line[k][1];
+      q2[k] = line[k][2];
+      q3[k] = line[k][3];
     }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -268,12 +278,17 @@ __device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_
 #pragma unroll
       for (int k = 0; k < K; ++k) act |= hi[k] > lo[k];
       if (!act) break;
+      uint32_t mid[K];
+      uint64_t key[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) mid[k] = (lo[k] + hi[k] + 1) >> 1;  // = lo[k] once a search is done
+#pragma unroll
+      for (int k = 0; k < K; ++k) key[k] = r.lo[mid[k]];
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         if (hi[k] > lo[k]) {
-          const uint32_t mid = (lo[k] + hi[k] + 1) >> 1;
-          if (r.lo[mid] <= w[k]) lo[k] = mid;
-          else hi[k] = mid - 1;
+          if (key[k] <= w[k]) lo[k] = mid[k];
+          else hi[k] = mid[k] - 1;
         }
       }
     }
@@ -282,7 +297,7 @@ __device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_
   }
   RelocRec iv[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) iv[k] = ok[k] ? r.rec[i[k]] : RelocRec{0, 0};
+  for (int k = 0; k < K; ++k) iv[k] = r.rec[ok[k] ? i[k] : 0];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const bool inside = ok[k] && (r.policy ? (w[k] <= iv[k].hi) : (w[k] < iv[k].hi));
