@@ -151,6 +151,18 @@ __device__ inline uint64_t ld_u64(const uint8_t* p) {
   return (uint64_t)ld_u32(p) | ((uint64_t)ld_u32(p + 4) << 32);
 }
 
+// The 8 bytes at p (any alignment) from the two aligned words covering
+// them, loaded unconditionally so that a run of these issues together.
+// Reads up to 15 bytes past p: callers keep p inside the archive-image
+// buffer, whose 4 KB zero tail covers the overrun.
+__device__ __forceinline__ uint64_t ld_u64_any(const uint8_t* p) {
+  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+  const uint64_t* q = reinterpret_cast<const uint64_t*>(a & ~(uintptr_t)7);
+  const uint32_t sh = (uint32_t)(a & 7) * 8;
+  const uint64_t w0 = q[0], w1 = q[1];
+  return sh ? (w0 >> sh) | (w1 << (64 - sh)) : w0;
+}
+
 // Fields of a node entry, its kernel-attribute block or the common attrs:
 // these start 8-byte aligned (sections are validated 8-byte aligned and an
 // entry is 168 = 8 * 21 bytes), so every 4-byte field is 4-byte aligned and
