@@ -61,12 +61,11 @@ struct DevBuf {
 
 int dev_alloc(DevBuf& b, size_t bytes, const char* what);
 
-// The interval search structure: a bucket index of 64-byte lines with about
-// one root bucket per two intervals (crowded buckets split into sub-bucket
-// lines), 16-byte {hi, delta} records, and the lo keys for leaves still
-// crowded at the depth limit (see RelocDev).
+// The interval search structure: an index of 64-byte lines, one to two
+// root lines per interval, each answering the searches inside it or naming
+// the lines that do (see RelocLine).
 struct RelocPlan {
-  DevBuf bucket, rec, lo;
+  DevBuf line;
   RelocDev dev{};
 };
 

@@ -14,7 +14,7 @@
 //             template's results, chunk CRCs joined into the four digests,
 //             word offsets by block scans, the diff-tile -> first-node table,
 //             ragged-word sources, slot descriptors.
-//   k_diff_t  the template graphs' words, relocated through a bucket-indexed
+//   k_diff_t  the template graphs' words, relocated through the line-indexed
 //             interval search into R and the live image (1024-word units).
 //   k_diff_m  eight workgroups per 4096-word tile of every other graph: coalesced
 //             8-byte loads of the graph's and the template's words, the

@@ -22,6 +22,7 @@
 #include "cugraph.h"
 #include "json_min.h"
 #include "kernels.h"
+#include "reloc_index.h"
 #include "writer.h"
 
 namespace fdy {
@@ -80,127 +81,11 @@ struct HostStage {
   }
 };
 
-// The interval search structure of a table, built on the host: the bucket
-// lines, the {hi, delta} records and the lo keys, with the search
-// parameters (dev's pointers are set when the arrays are placed on the
-// device).
-struct HostIndex {
-  std::vector<RelocBucket> bucket;
-  std::vector<RelocRec> rec;
-  const uint64_t* lo = nullptr;
-  RelocDev dev{};
-};
-
 int build_reloc_index(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
                       HostIndex* out) {
-  std::memset(&out->dev, 0, sizeof(out->dev));
-  if (policy > FDY_RELOC_INCLUSIVE) return err(FDY_E_INVALID, "unknown relocation policy");
-  if (n == 0) return FDY_OK;
-  if (!lo || !hi || !nlo) return err(FDY_E_INVALID, "null interval array");
-  for (uint64_t i = 0; i < n; ++i) {
-    if (lo[i] >= hi[i]) return err(FDY_E_INVALID, "interval " + std::to_string(i) + " is empty (lo >= hi)");
-    if (hi[i] == UINT64_MAX) return err(FDY_E_INVALID, "interval " + std::to_string(i) + " ends at 2^64-1");
-    if (i && hi[i - 1] > lo[i])
-      return err(FDY_E_INVALID, "intervals " + std::to_string(i - 1) + " and " + std::to_string(i) +
-                                    " overlap or are not sorted by lo");
-  }
-  if (n > 0xFFFFFFF0ull) return err(FDY_E_INVALID, "more than 2^32 intervals");
-  const uint64_t span = hi[n - 1] - lo[0];
-  if (span >> 54) return err(FDY_E_INVALID, "intervals span more than 2^54 bytes");
-  std::vector<RelocRec>& rec = out->rec;
-  rec.resize(n);
-  for (uint64_t i = 0; i < n; ++i) rec[i] = RelocRec{hi[i], nlo[i] - lo[i]};
-  // Bucket width: the smallest power of two giving at most ~n/2 buckets over
-  // [lo_min, hi_max], and at most 2^32 so in-bucket offsets fit in 32 bits.
-  uint64_t target = 1;
-  while (target * 2 < n) target <<= 1;
-  uint32_t shift = 0;
-  while ((span >> shift) + 1 > target) ++shift;
-  if (shift > 32) shift = 32;
-  const uint64_t nb = (span >> shift) + 1;  // w - lo_min <= span, so (w - lo_min) >> shift < nb
-  auto start = [&](uint64_t b) -> uint64_t {
-    const uint64_t off = b << shift;  // b <= nb, so no overflow below 2^55
-    return off > UINT64_MAX - lo[0] ? UINT64_MAX : lo[0] + off;
-  };
-  std::vector<RelocBucket>& bucket = out->bucket;
-  bucket.assign(nb, RelocBucket{});
-  auto leaf = [&](RelocBucket& e, uint64_t s0, uint64_t i, uint64_t j) {
-    e.first = (uint32_t)i;
-    e.count = (uint32_t)(j - i);
-    for (uint32_t k = 0; k < kBucketOffsets; ++k)
-      e.off[k] = k < e.count ? (uint32_t)(lo[i + 1 + k] - s0) : 0xFFFFFFFFu;
-  };
-  std::vector<uint64_t> crowded;  // root buckets with more starts than a line holds
-  uint64_t i = 0, j = 0;          // i: last lo <= bucket start; j: last lo < next bucket's start
-  for (uint64_t b = 0; b < nb; ++b) {
-    const uint64_t s0 = start(b), s1 = start(b + 1);
-    while (i + 1 < n && lo[i + 1] <= s0) ++i;
-    if (j < i) j = i;
-    while (j + 1 < n && lo[j + 1] < s1) ++j;
-    leaf(bucket[b], s0, i, j);
-    if (j - i > kBucketOffsets) crowded.push_back(b);
-  }
-  // Split crowded buckets into 2^s sub-buckets: the smallest s whose
-  // sub-buckets all hold at most kBucketOffsets starts, at most
-  // log2(count) + 3 per level (so a level adds at most 8 lines per start),
-  // for at most kMaxSplitDepth levels; deeper leaves fall back to a binary
-  // search over lo[] on the device.
-  constexpr int kMaxSplitDepth = 6;
-  struct Pending {
-    uint64_t line, s0, i, j;
-    uint32_t width;
-    int depth;
-  };
-  std::vector<Pending> todo;
-  for (uint64_t b : crowded) {
-    const RelocBucket& e = bucket[b];
-    todo.push_back({b, start(b), e.first, (uint64_t)e.first + e.count, shift, 0});
-  }
-  while (!todo.empty()) {
-    const Pending p = todo.back();
-    todo.pop_back();
-    if (p.depth >= kMaxSplitDepth || p.width == 0) continue;  // stays a crowded leaf
-    const uint64_t cnt = p.j - p.i;
-    uint32_t smax = 1;
-    while (smax < p.width && (1ull << smax) < 8 * cnt) ++smax;
-    uint32_t s = 1;
-    for (; s < smax; ++s) {
-      // Largest number of starts in one sub-bucket of width 2^(width - s).
-      uint64_t best = 0, run = 0, cur = UINT64_MAX;
-      for (uint64_t q = p.i + 1; q <= p.j; ++q) {
-        const uint64_t sub = (lo[q] - p.s0) >> (p.width - s);
-        run = sub == cur ? run + 1 : 1;
-        cur = sub;
-        best = std::max(best, run);
-      }
-      if (best <= kBucketOffsets) break;
-    }
-    const uint64_t base = bucket.size();
-    if (base + (1ull << s) > 0xFFFFFFF0ull) return err(FDY_E_INVALID, "interval index too large");
-    bucket.resize(base + (1ull << s));
-    RelocBucket& e = bucket[p.line];
-    e.first = (uint32_t)base;
-    e.count = kBucketSplit | s;
-    for (uint32_t k = 0; k < kBucketOffsets; ++k) e.off[k] = 0xFFFFFFFFu;
-    const uint32_t cw = p.width - s;
-    uint64_t ci = p.i, cj = p.i;
-    for (uint64_t c = 0; c < (1ull << s); ++c) {
-      const uint64_t s0 = p.s0 + (c << cw);
-      const uint64_t s1 = s0 > UINT64_MAX - (1ull << cw) ? UINT64_MAX : s0 + (1ull << cw);
-      while (ci + 1 <= p.j && lo[ci + 1] <= s0) ++ci;
-      if (cj < ci) cj = ci;
-      while (cj + 1 <= p.j && lo[cj + 1] < s1) ++cj;
-      leaf(bucket[base + c], s0, ci, cj);
-      if (cj - ci > kBucketOffsets) todo.push_back({base + c, s0, ci, cj, cw, p.depth + 1});
-    }
-  }
-  out->lo = lo;
-  out->dev.n = n;
-  out->dev.lo_min = lo[0];
-  out->dev.hi_max = hi[n - 1];
-  out->dev.shift = shift;
-  out->dev.policy = policy;
-  return FDY_OK;
+  std::string why;
+  const int rc = build_reloc_index(lo, hi, nlo, n, policy, out, &why);
+  return rc ? err(rc, why) : FDY_OK;
 }
 
 int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
@@ -209,16 +94,10 @@ int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo
   int rc = build_reloc_index(lo, hi, nlo, n, policy, &x);
   out->dev = x.dev;
   if (rc || n == 0) return rc;
-  rc = dev_alloc(out->bucket, x.bucket.size() * sizeof(RelocBucket), "interval buckets");
-  if (!rc) rc = dev_alloc(out->rec, n * sizeof(RelocRec), "interval records");
-  if (!rc) rc = dev_alloc(out->lo, n * 8, "interval starts");
+  rc = dev_alloc(out->line, x.line.size() * sizeof(RelocLine), "interval index lines");
   if (rc) return rc;
-  FDY_HIP(hipMemcpy(out->bucket.p, x.bucket.data(), x.bucket.size() * sizeof(RelocBucket), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(out->rec.p, x.rec.data(), n * sizeof(RelocRec), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(out->lo.p, lo, n * 8, hipMemcpyHostToDevice));
-  out->dev.bucket = out->bucket.as<RelocBucket>();
-  out->dev.rec = out->rec.as<RelocRec>();
-  out->dev.lo = out->lo.as<uint64_t>();
+  FDY_HIP(hipMemcpy(out->line.p, x.line.data(), x.line.size() * sizeof(RelocLine), hipMemcpyHostToDevice));
+  out->dev.line = out->line.as<RelocLine>();
   return FDY_OK;
 }
 
@@ -401,7 +280,7 @@ int compact_for_serving(fdy_archive* a, hipStream_t s) {
 
 uint64_t held_bytes(const fdy_archive* a) {
   const DevBuf* bufs[] = {&a->arena, &a->img, &a->image, &a->aux, &a->live, &a->ovr, &a->cand,
-                          &a->reloc.bucket, &a->reloc.rec, &a->reloc.lo};
+                          &a->reloc.line};
   uint64_t n = 0;
   for (const DevBuf* b : bufs) n += b->bytes;
   return n;
@@ -1083,9 +962,7 @@ int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint
   HostIndex x;
   int rc = build_reloc_index(lo, hi, nlo, n_iv, policy, &x);
   if (rc) return rc;
-  const uint64_t b_bytes = x.bucket.size() * sizeof(RelocBucket), r_bytes = n_iv * sizeof(RelocRec);
-  const uint64_t at_rec = align_up(b_bytes, 256), at_lo = align_up(at_rec + r_bytes, 256);
-  const uint64_t total = at_lo + 8 * n_iv;
+  const uint64_t total = x.line.size() * sizeof(RelocLine);
   if (total > FDY_STATIC_INDEX_BYTES)
     return err(FDY_E_CAPACITY, "the index of " + std::to_string(n_iv) + " intervals takes " + std::to_string(total) +
                                    " bytes; the static index holds " + std::to_string(FDY_STATIC_INDEX_BYTES));
@@ -1099,13 +976,9 @@ int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint
   if (n_iv) {
     // In stream order, so after any earlier call's kernel on this stream;
     // then wait for the copies, after which the host arrays may go.
-    FDY_HIP(hipMemcpyAsync(base, x.bucket.data(), b_bytes, hipMemcpyHostToDevice, s));
-    FDY_HIP(hipMemcpyAsync(base + at_rec, x.rec.data(), r_bytes, hipMemcpyHostToDevice, s));
-    FDY_HIP(hipMemcpyAsync(base + at_lo, lo, 8 * n_iv, hipMemcpyHostToDevice, s));
+    FDY_HIP(hipMemcpyAsync(base, x.line.data(), total, hipMemcpyHostToDevice, s));
     FDY_HIP(hipStreamSynchronize(s));
-    d.bucket = reinterpret_cast<const RelocBucket*>(base);
-    d.rec = reinterpret_cast<const RelocRec*>(base + at_rec);
-    d.lo = reinterpret_cast<const uint64_t*>(base + at_lo);
+    d.line = reinterpret_cast<const RelocLine*>(base);
   }
   FDY_HIP(launch_reloc_words(d, in, out, n, s));
   return FDY_OK;

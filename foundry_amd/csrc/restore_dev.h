@@ -105,39 +105,48 @@ struct NodeDesc {
 };
 static_assert(sizeof(NodeDesc) == 32, "NodeDesc is 32 B");
 
-// End and shift of one saved allocation interval (its lo is implied by the search).
-struct RelocRec {
-  uint64_t hi;
+// The interval index: 64-byte lines, each answering every search inside
+// its address range from that one line or naming the line that does.  Root
+// line b covers addresses [lo_min + b*2^shift, lo_min + (b+1)*2^shift)
+// (shift <= 31, so offsets inside a line fit in 31 bits).
+//   A leaf line with first address B holds four 16-byte slots: slot 0 the
+// last interval whose lo is at or before B (it moves the line's addresses
+// below the first start inside it), slots 1-3 the intervals starting inside
+// the line, in order.  A slot holds lo - B (slot 0: the line's kind, zero
+// for a leaf), hi - B + 1 clamped into [0, 2^32 - 1], and new_lo - lo;
+// unused slots have lo - B = 2^32 - 1.  A word at offset x of a leaf moves
+// by the delta of the last slot whose lo - B is <= x, if x + 1 < that
+// slot's end (x + 1 <= end under the inclusive policy).
+//   A line whose range holds more than four intervals is a fence line
+// (kind kLineFence): up to 14 fences, the lo - B of intervals starting
+// inside it, in order (unused: 2^32 - 1), cut it into up to 15 child lines
+// first, first + 1, ... (first in slot 0's end field); child c starts at
+// fence c - 1 (child 0 at B) and is itself a leaf or a fence line, so a
+// search reads one line per level: one for a leaf root, two for up to 60
+// intervals under one root, three for up to 900.
+constexpr uint32_t kLineSlots = 4;
+constexpr uint32_t kLineFence = 0x80000000u;
+constexpr uint32_t kLineFences = 14;
+constexpr uint32_t kLineNone = 0xFFFFFFFFu;  // lo - B of an unused slot, an unused fence
+constexpr uint32_t kMaxLineShift = 31;
+struct RelocSlot {
+  uint32_t lo;     // lo - B (slot 0: the line's kind)
+  uint32_t end;    // hi - B + 1, clamped into [0, 2^32 - 1] (fence line, slot 0: first child)
   uint64_t delta;  // new_lo - lo (mod 2^64)
 };
-static_assert(sizeof(RelocRec) == 16, "RelocRec is 16 B");
-
-// One 64-byte line of the bucket index.  Root bucket b covers addresses
-// [lo_min + b*2^shift, lo_min + (b+1)*2^shift).  A leaf line: `first` is
-// the last interval whose lo is <= the bucket's first address; intervals
-// first+1 .. first+count start inside the bucket, and off[k] holds
-// lo - bucket start of interval first+1+k for the first min(count, 14) of
-// them.  A split line (count has kBucketSplit set) stands for 2^s
-// sub-buckets, s = count & 63, of 2^(width - s) bytes each, whose lines
-// are bucket[first .. first + 2^s); crowded buckets are split until their
-// leaves hold at most 14 starts (or a depth limit is reached).
-constexpr uint32_t kBucketOffsets = 14;
-constexpr uint32_t kBucketSplit = 0x80000000u;
-struct RelocBucket {
-  uint32_t first;
-  uint32_t count;
-  uint32_t off[kBucketOffsets];
+struct RelocLine {
+  RelocSlot s[kLineSlots];
 };
-static_assert(sizeof(RelocBucket) == 64, "RelocBucket is one 64-byte line");
+static_assert(sizeof(RelocLine) == 64, "RelocLine is one 64-byte line");
+// Fence f of a fence line: its 32-bit word 2 + f.
+__host__ __device__ inline uint32_t* line_fences(RelocLine& L) { return reinterpret_cast<uint32_t*>(&L) + 2; }
 
 struct RelocDev {
-  const RelocBucket* bucket;
-  const RelocRec* rec;
-  const uint64_t* lo;  // every interval's lo (for buckets with > 14 starts)
-  uint64_t n;          // intervals; 0 = relocation off
+  const RelocLine* line;
+  uint64_t n;           // intervals; 0 = relocation off
   uint64_t lo_min;
   uint64_t hi_max;
-  uint32_t shift;      // <= 32, so offsets inside a bucket fit in 32 bits
+  uint32_t shift;       // <= kMaxLineShift
   uint32_t policy;
 };
 
@@ -195,129 +204,79 @@ __device__ inline void stage_words(uint64_t* dst, const uint64_t* src, uint32_t 
 }
 
 // Relocate K words at once (the words whose bit is set in `mask`; the others
-// pass through): the last interval with lo <= w moves w if w < hi (w <= hi
-// under the inclusive policy).  The K searches advance in lockstep, so each
-// step issues its K loads before waiting for any of them.
+// pass through): the interval containing w (the last one with lo <= w)
+// moves w if w < hi (w <= hi under the inclusive policy).  The K searches
+// advance in lockstep, so each step issues its K line reads before waiting
+// for any of them.
 template <int K>
-__device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_t* out, uint32_t mask) {
+__host__ __device__ inline void reloc_batch(const RelocDev& r, const uint64_t* w, uint64_t* out, uint32_t mask) {
   if (r.n == 0) {  // relocation off (uniform)
 #pragma unroll
     for (int k = 0; k < K; ++k) out[k] = w[k];
     return;
   }
   bool ok[K];
-  uint32_t x[K], width[K];
-  const uint4* line[K];
-  uint4 h[K];
-  // Every search's root line is loaded without a branch (bucket 0 stands in
-  // for words outside the table and is masked off): a load behind a per-word
-  // branch is followed by its own wait, and the K searches would go one
-  // after another instead of together.
+  uint32_t x[K];
+  uint4 q[K][kLineSlots];
+  // Every search's root line is loaded without a branch (line 0 stands in
+  // for words outside the table and is masked off): a load behind a
+  // per-word branch is followed by its own wait, and the K searches would
+  // go one after another instead of together.
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     ok[k] = ((mask >> k) & 1) && w[k] >= r.lo_min && (r.policy ? w[k] <= r.hi_max : w[k] < r.hi_max);
     const uint64_t rel = w[k] - r.lo_min;
     const uint64_t b = ok[k] ? rel >> r.shift : 0;
-    x[k] = (uint32_t)(rel - (b << r.shift));
-    width[k] = r.shift;
-    line[k] = reinterpret_cast<const uint4*>(r.bucket + b);
+    x[k] = ok[k] ? (uint32_t)(rel - (b << r.shift)) : 0u;
+    const uint4* p = reinterpret_cast<const uint4*>(r.line + b);
+#pragma unroll
+    for (uint32_t j = 0; j < kLineSlots; ++j) q[k][j] = p[j];
   }
-#pragma unroll
-  for (int k = 0; k < K; ++k) h[k] = line[k][0];
-#pragma unroll
-  for (int k = 0; k < K; ++k)
-    if (!ok[k]) h[k] = make_uint4(0, 0, 0, 0);
-  // Descend through split lines (crowded buckets) to the leaves.
+  // Descend through fence lines to the leaves: the child after the last
+  // fence at or before x (fences are in order; unused ones are 2^32 - 1 > x).
   for (;;) {
     bool any = false;
 #pragma unroll
-    for (int k = 0; k < K; ++k) any |= (h[k].y & kBucketSplit) != 0;
+    for (int k = 0; k < K; ++k) any |= ok[k] && (q[k][0].x & kLineFence);
     if (!any) break;
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      if (h[k].y & kBucketSplit) {
-        width[k] -= h[k].y & 63;
-        const uint32_t sub = width[k] >= 32 ? 0u : x[k] >> width[k];
-        x[k] -= width[k] >= 32 ? 0u : sub << width[k];
-        line[k] = reinterpret_cast<const uint4*>(r.bucket + h[k].x + sub);
-        h[k] = line[k][0];
-      }
-    }
-  }
-  // `first`, `count` and two offsets are in the line's first 16 bytes; the
-  // other 48 are read only for leaves with more than two starts.
-  uint32_t c[K];
-  bool more = false;
+      if (ok[k] && (q[k][0].x & kLineFence)) {
+        const uint32_t f[kLineFences] = {q[k][0].z, q[k][0].w, q[k][1].x, q[k][1].y, q[k][1].z,
+                                         q[k][1].w, q[k][2].x, q[k][2].y, q[k][2].z, q[k][2].w,
+                                         q[k][3].x, q[k][3].y, q[k][3].z, q[k][3].w};
+        uint32_t c = 0, at = 0;
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    c[k] = (h[k].y > 0 && h[k].z <= x[k]) + (h[k].y > 1 && h[k].w <= x[k]);
-    more |= h[k].y > 2;
-  }
-  if (more) {
-    uint4 q1[K], q2[K], q3[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) {  // the rest of the line just read: no branch, one wait
-      q1[k] = line[k][1];
-      q2[k] = line[k][2];
-      q3[k] = line[k][3];
-    }
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      if (h[k].y > 2) {
-        const uint32_t m = h[k].y < kBucketOffsets ? h[k].y : kBucketOffsets;
-        const uint32_t off[kBucketOffsets - 2] = {q1[k].x, q1[k].y, q1[k].z, q1[k].w, q2[k].x, q2[k].y,
-                                                  q2[k].z, q2[k].w, q3[k].x, q3[k].y, q3[k].z, q3[k].w};
-#pragma unroll
-        for (uint32_t e = 0; e < kBucketOffsets - 2; ++e) c[k] += (e + 2 < m) & (off[e] <= x[k]);
-      }
-    }
-  }
-  // A leaf with more starts than its line holds (depth limit reached):
-  // binary search over lo[] for the rest, in lockstep.
-  uint32_t i[K], lo[K], hi[K];
-  bool bs = false;
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    i[k] = h[k].x + c[k];
-    const bool s = ok[k] && h[k].y > kBucketOffsets && c[k] == kBucketOffsets;
-    lo[k] = i[k];
-    hi[k] = s ? h[k].x + h[k].y : i[k];
-    bs |= s;
-  }
-  if (bs) {
-    for (;;) {
-      bool act = false;
-#pragma unroll
-      for (int k = 0; k < K; ++k) act |= hi[k] > lo[k];
-      if (!act) break;
-      uint32_t mid[K];
-      uint64_t key[K];
-#pragma unroll
-      for (int k = 0; k < K; ++k) mid[k] = (lo[k] + hi[k] + 1) >> 1;  // = lo[k] once a search is done
-#pragma unroll
-      for (int k = 0; k < K; ++k) key[k] = r.lo[mid[k]];
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        if (hi[k] > lo[k]) {
-          if (key[k] <= w[k]) lo[k] = mid[k];
-          else hi[k] = mid[k] - 1;
+        for (uint32_t e = 0; e < kLineFences; ++e) {
+          const bool le = f[e] <= x[k];
+          c += le;
+          at = le ? f[e] : at;
         }
+        x[k] -= at;
+        const uint4* p = reinterpret_cast<const uint4*>(r.line + q[k][0].y + c);
+#pragma unroll
+        for (uint32_t j = 0; j < kLineSlots; ++j) q[k][j] = p[j];
       }
     }
-#pragma unroll
-    for (int k = 0; k < K; ++k) i[k] = lo[k];
   }
-  RelocRec iv[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) iv[k] = r.rec[ok[k] ? i[k] : 0];
+  // The last slot starting at or before x (slots are in lo order; unused
+  // ones start at 2^32 - 1 > x).
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const bool inside = ok[k] && (r.policy ? (w[k] <= iv[k].hi) : (w[k] < iv[k].hi));
-    out[k] = inside ? w[k] + iv[k].delta : w[k];
+    uint32_t end = q[k][0].y;
+    uint64_t delta = (uint64_t)q[k][0].z | ((uint64_t)q[k][0].w << 32);
+#pragma unroll
+    for (uint32_t j = 1; j < kLineSlots; ++j) {
+      const bool at = q[k][j].x <= x[k];
+      end = at ? q[k][j].y : end;
+      delta = at ? ((uint64_t)q[k][j].z | ((uint64_t)q[k][j].w << 32)) : delta;
+    }
+    const bool inside = ok[k] && (r.policy ? x[k] + 1 <= end : x[k] + 1 < end);
+    out[k] = inside ? w[k] + delta : w[k];
   }
 }
 
-__device__ inline uint64_t reloc_word(const RelocDev& r, uint64_t w) {
+__host__ __device__ inline uint64_t reloc_word(const RelocDev& r, uint64_t w) {
   uint64_t o;
   reloc_batch<1>(r, &w, &o, 1u);
   return o;

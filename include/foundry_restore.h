@@ -260,7 +260,7 @@ int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* 
  * the array: calls on different streams that overlap race (the later index
  * can replace the earlier one under its running kernel); calls in one
  * stream's order do not. */
-#define FDY_STATIC_INDEX_BYTES (8u << 20)
+#define FDY_STATIC_INDEX_BYTES (16u << 20)
 int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
                               uint32_t policy, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
                               void* stream);
