@@ -80,12 +80,13 @@ struct fdy_archive {
   uint64_t total_cap = 0;
   uint32_t num_slots = 0;
   uint32_t num_chunks = 0;
+  uint32_t num_units = 0;
 
   // `arena` holds every open-time buffer other than the images, R and the
   // restore's scratch, as parts (one allocation instead of some twenty).
   fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, chunks, slot_desc, live_cur, tslots;
+  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, units, chunks, slot_desc, live_cur, tslots;
   fdy::DevBuf aux, image, live, ovr, cand, sub_count, graph_count, node_pbytes, key_hash;
 
   fdy::RelocPlan reloc;

@@ -18,6 +18,8 @@ struct RestoreArgs {
   uint32_t num_slots;
   uint32_t num_chunks;        // node chunks over all graphs
   const uint32_t* chunk_graph;  // graph of each node chunk
+  uint32_t num_units;         // digest units (4 KB slices of keys and dependency tables) over all graphs
+  const DigestUnit* units;
   NodeChunk* chunks;          // per node chunk
   uint64_t* digests;          // 4 per graph
   const uint32_t* explicit_template;  // or null
@@ -46,7 +48,7 @@ struct RestoreArgs {
   RelocDev reloc;
 };
 
-hipError_t launch_digests(const RestoreArgs& a, hipStream_t s);
+hipError_t launch_key_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);

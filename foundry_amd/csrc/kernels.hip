@@ -1,7 +1,6 @@
 // kernels.hip -- the restore kernels for gfx950 (wave64, 160 KB LDS per CU).
 //
-//   k_digest  per graph: a word hash of its saved key, and the CRC-64/XZ
-//             digests of its key and its dependency table.
+//   k_khash   per graph: a word hash of its saved key.
 //   k_group   template_of[g] = lowest graph with the same key bytes (by the
 //             word hash, then a byte compare).
 //   k_node_a  one workgroup per 256-node chunk of a graph: for a
@@ -11,9 +10,11 @@
 //             pointer relocation, node-type and kernel-entry records) for
 //             every node that differs or has nothing to compare with.
 //   k_node_b  one workgroup per graph: clean nodes completed from the
-//             template's results, chunk CRCs joined into the four digests,
-//             word offsets by block scans, the diff-tile -> first-node table,
-//             ragged-word sources, slot descriptors.
+//             template's results, chunk CRCs joined into the node-type and
+//             kernel-entry digests, word offsets by block scans, the
+//             diff-tile -> first-node table, ragged-word sources, slot
+//             descriptors; beside them, one wave per 4 KB slice of every key
+//             and dependency table: their CRC-64/XZ digests.
 //   k_diff_t  the template graphs' words, relocated through the line-indexed
 //             interval search into R and the live image (1024-word units).
 //   k_diff_m  eight workgroups per 4096-word tile of every other graph: coalesced
@@ -75,14 +76,15 @@ __device__ __forceinline__ uint64_t stream_window(const uint8_t* p, uint64_t L, 
   return sh ? (w0 >> (8 * sh)) | (w1 << (64 - 8 * sh)) : w0;
 }
 
-// A 4 KB unit: a chunk's records, or a slice of a key or dependency table.
-constexpr uint32_t kSliceBytes = 4096;
 static_assert(kSliceBytes == 16 * kPosRecords, "a slice is as long as a chunk's records");
 
 // Shift a raw CRC z past k 4 KB units (a chunk's records, or a stream
 // slice): lane i holds x^(8 * 4096 * k) * x^i and keeps it where z has x^i
 // (bit 63 - i); the caller XORs over the wave.  Past the table, one lane
 // multiplies.
+__device__ __noinline__ uint64_t far_shift(const CrcConsts* cc, uint64_t z, uint32_t k) {
+  return gf2_mulmod(x2n_mod(cc->x2n.v, (uint64_t)kSliceBytes * k, 3), z);
+}
 __device__ __forceinline__ uint64_t shift_share(const CrcConsts* cc, uint64_t z, uint32_t k, uint32_t lane) {
   if (k < (uint32_t)kChunkShifts) return ((z >> (63 - lane)) & 1) ? cc->chunk_shift[k][lane] : 0ull;
   return lane == 0 ? gf2_mulmod(x2n_mod(cc->x2n.v, (uint64_t)kSliceBytes * k, 3), z) : 0ull;
@@ -130,65 +132,44 @@ __device__ __forceinline__ uint64_t wave_slice_crc(const uint8_t* p, uint64_t L,
   return ((uint64_t)__shfl((uint32_t)(z >> 32), 0, 64) << 32) | __shfl((uint32_t)z, 0, 64);
 }
 
-constexpr uint32_t kGroupThreads = 256;
-
 // Per graph, one workgroup: the grouping hash of its saved key (key_term
-// over its words), and the CRC-64/XZ digests of its key and its dependency
-// table: the two streams' 4 KB slices (counted from each stream's end) go
-// round the waves, and each wave shifts a slice's CRC past the slices after
-// it.  (The hash in a launch of its own after this one: 210.5 against 203.3
-// us per restore of the 256 x 1200 archive.  This kernel on a second stream
-// beside the grouping and node passes: 216.6 against 208.8 us, the node
-// pass losing CUs to it and the fork and join adding latency.)
-constexpr uint32_t kDigestThreads = 512;
+// over its words, kHashBatch loads per thread issued together), and the
+// finishing terms the key and dependency digests start from (the second
+// node pass XORs every slice's share into them).
+constexpr uint32_t kHashThreads = 512;
+constexpr uint32_t kHashBatch = 8;
 
-__global__ __launch_bounds__(kDigestThreads) void k_digest(RestoreArgs a) {
-  __shared__ uint64_t s_x[3][kDigestThreads / 64];
-  __shared__ uint64_t s_slice[8][256];
+__global__ __launch_bounds__(kHashThreads) void k_khash(RestoreArgs a) {
+  __shared__ uint64_t s_x[kHashThreads / 64];
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
-  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
   const DevGraph& Gi = a.graphs[i];
-  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY], Ld = 8ull * Gi.num_deps;
+  if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
+  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
   const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
-  const uint8_t* pd = a.img + Gi.sec_off[FDY_SEC_DEPS];
+  const uint64_t nw = (L + 7) / 8;
   uint64_t x = 0;
-  for (uint64_t k = tid; 8 * k < L; k += kDigestThreads) x ^= key_term(stream_word(p, L, (int64_t)k), k);
-  __syncthreads();
-  const uint64_t nk = (L + kSliceBytes - 1) / kSliceBytes, nd = (Ld + kSliceBytes - 1) / kSliceBytes;
-  uint64_t ck = 0, cd = 0;  // lane shares of the shifted slice CRCs
-  for (uint64_t u = wave; u < nk + nd; u += kDigestThreads / 64) {
-    const bool key = u < nk;
-    const uint64_t back = key ? u : u - nk;
-    const uint64_t z = key ? wave_slice_crc(p, L, kSliceBytes * back, s_slice, a.cc, lane)
-                           : wave_slice_crc(pd, Ld, kSliceBytes * back, s_slice, a.cc, lane);
-    const uint64_t sh = back ? shift_share(a.cc, z, (uint32_t)back, lane) : (lane == 0 ? z : 0);
-    if (key) ck ^= sh;
-    else cd ^= sh;
+  for (uint64_t k0 = tid; k0 < nw; k0 += kHashBatch * kHashThreads) {
+    uint64_t w[kHashBatch];
+#pragma unroll
+    for (uint32_t m = 0; m < kHashBatch; ++m) w[m] = stream_word(p, L, (int64_t)(k0 + m * kHashThreads));
+#pragma unroll
+    for (uint32_t m = 0; m < kHashBatch; ++m) {
+      const uint64_t k = k0 + m * kHashThreads;
+      x ^= k < nw ? key_term(w[m], k) : 0ull;
+    }
   }
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    x ^= shfl_down64(x, d);
-    ck ^= shfl_down64(ck, d);
-    cd ^= shfl_down64(cd, d);
-  }
-  if (lane == 0) {
-    s_x[0][wave] = x;
-    s_x[1][wave] = ck;
-    s_x[2][wave] = cd;
-  }
+  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
+  if (lane == 0) s_x[wave] = x;
   __syncthreads();
   if (tid == 0) {
-    for (uint32_t w = 1; w < kDigestThreads / 64; ++w) {
-      x ^= s_x[0][w];
-      ck ^= s_x[1][w];
-      cd ^= s_x[2][w];
-    }
+    for (uint32_t w = 1; w < kHashThreads / 64; ++w) x ^= s_x[w];
     a.key_hash[i] = x;
-    a.digests[4ull * i + 0] = ck ^ Gi.crc_fin[0];
-    a.digests[4ull * i + 1] = cd ^ Gi.crc_fin[1];
   }
 }
+
+constexpr uint32_t kGroupThreads = 256;
 
 // template_of[i] = the lowest j <= i whose saved key has the same bytes
 // (the reference partitions graphs by exact key string,
@@ -226,9 +207,20 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
     const uint32_t j = s_found;
     if (j == i) break;  // uniform over the workgroup
     const uint8_t* pj = a.img + a.graphs[j].sec_off[FDY_SEC_TOPOLOGY_KEY];
+    // Both keys start 8-byte aligned: compare whole words, kHashBatch per
+    // side per thread in flight.
     bool d = false;
-    for (uint64_t q = tid; q * 8 < L; q += kGroupThreads)
-      d |= stream_window(pi, L, (int64_t)q * 8) != stream_window(pj, L, (int64_t)q * 8);
+    const uint64_t nw = (L + 7) / 8;
+    for (uint64_t q0 = tid; q0 < nw; q0 += kHashBatch * kGroupThreads) {
+      uint64_t vi[kHashBatch], vj[kHashBatch];
+#pragma unroll
+      for (uint32_t m = 0; m < kHashBatch; ++m) {
+        vi[m] = stream_word(pi, L, (int64_t)(q0 + m * kGroupThreads));
+        vj[m] = stream_word(pj, L, (int64_t)(q0 + m * kGroupThreads));
+      }
+#pragma unroll
+      for (uint32_t m = 0; m < kHashBatch; ++m) d |= vi[m] != vj[m];
+    }
     if (d) s_differs = 1;
     __syncthreads();
     if (!s_differs) {
@@ -965,11 +957,66 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   }
 }
 
-__global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
+__global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
   __shared__ uint32_t s_tmp[kNodeThreads / 64];
   __shared__ uint64_t s_x[4][kNodeThreads / 64];
   __shared__ unsigned long long s_pb;
   __shared__ uint32_t s_status, s_words, s_flat, s_tbase;
+  if (blockIdx.x >= a.num_graphs) {
+    // Workgroups past the graphs: the digest units, one per wave (the key
+    // and dependency digests are off the grouping chain, so they run beside
+    // this pass).  A wave takes the raw CRC of its 4 KB slice (lane l absorbs
+    // 64 bytes through the slicing tables and is moved into place by
+    // x^(8*64*(63-l))), shifts it past the slices after it and XORs it into
+    // the digest (XOR is order-free).  Every load that does not depend on
+    // the slice's bytes is issued with them, before the tables are staged.
+    __shared__ uint64_t s_slice[8][256];
+    static_assert(8 * 256 == 2 * kNodeThreads, "two table words per thread");
+    const uint32_t lane = threadIdx.x & 63;
+    const uint64_t* tab = &a.cc->slice.t[0][0];
+    const uint64_t t0 = tab[threadIdx.x], t1 = tab[threadIdx.x + kNodeThreads];
+    const uint32_t u = (blockIdx.x - a.num_graphs) * (kNodeThreads / 64) + (threadIdx.x >> 6);
+    const bool on = u < a.num_units;
+    const DigestUnit du = a.units[on ? u : 0];
+    const int64_t b0 = (int64_t)du.len - (int64_t)kSliceBytes * du.back - 64 * (64 - (int64_t)lane);
+    const int64_t q0 = b0 >> 3;  // b0 = 8 q0 + (len mod 8) in every lane
+    const uint32_t sh = (uint32_t)(du.len & 7);
+    const uint8_t* p = a.img + du.src;
+    // Words before the stream read as zero.  Past its end only word q0 + 8
+    // of the last lane can lie (one word, when len is a multiple of 8, and
+    // then unused): inside the image buffer, whose 4 KB zero tail covers it.
+    uint64_t w[9];
+#pragma unroll
+    for (uint32_t k = 0; k < 9; ++k) {
+      const int64_t q = q0 + k;
+      const uint64_t v = reinterpret_cast<const uint64_t*>(p)[q < 0 ? 0 : q];
+      w[k] = q < 0 ? 0 : v;
+    }
+    uint64_t pm = a.cc->pos64[kPosLanes - 64 + lane];
+    const uint64_t cs = a.cc->chunk_shift[min(du.back, (uint32_t)kChunkShifts - 1)][lane];
+    (&s_slice[0][0])[threadIdx.x] = t0;
+    (&s_slice[0][0])[threadIdx.x + kNodeThreads] = t1;
+    __syncthreads();
+    if (!on) return;
+    // pm opaque from here: otherwise the multiply's 64 per-bit masks of pm
+    // are computed before the barrier and spilled.
+    asm volatile("" : "+v"(pm));
+    uint64_t z = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) z = crc_slice8(s_slice, z, sh ? (w[k] >> (8 * sh)) | (w[k + 1] << (64 - 8 * sh)) : w[k]);
+    z = gf2_mulmod(pm, z);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) z ^= shfl_down64(z, d);
+    z = ((uint64_t)__shfl((uint32_t)(z >> 32), 0, 64) << 32) | __shfl((uint32_t)z, 0, 64);  // the slice's raw CRC
+    uint64_t share;
+    if (du.back == 0) share = lane == 0 ? z : 0;
+    else if (du.back < (uint32_t)kChunkShifts) share = ((z >> (63 - lane)) & 1) ? cs : 0;
+    else share = lane == 0 ? far_shift(a.cc, z, du.back) : 0;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) share ^= shfl_down64(share, d);
+    if (lane == 0 && share) atomicXor(reinterpret_cast<unsigned long long*>(a.digests + du.dst), share);
+    return;
+  }
 
   const uint32_t g = blockIdx.x;
   const uint32_t t = a.template_of[g];
@@ -1113,7 +1160,7 @@ __global__ __launch_bounds__(kNodeThreads) void k_node_b(RestoreArgs a) {
     a.status[g] = stat;
     a.gwords[g] = s_words;
     a.pbytes[g] = s_pb;
-    for (int k = 2; k < 4; ++k) a.digests[4ull * g + k] = acc[k] ^ Gg.crc_fin[k];  // key and deps: k_digest's
+    for (int k = 2; k < 4; ++k) a.digests[4ull * g + k] = acc[k] ^ Gg.crc_fin[k];  // 0, 1: the digest units
     if (is_t) {
       a.live_cur[g] = g;
       // List the template's slots that hold words for k_diff_t.
@@ -1913,8 +1960,8 @@ __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint6
 
 }  // namespace
 
-hipError_t launch_digests(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_digest, dim3(a.num_graphs), dim3(kDigestThreads), 0, s, a);
+hipError_t launch_key_hash(const RestoreArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(k_khash, dim3(a.num_graphs), dim3(kHashThreads), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1931,7 +1978,8 @@ hipError_t launch_node(const RestoreArgs& a, hipStream_t s) {
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k_node_b, dim3(a.num_graphs), dim3(kNodeThreads), 0, s, a);
+  const uint32_t unit_blocks = (a.num_units + kNodeThreads / 64 - 1) / (kNodeThreads / 64);
+  hipLaunchKernelGGL(k_node_b, dim3(a.num_graphs + unit_blocks), dim3(kNodeThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -177,6 +177,18 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
               chunk_graph.begin() + a->graphs[i].chunk_base +
                   std::max<uint64_t>(1, (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk),
               i);
+  // The digest units: every 4 KB slice of every key and dependency table.
+  std::vector<DigestUnit> units;
+  for (uint32_t i = 0; i < G; ++i) {
+    const DevGraph& d = a->graphs[i];
+    const uint64_t src[2] = {d.sec_off[FDY_SEC_TOPOLOGY_KEY], d.sec_off[FDY_SEC_DEPS]};
+    const uint64_t len[2] = {d.sec_size[FDY_SEC_TOPOLOGY_KEY], 8ull * d.num_deps};
+    for (uint32_t k = 0; k < 2; ++k)
+      for (uint64_t b = 0; b * kSliceBytes < len[k]; ++b) units.push_back({src[k], len[k], (uint32_t)b, 4 * i + k, 0});
+  }
+  if (units.size() >= (1ull << 31)) return err(FDY_E_FORMAT, "archive too large (keys and dependency tables past 8 TB)");
+  a->num_units = (uint32_t)units.size();
+  if (units.empty()) units.push_back({0, 0, 0, 0, 0});  // never read (no unit workgroups)
 
   // The tables: parts of one arena allocation, each 256-byte aligned.
   const std::pair<DevBuf*, uint64_t> parts[] = {
@@ -188,6 +200,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
       {&a->ndesc, nodes * sizeof(NodeDesc)}, {&a->nptrs, 16 * nodes},
       {&a->live_src, 4 * nodes},            {&a->tile_node, 4 * slots},
       {&a->chunk_graph, 4 * chunks},        {&a->node_pbytes, 8 * nodes},
+      {&a->units, sizeof(DigestUnit) * units.size()},
       {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
       {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
       {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->graph_count, 4ull * G},
@@ -216,6 +229,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(a->chunk_graph.p, chunk_graph.data(), 4 * chunks, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(a->units.p, units.data(), sizeof(DigestUnit) * units.size(), hipMemcpyHostToDevice));
   return FDY_OK;
 }
 
@@ -668,6 +682,8 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.num_slots = a->num_slots;
   r.num_chunks = a->num_chunks;
   r.chunk_graph = a->chunk_graph.as<uint32_t>();
+  r.num_units = a->num_units;
+  r.units = a->units.as<DigestUnit>();
   r.chunks = a->chunks.as<NodeChunk>();
   r.digests = a->digests.as<uint64_t>();
   r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
@@ -699,9 +715,9 @@ int fdy_restore(fdy_archive* a, void* stream) {
       if (!e) FDY_HIP(hipEventCreate(&e));
     FDY_HIP(hipEventRecord(a->ev[0], s));
   }
-  // The key and dependency digests first: the grouping hash then reads the
-  // keys from L2.
-  FDY_HIP(launch_digests(r, s));
+  // The grouping hash of the keys first (the key and dependency digests run
+  // beside the second node pass).
+  FDY_HIP(launch_key_hash(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
   FDY_HIP(launch_group(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));

@@ -32,6 +32,10 @@ constexpr uint32_t kNodeClean = 0x100;   // entry and param entries equal the te
 constexpr uint32_t kGraphNodeCount = 0x10;    // node count differs from the template
 constexpr uint32_t kGraphOverflow = 0x20;     // param image larger than its capacity
 
+// A 4 KB unit of the CRC digests: a node chunk's records, or a slice of a
+// saved key or dependency table.
+constexpr uint32_t kSliceBytes = 4096;
+
 // Per-graph metadata, computed on the host at open and uploaded once.
 struct DevGraph {
   uint64_t sec_off[FDY_SEC_COUNT];   // absolute byte offsets into the device file image
@@ -48,6 +52,17 @@ struct DevGraph {
   uint32_t chunk_base;   // first node chunk (kNodeChunk nodes each)
   uint32_t pad_;
 };
+
+// One unit of the key and dependency digests: a 4 KB slice of one graph's
+// saved key or dependency table, built on the host at open.
+struct DigestUnit {
+  uint64_t src;   // byte offset of the stream in the file image (8-byte aligned)
+  uint64_t len;   // stream bytes
+  uint32_t back;  // the slice ends 4096 * back bytes before the stream's end
+  uint32_t dst;   // digest word: 4 * graph + 0 (key) or 1 (dependency table)
+  uint64_t pad_;
+};
+static_assert(sizeof(DigestUnit) == 32, "DigestUnit is 32 B");
 
 // Nodes per chunk of the node pass (a graph has at least one chunk), and
 // what a chunk reports to its graph.

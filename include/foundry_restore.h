@@ -278,9 +278,9 @@ void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int3
 /* Timing of the last fdy_restore, from HIP events recorded on its stream
  * around each kernel (milliseconds).  Synchronizes. */
 typedef struct fdy_restore_timing {
-  float hash_ms;    /* saved-key and dependency digests, and the grouping hash of every key */
+  float hash_ms;    /* the grouping hash of every key */
   float group_ms;   /* template assignment */
-  float node_ms;    /* per-node compare, layout, and the node-type and kernel-entry digests */
+  float node_ms;    /* per-node compare, layout, and the four digests */
   float tmpl_ms;    /* relocation of the template graphs' param words */
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
   float search_ms;  /* interval searches and override records of the words left over by the diff */
