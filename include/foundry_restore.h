@@ -253,15 +253,15 @@ int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* 
  * would, but builds the interval index on the host and keeps it in a static
  * device array of FDY_STATIC_INDEX_BYTES bytes that each GPU holds until the
  * process ends: no hipMalloc, hipFree or other device or pinned allocation.
- * An index larger than the array (past about 130 thousand intervals spread
- * like the relocation-heavy workload's: 64-byte lines, two root lines per
- * interval rounded to a power of two, plus a line per four intervals in
+ * An index larger than the array (past 65,536 intervals spread like the
+ * relocation-heavy workload's: 64-byte lines, two root lines per interval
+ * rounded down to a power of two, plus about a line per four intervals in
  * crowded ranges) is FDY_E_CAPACITY before anything is enqueued.  The index is copied in `stream`'s order and the call waits for
  * those copies, then enqueues the relocation.  Every call on one GPU shares
  * the array: calls on different streams that overlap race (the later index
  * can replace the earlier one under its running kernel); calls in one
  * stream's order do not. */
-#define FDY_STATIC_INDEX_BYTES (16u << 20)
+#define FDY_STATIC_INDEX_BYTES (8u << 20)
 int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
                               uint32_t policy, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
                               void* stream);
