@@ -1382,8 +1382,9 @@ constexpr uint32_t kMThreads = kSubsPerSlot * 64 / kMSplit;
 static_assert(kSubsPerSlot % kMSplit == 0, "whole sub-ranges per workgroup");
 constexpr uint32_t kSlots = 2;  // searches per batch in the overflowed-template path
 
-// Five waves per SIMD: the node window in LDS allows no more.
-__global__ __launch_bounds__(kMThreads, 5) void k_diff_m(RestoreArgs a) {
+// Six waves per SIMD: the node window in LDS (12 KB per workgroup) allows
+// no more.
+__global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   constexpr uint32_t J = kMWords;
   static_assert((kMThreads / 64) * kSubWords * sizeof(Candidate) <= kDiffWindow * sizeof(NodeDesc),
                 "each wave's candidates fit its part of the node window");
