@@ -73,7 +73,6 @@ class RestoreTiming(C.Structure):
         ("tmpl_ms", C.c_float),
         ("diff_ms", C.c_float),
         ("search_ms", C.c_float),
-        ("compact_ms", C.c_float),
         ("total_ms", C.c_float),
     ]
 

@@ -87,7 +87,7 @@ struct fdy_archive {
   fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
   fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, units, chunks, slot_desc, live_cur, tslots;
-  fdy::DevBuf aux, image, live, ovr, cand, sub_count, graph_count, node_pbytes, key_hash;
+  fdy::DevBuf aux, image, live, ovr, cand, sub_count, slot_rec, gaps, node_pbytes, key_hash;
 
   fdy::RelocPlan reloc;
   // Serving layout, taken when the first group graph is bound (no restore

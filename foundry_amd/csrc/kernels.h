@@ -42,8 +42,9 @@ struct RestoreArgs {
   uint32_t* live_cur;         // per graph
   fdy_override* ovr;          // override records: graph g's in canonical order from index word_base(g)
   Candidate* cand;            // per (slot, sub-range): kSubWords candidates, then as many records
-  uint32_t* sub_count;        // records per (slot, sub-range)
-  uint32_t* graph_count;      // records per graph
+  uint32_t* sub_count;        // per (slot, sub-range): candidates | compared candidates << 16
+  uint32_t* slot_rec;         // records per slot
+  uint32_t* gaps;             // nonzero: some slot made fewer records than its bound
   uint64_t* node_pbytes;      // param bytes per node (nodes the first node pass handles itself)
   RelocDev reloc;
 };
@@ -54,7 +55,16 @@ hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_members(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s);
-hipError_t launch_compact(const RestoreArgs& a, hipStream_t s);
+
+// Closing the gaps in override arrays (k_repack).
+struct RepackArgs {
+  const DevGraph* graphs;
+  const uint32_t* sub_count;
+  const uint32_t* slot_rec;
+  fdy_override* ovr;
+  uint32_t num_graphs;
+};
+hipError_t launch_repack(const RepackArgs& a, hipStream_t s);
 
 struct SwitchArgs {
   const fdy_override* ovr_cur;  // current graph's overrides

@@ -16,18 +16,19 @@
 //             descriptors; beside them, one wave per 4 KB slice of every key
 //             and dependency table: their CRC-64/XZ digests.
 //   k_diff_t  the template graphs' words, relocated through the line-indexed
-//             interval search into R and the live image (1024-word units).
+//             interval search into R and the live image (1024-word units);
+//             the key-digest collision report.
 //   k_diff_m  eight workgroups per 4096-word tile of every other graph: coalesced
 //             8-byte loads of the graph's and the template's words, the
 //             template's relocated word reused where the raw words are equal,
 //             the relocated image store, and per-wave ballot compaction of
 //             the words left to search or compare into candidate regions.
 //   k_diff_s  one wave per tile: the candidates' interval searches, and the
-//             differing words as override records.
-//   k_compact record regions -> each graph's dense override array (at the
-//             graph's word base) in canonical order, completing each
-//             record's node and template word index; per-graph counts and
-//             the collision report.
+//             differing words as completed override records, written at
+//             their place in the graph's dense override array.
+//   k_repack  per graph, only when flagged (before results are read): the
+//             gaps that compared words equal after relocation leave in a
+//             graph's override array closed.
 //   k_switch  override scatter for one graph switch.
 //   k_mirror  dirty nodes' live words -> a group graph's host mirror.
 //   k_fill    memset node of a restored graph, as a kernel node.
@@ -142,7 +143,10 @@ constexpr uint32_t kHashBatch = 8;
 __global__ __launch_bounds__(kHashThreads) void k_khash(RestoreArgs a) {
   __shared__ uint64_t s_x[kHashThreads / 64];
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (i == 0 && tid == 0) *a.tslot_count = 0;  // the node pass lists template slots here
+  if (i == 0 && tid == 0) {
+    *a.tslot_count = 0;  // the node pass lists template slots here
+    *a.gaps = 0;         // the search pass flags gapped override arrays here
+  }
   const DevGraph& Gi = a.graphs[i];
   if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
   const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
@@ -1361,6 +1365,20 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
       }
     }
   }
+  // The collision report, one graph per workgroup in turn (the digests are
+  // final after the node pass): a graph below this graph's template whose
+  // key has the same CRC-64/XZ and length.  Its key bytes differ, or it
+  // would be the template (grouping is by exact bytes).
+  if (a.explicit_template) return;
+  for (uint32_t g = blockIdx.x; g < a.num_graphs; g += gridDim.x) {
+    const uint32_t t = a.template_of[g];
+    const uint64_t dg = a.digests[4ull * g];
+    const uint64_t Lg = a.graphs[g].sec_size[FDY_SEC_TOPOLOGY_KEY];
+    bool coll = false;
+    for (uint32_t j = tid; j < t; j += kTThreads)
+      coll |= a.digests[4ull * j] == dg && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == Lg;
+    if (__ballot(coll) && (tid & 63) == 0) atomicOr(&a.status[g], FDY_GRAPH_COLLISION);
+  }
 }
 
 // The other graphs: kMSplit workgroups per slot, each of kMThreads / 64
@@ -1517,10 +1535,11 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   const uint64_t lt = (1ull << lane) - 1;
   if (!flat) __syncthreads();  // every wave of the workgroup is done with the node window
   Candidate* stage = reinterpret_cast<Candidate*>(s_nd) + (tid >> 6) * kSubWords;
-  uint32_t run = 0;
+  uint32_t run = 0, ncmp = 0;
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
     const uint64_t mk = __ballot((cand >> j) & 1);
+    ncmp += (uint32_t)__popcll(__ballot(((cand & cmp) >> j) & 1));
     if ((cand >> j) & 1) {
       Candidate c;
       c.word = (uint32_t)(w0 + 64 * j);
@@ -1538,7 +1557,10 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
     uint64_t* dst = reinterpret_cast<uint64_t*>(out);
     for (uint32_t i = lane; i < run * kCandWords; i += 64) dst[i] = src[i];
   }
-  if (lane == 0) sub_count[wave] = run;
+  // Candidates in the low half, compared candidates (a bound on the
+  // records they make) in the high half: the search pass places a slot's
+  // records after the bounds of its graph's earlier slots.
+  if (lane == 0) sub_count[wave] = run | (ncmp << 16);
   if (tid == 0 && part == 0 && (sd.flags & kSlotFirst)) {
     if (a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
   }
@@ -1547,40 +1569,111 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
 // Candidates of the member pass, one wave per slot: the slot's sub-range
 // lists are taken as one list in word order, kSBatch / 64 candidates per
 // lane searched in one lockstep batch.  The relocated word goes to R, and
-// the words whose value differs from the template's become override records,
-// compacted in word order at the start of the slot's region; the slot's
-// record count replaces the first sub-range count (the others become 0).
-// Writing over the candidates is safe: record r takes bytes [16r, 16r + 16)
-// and every candidate at or after list index r lies at or past byte 24r of
-// its own sub-range region, hence past them; a batch reads all its
-// candidates before writing any record.
+// the words whose value differs from the template's become override
+// records, written straight to their place in the graph's override array
+// (which starts at the graph's word base: a graph has at most one record
+// per word).  A slot's place is the sum of its graph's earlier slots'
+// compared-candidate counts (the member pass's bound on their records, in
+// the high halves of the sub-range counts), so no pass over the slots'
+// actual counts has to come first, and records keep the canonical order.
+// Each record is completed here: the node holding its word (searched in the
+// slot's node window, staged in LDS) and the word's index in the template's
+// image.  A compared candidate whose relocated value equals the template's
+// makes no record and leaves a gap at the end of its slot's range: the slot
+// raises the archive's gap flag, and k_repack closes the gaps before any
+// result is read.  The slot's record count goes to slot_rec.
 constexpr uint32_t kSThreads = 256;  // four slots per workgroup
 constexpr uint32_t kSBatch = 128;  // two per lane: 256 measured slower (fewer waves in flight)
+
+// The last node of the window (whose first word is <= w), or past a full
+// window the last such node of the graph.
+__device__ __forceinline__ void window_node(const uint2* s_gt, uint32_t nwin, uint32_t n0, const NodeDesc* nd,
+                                            uint32_t N, uint64_t w, uint32_t* node, uint32_t* gw, uint32_t* tw) {
+  uint32_t lo = 0;
+  for (uint32_t len = nwin; len > 1;) {
+    const uint32_t half = len >> 1;
+    if (s_gt[lo + half].x <= w) lo += half;
+    len -= half;
+  }
+  *node = n0 + lo;
+  *gw = s_gt[lo].x;
+  *tw = s_gt[lo].y;
+  if (nwin == kDiffWindow && lo == kDiffWindow - 1 && w >= (uint64_t)nd[*node].gword + nd[*node].nwords) {
+    uint32_t l2 = *node, h2 = N;
+    while (h2 - l2 > 1) {
+      const uint32_t mid = (l2 + h2) >> 1;
+      if (nd[mid].gword <= w) l2 = mid;
+      else h2 = mid;
+    }
+    *node = l2;
+    *gw = nd[l2].gword;
+    *tw = nd[l2].tword;
+  }
+}
 
 __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
   static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
+  // Per wave: {first graph word, first template word} of its window's nodes.
+  __shared__ uint2 s_win[kSThreads / 64][kDiffWindow];
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t slot = blockIdx.x * (kSThreads / 64) + (threadIdx.x >> 6);
   if (slot >= a.num_slots) return;  // per wave: this kernel has no barrier
+  uint2* const s_gt = s_win[threadIdx.x >> 6];
   uint32_t* counts = a.sub_count + (uint64_t)slot * kSubsPerSlot;
-  // Lane q < kSubsPerSlot holds sub-range q's count; inclusive prefix over lanes.
+  // What depends on the slot alone is loaded first.
   const uint32_t cnt = lane < kSubsPerSlot ? counts[lane] : 0;
+  const SlotDesc sd = load_slot(a.slot_desc + slot);
+  const uint32_t n0 = a.tile_node[slot];
+  const uint32_t n_after = slot + 1 < a.num_slots ? a.tile_node[slot + 1] : kNoTile;
+  // Lane q < kSubsPerSlot holds sub-range q's count; inclusive prefix over lanes.
   uint32_t incl = cnt;
 #pragma unroll
   for (int d = 1; d < (int)kSubsPerSlot; d <<= 1) {
     const uint32_t y = shfl_up32(incl, d);
     if (lane >= (uint32_t)d) incl += y;
   }
-  const uint32_t total = __shfl(incl, kSubsPerSlot - 1, 64);
-  if (total == 0) return;
-  uint32_t start[kSubsPerSlot];  // exclusive prefix, the same in every lane
+  const uint32_t total = __shfl(incl, kSubsPerSlot - 1, 64) & 0xFFFFu;
+  const uint32_t bound = __shfl(incl, kSubsPerSlot - 1, 64) >> 16;
+  if (total == 0) {  // an inactive slot, a template's, or no candidates: no records
+    if (lane == 0) a.slot_rec[slot] = 0;
+    return;
+  }
+  uint32_t start[kSubsPerSlot];  // exclusive prefix of the candidate counts, the same in every lane
 #pragma unroll
-  for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __shfl(incl - cnt, q, 64);
-  const uint64_t word_base = a.slot_desc[slot].word_base;
-  uint64_t* img_out = a.image + word_base;
-  Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
-  fdy_override* rec = reinterpret_cast<fdy_override*>(base);
+  for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __shfl(incl - cnt, q, 64) & 0xFFFFu;
+  // A slot with candidates holds words, so it starts at k * kTileWords: its
+  // index in the graph, and the graph's first slot, follow.  The earlier
+  // slots' bounds: the high halves of their sub-range counts, four to a
+  // 16-byte load.
+  const uint32_t k = sd.wbeg / kTileWords;
+  const uint4* earlier = reinterpret_cast<const uint4*>(a.sub_count + (uint64_t)(slot - k) * kSubsPerSlot);
+  uint32_t before = 0;
+  for (uint32_t j = lane; j < k * (kSubsPerSlot / 4); j += 64) {
+    const uint4 v = earlier[j];
+    before += (v.x >> 16) + (v.y >> 16) + (v.z >> 16) + (v.w >> 16);
+  }
+  const DevGraph& G = a.graphs[sd.graph];
+  const uint32_t N = G.num_nodes;
+  const NodeDesc* nd = a.node_desc + G.node_base;
+  const uint32_t n_next = k + 1 < G.tile_cap ? n_after : kNoTile;
+  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
+  const uint32_t nwin = min(kDiffWindow, n_last - n0 + 1);
+  for (uint32_t i = lane; i < nwin; i += 64) {
+    const uint4 v = *reinterpret_cast<const uint4*>(nd + n0 + i);  // gword, nwords, tword, flags
+    s_gt[i] = make_uint2(v.x, v.z);
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) before += __shfl_down(before, (unsigned)d, 64);
+  before = __shfl(before, 0, 64);
+  // The window is this wave's own: its LDS writes precede its reads in
+  // program order.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  uint64_t* img_out = a.image + sd.word_base;
+  const Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  fdy_override* rec = a.ovr + sd.word_base + before;
   const uint64_t lt = (1ull << lane) - 1;
   uint32_t run = 0;
   for (uint32_t b = 0; b < total; b += kSBatch) {
@@ -1591,8 +1684,8 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
     // together rather than each behind its own branch and wait.
     Candidate cand[K];
 #pragma unroll
-    for (uint32_t k = 0; k < K; ++k) {
-      const uint32_t i0 = b + 64 * k + lane;  // list index
+    for (uint32_t kk = 0; kk < K; ++kk) {
+      const uint32_t i0 = b + 64 * kk + lane;  // list index
       const uint32_t i = i0 < total ? i0 : 0u;
       uint32_t q = 0;
 #pragma unroll
@@ -1600,147 +1693,90 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
       uint32_t sq = start[0];
 #pragma unroll
       for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
-      cand[k] = base[(uint64_t)q * kSubWords + (i - sq)];
+      cand[kk] = base[(uint64_t)q * kSubWords + (i - sq)];
     }
 #pragma unroll
-    for (uint32_t k = 0; k < K; ++k) {
-      const bool in = b + 64 * k + lane < total;
-      raw[k] = in ? cand[k].raw : 0;
-      tval[k] = in ? cand[k].tval : 0;
-      word[k] = in ? cand[k].word : 0;
-      fl[k] = in ? cand[k].flags : 0;
-      if (fl[k] & kCandReloc) m |= 1u << k;
+    for (uint32_t kk = 0; kk < K; ++kk) {
+      const bool in = b + 64 * kk + lane < total;
+      raw[kk] = in ? cand[kk].raw : 0;
+      tval[kk] = in ? cand[kk].tval : 0;
+      word[kk] = in ? cand[kk].word : 0;
+      fl[kk] = in ? cand[kk].flags : 0;
+      if (fl[kk] & kCandReloc) m |= 1u << kk;
     }
     reloc_batch<K>(a.reloc, raw, res, m);
     // The member pass stored each candidate's raw word; only the words the
     // relocation moved are stored again (a scattered 8-byte store costs a
     // partly written line).
 #pragma unroll
-    for (uint32_t k = 0; k < K; ++k)
-      if (((m >> k) & 1) && res[k] != raw[k]) img_out[word[k]] = res[k];
+    for (uint32_t kk = 0; kk < K; ++kk)
+      if (((m >> kk) & 1) && res[kk] != raw[kk]) img_out[word[kk]] = res[kk];
 #pragma unroll
-    for (uint32_t k = 0; k < K; ++k) {
-      const bool d = (fl[k] & kCandCompare) && res[k] != tval[k];
+    for (uint32_t kk = 0; kk < K; ++kk) {
+      const bool d = (fl[kk] & kCandCompare) && res[kk] != tval[kk];
       const uint64_t mk = __ballot(d);
       if (d) {
+        uint32_t node, gw, tw;
+        window_node(s_gt, nwin, n0, nd, N, word[kk], &node, &gw, &tw);
         fdy_override o;
-        o.word = word[k];
-        o.node = 0;
-        o.value = res[k];
+        o.word = tw + (word[kk] - gw);
+        o.node = node;
+        o.value = res[kk];
         rec[run + (uint32_t)__popcll(mk & lt)] = o;
       }
       run += (uint32_t)__popcll(mk);
     }
   }
-  if (lane < kSubsPerSlot) counts[lane] = lane == 0 ? run : 0u;
+  if (lane == 0) {
+    a.slot_rec[slot] = run;
+    if (run != bound) atomicOr(a.gaps, 1u);  // rare: a compared word equal once relocated
+  }
 }
 
-// Move each slot's records to their place in the graph's dense override
-// array, completing them: the node holding the word (searched in the slot's
-// node window) and the word's index in the template's image.  The search
-// pass leaves a slot's records at the start of its region in word order,
-// their number in the slot's first sub-range count (the others are zero).
-// A graph's records start at its own word base in the override array (a
-// graph has at most one record per word), so no scan across graphs is
-// needed: a slot's place is the sum of the counts of the graph's earlier
-// slots, summed by the wave (64 counts per load), and the graph's first
-// slot also writes the graph's total.  Everything that depends on the slot
-// alone (the count, the first records, the window's bounds) is loaded
-// before what depends on its graph, to keep the chain of dependent loads
-// short.  One wave per slot: a slot holds about a hundred records on the
-// presets, and more slots in flight per CU beat more lanes per slot.
-constexpr uint32_t kCompactThreads = 64;
-constexpr uint32_t kCompactPre = 4;  // records per thread loaded up front
+// Closing the gaps (launched before results are read, only when the search
+// pass raised the gap flag), one workgroup per graph: a graph whose slots
+// made fewer records than their bounds has its slots' records moved down to
+// their canonical places, slot by slot in word order.  A batch's records are
+// all read before any is written, and records only move to lower indices,
+// so nothing is overwritten before it is read.
+constexpr uint32_t kRepackThreads = 256;
 
-__global__ __launch_bounds__(kCompactThreads) void k_compact(RestoreArgs a) {
-  __shared__ uint2 s_gt[kDiffWindow];  // {first graph word, first template word} of the window's nodes
-  const uint32_t slot = blockIdx.x, tid = threadIdx.x;
-  const uint32_t total = a.sub_count[(uint64_t)slot * kSubsPerSlot];
-  const fdy_override* recs = reinterpret_cast<const fdy_override*>(a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords);
-  fdy_override pre[kCompactPre];
-#pragma unroll
-  for (uint32_t p = 0; p < kCompactPre; ++p) {
-    const uint32_t i = tid + p * kCompactThreads;
-    if (i < total) pre[p] = recs[i];
-  }
-  const SlotDesc sd = load_slot(a.slot_desc + slot);
-  const DevGraph& G = a.graphs[sd.graph];
-  const uint32_t k = slot - G.tile_base;
-  // The records of the graph's slots before this one (all of them for the
-  // first slot, which also reports the graph's total).
-  const uint32_t upto = k == 0 ? G.tile_cap : k;
-  uint32_t before = 0, all = 0;
-  for (uint32_t j = tid; j < upto; j += kCompactThreads) {
-    const uint32_t c = a.sub_count[(uint64_t)(G.tile_base + j) * kSubsPerSlot];
-    all += c;
-    before += j < k ? c : 0u;
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    before += __shfl_down(before, (unsigned)d, 64);
-    all += __shfl_down(all, (unsigned)d, 64);
-  }
-  before = __shfl(before, 0, 64);
-  if (k == 0) {
-    if (tid == 0) a.graph_count[sd.graph] = all;
-    // Collision report (the digests are final now): a graph below this
-    // graph's template whose key has the same CRC-64/XZ and length.  Its key
-    // bytes differ, or it would be the template (grouping is by exact bytes).
-    if (!a.explicit_template) {
-      const uint64_t dg = a.digests[4ull * sd.graph];
-      const uint64_t Lg = G.sec_size[FDY_SEC_TOPOLOGY_KEY];
-      bool coll = false;
-      for (uint32_t j = tid; j < sd.tmpl; j += kCompactThreads)
-        coll |= a.digests[4ull * j] == dg && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == Lg;
-      if (__ballot(coll) && tid == 0) atomicOr(&a.status[sd.graph], FDY_GRAPH_COLLISION);
-    }
-  }
-  if (total == 0) return;  // uniform over the workgroup
-  const uint32_t n0 = a.tile_node[slot];
-  const uint32_t N = G.num_nodes;
-  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
-  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
-  const uint32_t nwin = min(kDiffWindow, n_last - n0 + 1);
-  const NodeDesc* nd = a.node_desc + G.node_base;
-  const uint64_t base = G.word_base + before;
-  for (uint32_t i = tid; i < nwin; i += kCompactThreads) {
-    const uint4 v = *reinterpret_cast<const uint4*>(nd + n0 + i);  // gword, nwords, tword, flags
-    s_gt[i] = make_uint2(v.x, v.z);
-  }
-  __syncthreads();
-  auto finish = [&](fdy_override o, uint32_t i) {
-    const uint64_t w = o.word;
-    // The last node whose first word is <= w (nodes without words never
-    // match: the node holding w follows them); past a full window the
-    // search continues in global memory.
-    uint32_t lo = 0;
-    for (uint32_t len = nwin; len > 1;) {
-      const uint32_t half = len >> 1;
-      if (s_gt[lo + half].x <= w) lo += half;
-      len -= half;
-    }
-    uint32_t node = n0 + lo, gw = s_gt[lo].x, tw = s_gt[lo].y;
-    if (nwin == kDiffWindow && lo == kDiffWindow - 1 && w >= (uint64_t)nd[node].gword + nd[node].nwords) {
-      uint32_t l2 = node, h2 = N;
-      while (h2 - l2 > 1) {
-        const uint32_t mid = (l2 + h2) >> 1;
-        if (nd[mid].gword <= w) l2 = mid;
-        else h2 = mid;
-      }
-      node = l2;
-      gw = nd[node].gword;
-      tw = nd[node].tword;
-    }
-    o.word = tw + (uint32_t)(w - gw);
-    o.node = node;
-    a.ovr[base + i] = o;
+__global__ __launch_bounds__(kRepackThreads) void k_repack(RepackArgs a) {
+  __shared__ uint32_t s_part[kRepackThreads / 64];
+  const uint32_t g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const DevGraph& G = a.graphs[g];
+  auto slot_bound = [&](uint32_t slot) {
+    uint32_t b = 0;
+    for (uint32_t q = 0; q < kSubsPerSlot; ++q) b += a.sub_count[(uint64_t)slot * kSubsPerSlot + q] >> 16;
+    return b;
   };
+  uint32_t gap = 0;
+  for (uint32_t j = tid; j < G.tile_cap; j += kRepackThreads) gap |= slot_bound(G.tile_base + j) != a.slot_rec[G.tile_base + j];
+  gap = __ballot(gap != 0) != 0;
+  if (lane == 0) s_part[wave] = gap;
+  __syncthreads();
+  gap = 0;
 #pragma unroll
-  for (uint32_t p = 0; p < kCompactPre; ++p) {
-    const uint32_t i = tid + p * kCompactThreads;
-    if (i < total) finish(pre[p], i);
+  for (uint32_t w = 0; w < kRepackThreads / 64; ++w) gap |= s_part[w];
+  if (!gap) return;  // uniform over the workgroup
+  fdy_override* ovr = a.ovr + G.word_base;
+  uint32_t bound_at = 0, rec_at = 0;  // the slot's place by the bounds, and its canonical place
+  for (uint32_t k = 0; k < G.tile_cap; ++k) {
+    const uint32_t slot = G.tile_base + k;
+    const uint32_t c = a.slot_rec[slot];
+    if (bound_at != rec_at) {
+      for (uint32_t b0 = 0; b0 < c; b0 += kRepackThreads) {
+        const uint32_t i = b0 + tid;
+        fdy_override o{};
+        if (i < c) o = ovr[bound_at + i];
+        __syncthreads();
+        if (i < c) ovr[rec_at + i] = o;
+        __syncthreads();
+      }
+    }
+    bound_at += slot_bound(slot);
+    rec_at += c;
   }
-  for (uint32_t i = tid + kCompactPre * kCompactThreads; i < total; i += kCompactThreads) finish(recs[i], i);
 }
 
 // ---- switch --------------------------------------------------------------
@@ -2002,8 +2038,9 @@ hipError_t launch_diff_search(const RestoreArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_compact(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_compact, dim3(a.num_slots), dim3(kCompactThreads), 0, s, a);
+hipError_t launch_repack(const RepackArgs& a, hipStream_t s) {
+  if (a.num_graphs == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_repack, dim3(a.num_graphs), dim3(kRepackThreads), 0, s, a);
   return hipGetLastError();
 }
 

@@ -203,7 +203,8 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
       {&a->units, sizeof(DigestUnit) * units.size()},
       {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
       {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
-      {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->graph_count, 4ull * G},
+      {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->slot_rec, 4 * slots},
+      {&a->gaps, 4},
   };
   uint64_t arena_bytes = 0;
   for (const auto& pt : parts) arena_bytes += (pt.second + 255) / 256 * 256;
@@ -310,16 +311,33 @@ int ensure_cache(fdy_archive* a, hipStream_t s) {
   a->h_gwords.resize(G);
   a->h_pbytes.resize(G);
   a->h_ovr_off.resize(G + 1);
-  std::vector<uint32_t> counts(G);
+  // A compared word equal to the template's only once relocated makes no
+  // record and leaves a gap where the search pass placed its slot's records
+  // by their bounds: such override arrays are closed up before anything
+  // reads them (rare; never in archives without such words).
+  uint32_t gaps = 0;
+  FDY_HIP(hipMemcpy(&gaps, a->gaps.p, 4, hipMemcpyDeviceToHost));
+  if (gaps) {
+    RepackArgs rp{a->dgraphs.as<DevGraph>(), a->sub_count.as<uint32_t>(), a->slot_rec.as<uint32_t>(),
+                  a->ovr.as<fdy_override>(), G};
+    FDY_HIP(launch_repack(rp, s));
+    FDY_HIP(hipStreamSynchronize(s));
+  }
+  std::vector<uint32_t> slot_rec(a->num_slots);
   FDY_HIP(hipMemcpy(a->h_tmpl.data(), a->tmpl.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_status.data(), a->status.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_gwords.data(), a->gwords.p, 4ull * G, hipMemcpyDeviceToHost));
   FDY_HIP(hipMemcpy(a->h_pbytes.data(), a->pbytes.p, 8ull * G, hipMemcpyDeviceToHost));
-  FDY_HIP(hipMemcpy(counts.data(), a->graph_count.p, 4ull * G, hipMemcpyDeviceToHost));
+  FDY_HIP(hipMemcpy(slot_rec.data(), a->slot_rec.p, 4ull * a->num_slots, hipMemcpyDeviceToHost));
   // Offsets of each graph's records in canonical order over all graphs (the
-  // device keeps graph g's records from index word_base(g) instead).
+  // device keeps graph g's records from index word_base(g) instead): the
+  // sums of its slots' record counts.
   a->h_ovr_off[0] = 0;
-  for (uint32_t i = 0; i < G; ++i) a->h_ovr_off[i + 1] = a->h_ovr_off[i] + counts[i];
+  for (uint32_t i = 0; i < G; ++i) {
+    uint64_t n = 0;
+    for (uint32_t k = 0; k < a->graphs[i].tile_cap; ++k) n += slot_rec[a->graphs[i].tile_base + k];
+    a->h_ovr_off[i + 1] = a->h_ovr_off[i] + n;
+  }
   a->h_current.resize(G);
   for (uint32_t i = 0; i < G; ++i) a->h_current[i] = i;
   a->cached = true;
@@ -707,7 +725,8 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.ovr = a->ovr.as<fdy_override>();
   r.cand = a->cand.as<Candidate>();
   r.sub_count = a->sub_count.as<uint32_t>();
-  r.graph_count = a->graph_count.as<uint32_t>();
+  r.slot_rec = a->slot_rec.as<uint32_t>();
+  r.gaps = a->gaps.as<uint32_t>();
   r.node_pbytes = a->node_pbytes.as<uint64_t>();
   r.reloc = a->reloc.dev;
   if (a->timing) {
@@ -729,8 +748,6 @@ int fdy_restore(fdy_archive* a, void* stream) {
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
   FDY_HIP(launch_diff_search(r, s));
   if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
-  FDY_HIP(launch_compact(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[7], s));
   a->timed = a->timing;
   a->restored = true;
   a->cached = false;
@@ -747,15 +764,14 @@ int fdy_set_timing(fdy_archive* a, int enabled) {
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
-  FDY_HIP(hipEventSynchronize(a->ev[7]));
+  FDY_HIP(hipEventSynchronize(a->ev[6]));
   FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
   FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
   FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
   FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));
   FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[4], a->ev[5]));
   FDY_HIP(hipEventElapsedTime(&o->search_ms, a->ev[5], a->ev[6]));
-  FDY_HIP(hipEventElapsedTime(&o->compact_ms, a->ev[6], a->ev[7]));
-  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[7]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[6]));
   return FDY_OK;
 }
 

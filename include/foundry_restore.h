@@ -283,8 +283,7 @@ typedef struct fdy_restore_timing {
   float node_ms;    /* per-node compare, layout, and the four digests */
   float tmpl_ms;    /* relocation of the template graphs' param words */
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
-  float search_ms;  /* interval searches and override records of the words left over by the diff */
-  float compact_ms; /* record counts, offsets, dense canonical override array */
+  float search_ms;  /* interval searches of the words left over by the diff; completed override records in place */
   float total_ms;
 } fdy_restore_timing;
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
