@@ -67,7 +67,6 @@ class ArchiveInfo(C.Structure):
 
 class RestoreTiming(C.Structure):
     _fields_ = [
-        ("hash_ms", C.c_float),
         ("group_ms", C.c_float),
         ("node_ms", C.c_float),
         ("tmpl_ms", C.c_float),

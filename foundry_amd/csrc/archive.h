@@ -115,8 +115,9 @@ struct fdy_archive {
   uint32_t num_bound = 0;
 
   bool timing = false;
+  uint32_t epoch = 0;  // tag of the last restore's published key hashes (1..65535)
   bool timed = false;
-  hipEvent_t ev[8] = {};
+  hipEvent_t ev[6] = {};
 
   ~fdy_archive() {
     for (hipEvent_t& e : ev)

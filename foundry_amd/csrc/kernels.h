@@ -23,7 +23,8 @@ struct RestoreArgs {
   NodeChunk* chunks;          // per node chunk
   uint64_t* digests;          // 4 per graph
   const uint32_t* explicit_template;  // or null
-  uint64_t* key_hash;                 // per graph: the grouping pass's key hash
+  uint64_t* key_hash;                 // per graph: the grouping pass's published key hash (epoch-tagged)
+  uint32_t epoch;                     // this restore's tag for published key hashes (1..65535)
   uint32_t* template_of;
   uint32_t* status;
   uint32_t* gwords;
@@ -49,7 +50,6 @@ struct RestoreArgs {
   RelocDev reloc;
 };
 
-hipError_t launch_key_hash(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_node(const RestoreArgs& a, hipStream_t s);
 hipError_t launch_diff_templates(const RestoreArgs& a, hipStream_t s);

@@ -1,8 +1,8 @@
 // kernels.hip -- the restore kernels for gfx950 (wave64, 160 KB LDS per CU).
 //
-//   k_khash   per graph: a word hash of its saved key.
-//   k_group   template_of[g] = lowest graph with the same key bytes (by the
-//             word hash, then a byte compare).
+//   k_group   per graph: a word hash of its saved key, published with an
+//             atomic store; template_of[g] = lowest graph with the same key
+//             bytes (by the published hashes, then a byte compare).
 //   k_node_a  one workgroup per 256-node chunk of a graph: for a
 //             member, a coalesced compare of the chunk's node entries and
 //             param entries with its template's; the per-node path (param
@@ -91,6 +91,27 @@ __device__ __forceinline__ uint64_t shift_share(const CrcConsts* cc, uint64_t z,
   return lane == 0 ? gf2_mulmod(x2n_mod(cc->x2n.v, (uint64_t)kSliceBytes * k, 3), z) : 0ull;
 }
 
+// Per graph, one workgroup: template_of[i] = the lowest j <= i whose saved
+// key has the same bytes (the reference partitions graphs by exact key
+// string, csrc/CUDAGraphParallel.cpp:1788-1851).
+//   - The workgroup hashes its own key (key_term over its words, kHashBatch
+//     loads per thread issued together) and publishes the hash with one
+//     64-bit atomic store, tagged with the restore's epoch in its low 16
+//     bits.  Nothing else is shared, so no fence is needed: only atomics
+//     touch the published hashes.
+//   - Its first wave then scans the lower graphs' hashes, 64 per step, with
+//     atomic loads; a hash not yet published this restore is waited for a
+//     bounded time and then computed by the wave itself, so no workgroup
+//     depends on another's progress.  The lowest j with i's hash and key
+//     length is confirmed byte for byte by the workgroup; on a difference
+//     scanning goes on past j.
+// The restore's first kernel: it also resets the counters later kernels
+// accumulate into and starts the key and dependency digests from their
+// finishing terms (the node pass's digest units XOR every slice's share in).
+constexpr uint32_t kGroupThreads = 512;
+constexpr uint32_t kHashBatch = 8;
+constexpr uint32_t kHashWaitSpins = 1u << 14;  // ~1 ms of s_sleep before a wave hashes a key itself
+
 // A 64-bit hash of a key for finding grouping candidates (not a digest the
 // restore reports): the XOR over the key's 8-byte words w_k (the last one
 // zero-padded) of the SplitMix64 finaliser (Steele, Lea and Flood 2014) of
@@ -104,44 +125,30 @@ __device__ __forceinline__ uint64_t key_term(uint64_t w, uint64_t k) {
   return z ^ (z >> 31);
 }
 
-// Raw CRC (zero initial value) of one 4 KB slice of an L-byte stream (p
-// 8-byte aligned), by one wave: the slice ends `back` bytes before the
-// stream's end, and bytes before 0 read as zero.  Lane l absorbs the 64
-// bytes [end - 64 (64 - l), end - 64 (63 - l)) through the slicing tables
-// and moves its CRC into place, times x^(8 * 64 * (63 - l)) (an entry of the
-// 64-byte position table); the wave XORs the shares
-// (crc(A || B) = crc(A) * x^(8|B|) xor crc(B)).  The result is valid in
-// every lane.
-__device__ __forceinline__ uint64_t wave_slice_crc(const uint8_t* p, uint64_t L, uint64_t back,
-                                                   const uint64_t (*slice)[256], const CrcConsts* cc, uint32_t lane) {
-  const int64_t b0 = (int64_t)L - (int64_t)back - 64 * (64 - (int64_t)lane);
-  uint64_t z = 0;
-  if (b0 + 64 > 0) {
-    // b0 = 8 q0 + sh with sh = L mod 8 for every lane (the slice and lane
-    // offsets are multiples of 8), so the shift is uniform.
-    const int64_t q0 = b0 >> 3;
-    const uint32_t sh = (uint32_t)(L & 7);
-    uint64_t w[9];
+// This thread's share of the hash of the L-byte key at p (threads
+// `first`, `first + stride`, ... take its words).
+__device__ __forceinline__ uint64_t key_share(const uint8_t* p, uint64_t L, uint32_t first, uint32_t stride) {
+  const uint64_t nw = (L + 7) / 8;
+  uint64_t x = 0;
+  for (uint64_t k0 = first; k0 < nw; k0 += (uint64_t)kHashBatch * stride) {
+    uint64_t w[kHashBatch];
 #pragma unroll
-    for (uint32_t k = 0; k < 9; ++k) w[k] = stream_word(p, L, q0 + k);
+    for (uint32_t m = 0; m < kHashBatch; ++m) w[m] = stream_word(p, L, (int64_t)(k0 + (uint64_t)m * stride));
 #pragma unroll
-    for (uint32_t k = 0; k < 8; ++k) z = crc_slice8(slice, z, sh ? (w[k] >> (8 * sh)) | (w[k + 1] << (64 - 8 * sh)) : w[k]);
-    z = z ? gf2_mulmod(cc->pos64[kPosLanes - 64 + lane], z) : 0;
+    for (uint32_t m = 0; m < kHashBatch; ++m) {
+      const uint64_t k = k0 + (uint64_t)m * stride;
+      x ^= k < nw ? key_term(w[m], k) : 0ull;
+    }
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) z ^= shfl_down64(z, d);
-  return ((uint64_t)__shfl((uint32_t)(z >> 32), 0, 64) << 32) | __shfl((uint32_t)z, 0, 64);
+  return x;
 }
 
-// Per graph, one workgroup: the grouping hash of its saved key (key_term
-// over its words, kHashBatch loads per thread issued together), and the
-// finishing terms the key and dependency digests start from (the second
-// node pass XORs every slice's share into them).
-constexpr uint32_t kHashThreads = 512;
-constexpr uint32_t kHashBatch = 8;
+// The published form of a key hash: its upper 48 bits, and the epoch.
+__device__ __forceinline__ uint64_t tag_hash(uint64_t h, uint32_t epoch) { return (h & ~0xFFFFull) | epoch; }
 
-__global__ __launch_bounds__(kHashThreads) void k_khash(RestoreArgs a) {
-  __shared__ uint64_t s_x[kHashThreads / 64];
+__global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
+  __shared__ uint64_t s_x[kGroupThreads / 64];
+  __shared__ uint32_t s_found, s_differs;
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (i == 0 && tid == 0) {
     *a.tslot_count = 0;  // the node pass lists template slots here
@@ -149,56 +156,51 @@ __global__ __launch_bounds__(kHashThreads) void k_khash(RestoreArgs a) {
   }
   const DevGraph& Gi = a.graphs[i];
   if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
-  const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
-  const uint8_t* p = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
-  const uint64_t nw = (L + 7) / 8;
-  uint64_t x = 0;
-  for (uint64_t k0 = tid; k0 < nw; k0 += kHashBatch * kHashThreads) {
-    uint64_t w[kHashBatch];
-#pragma unroll
-    for (uint32_t m = 0; m < kHashBatch; ++m) w[m] = stream_word(p, L, (int64_t)(k0 + m * kHashThreads));
-#pragma unroll
-    for (uint32_t m = 0; m < kHashBatch; ++m) {
-      const uint64_t k = k0 + m * kHashThreads;
-      x ^= k < nw ? key_term(w[m], k) : 0ull;
-    }
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
-  if (lane == 0) s_x[wave] = x;
-  __syncthreads();
-  if (tid == 0) {
-    for (uint32_t w = 1; w < kHashThreads / 64; ++w) x ^= s_x[w];
-    a.key_hash[i] = x;
-  }
-}
-
-constexpr uint32_t kGroupThreads = 256;
-
-// template_of[i] = the lowest j <= i whose saved key has the same bytes
-// (the reference partitions graphs by exact key string,
-// csrc/CUDAGraphParallel.cpp:1788-1851), one workgroup per graph: its first
-// wave finds the lowest j with i's key hash and length, 64 candidates per
-// step; the workgroup compares the two keys byte for byte, and on a
-// difference goes on scanning past j.
-__global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
-  __shared__ uint32_t s_found, s_differs;
-  const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
   if (a.explicit_template) {
     if (tid == 0) a.template_of[i] = a.explicit_template[i];
     return;
   }
-  const DevGraph& Gi = a.graphs[i];
   const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
   const uint8_t* pi = a.img + Gi.sec_off[FDY_SEC_TOPOLOGY_KEY];
-  const uint64_t hi = a.key_hash[i];
+  uint64_t x = key_share(pi, L, tid, kGroupThreads);
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) x ^= shfl_down64(x, d);
+  if (lane == 0) s_x[wave] = x;
+  __syncthreads();
+  for (uint32_t w = 0; w < kGroupThreads / 64; ++w)
+    if (w != wave) x ^= s_x[w];  // lane 0 of every wave holds the whole hash
+  const uint64_t hi = tag_hash(x, a.epoch);
+  if (tid == 0) __hip_atomic_store(a.key_hash + i, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
   uint32_t from = 0, tmpl = i;
   for (;;) {
     if (tid < 64) {
+      const uint64_t hiw = ((uint64_t)__shfl((uint32_t)(hi >> 32), 0, 64) << 32) | __shfl((uint32_t)hi, 0, 64);
       uint32_t found = i;
       for (uint32_t base = from; base < i && found == i; base += 64) {
         const uint32_t j = base + lane;
-        const bool m = j < i && a.key_hash[j] == hi && a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] == L;
+        const bool in = j < i;
+        uint64_t hj = in ? __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        const uint64_t Lj = in ? a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] : ~0ull;
+        // Hashes of this restore carry its epoch; wait (bounded) for the rest.
+        for (uint32_t spin = 0; __ballot(in && (hj & 0xFFFF) != a.epoch) && spin < kHashWaitSpins; ++spin) {
+          __builtin_amdgcn_s_sleep(2);
+          if (in && (hj & 0xFFFF) != a.epoch)
+            hj = __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        // Still missing: the wave hashes those keys itself, one at a time.
+        uint64_t miss = __ballot(in && (hj & 0xFFFF) != a.epoch);
+        while (miss) {
+          const uint32_t l = (uint32_t)__ffsll((long long)miss) - 1;
+          miss &= miss - 1;
+          const DevGraph& Gj = a.graphs[base + l];
+          uint64_t y = key_share(a.img + Gj.sec_off[FDY_SEC_TOPOLOGY_KEY], Gj.sec_size[FDY_SEC_TOPOLOGY_KEY], lane, 64);
+#pragma unroll
+          for (int d = 32; d >= 1; d >>= 1) y ^= shfl_down64(y, d);
+          const uint64_t yl = ((uint64_t)__shfl((uint32_t)(y >> 32), 0, 64) << 32) | __shfl((uint32_t)y, 0, 64);
+          if (lane == l) hj = tag_hash(yl, a.epoch);
+        }
+        const bool m = in && (hj >> 16) == (hiw >> 16) && Lj == L;
         const uint64_t mk = __ballot(m);
         if (mk) found = base + (uint32_t)__ffsll((long long)mk) - 1;
       }
@@ -1997,14 +1999,7 @@ __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint6
 
 }  // namespace
 
-hipError_t launch_key_hash(const RestoreArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_khash, dim3(a.num_graphs), dim3(kHashThreads), 0, s, a);
-  return hipGetLastError();
-}
-
 hipError_t launch_group(const RestoreArgs& a, hipStream_t s) {
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_group, dim3(a.num_graphs), dim3(kGroupThreads), 0, s, a);
   return hipGetLastError();
 }

@@ -230,6 +230,9 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
   FDY_HIP(hipMemcpy(a->chunk_graph.p, chunk_graph.data(), 4 * chunks, hipMemcpyHostToDevice));
+  // No key hash is published yet (the grouping pass tags its hashes with the
+  // restore's epoch, never 0).
+  FDY_HIP(hipMemset(a->key_hash.p, 0, 8ull * G));
   FDY_HIP(hipMemcpy(a->units.p, units.data(), sizeof(DigestUnit) * units.size(), hipMemcpyHostToDevice));
   return FDY_OK;
 }
@@ -706,6 +709,8 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.digests = a->digests.as<uint64_t>();
   r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
   r.key_hash = a->key_hash.as<uint64_t>();
+  a->epoch = a->epoch % 65535 + 1;
+  r.epoch = a->epoch;
   r.template_of = a->tmpl.as<uint32_t>();
   r.status = a->status.as<uint32_t>();
   r.gwords = a->gwords.as<uint32_t>();
@@ -734,20 +739,18 @@ int fdy_restore(fdy_archive* a, void* stream) {
       if (!e) FDY_HIP(hipEventCreate(&e));
     FDY_HIP(hipEventRecord(a->ev[0], s));
   }
-  // The grouping hash of the keys first (the key and dependency digests run
-  // beside the second node pass).
-  FDY_HIP(launch_key_hash(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
+  // Grouping first (the key and dependency digests run beside the second
+  // node pass).
   FDY_HIP(launch_group(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
   FDY_HIP(launch_node(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
   FDY_HIP(launch_diff_templates(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
   FDY_HIP(launch_diff_members(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
   FDY_HIP(launch_diff_search(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[6], s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
   a->timed = a->timing;
   a->restored = true;
   a->cached = false;
@@ -764,14 +767,13 @@ int fdy_set_timing(fdy_archive* a, int enabled) {
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* o) {
   if (!a || !o) return err(FDY_E_INVALID, "null argument");
   if (!a->timed) return err(FDY_E_STATE, "enable timing with fdy_set_timing before fdy_restore");
-  FDY_HIP(hipEventSynchronize(a->ev[6]));
-  FDY_HIP(hipEventElapsedTime(&o->hash_ms, a->ev[0], a->ev[1]));
-  FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[1], a->ev[2]));
-  FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[2], a->ev[3]));
-  FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[3], a->ev[4]));
-  FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[4], a->ev[5]));
-  FDY_HIP(hipEventElapsedTime(&o->search_ms, a->ev[5], a->ev[6]));
-  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[6]));
+  FDY_HIP(hipEventSynchronize(a->ev[5]));
+  FDY_HIP(hipEventElapsedTime(&o->group_ms, a->ev[0], a->ev[1]));
+  FDY_HIP(hipEventElapsedTime(&o->node_ms, a->ev[1], a->ev[2]));
+  FDY_HIP(hipEventElapsedTime(&o->tmpl_ms, a->ev[2], a->ev[3]));
+  FDY_HIP(hipEventElapsedTime(&o->diff_ms, a->ev[3], a->ev[4]));
+  FDY_HIP(hipEventElapsedTime(&o->search_ms, a->ev[4], a->ev[5]));
+  FDY_HIP(hipEventElapsedTime(&o->total_ms, a->ev[0], a->ev[5]));
   return FDY_OK;
 }
 

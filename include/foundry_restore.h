@@ -278,8 +278,7 @@ void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int3
 /* Timing of the last fdy_restore, from HIP events recorded on its stream
  * around each kernel (milliseconds).  Synchronizes. */
 typedef struct fdy_restore_timing {
-  float hash_ms;    /* the grouping hash of every key */
-  float group_ms;   /* template assignment */
+  float group_ms;   /* key hashes and template assignment */
   float node_ms;    /* per-node compare, layout, and the four digests */
   float tmpl_ms;    /* relocation of the template graphs' param words */
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
