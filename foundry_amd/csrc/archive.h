@@ -86,7 +86,7 @@ struct fdy_archive {
   // restore's scratch, as parts (one allocation instead of some twenty).
   fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_graph, units, chunks, slot_desc, live_cur, tslots;
+  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_gt, units, chunks, slot_desc, live_cur, tslots;
   fdy::DevBuf aux, image, live, ovr, cand, sub_count, slot_rec, gaps, node_pbytes, key_hash;
 
   fdy::RelocPlan reloc;

@@ -17,7 +17,7 @@ struct RestoreArgs {
   uint32_t num_graphs;
   uint32_t num_slots;
   uint32_t num_chunks;        // node chunks over all graphs
-  const uint32_t* chunk_graph;  // graph of each node chunk
+  uint2* chunk_gt;            // per node chunk: {graph, template} (the grouping pass writes both)
   uint32_t num_units;         // digest units (4 KB slices of keys and dependency tables) over all graphs
   const DigestUnit* units;
   NodeChunk* chunks;          // per node chunk

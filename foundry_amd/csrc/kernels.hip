@@ -156,8 +156,12 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
   }
   const DevGraph& Gi = a.graphs[i];
   if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
+  // The node pass reads {graph, template} per node chunk.
+  const uint32_t nch = Gi.num_nodes ? (Gi.num_nodes + kNodeChunk - 1) / kNodeChunk : 1;
   if (a.explicit_template) {
-    if (tid == 0) a.template_of[i] = a.explicit_template[i];
+    const uint32_t t = a.explicit_template[i];
+    if (tid == 0) a.template_of[i] = t;
+    for (uint32_t c = tid; c < nch; c += kGroupThreads) a.chunk_gt[Gi.chunk_base + c] = make_uint2(i, t);
     return;
   }
   const uint64_t L = Gi.sec_size[FDY_SEC_TOPOLOGY_KEY];
@@ -237,6 +241,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
     __syncthreads();  // every thread has read s_found and s_differs
   }
   if (tid == 0) a.template_of[i] = tmpl;
+  for (uint32_t c = tid; c < nch; c += kGroupThreads) a.chunk_gt[Gi.chunk_base + c] = make_uint2(i, tmpl);
 }
 
 // ---- node pass ----------------------------------------------------------
@@ -327,13 +332,24 @@ __device__ __forceinline__ void scan_params(const uint8_t* img, const DevGraph& 
   // wait per entry.
   const uint8_t* bg = ng ? g.pidx : img;
   const uint8_t* bt = nt ? t.pidx : img;
+  // Entries 8-byte aligned in every lane (the usual case): one load each.
+  const bool aligned = __all(((reinterpret_cast<uintptr_t>(bg) | reinterpret_cast<uintptr_t>(bt)) & 7) == 0);
   for (uint32_t jb = 0; jb < max(ng, nt); jb += kParamBatch) {
     uint64_t eg[kParamBatch], et[kParamBatch];
+    if (aligned) {
 #pragma unroll
-    for (uint32_t k = 0; k < kParamBatch; ++k) {
-      const uint32_t j = jb + k;
-      eg[k] = ld_u64_any(bg + 8ull * (j < ng ? j : 0));
-      et[k] = ld_u64_any(bt + 8ull * (j < nt ? j : 0));
+      for (uint32_t k = 0; k < kParamBatch; ++k) {
+        const uint32_t j = jb + k;
+        eg[k] = *reinterpret_cast<const uint64_t*>(bg + 8ull * (j < ng ? j : 0));
+        et[k] = *reinterpret_cast<const uint64_t*>(bt + 8ull * (j < nt ? j : 0));
+      }
+    } else {
+#pragma unroll
+      for (uint32_t k = 0; k < kParamBatch; ++k) {
+        const uint32_t j = jb + k;
+        eg[k] = ld_u64_any(bg + 8ull * (j < ng ? j : 0));
+        et[k] = ld_u64_any(bt + 8ull * (j < nt ? j : 0));
+      }
     }
 #pragma unroll
     for (uint32_t k = 0; k < kParamBatch; ++k) {
@@ -722,8 +738,8 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax;
 
   const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t g = a.chunk_graph[chunk];
-  const uint32_t t = a.template_of[g];
+  const uint2 gt = a.chunk_gt[chunk];  // {graph, template}: the grouping pass filled in the template
+  const uint32_t g = gt.x, t = gt.y;
   const bool is_t = t == g;
   const DevGraph& Gg = a.graphs[g];
   const DevGraph& Gt = a.graphs[t];
@@ -740,6 +756,48 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
                     Gg.sec_size[FDY_SEC_PARAM_DATA] == Gt.sec_size[FDY_SEC_PARAM_DATA] &&
                     Gg.sec_size[FDY_SEC_ARG_DATA] == Gt.sec_size[FDY_SEC_ARG_DATA];
 
+  const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
+  const int64_t first = (int64_t)c * kNodeChunk - pad;  // node of thread 0
+  // The chunk's entries against the template's: word w of the chunk is word
+  // w % 21 of its node w / 21 (168 = 21 * 8), read coalesced.
+  const uint8_t* eg0 = img + Gg.sec_off[FDY_SEC_NODES];
+  const uint8_t* et0 = img + Gt.sec_off[FDY_SEC_NODES];
+  const int64_t b0 = first * 168, bend = 168 * (int64_t)N;
+  auto load_batch = [&](uint32_t mb, uint64_t* vg, uint64_t* vt) {
+#pragma unroll
+    for (uint32_t m = 0; m < kCompareBatch; ++m) {
+      const int64_t off = b0 + 8 * (int64_t)(tid + kNodeChunk * (mb + m));
+      const bool ok = off >= 0 && off < bend;
+      vg[m] = ok ? *reinterpret_cast<const uint64_t*>(eg0 + off) : 0;
+      vt[m] = ok ? *reinterpret_cast<const uint64_t*>(et0 + off) : 0;
+    }
+  };
+  auto take_batch = [&](uint32_t mb, const uint64_t* vg, const uint64_t* vt) {
+#pragma unroll
+    for (uint32_t m = 0; m < kCompareBatch; ++m) {
+      const uint32_t w = tid + kNodeChunk * (mb + m), node = w / kEntryWords, k = w % kEntryWords;
+      // Words 1-3 and the low half of word 4 of a kernel entry are its
+      // launch dimensions and shared memory (bytes 8-36): a difference there
+      // alone changes the node's descriptor and nothing else.
+      const uint64_t x = vg[m] ^ vt[m];
+      if (x) {
+        if ((k >= 1 && k <= 3) || (k == 4 && (x >> 32) == 0)) s_launch[node] = 1;
+        else s_dirty[node] = 1;
+      }
+      // Fields the param-entry check needs: type (word 0), param index
+      // offset and count (word 16), arg buffer offset (word 17).
+      if (k == 0) s_type[node] = (uint8_t)(vg[m] >> 32);
+      if (k == FDY_KOFF_PARAM_INDEX / 8) {
+        s_pio[node] = (uint32_t)vg[m];
+        s_np[node] = (uint32_t)(vg[m] >> 32);
+      }
+      if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg[m] == FDY_NO_ARG_BUFFER;
+    }
+  };
+  // A member's first batch of entry loads goes out before the staging below.
+  uint64_t vg0[kCompareBatch], vt0[kCompareBatch];
+  if (fast) load_batch(0, vg0, vt0);
+
   if (tid == 0) {
     s_flags = 0;
     s_status = 0;
@@ -749,8 +807,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   s_dirty[tid] = 0;
   s_launch[tid] = 0;
 
-  // CRC tables, the (small) string sections and the common attrs in LDS;
-  // sections start 8-byte aligned.
+  // The (small) string sections and the common attrs in LDS (sections start
+  // 8-byte aligned); the CRC tables too, unless the chunk is a member's,
+  // which needs them only if some node takes the per-node path.
   auto stage_strings = [&](const DevGraph& G, uint64_t* buf) -> Strings {
     Strings S{img + G.sec_off[FDY_SEC_STRINGS], G.sec_size[FDY_SEC_STRINGS]};
     if (S.size <= kStrStage) {
@@ -768,46 +827,16 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   const Strings st_str = is_t ? sg_str : stage_strings(Gt, s_str[1]);
   const uint8_t* common_g = stage_common(common_g_on, Gg, s_common[0]);
   const uint8_t* common_t = is_t ? common_g : stage_common(common_t_on, Gt, s_common[1]);
-  stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  if (!fast) stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  __syncthreads();  // the marks are zero before any thread sets one
 
-  const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
-  const int64_t first = (int64_t)c * kNodeChunk - pad;  // node of thread 0
   if (fast) {
-    // The chunk's entries against the template's: word w of the chunk is
-    // word w % 21 of its node w / 21 (168 = 21 * 8), read coalesced.
-    const uint8_t* eg0 = img + Gg.sec_off[FDY_SEC_NODES];
-    const uint8_t* et0 = img + Gt.sec_off[FDY_SEC_NODES];
-    const int64_t b0 = first * 168, bend = 168 * (int64_t)N;
+    take_batch(0, vg0, vt0);
 #pragma unroll
-    for (uint32_t mb = 0; mb < kEntryWords; mb += kCompareBatch) {
+    for (uint32_t mb = kCompareBatch; mb < kEntryWords; mb += kCompareBatch) {
       uint64_t vg[kCompareBatch], vt[kCompareBatch];
-#pragma unroll
-      for (uint32_t m = 0; m < kCompareBatch; ++m) {
-        const int64_t off = b0 + 8 * (int64_t)(tid + kNodeChunk * (mb + m));
-        const bool ok = off >= 0 && off < bend;
-        vg[m] = ok ? *reinterpret_cast<const uint64_t*>(eg0 + off) : 0;
-        vt[m] = ok ? *reinterpret_cast<const uint64_t*>(et0 + off) : 0;
-      }
-#pragma unroll
-      for (uint32_t m = 0; m < kCompareBatch; ++m) {
-        const uint32_t w = tid + kNodeChunk * (mb + m), node = w / kEntryWords, k = w % kEntryWords;
-        // Words 1-3 and the low half of word 4 of a kernel entry are its
-        // launch dimensions and shared memory (bytes 8-36): a difference
-        // there alone changes the node's descriptor and nothing else.
-        const uint64_t x = vg[m] ^ vt[m];
-        if (x) {
-          if ((k >= 1 && k <= 3) || (k == 4 && (x >> 32) == 0)) s_launch[node] = 1;
-          else s_dirty[node] = 1;
-        }
-        // Fields the param-entry check needs: type (word 0), param index
-        // offset and count (word 16), arg buffer offset (word 17).
-        if (k == 0) s_type[node] = (uint8_t)(vg[m] >> 32);
-        if (k == FDY_KOFF_PARAM_INDEX / 8) {
-          s_pio[node] = (uint32_t)vg[m];
-          s_np[node] = (uint32_t)(vg[m] >> 32);
-        }
-        if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg[m] == FDY_NO_ARG_BUFFER;
-      }
+      load_batch(mb, vg, vt);
+      take_batch(mb, vg, vt);
     }
   }
   __syncthreads();
@@ -897,6 +926,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     total += s_wave_n[w];
   }
   if (mine) s_list[before + (uint32_t)__popcll(mb & ((1ull << lane) - 1))] = (uint16_t)tid;
+  if (fast && total) stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);  // uniform
   __syncthreads();
 
   uint64_t pbytes = 0;

@@ -171,12 +171,6 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   a->num_slots = (uint32_t)slots;
   a->num_chunks = (uint32_t)chunks;
 
-  std::vector<uint32_t> chunk_graph(chunks);
-  for (uint32_t i = 0; i < G; ++i)
-    std::fill(chunk_graph.begin() + a->graphs[i].chunk_base,
-              chunk_graph.begin() + a->graphs[i].chunk_base +
-                  std::max<uint64_t>(1, (a->graphs[i].num_nodes + kNodeChunk - 1) / kNodeChunk),
-              i);
   // The digest units: every 4 KB slice of every key and dependency table.
   std::vector<DigestUnit> units;
   for (uint32_t i = 0; i < G; ++i) {
@@ -199,7 +193,7 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
       {&a->live_cur, 4ull * G},             {&a->nflags, nodes},
       {&a->ndesc, nodes * sizeof(NodeDesc)}, {&a->nptrs, 16 * nodes},
       {&a->live_src, 4 * nodes},            {&a->tile_node, 4 * slots},
-      {&a->chunk_graph, 4 * chunks},        {&a->node_pbytes, 8 * nodes},
+      {&a->chunk_gt, 8 * chunks},          {&a->node_pbytes, 8 * nodes},
       {&a->units, sizeof(DigestUnit) * units.size()},
       {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
       {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
@@ -229,7 +223,6 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   auto consts = std::make_unique<CrcConsts>();
   make_crc_consts(consts.get());
   FDY_HIP(hipMemcpy(a->cc.p, consts.get(), sizeof(CrcConsts), hipMemcpyHostToDevice));
-  FDY_HIP(hipMemcpy(a->chunk_graph.p, chunk_graph.data(), 4 * chunks, hipMemcpyHostToDevice));
   // No key hash is published yet (the grouping pass tags its hashes with the
   // restore's epoch, never 0).
   FDY_HIP(hipMemset(a->key_hash.p, 0, 8ull * G));
@@ -702,7 +695,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.num_graphs = a->G;
   r.num_slots = a->num_slots;
   r.num_chunks = a->num_chunks;
-  r.chunk_graph = a->chunk_graph.as<uint32_t>();
+  r.chunk_gt = a->chunk_gt.as<uint2>();
   r.num_units = a->num_units;
   r.units = a->units.as<DigestUnit>();
   r.chunks = a->chunks.as<NodeChunk>();
