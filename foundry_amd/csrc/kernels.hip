@@ -1340,9 +1340,14 @@ constexpr uint32_t kTUnit = kTThreads * kTWords;
 constexpr uint32_t kTUnitsPerTile = kTileWords / kTUnit;
 static_assert(kTileWords % kTUnit == 0, "template units tile a slot");
 
+constexpr uint32_t kTSearch = 2;  // searches per lane in one lockstep batch
+
 __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
   __shared__ NodeDesc s_nd[kDiffWindow];
-  const uint32_t tid = threadIdx.x;
+  __shared__ uint64_t s_q[kTThreads / 64][64 * kTWords];  // per wave: the words it searches
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint64_t lt = (1ull << lane) - 1;
+  const RelocDev& R = a.reloc;
   const uint32_t units = *a.tslot_count * kTUnitsPerTile;
   for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
     const uint32_t slot = a.tslots[u / kTUnitsPerTile];
@@ -1385,7 +1390,51 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
         }
       }
     }
-    reloc_batch<kTWords>(a.reloc, v, r, m);
+    // The whole words inside the table's range need an interval search:
+    // about a quarter of them on the presets (the pointers).  Each wave
+    // compacts its words to search in LDS, searches them kTSearch per lane
+    // in lockstep, and every lane reads its results back, so no lane holds
+    // line registers for words that need no search.
+    uint32_t need = 0;
+    if (R.n != 0) {
+#pragma unroll
+      for (uint32_t q = 0; q < kTWords; ++q)
+        if (((m >> q) & 1) && v[q] >= R.lo_min && (R.policy ? v[q] <= R.hi_max : v[q] < R.hi_max)) need |= 1u << q;
+    }
+    uint64_t* sq = s_q[tid >> 6];
+    uint32_t rank[kTWords], cnt = 0;
+#pragma unroll
+    for (uint32_t q = 0; q < kTWords; ++q) {
+      const uint64_t mk = __ballot((need >> q) & 1);
+      rank[q] = cnt + (uint32_t)__popcll(mk & lt);
+      if ((need >> q) & 1) sq[rank[q]] = v[q];
+      cnt += (uint32_t)__popcll(mk);
+    }
+    // The wave's own LDS words: its writes precede its reads in program order.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t b = 0; b < cnt; b += 64 * kTSearch) {
+      uint64_t x[kTSearch], y[kTSearch];
+      uint32_t mm = 0;
+#pragma unroll
+      for (uint32_t k = 0; k < kTSearch; ++k) {
+        const uint32_t i = b + 64 * k + lane;
+        x[k] = i < cnt ? sq[i] : 0;
+        mm |= (i < cnt ? 1u : 0u) << k;
+      }
+      reloc_batch<kTSearch>(R, x, y, mm);
+#pragma unroll
+      for (uint32_t k = 0; k < kTSearch; ++k) {
+        const uint32_t i = b + 64 * k + lane;
+        if (i < cnt) sq[i] = y[k];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (uint32_t q = 0; q < kTWords; ++q) r[q] = ((need >> q) & 1) ? sq[rank[q]] : v[q];
     uint64_t* img_out = a.image + sd.word_base;
     uint64_t* live_out = a.live + sd.word_base;
 #pragma unroll
@@ -1397,12 +1446,13 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
       }
     }
   }
-  // The collision report, one graph per workgroup in turn (the digests are
+  // The collision report, one graph per workgroup in turn, from the last
+  // workgroup down (the first ones hold the template units; the digests are
   // final after the node pass): a graph below this graph's template whose
   // key has the same CRC-64/XZ and length.  Its key bytes differ, or it
   // would be the template (grouping is by exact bytes).
   if (a.explicit_template) return;
-  for (uint32_t g = blockIdx.x; g < a.num_graphs; g += gridDim.x) {
+  for (uint32_t g = gridDim.x - 1 - blockIdx.x; g < a.num_graphs; g += gridDim.x) {
     const uint32_t t = a.template_of[g];
     const uint64_t dg = a.digests[4ull * g];
     const uint64_t Lg = a.graphs[g].sec_size[FDY_SEC_TOPOLOGY_KEY];
