@@ -177,43 +177,44 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
   if (tid == 0) __hip_atomic_store(a.key_hash + i, hi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   uint32_t from = 0, tmpl = i;
+  const uint64_t hiw = ((uint64_t)__shfl((uint32_t)(hi >> 32), 0, 64) << 32) | __shfl((uint32_t)hi, 0, 64);
   for (;;) {
-    if (tid < 64) {
-      const uint64_t hiw = ((uint64_t)__shfl((uint32_t)(hi >> 32), 0, 64) << 32) | __shfl((uint32_t)hi, 0, 64);
-      uint32_t found = i;
-      for (uint32_t base = from; base < i && found == i; base += 64) {
-        const uint32_t j = base + lane;
-        const bool in = j < i;
-        uint64_t hj = in ? __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        const uint64_t Lj = in ? a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] : ~0ull;
-        // Hashes of this restore carry its epoch; wait (bounded) for the rest.
-        for (uint32_t spin = 0; __ballot(in && (hj & 0xFFFF) != a.epoch) && spin < kHashWaitSpins; ++spin) {
-          __builtin_amdgcn_s_sleep(2);
-          if (in && (hj & 0xFFFF) != a.epoch)
-            hj = __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        // Still missing: the wave hashes those keys itself, one at a time.
-        uint64_t miss = __ballot(in && (hj & 0xFFFF) != a.epoch);
-        while (miss) {
-          const uint32_t l = (uint32_t)__ffsll((long long)miss) - 1;
-          miss &= miss - 1;
-          const DevGraph& Gj = a.graphs[base + l];
-          uint64_t y = key_share(a.img + Gj.sec_off[FDY_SEC_TOPOLOGY_KEY], Gj.sec_size[FDY_SEC_TOPOLOGY_KEY], lane, 64);
-#pragma unroll
-          for (int d = 32; d >= 1; d >>= 1) y ^= shfl_down64(y, d);
-          const uint64_t yl = ((uint64_t)__shfl((uint32_t)(y >> 32), 0, 64) << 32) | __shfl((uint32_t)y, 0, 64);
-          if (lane == l) hj = tag_hash(yl, a.epoch);
-        }
-        const bool m = in && (hj >> 16) == (hiw >> 16) && Lj == L;
-        const uint64_t mk = __ballot(m);
-        if (mk) found = base + (uint32_t)__ffsll((long long)mk) - 1;
-      }
-      if (tid == 0) {
-        s_found = found;
-        s_differs = 0;
-      }
+    // Every thread takes one lower graph per step (kGroupThreads per step);
+    // the lowest match wins.
+    if (tid == 0) {
+      s_found = i;
+      s_differs = 0;
     }
     __syncthreads();
+    for (uint32_t base = from; base < i; base += kGroupThreads) {
+      const uint32_t j = base + tid;
+      const bool in = j < i;
+      uint64_t hj = in ? __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      const uint64_t Lj = in ? a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] : ~0ull;
+      // Hashes of this restore carry its epoch; wait (bounded) for the rest.
+      for (uint32_t spin = 0; __ballot(in && (hj & 0xFFFF) != a.epoch) && spin < kHashWaitSpins; ++spin) {
+        __builtin_amdgcn_s_sleep(2);
+        if (in && (hj & 0xFFFF) != a.epoch)
+          hj = __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      // Still missing: the wave hashes those keys itself, one at a time.
+      uint64_t miss = __ballot(in && (hj & 0xFFFF) != a.epoch);
+      while (miss) {
+        const uint32_t l = (uint32_t)__ffsll((long long)miss) - 1;
+        miss &= miss - 1;
+        const DevGraph& Gj = a.graphs[base + (tid & ~63u) + l];
+        uint64_t y = key_share(a.img + Gj.sec_off[FDY_SEC_TOPOLOGY_KEY], Gj.sec_size[FDY_SEC_TOPOLOGY_KEY], lane, 64);
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) y ^= shfl_down64(y, d);
+        const uint64_t yl = ((uint64_t)__shfl((uint32_t)(y >> 32), 0, 64) << 32) | __shfl((uint32_t)y, 0, 64);
+        if (lane == l) hj = tag_hash(yl, a.epoch);
+      }
+      const bool m = in && (hj >> 16) == (hiw >> 16) && Lj == L;
+      const uint64_t mk = __ballot(m);
+      if (mk && lane == 0) atomicMin(&s_found, base + (tid & ~63u) + (uint32_t)__ffsll((long long)mk) - 1);
+      __syncthreads();
+      if (s_found != i) break;  // uniform over the workgroup
+    }
     const uint32_t j = s_found;
     if (j == i) break;  // uniform over the workgroup
     const uint8_t* pj = a.img + a.graphs[j].sec_off[FDY_SEC_TOPOLOGY_KEY];
