@@ -136,8 +136,7 @@ def bench_switches(arch, s, stream, torch, np):
     offs = arch.override_offsets().astype(np.int64)
     groups = arch.groups()
     count = np.diff(offs)
-    for g in seq[:100]:
-        arch.switch(int(g), stream)
+    arch.switch_sequence(seq[:100], stream)
     torch.cuda.synchronize()
     # Bytes: 16-B record read + 8-B word write for the outgoing and the incoming set.
     current = {int(t): int(t) for t in np.unique(groups)}
@@ -149,13 +148,27 @@ def bench_switches(arch, s, stream, torch, np):
         if current[t] != int(g):
             b_s += 24 * (int(count[current[t]]) + int(count[g]))
             current[t] = int(g)
+    # The whole sequence in one call (fdy_switch_sequence: one check and one
+    # device selection, then one scatter launch per switch).
     t0 = time.perf_counter()
+    arch.switch_sequence(seq, stream)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    # The same switches one call each (back to the same start state first).
+    for t in current:
+        current[t] = t
+    arch.switch_sequence(np.asarray(sorted(current)), stream)
+    for g in seq[:100]:
+        arch.switch(int(g), stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     for g in seq:
         arch.switch(int(g), stream)
     torch.cuda.synchronize()
-    sec = time.perf_counter() - t0
+    sec1 = time.perf_counter() - t1
     return {"switches": SWITCHES, "seconds": round(sec, 4), "switches_per_s": round(SWITCHES / sec, 1),
-            "scatter_bytes": b_s, "GBps": round(b_s / sec / 1e9, 3)}
+            "scatter_bytes": b_s, "GBps": round(b_s / sec / 1e9, 3),
+            "one_call_each_switches_per_s": round(SWITCHES / sec1, 1)}
 
 
 def _progress(msg: str) -> None:

@@ -186,6 +186,7 @@ _SIGS = {
                               C.POINTER(C.c_int64), C.c_uint8, C.c_uint8]),
     "fdy_cugraph_save_binary": (C.c_int, [C.c_char_p, C.c_char_p, C.c_uint64]),
     "fdy_switch": (C.c_int, [_vp, C.c_uint32, _vp]),
+    "fdy_switch_sequence": (C.c_int, [_vp, u32p, C.c_uint64, _vp]),
     "fdy_get_live": (C.c_int, [_vp, _vp, C.c_uint32, u64p, C.c_uint64, u32p, C.c_uint64, u32p]),
     "fdy_reloc_plan_create": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, C.POINTER(_vp)]),
     "fdy_reloc_plan_destroy": (C.c_int, [_vp]),

@@ -137,7 +137,7 @@ int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t);
 // its current graph to g, and record g as current.  With `dirty` (device
 // memory, one byte per node of the group) the scatter also marks the nodes
 // whose params, descriptor or layout change.
-int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty);
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty, bool set_device = true);
 // Switch of a group that has a bound group graph (graph.hip).
 int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* stats);
 

@@ -83,6 +83,18 @@ struct SwitchArgs {
 };
 hipError_t launch_switch(const SwitchArgs& a, hipStream_t s);
 
+// Up to kSwitchBatch switches of different groups in one launch.
+constexpr uint32_t kSwitchBatch = 16;
+struct SwitchBatch {
+  SwitchArgs sw[kSwitchBatch];
+  uint32_t end[kSwitchBatch];  // running block counts
+  uint32_t n;
+};
+static_assert(sizeof(SwitchBatch) <= 2048, "a switch batch travels as kernel arguments");
+// Blocks of one switch's scatter (the same split as launch_switch's).
+uint32_t switch_blocks(const SwitchArgs& a);
+hipError_t launch_switch_many(const SwitchBatch& b, hipStream_t s);
+
 // Copy of the dirty nodes' live words (or of every node's) into the host
 // mirror of a group graph, with the dirty marks; clears the device marks.
 struct MirrorArgs {

@@ -1885,13 +1885,12 @@ constexpr uint32_t kSwitchSeg = 2048;     // target words held in LDS per block
 
 __device__ inline uint64_t switch_chunk_blocks(uint64_t n_cur) { return (n_cur + kSwitchThreads - 1) / kSwitchThreads; }
 
-__global__ __launch_bounds__(kSwitchThreads) void k_switch(SwitchArgs a) {
-  __shared__ uint32_t s_sample[kSwitchSamples];
-  __shared__ uint32_t s_seg[kSwitchSeg];
+__device__ __forceinline__ void switch_block(const SwitchArgs& a, uint32_t blk, uint32_t nblk, uint32_t* s_sample,
+                                             uint32_t* s_seg) {
   const uint32_t tid = threadIdx.x;
   const uint64_t cb = switch_chunk_blocks(a.n_cur);
-  if (blockIdx.x < cb) {
-    const uint64_t i = (uint64_t)blockIdx.x * kSwitchThreads + tid;
+  if (blk < cb) {
+    const uint64_t i = (uint64_t)blk * kSwitchThreads + tid;
     const bool have = i < a.n_cur;
     fdy_override r{};
     if (have) r = a.ovr_cur[i];
@@ -1902,8 +1901,8 @@ __global__ __launch_bounds__(kSwitchThreads) void k_switch(SwitchArgs a) {
     if (staged)
       for (uint64_t k = tid; k < ns; k += kSwitchThreads) s_sample[k] = a.ovr_new[k * kSwitchSample].word;
     // The block's word range: its first and last records' words.
-    const uint64_t last = min(a.n_cur, (uint64_t)(blockIdx.x + 1) * kSwitchThreads) - 1;
-    const uint32_t w_a = a.ovr_cur[(uint64_t)blockIdx.x * kSwitchThreads].word, w_b = a.ovr_cur[last].word;
+    const uint64_t last = min(a.n_cur, (uint64_t)(blk + 1) * kSwitchThreads) - 1;
+    const uint32_t w_a = a.ovr_cur[(uint64_t)blk * kSwitchThreads].word, w_b = a.ovr_cur[last].word;
     __syncthreads();
     // Target records with words in [w_a, w_b] lie in [beg, end).
     uint64_t beg = 0, end = a.n_new;
@@ -1963,8 +1962,8 @@ __global__ __launch_bounds__(kSwitchThreads) void k_switch(SwitchArgs a) {
     return;
   }
   const uint64_t lim = a.n_new > a.num_nodes ? a.n_new : a.num_nodes;
-  const uint64_t nb = gridDim.x - cb;
-  for (uint64_t i = (uint64_t)(blockIdx.x - cb) * kSwitchThreads + tid; i < lim; i += nb * kSwitchThreads) {
+  const uint64_t nb = nblk - cb;
+  for (uint64_t i = (uint64_t)(blk - cb) * kSwitchThreads + tid; i < lim; i += nb * kSwitchThreads) {
     if (i < a.n_new) {
       const fdy_override r = a.ovr_new[i];
       a.live[r.word] = r.value;
@@ -1978,6 +1977,23 @@ __global__ __launch_bounds__(kSwitchThreads) void k_switch(SwitchArgs a) {
       if (a.dirty && ((fn | a.flags_cur[i]) & (FDY_NODE_LAYOUT | FDY_NODE_DESC))) a.dirty[i] = 1;
     }
   }
+}
+
+__global__ __launch_bounds__(kSwitchThreads) void k_switch(SwitchArgs a) {
+  __shared__ uint32_t s_sample[kSwitchSamples];
+  __shared__ uint32_t s_seg[kSwitchSeg];
+  switch_block(a, blockIdx.x, gridDim.x, s_sample, s_seg);
+}
+
+// Switches of different groups in one launch (they touch disjoint live
+// images and node sources): switch k takes blocks [end[k-1], end[k]).
+__global__ __launch_bounds__(kSwitchThreads) void k_switch_many(SwitchBatch b) {
+  __shared__ uint32_t s_sample[kSwitchSamples];
+  __shared__ uint32_t s_seg[kSwitchSeg];
+  uint32_t k = 0;
+  while (k + 1 < b.n && b.end[k] <= blockIdx.x) ++k;
+  const uint32_t first = k ? b.end[k - 1] : 0u;
+  switch_block(b.sw[k], blockIdx.x - first, b.end[k] - first, s_sample, s_seg);
 }
 
 // ---- host mirror of a group graph's live image ---------------------------
@@ -2128,6 +2144,21 @@ hipError_t launch_switch(const SwitchArgs& a, hipStream_t s) {
   if (wb == 0) wb = 1;
   if (cb + wb > 0x7FFFFFFFull) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_switch, dim3((uint32_t)(cb + wb)), dim3(kSwitchThreads), 0, s, a);
+  return hipGetLastError();
+}
+
+uint32_t switch_blocks(const SwitchArgs& a) {
+  const uint64_t cb = (a.n_cur + kSwitchThreads - 1) / kSwitchThreads;  // switch_chunk_blocks
+  const uint64_t lim = a.n_new > a.num_nodes ? a.n_new : a.num_nodes;
+  uint64_t wb = (lim + kSwitchThreads - 1) / kSwitchThreads;
+  if (wb > 2048) wb = 2048;
+  if (wb == 0) wb = 1;
+  return (uint32_t)std::min<uint64_t>(cb + wb, 0x7FFFFFFFull);
+}
+
+hipError_t launch_switch_many(const SwitchBatch& b, hipStream_t s) {
+  if (b.n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_switch_many, dim3(b.end[b.n - 1]), dim3(kSwitchThreads), 0, s, b);
   return hipGetLastError();
 }
 

@@ -362,11 +362,11 @@ int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t_out) {
   return FDY_OK;
 }
 
-int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty) {
+// The scatter that moves the live image of g's group from its current graph
+// to g.
+SwitchArgs switch_args(const fdy_archive* a, uint32_t g, uint8_t* dirty) {
   const uint32_t t = a->h_tmpl[g];
   const uint32_t c = a->h_current[t];
-  if (c == g) return FDY_OK;
-  FDY_HIP(hipSetDevice(a->device));
   SwitchArgs w{};
   w.ovr_cur = a->ovr.as<fdy_override>() + ovr_base(a, c);
   w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
@@ -381,6 +381,14 @@ int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty) {
   w.num_nodes = a->graphs[t].num_nodes;
   w.target = g;
   w.tmpl = t;
+  return w;
+}
+
+int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty, bool set_device) {
+  const uint32_t t = a->h_tmpl[g];
+  if (a->h_current[t] == g) return FDY_OK;
+  if (set_device) FDY_HIP(hipSetDevice(a->device));
+  const SwitchArgs w = switch_args(a, g, dirty);
   FDY_HIP(launch_switch(w, s));
   a->h_current[t] = g;
   return FDY_OK;
@@ -874,7 +882,61 @@ int fdy_switch(fdy_archive* a, uint32_t g, void* stream) {
   if (!rc) rc = check_switchable(a, g, &t);
   if (rc) return rc;
   if (a->bound.size() == a->G && a->bound[t]) return group_graph_select(a->bound[t], g, s, nullptr);
-  return enqueue_switch(a, g, s, nullptr);
+  return enqueue_switch(a, g, s, nullptr, true);
+}
+
+int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  if (n && !targets) return err(FDY_E_INVALID, "null target list");
+  int rc = ensure_cache(a, s);
+  if (rc) return rc;
+  for (uint64_t i = 0; i < n; ++i) {
+    uint32_t t = 0;
+    rc = check_graph(a, targets[i]);
+    if (!rc) rc = check_switchable(a, targets[i], &t);
+    if (rc) return rc;
+  }
+  FDY_HIP(hipSetDevice(a->device));
+  // Consecutive switches of different groups touch disjoint live images and
+  // node sources: up to kSwitchBatch of them share one launch.  A switch of
+  // a group already in the batch, or of a group whose live image a group
+  // graph holds, first launches the batch so far (stream order keeps the
+  // sequence's order where it matters).
+  const bool bound = a->bound.size() == a->G;
+  SwitchBatch b{};
+  std::vector<uint32_t> in_batch;
+  auto flush = [&]() -> int {
+    if (b.n) FDY_HIP(launch_switch_many(b, s));
+    b.n = 0;
+    in_batch.clear();
+    return FDY_OK;
+  };
+  for (uint64_t i = 0; i < n; ++i) {
+    const uint32_t g = targets[i];
+    const uint32_t t = a->h_tmpl[g];
+    if (bound && a->bound[t]) {
+      rc = flush();
+      if (!rc) rc = group_graph_select(a->bound[t], g, s, nullptr);
+      if (rc) return rc;
+      continue;
+    }
+    if (a->h_current[t] == g) continue;
+    const SwitchArgs w = switch_args(a, g, nullptr);
+    const uint64_t blocks = switch_blocks(w);
+    if (blocks >= 0x7FFFFFFFull) return err(FDY_E_CAPACITY, "override sets too large for one switch launch");
+    if (b.n == kSwitchBatch || std::find(in_batch.begin(), in_batch.end(), t) != in_batch.end() ||
+        (b.n && b.end[b.n - 1] + blocks >= 0x7FFFFFFFull)) {
+      rc = flush();
+      if (rc) return rc;
+    }
+    b.sw[b.n] = w;
+    b.end[b.n] = (b.n ? b.end[b.n - 1] : 0u) + (uint32_t)blocks;
+    ++b.n;
+    in_batch.push_back(t);
+    a->h_current[t] = g;
+  }
+  return flush();
 }
 
 int fdy_get_live(fdy_archive* a, void* stream, uint32_t t, uint64_t* words, uint64_t cap, uint32_t* node_src,

@@ -204,6 +204,11 @@ class Archive:
     def switch(self, g: int, stream=None) -> None:
         check(restore_lib().fdy_switch(self._h, g, _stream(stream)))
 
+    def switch_sequence(self, targets, stream=None) -> None:
+        """fdy_switch for each target in order, checked and enqueued in one call."""
+        t = np.ascontiguousarray(np.asarray(targets, dtype=np.uint32))
+        check(restore_lib().fdy_switch_sequence(self._h, t.ctypes.data_as(_lib.u32p), t.size, _stream(stream)))
+
     def live(self, template: int, stream=None) -> tuple[np.ndarray, np.ndarray, int]:
         words = self.param_image(template, stream).size
         nodes = self.node_flags(template, stream).size

@@ -231,6 +231,15 @@ int fdy_get_section(fdy_archive* a, uint32_t graph, uint32_t section, uint8_t* o
  * every node without FDY_NODE_LAYOUT.  Counterpart of the all-node re-set
  * in csrc/CUDAGraph.cpp:340-461.  Enqueued on `stream`; no-op if current. */
 int fdy_switch(fdy_archive* a, uint32_t graph, void* stream);
+
+/* fdy_switch for each of targets[0..n) in order, enqueued on `stream`: the
+ * same end state and the same scatter work per switch, with the checks and
+ * the device selection done once for the whole sequence instead of per call
+ * (for callers that switch graphs many times between launches, and for
+ * measuring sustained switches).  Every target is checked before any switch
+ * is enqueued; on an error nothing is enqueued.  Counterpart of n calls of
+ * the on-demand branch of csrc/CUDAGraph.cpp:330-461. */
+int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, void* stream);
 /* Live state of the group whose template is `template_graph`.  Synchronizes.
  * node_src[n] = graph whose own image supplies node n (template unless the
  * node has a layout or descriptor difference). */

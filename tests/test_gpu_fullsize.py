@@ -86,8 +86,11 @@ def test_1024_graph_archive_switch_sequence(c5):
     groups = arch.groups()
     seq = synth.switch_sequence(p.seed, s.num_graphs, 10_000)
     print(f"[case] preset5-full: {len(seq)} seeded switches", flush=True)
-    for g in seq:
+    # The first half one call each, the second half in one sequence call
+    # (switches of different groups batched into shared launches).
+    for g in seq[:5000]:
         arch.switch(int(g))
+    arch.switch_sequence(seq[5000:])
     last = {int(t): int(t) for t in set(groups.tolist())}
     for g in seq:
         last[int(groups[g])] = int(g)

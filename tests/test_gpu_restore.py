@@ -152,6 +152,34 @@ def test_switch_sequence(cuda):
             np.testing.assert_array_equal(words[tw[n]:tw[n + 1]], img[gw[n]:gw[n + 1]])
 
 
+def test_switch_sequence_in_one_call(cuda):
+    # The same seeded targets through fdy_switch_sequence, in chunks (so the
+    # sequence continues from a live state left by an earlier call), against
+    # the oracle after every chunk; a bad target anywhere refuses the whole
+    # call and enqueues nothing.
+    p = synth.preset(2, num_graphs=16, nodes_per_graph=250, num_groups=2, layout_var_pct=5)
+    _print_case("switch-sequence", p)
+    s = synth.SynthArchive(p)
+    arch, ref = gpu_and_oracle(s)
+    seq = synth.switch_sequence(0x5EED, s.num_graphs, 200)
+    templates = sorted(set(ref.groups().tolist()))
+    for k in range(0, 200, 50):
+        chunk = seq[k:k + 50]
+        arch.switch_sequence(chunk)
+        for g in chunk.tolist():
+            ref.switch(g)
+        for t in templates:
+            assert_live_matches(arch, ref, t)
+    before = {t: arch.live(t) for t in templates}
+    with pytest.raises(FoundryError):
+        arch.switch_sequence([int(seq[0]), s.num_graphs])
+    for t in templates:
+        w, src, cur = arch.live(t)
+        assert cur == before[t][2]
+        np.testing.assert_array_equal(w, before[t][0])
+    arch.switch_sequence([])  # nothing to do
+
+
 def test_graph_longer_than_the_chunk_shift_table(cuda):
     # 66,000 nodes = 258 chunks of 256: the first two chunks of each graph are
     # shifted past the node-type and kernel-entry streams without the table.
