@@ -180,7 +180,7 @@ def _pct(v, q):
     return v[min(len(v) - 1, int(q * (len(v) - 1) + 0.5))] if v else None
 
 
-def bench_group_graphs(preset, torch, np, stream):
+def bench_group_graphs(preset, torch, np, stream, diff_node_pct=0):
     """Group graphs (one hipGraph + exec per topology group) of an archive of
     the same shape whose kernel nodes all resolve to one sink kernel: host
     time to build each group's graph from its restored template, host time
@@ -188,7 +188,9 @@ def bench_group_graphs(preset, torch, np, stream):
     changed nodes) once every graph has been selected, and, on the same
     execs, the re-set of every node that the reference performs on each
     switch.  The graphs are built and switched,
-    never launched (their saved pointers are synthetic)."""
+    never launched (their saved pointers are synthetic).  With diff_node_pct
+    the differing words (and batch-size-dependent grids) sit in that percent
+    of the kernel nodes only, at the same overall fraction of differing words."""
     from foundry_amd import synth
     from foundry_amd.graph import GroupGraph, Registry
     from foundry_amd.restore import Archive
@@ -201,6 +203,7 @@ def bench_group_graphs(preset, torch, np, stream):
     if preset == 3:
         params.memcpy_pct = 0  # a memcpy node is built from real device pointers; these are synthetic
     params.sink_hash = reg.add_file(PROBE_CO)
+    params.diff_node_pct = diff_node_pct
     s = synth.SynthArchive(params)
     arch = Archive.from_synth(s)
     arch.set_relocation(*s.intervals())
@@ -240,6 +243,7 @@ def bench_group_graphs(preset, torch, np, stream):
     return {
         "sample": f"{s.num_graphs} graphs x {nodes} nodes, {len(ggs)} groups"
                   + (" (no memcpy nodes)" if preset == 3 else "")
+                  + (f", differences in {diff_node_pct}% of the kernel nodes" if diff_node_pct else "")
                   + f"; {len(sel_us)} switches that changed the exec out of {GRAPH_SWITCHES} seeded targets",
         "build_ms_per_group": round(statistics.mean(build_ms), 3),
         "instantiate_ms_per_group": round(statistics.mean(inst_ms), 3),
@@ -396,6 +400,9 @@ def main():
     if args.preset in (1, 2, 3, 5) and not args.no_group_graphs:
         result["group_graph"] = bench_group_graphs(args.preset, torch, np, stream)
         _progress("group graphs timed")
+        if args.preset == 2:
+            result["group_graph_few_nodes"] = bench_group_graphs(args.preset, torch, np, stream, diff_node_pct=10)
+            _progress("group graphs with differences in few nodes timed")
 
     if not args.no_cpu_baseline:
         import oracle

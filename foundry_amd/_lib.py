@@ -152,6 +152,8 @@ class SynthParams(C.Structure):
         ("num_words", C.c_uint64),
         ("boundary_frac", C.c_double),
         ("sink_hash", C.c_uint64),
+        ("diff_node_pct", C.c_uint32),
+        ("pad_", C.c_uint32),
     ]
 
 

@@ -58,6 +58,7 @@ struct NodeLayout {
   bool grid_bs = false;
   bool extra = false;
   bool layout_var = false;
+  bool diff_ok = true;  // differing words may fall in this node
   std::vector<uint32_t> sizes[2];  // [0] base layout, [1] variant used by large batch sizes
   std::vector<uint8_t> kinds[2];   // per 8-byte word of the padded blob
   std::vector<uint64_t> base[2];   // group-base words
@@ -255,6 +256,11 @@ Group make_group(const fdy_synth_params& p, uint32_t g, const Intervals& iv) {
     L.grid_bs = r.below(100) < p.grid_bs_pct;
     L.extra = r.below(100) < p.extra_style_pct;
     L.layout_var = r.below(100) < p.layout_var_pct;
+    if (p.diff_node_pct) {  // no draw when 0: presets unchanged
+      L.diff_ok = r.below(100) < p.diff_node_pct;
+      L.grid_bs = L.grid_bs && L.diff_ok;  // all batch-size dependence sits in the same nodes
+      L.layout_var = L.layout_var && L.diff_ok;
+    }
     if (n == 0 && p.num_groups > 1 && !p.sink_hash) L.cluster_x = g + 1;
     uint32_t lo = std::max<uint32_t>(8, p.min_blob_bytes) / 8, hi = std::max<uint32_t>(lo * 8, p.max_blob_bytes) / 8;
     for (int v = 0; v < 2; ++v) {
@@ -290,7 +296,10 @@ std::vector<uint8_t> make_graph(const fdy_synth_params& p, const Group& grp, uin
   double rate = p.diff_lo + (p.diff_hi - p.diff_lo) * r.unit();
   uint32_t run_lo = p.run_min_bytes / 8, run_hi = std::max(p.run_min_bytes, p.run_max_bytes) / 8;
   double mean_run = run_lo ? 0.5 * (run_lo + run_hi) : 1.0;
-  double p_start = rate / mean_run;
+  // Differing words concentrated in diff_node_pct % of the kernel nodes keep
+  // the graph's overall fraction of differing words.
+  const double krate = p.diff_node_pct ? std::min(1.0, rate * 100.0 / p.diff_node_pct) : rate;
+  double p_start = krate / mean_run;
   bool large_bs = gidx > group_first && (gidx - group_first) * 2 >= 1;  // every member but the base
   fdy::GraphSpec spec;
   spec.nodes.resize(grp.nodes.size());
@@ -352,14 +361,14 @@ std::vector<uint8_t> make_graph(const fdy_synth_params& p, const Group& grp, uin
     for (uint32_t sz : sizes) {
       for (uint32_t off = 0; off < sz; off += 8, ++w) {
         uint64_t val = base[w];
-        if (!is_base) {
+        if (!is_base && L.diff_ok) {
           bool hit;
           if (run_lo) {
             if (!run_left && r.unit() < p_start) run_left = (uint32_t)r.range(run_lo, run_hi);
             hit = run_left > 0;
             if (run_left) --run_left;
           } else {
-            hit = r.unit() < rate;
+            hit = r.unit() < krate;
           }
           if (hit) {
             uint64_t nv = draw_word(r, kinds[w], iv);

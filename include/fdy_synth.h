@@ -64,6 +64,10 @@ typedef struct fdy_synth_params {
   uint64_t sink_hash;        /* nonzero: every kernel node names kernel "fdy_sink" of the code object
                                 with this hash, and groups differ by a kernel/empty pattern in nodes
                                 1..6 instead of by cluster dims (graphs a gfx950 group graph can build) */
+  uint32_t diff_node_pct;    /* 0: differing words may fall in any kernel node; else only in this % of the
+                                kernel nodes, the same ones in every graph of a group (arguments that
+                                depend on the batch size live in a few kernels) */
+  uint32_t pad_;
 } fdy_synth_params;
 
 typedef struct fdy_synth fdy_synth;

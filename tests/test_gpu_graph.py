@@ -258,15 +258,18 @@ def test_unresolvable_templates_are_refused_before_launch(env):
         arch.close()
 
 
-def test_synthetic_groups_build_and_switch_without_launch(env):
+@pytest.mark.parametrize("diff_node_pct", [0, 10])
+def test_synthetic_groups_build_and_switch_without_launch(env, diff_node_pct):
     """Group graphs of a synthetic decode-style archive whose kernels all
     resolve to the probe's sink kernel (built and switched, never launched:
     the saved pointers are synthetic).  Every switch re-sets exactly the
-    nodes the override sets and flags name."""
+    nodes the override sets and flags name; with the differences confined to
+    10% of the kernel nodes, a switch re-sets only those."""
     from foundry_amd import synth
 
     p = synth.preset(2, num_graphs=24, num_groups=3, nodes_per_graph=300, num_intervals=2000)
     p.sink_hash = env.bhash
+    p.diff_node_pct = diff_node_pct
     s = synth.SynthArchive(p)
     arch = Archive.from_synth(s)
     arch.set_relocation(*s.intervals())
@@ -289,6 +292,8 @@ def test_synthetic_groups_build_and_switch_without_launch(env):
         st = ggs[t].select(g, env.stream)
         want = 0 if current[t] == g else len(touched(current[t]) | touched(g))
         assert st["nodes_reset"] == want, (current[t], g)
+        if diff_node_pct:
+            assert want <= 75, want  # about 30 of 300 nodes may differ
         current[t] = g
     full = ggs[temps[0]].reset_all(env.stream)
     assert full["nodes_reset"] == 300

@@ -55,3 +55,30 @@ def test_sink_mode_names_one_kernel_and_keeps_groups_apart():
                 assert n.kernel.kna_flags == 0  # no cluster dims
     ref = oracle.Restore(imgs, s.intervals())
     assert len(set(int(t) for t in ref.groups())) == 8
+
+
+def test_differences_confined_to_a_few_nodes():
+    """diff_node_pct=10: the members' differing words fall in about a tenth
+    of the kernel nodes, the same ones in every member, and the overall
+    fraction of differing words stays about that of the unconfined archive."""
+    from oracle import Restore
+
+    def node_sets(pct):
+        p = synth.preset(2, num_graphs=12, num_groups=1, nodes_per_graph=400, num_intervals=500)
+        p.diff_node_pct = pct
+        s = synth.SynthArchive(p)
+        ref = Restore([s.image(g) for g in range(12)], s.intervals(), threads=4)
+        sets = []
+        for g in range(1, 12):
+            nodes = set(ref.overrides(g)["node"].tolist())
+            nodes |= set(np.flatnonzero(ref.node_flags(g)).tolist())
+            sets.append(nodes)
+        records = sum(len(ref.overrides(g)["node"]) for g in range(1, 12))
+        return sets, records
+
+    wide, r_wide = node_sets(0)
+    few, r_few = node_sets(10)
+    union = set().union(*few)
+    assert 15 <= len(union) <= 70, len(union)  # about 40 of 400
+    assert min(len(x) for x in wide) > 200
+    assert 0.5 < r_few / r_wide < 2.0, (r_few, r_wide)
