@@ -1703,7 +1703,7 @@ __device__ __forceinline__ void window_node(const uint2* s_gt, uint32_t nwin, ui
   }
 }
 
-__global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
+__global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
   static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
   // Per wave: {first graph word, first template word} of its window's nodes.
@@ -1734,6 +1734,28 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   uint32_t start[kSubsPerSlot];  // exclusive prefix of the candidate counts, the same in every lane
 #pragma unroll
   for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __shfl(incl - cnt, q, 64) & 0xFFFFu;
+  // Batch b's K candidates per lane, loaded unconditionally (a list index
+  // past the end reads the first candidate and is masked off later) so that
+  // they are issued together rather than each behind its own branch.  The
+  // first batch is loaded before the bounds and the node window, the next
+  // one before the current one's searches, so no load waits alone.
+  const Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  auto load_batch = [&](uint32_t b, Candidate* cand) {
+#pragma unroll
+    for (uint32_t kk = 0; kk < K; ++kk) {
+      const uint32_t i0 = b + 64 * kk + lane;  // list index
+      const uint32_t i = i0 < total ? i0 : 0u;
+      uint32_t q = 0;
+#pragma unroll
+      for (uint32_t s = 1; s < kSubsPerSlot; ++s) q += start[s] <= i;
+      uint32_t sq = start[0];
+#pragma unroll
+      for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
+      cand[kk] = base[(uint64_t)q * kSubWords + (i - sq)];
+    }
+  };
+  Candidate cur[K];
+  load_batch(0, cur);
   // A slot with candidates holds words, so it starts at k * kTileWords: its
   // index in the graph, and the graph's first slot, follow.  The earlier
   // slots' bounds: the high halves of their sub-range counts, four to a
@@ -1764,38 +1786,22 @@ __global__ __launch_bounds__(kSThreads) void k_diff_s(RestoreArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   uint64_t* img_out = a.image + sd.word_base;
-  const Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
   fdy_override* rec = a.ovr + sd.word_base + before;
   const uint64_t lt = (1ull << lane) - 1;
   uint32_t run = 0;
   for (uint32_t b = 0; b < total; b += kSBatch) {
     uint64_t raw[K], tval[K], res[K];
     uint32_t word[K], fl[K], m = 0;
-    // The K candidates' loads are unconditional (a list index past the end
-    // reads the first candidate, then is masked off), so they are issued
-    // together rather than each behind its own branch and wait.
-    Candidate cand[K];
-#pragma unroll
-    for (uint32_t kk = 0; kk < K; ++kk) {
-      const uint32_t i0 = b + 64 * kk + lane;  // list index
-      const uint32_t i = i0 < total ? i0 : 0u;
-      uint32_t q = 0;
-#pragma unroll
-      for (uint32_t s = 1; s < kSubsPerSlot; ++s) q += start[s] <= i;
-      uint32_t sq = start[0];
-#pragma unroll
-      for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
-      cand[kk] = base[(uint64_t)q * kSubWords + (i - sq)];
-    }
 #pragma unroll
     for (uint32_t kk = 0; kk < K; ++kk) {
       const bool in = b + 64 * kk + lane < total;
-      raw[kk] = in ? cand[kk].raw : 0;
-      tval[kk] = in ? cand[kk].tval : 0;
-      word[kk] = in ? cand[kk].word : 0;
-      fl[kk] = in ? cand[kk].flags : 0;
+      raw[kk] = in ? cur[kk].raw : 0;
+      tval[kk] = in ? cur[kk].tval : 0;
+      word[kk] = in ? cur[kk].word : 0;
+      fl[kk] = in ? cur[kk].flags : 0;
       if (fl[kk] & kCandReloc) m |= 1u << kk;
     }
+    if (b + kSBatch < total) load_batch(b + kSBatch, cur);  // uniform over the wave
     reloc_batch<K>(a.reloc, raw, res, m);
     // The member pass stored each candidate's raw word; only the words the
     // relocation moved are stored again (a scattered 8-byte store costs a
