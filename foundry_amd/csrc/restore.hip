@@ -82,16 +82,16 @@ struct HostStage {
 };
 
 int build_reloc_index(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
-                      HostIndex* out) {
+                      HostIndex* out, uint64_t root_lines_per_interval = kRootLinesPerInterval) {
   std::string why;
-  const int rc = build_reloc_index(lo, hi, nlo, n, policy, out, &why);
+  const int rc = build_reloc_index(lo, hi, nlo, n, policy, out, &why, root_lines_per_interval);
   return rc ? err(rc, why) : FDY_OK;
 }
 
 int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
-                     RelocPlan* out) {
+                     RelocPlan* out, uint64_t root_lines_per_interval = kRootLinesPerInterval) {
   HostIndex x;
-  int rc = build_reloc_index(lo, hi, nlo, n, policy, &x);
+  int rc = build_reloc_index(lo, hi, nlo, n, policy, &x, root_lines_per_interval);
   out->dev = x.dev;
   if (rc || n == 0) return rc;
   rc = dev_alloc(out->line, x.line.size() * sizeof(RelocLine), "interval index lines");
@@ -1078,7 +1078,7 @@ int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t
   if (!out) return err(FDY_E_INVALID, "null output");
   auto p = std::make_unique<fdy_reloc_plan>();
   (void)hipGetDevice(&p->device);
-  int rc = build_reloc_plan(lo, hi, nlo, n, policy, &p->plan);
+  int rc = build_reloc_plan(lo, hi, nlo, n, policy, &p->plan, kPlanRootLinesPerInterval);
   if (rc) return rc;
   *out = p.release();
   return FDY_OK;

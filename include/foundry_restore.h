@@ -247,7 +247,10 @@ int fdy_get_live(fdy_archive* a, void* stream, uint32_t template_graph, uint64_t
                  uint32_t* node_src, uint64_t node_cap, uint32_t* current_graph);
 
 /* Standalone relocation of packed u64 words already in device memory
- * (in and out may alias).  The plan holds the interval search structure. */
+ * (in and out may alias).  The plan holds the interval search structure:
+ * about 16 root lines of 64 B per interval (2M intervals: about 2 GB of device
+ * memory), built once for many relocations, against about 2 per interval for
+ * the index beside a restored archive. */
 int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
                           uint32_t policy, fdy_reloc_plan** out);
 int fdy_reloc_plan_destroy(fdy_reloc_plan* p);

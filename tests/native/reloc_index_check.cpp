@@ -32,8 +32,8 @@ static std::vector<uint64_t> read_all(const char* path) {
 }
 
 int main(int argc, char** argv) {
-  if (argc != 4) {
-    std::fprintf(stderr, "usage: %s TABLE WORDS OUT\n", argv[0]);
+  if (argc != 4 && argc != 5) {
+    std::fprintf(stderr, "usage: %s TABLE WORDS OUT [ROOT_LINES_PER_INTERVAL]\n", argv[0]);
     return 2;
   }
   const std::vector<uint64_t> t = read_all(argv[1]);
@@ -50,7 +50,8 @@ int main(int argc, char** argv) {
 
   HostIndex x;
   std::string why;
-  const int rc = build_reloc_index(lo, hi, nlo, n, policy, &x, &why);
+  const uint64_t per = argc == 5 ? std::strtoull(argv[4], nullptr, 10) : kRootLinesPerInterval;
+  const int rc = build_reloc_index(lo, hi, nlo, n, policy, &x, &why, per);
   if (rc) {
     std::printf("{\"error\": %d}\n", rc);
     std::fprintf(stderr, "%s\n", why.c_str());

@@ -20,12 +20,13 @@ from foundry_amd import synth
 CHECK = os.path.join(os.path.dirname(os.path.abspath(__file__)), "native", "_build", "reloc_index_check")
 
 
-def _run(tmp_path, lo, hi, nlo, words, policy):
+def _run(tmp_path, lo, hi, nlo, words, policy, per=None):
     assert os.path.exists(CHECK), "build first: make -C tests/native"
     t, w, o = (str(tmp_path / f) for f in ("t.bin", "w.bin", "o.bin"))
     np.concatenate([np.array([len(lo), policy], np.uint64), lo, hi, nlo]).astype(np.uint64).tofile(t)
     np.asarray(words, np.uint64).tofile(w)
-    p = subprocess.run([CHECK, t, w, o], capture_output=True, text=True, timeout=120)
+    extra = [] if per is None else [str(per)]
+    p = subprocess.run([CHECK, t, w, o] + extra, capture_output=True, text=True, timeout=120)
     assert p.returncode == 0, p.stderr
     stats = json.loads(p.stdout)
     return stats, (None if "error" in stats else np.fromfile(o, np.uint64))
@@ -42,11 +43,11 @@ def _probe_words(lo, hi, rng, extra=20000):
     return np.concatenate([edges, inside, outside])
 
 
-def _check(tmp_path, lo, hi, nlo, rng, max_reads=None, words=None):
+def _check(tmp_path, lo, hi, nlo, rng, max_reads=None, words=None, per=None):
     lo, hi, nlo = (np.asarray(a, np.uint64) for a in (lo, hi, nlo))
     w = _probe_words(lo, hi, rng) if words is None else words
     for policy in (0, 1):
-        stats, got = _run(tmp_path, lo, hi, nlo, w, policy)
+        stats, got = _run(tmp_path, lo, hi, nlo, w, policy, per)
         assert stats["bad_refs"] == 0, stats
         want = oracle.relocate_words(w, lo, hi, nlo, policy, threads=8)
         np.testing.assert_array_equal(got, want)
@@ -118,6 +119,32 @@ def test_relocation_heavy_interval_mix(tmp_path):
                    words=np.array(s.words(), copy=True))
     print(stats)
     assert stats["line_reads"] <= 1.7 * stats["searched"], stats
+
+
+@pytest.mark.parametrize("per", [1, 16])
+def test_plan_sized_index(tmp_path, per):
+    """The same lookups with 1 and with 16 root lines per interval (the
+    relocation plan's index): the relocation-heavy mix, where 16 per interval
+    takes fewer line reads, and the dense fence-line and top-of-address-space
+    tables."""
+    p = synth.preset(4, num_words=1 << 19)
+    s = synth.SynthArchive(p)
+    lo, hi, nlo = s.intervals()
+    words = np.array(s.words(), copy=True)
+    stats = _check(tmp_path, lo, hi, nlo, np.random.default_rng(6), words=words, per=per)
+    base, _ = _run(tmp_path, np.asarray(lo, np.uint64), np.asarray(hi, np.uint64), np.asarray(nlo, np.uint64),
+                   words, 0)
+    if per == 16:
+        assert stats["line_reads"] < base["line_reads"], (stats, base)
+        assert stats["root_lines"] >= 4 * base["root_lines"], (stats, base)
+    rng = np.random.default_rng(7)
+    n = 20000
+    tlo = (1 << 40) + 16 * np.arange(n, dtype=np.uint64)
+    _check(tmp_path, tlo, tlo + 16, (1 << 44) + rng.permutation(n).astype(np.uint64) * (1 << 31), rng, per=per)
+    top = np.uint64((1 << 64) - (1 << 34)) + np.arange(0, 1 << 33, 1 << 20, dtype=np.uint64)
+    thi = top + np.uint64(1 << 19)
+    thi[-1] = np.uint64((1 << 64) - 2)
+    _check(tmp_path, top, thi, top - np.uint64(1 << 40), rng, per=per)
 
 
 def test_refused_tables(tmp_path):
