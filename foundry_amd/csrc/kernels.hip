@@ -1675,7 +1675,7 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
 // raises the archive's gap flag, and k_repack closes the gaps before any
 // result is read.  The slot's record count goes to slot_rec.
 constexpr uint32_t kSThreads = 256;  // four slots per workgroup
-constexpr uint32_t kSBatch = 128;  // two per lane: 256 measured slower (fewer waves in flight)
+constexpr uint32_t kSBatch = 128;  // two per lane: three or four per lane measured 1.8 and 4.4 times slower
 
 // The last node of the window (whose first word is <= w), or past a full
 // window the last such node of the graph.
