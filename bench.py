@@ -29,6 +29,18 @@ METRIC = "param bytes diffed+relocated GB/s (% HBM peak); graphs restored/sec"
 HBM_PEAK_GBS = 8000.0
 CALIB_BYTES = 256 << 20  # size of the plain copy that calibrates FETCH_SIZE / WRITE_SIZE
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_diff_m_decode256_traffic.txt")
+RELOC_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_reloc_relocation1g_traffic.txt")
+
+
+def _measured_traffic(path):
+    """HBM bytes per launch recorded from rocprofv3 counter runs, or None."""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
 WORKLOADS = {
     1: "archive of 64 graphs x 120 kernel nodes, 1 topology group, 1 interval (uniform rebase)",
     2: "decode-style archive of 256 graphs x 1200 kernel nodes, 4 topology groups, 40k intervals",
@@ -103,7 +115,8 @@ def bench_relocation(args, s, iv, torch, np, stream):
         "config": {"workload": WORKLOADS[4], "preset": 4, "words": n, "intervals": int(len(iv[0]))},
         "roofline": {"bound": "hbm", "kernel": "k_reloc", "achieved": round(b_r / (kms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(b_r / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "traffic": None, "algorithmic_bytes": b_r},
+                     "traffic": _measured_traffic(RELOC_TRAFFIC_FILE) if n == 1 << 27 else None,
+                     "algorithmic_bytes": b_r},
         "cpu_baseline": None,
     }
     if not args.no_cpu_baseline:
@@ -339,12 +352,7 @@ def main():
     b_m = 8 * int(words[~templ].sum()) + 8 * int(tw[~templ].sum()) + 8 * int(words[~templ].sum())
     b_dr = b_m + 16 * n_ovr + 24 * int(words[templ].sum()) + 16 * len(iv[0])
     diff_m_gbs = b_m / (kern["diff_ms"] * 1e-3) / 1e9
-    traffic = None  # measured for the default workload only
-    if args.preset == 2 and os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            for line in f:
-                if line.startswith("hbm_bytes_per_launch:"):
-                    traffic = int(line.split(":")[1])
+    traffic = _measured_traffic(TRAFFIC_FILE) if args.preset == 2 else None  # measured for this workload only
 
     value = P / (ms_per_step * 1e-3) / 1e9
     result = {
