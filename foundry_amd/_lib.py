@@ -196,6 +196,7 @@ _SIGS = {
     "fdy_relocate_words_static": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, _vp, _vp, C.c_uint64, _vp]),
     "fdy_restore_timing_get": (C.c_int, [_vp, C.POINTER(RestoreTiming)]),
     "fdy_set_timing": (C.c_int, [_vp, C.c_int]),
+    "fdy_set_group_wait": (C.c_int, [_vp, C.c_uint32]),
 }
 
 _GRAPH_SIGS = {

@@ -116,6 +116,7 @@ struct fdy_archive {
 
   bool timing = false;
   uint32_t epoch = 0;  // tag of the last restore's published key hashes (1..65535)
+  uint32_t hash_wait_spins = fdy::kHashWaitSpins;  // fdy_set_group_wait
   bool timed = false;
   hipEvent_t ev[6] = {};
 

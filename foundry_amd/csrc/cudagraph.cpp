@@ -11,6 +11,7 @@
 #include "../../include/foundry/CUDAGraph.h"
 
 #include <ATen/ATen.h>
+#include <ATen/hip/HIPContextLight.h>
 #include <c10/hip/HIPStream.h>
 #include <c10/util/Exception.h>
 
@@ -22,8 +23,10 @@
 #include <fstream>
 #include <map>
 #include <mutex>
+#include <set>
 #include <sstream>
 #include <stdexcept>
+#include <thread>
 
 #include "../../include/fdy_format.h"
 #include "../../include/foundry_graph.h"
@@ -43,13 +46,31 @@ void check(int rc, const char* what) {
 
 uint64_t align_up(uint64_t v, uint64_t a) { return (v + a - 1) / a * a; }
 
+// Regions alive in this process: memory placed in a region for a generator
+// state is freed by its tensor's deleter only while the region exists.
+std::mutex g_live_mu;
+std::set<fdy_region*> g_live_regions;
+
+void destroy_region(fdy_region* r) {
+  {
+    std::lock_guard<std::mutex> lk(g_live_mu);
+    g_live_regions.erase(r);
+  }
+  fdy_region_destroy(r);
+}
+
+void free_in_region(fdy_region* r, uint64_t p) {
+  std::lock_guard<std::mutex> lk(g_live_mu);
+  if (g_live_regions.count(r)) (void)fdy_region_free(r, p);
+}
+
 // The allocation region of this thread (the reference keeps it per thread,
 // csrc/hook.cpp:218-251).
 struct RegionState {
   fdy_region* r = nullptr;
   bool enabled = false;
   ~RegionState() {
-    if (r) fdy_region_destroy(r);
+    if (r) destroy_region(r);
   }
 };
 thread_local RegionState t_region;
@@ -133,6 +154,13 @@ struct PendingGraphLoads::Impl {
   std::vector<uint64_t> iv_lo, iv_hi, iv_new;  // relocation intervals (empty: none)
   std::vector<bool> finished;
   std::vector<GraphLoadResult> results;
+  std::thread worker;  // the background build; joined by ~PendingGraphLoads
+
+  // Point each graph at its group's exec (the reference's
+  // link_on_demand_shared_exec, csrc/CUDAGraphParallel.cpp:1998-2004).
+  static void link(PendingGraphLoads* p, const std::vector<uint32_t>& template_of) {
+    for (size_t i = 0; i < template_of.size(); ++i) p->graphs[i]->group_ = p->impl->groups.at(template_of[i]);
+  }
 
   std::string section(uint32_t g, uint32_t sec) {
     uint64_t n = 0;
@@ -161,18 +189,22 @@ MempoolId_t graph_pool_handle() {
 
 void set_allocation_region(uint64_t base, uint64_t size) {
   if (t_region.r) {
-    fdy_region_destroy(t_region.r);
+    destroy_region(t_region.r);
     t_region.r = nullptr;
   }
   fdy_region* r = nullptr;
   check(fdy_region_create(align_up(base, kRegionAlign), align_up(size, kRegionAlign), 0, 0, &r),
         "set_allocation_region");
+  {
+    std::lock_guard<std::mutex> lk(g_live_mu);
+    g_live_regions.insert(r);
+  }
   t_region.r = r;
   t_region.enabled = true;
 }
 
 void release_allocation_region() {
-  if (t_region.r) fdy_region_destroy(t_region.r);
+  if (t_region.r) destroy_region(t_region.r);
   t_region.r = nullptr;
   t_region.enabled = false;
 }
@@ -241,45 +273,86 @@ void pack_fatbins_to_folder(const std::string& dir) {
   check(fdy_registry_pack(registry(), dir.c_str(), &n), "pack_fatbins_to_folder");
 }
 
-// ---- generator state -------------------------------------------------------------
-
-GeneratorState::GeneratorState(uint64_t seed, uint64_t offset) : seed_(seed), offset_(offset) {}
-
-GeneratorState::~GeneratorState() {
-  if (in_region_ && t_region.r) (void)fdy_region_free(t_region.r, seed_ptr_);
+void preallocate_cublas_workspaces() {
+  at::globalContext().lazyInitDevice(at::kCUDA);  // torch's device allocator, as its tensor factories do first
+  TORCH_CHECK(at::cuda::getCurrentCUDABlasHandle() != nullptr, "Failed to get the hipBLAS handle");
+  TORCH_CHECK(at::cuda::getCurrentCUDABlasLtHandle() != nullptr, "Failed to get the hipBLASLt handle");
+  TORCH_CHECK(at::cuda::getCUDABlasLtWorkspace() != nullptr, "Failed to allocate the hipBLASLt workspace");
 }
 
-void GeneratorState::register_graph() {
-  if (seed_ptr_) return;
-  constexpr uint64_t kSegment = 2 * kMiB;
-  if (region_enabled()) {
-    seed_ptr_ = region_alloc(kSegment);
-    in_region_ = true;
-  } else {
-    words_ = at::empty({(int64_t)(kSegment / 8)}, at::TensorOptions().dtype(at::kLong).device(at::kCUDA));
-    seed_ptr_ = (uint64_t)words_.data_ptr();
+// ---- generator state -------------------------------------------------------------
+
+namespace {
+
+constexpr uint64_t kGenSegment = 2 * kMiB;
+constexpr int64_t kGenOffsetWord = 512 / 8;
+
+// A graph registers `st` (at::CUDAGeneratorState::register_graph as the
+// reference overrides it, csrc/CUDAGraph.cpp:35-47): the first registration
+// allocates the seed and offset words.
+void attach_words(at::CUDAGeneratorState& st, CUDAGraph* graph) {
+  if (!st.seed_extragraph_.defined()) {
+    const auto opts = at::TensorOptions().dtype(at::kLong).device(at::kCUDA);
+    at::Tensor seg;
+    if (region_enabled()) {
+      const uint64_t p = region_alloc(kGenSegment);
+      fdy_region* r = t_region.r;
+      seg = at::from_blob(reinterpret_cast<void*>(p), {(int64_t)(kGenSegment / 8)},
+                          [r](void* q) { free_in_region(r, reinterpret_cast<uint64_t>(q)); }, opts);
+    } else {
+      seg = at::empty({(int64_t)(kGenSegment / 8)}, opts);
+    }
+    st.seed_extragraph_ = seg.narrow(0, 0, 1);
+    st.offset_extragraph_ = seg.narrow(0, kGenOffsetWord, 1);
+  }
+  st.registered_graphs_.insert(reinterpret_cast<at::cuda::CUDAGraph*>(graph));
+}
+
+// unregister_graph (csrc/CUDAGraph.cpp:49-59): the last graph releases the words.
+void detach_words(at::CUDAGeneratorState& st, CUDAGraph* graph) {
+  st.registered_graphs_.erase(reinterpret_cast<at::cuda::CUDAGraph*>(graph));
+  if (st.registered_graphs_.empty()) {
+    st.seed_extragraph_.reset();
+    st.offset_extragraph_.reset();
   }
 }
 
-void GeneratorState::replay_prologue(uint64_t increment) {
+// replay_prologue and increase (csrc/CUDAGraph.cpp:60-86).
+void replay_prologue(at::CUDAGeneratorState& st, uint64_t increment) {
   if (!increment) return;
-  TORCH_CHECK(seed_ptr_, "replay_prologue: the generator state was never registered with a graph");
-  const auto opts = at::TensorOptions().dtype(at::kLong).device(at::kCUDA);
-  at::from_blob(reinterpret_cast<void*>(seed_ptr_), {1}, opts).fill_((int64_t)seed_);
-  at::from_blob(reinterpret_cast<void*>(offset_ptr()), {1}, opts).fill_((int64_t)offset_);
-  offset_ += (increment + 3) / 4 * 4;
+  TORCH_CHECK(st.seed_extragraph_.defined(), "replay_prologue: the generator state is registered with no graph");
+  at::Tensor(st.seed_extragraph_).fill_((int64_t)st.seed_);
+  at::Tensor(st.offset_extragraph_).fill_((int64_t)st.philox_offset_per_thread_);
+  st.philox_offset_per_thread_ += (increment + 3) / 4 * 4;
 }
+
+}  // namespace
 
 struct CUDAGeneratorStateRegistry::Impl {
   std::mutex mu;
-  std::map<uint64_t, std::shared_ptr<GeneratorState>> states;
+  uint64_t next_id = 0;
+  std::map<at::CUDAGeneratorState*, uint64_t> ids;
+  std::map<uint64_t, c10::intrusive_ptr<at::CUDAGeneratorState>> states;
 };
 
-std::shared_ptr<GeneratorState> CUDAGeneratorStateRegistry::get_state_from_id(uint64_t id, uint64_t seed) {
+uint64_t CUDAGeneratorStateRegistry::query_state_id(at::CUDAGeneratorState* state) {
+  if (!impl_) impl_ = std::make_shared<Impl>();
+  std::lock_guard<std::mutex> lk(impl_->mu);
+  auto it = impl_->ids.find(state);
+  if (it != impl_->ids.end()) return it->second;
+  const uint64_t id = impl_->next_id++;
+  impl_->ids.emplace(state, id);
+  return id;
+}
+
+c10::intrusive_ptr<at::CUDAGeneratorState> CUDAGeneratorStateRegistry::get_state_from_id(uint64_t id, uint64_t seed) {
   if (!impl_) impl_ = std::make_shared<Impl>();
   std::lock_guard<std::mutex> lk(impl_->mu);
   auto& st = impl_->states[id];
-  if (!st) st = std::make_shared<GeneratorState>(seed, 0);
+  if (!st) {
+    st = c10::make_intrusive<at::CUDAGeneratorState>(seed, 0, 0);
+    impl_->ids.emplace(st.get(), id);
+  }
   return st;
 }
 
@@ -293,11 +366,11 @@ CUDAGeneratorStateRegistry& global_generator_state_registry() {
 // ---- graphs ------------------------------------------------------------------------
 
 CUDAGraph::CUDAGraph(bool keep_graph) : keep_graph_(keep_graph) {}
-CUDAGraph::~CUDAGraph() = default;
+CUDAGraph::~CUDAGraph() { reset(); }
 
-void CUDAGraph::register_generator_state(std::shared_ptr<GeneratorState> state, uint64_t increment) {
+void CUDAGraph::register_generator_state(c10::intrusive_ptr<at::CUDAGeneratorState> state, uint64_t increment) {
   TORCH_CHECK(state, "register_generator_state: null state");
-  state->register_graph();
+  attach_words(*state, this);
   for (auto& g : generators_)
     if (g.first == state) {
       g.second = increment;
@@ -306,15 +379,27 @@ void CUDAGraph::register_generator_state(std::shared_ptr<GeneratorState> state, 
   generators_.emplace_back(std::move(state), increment);
 }
 
+void CUDAGraph::register_generator_state(c10::intrusive_ptr<at::CUDAGeneratorState> state) {
+  TORCH_CHECK(state, "register_generator_state: null state");
+  global_generator_state_registry().query_state_id(state.get());
+  register_generator_state(std::move(state), 0);
+}
+
+void CUDAGraph::register_generator_state(const at::Generator&) {
+  TORCH_CHECK(false, "register_generator_state(Generator) registers a generator during capture, which this ",
+              "library does not provide (LOAD path only)");
+}
+
 void CUDAGraph::replay() {
   TORCH_CHECK(group_, "replay: this CUDAGraph holds no restored graph");
   hipStream_t s = current_stream();
   check(fdy_group_graph_select(group_->gg, (uint32_t)index_, s, nullptr), "replay (select)");
-  for (auto& g : generators_) g.first->replay_prologue(g.second);  // csrc/CUDAGraph.cpp:469-472
+  for (auto& g : generators_) replay_prologue(*g.first, g.second);  // csrc/CUDAGraph.cpp:469-472
   check(fdy_group_graph_launch(group_->gg, s), "replay (launch)");
 }
 
 void CUDAGraph::reset() {
+  for (auto& g : generators_) detach_words(*g.first, this);
   generators_.clear();
   group_.reset();
   index_ = -1;
@@ -353,37 +438,103 @@ hipGraphExec_t CUDAGraph::raw_cuda_graph_exec() {
   return static_cast<hipGraphExec_t>(e);
 }
 
-std::shared_ptr<PendingGraphLoads> CUDAGraph::start_graph_builds(const std::vector<std::string>& json_paths,
-                                                                 MempoolId_t pool, int num_threads) {
-  TORCH_CHECK(!json_paths.empty(), "start_graph_builds: no graphs given");
-  TORCH_CHECK(hipDeviceSynchronize() == hipSuccess, "start_graph_builds: device synchronization failed");
-  auto pending = std::make_shared<PendingGraphLoads>();
-  pending->pool = pool;
-  auto impl = std::make_shared<PendingGraphLoads::Impl>();
-  pending->impl = impl;
-  impl->archive = std::make_shared<detail::Archive>();
+PendingGraphLoads::~PendingGraphLoads() {
+  if (impl && impl->worker.joinable()) impl->worker.join();
+}
+
+namespace {
+
+// A HIP stream of the worker's own, at the default priority.
+struct OwnStream {
+  hipStream_t s = nullptr;
+  OwnStream() {
+    TORCH_CHECK(hipStreamCreateWithFlags(&s, hipStreamNonBlocking) == hipSuccess, "start_graph_builds: ",
+                "cannot create a stream");
+  }
+  ~OwnStream() {
+    if (s) (void)hipStreamDestroy(s);
+  }
+};
+
+// The background build (the reference's Phase 2 thread,
+// csrc/CUDAGraphParallel.cpp:1887-2017, with its Phase 1 reads): open the
+// archives, group them, restore them on the GPU and build one exec per
+// topology group.  Runs on the worker thread; `p` outlives it.
+void build_graphs(PendingGraphLoads* p, const std::vector<std::string>& json_paths, int num_threads) {
+  auto& impl = *p->impl;
+  TORCH_CHECK(hipSetDevice(p->dev) == hipSuccess, "start_graph_builds: cannot make device ", (int)p->dev,
+              " current");
+  OwnStream stream;
+  hipStream_t s = stream.s;
   std::vector<const char*> cpaths;
-  for (const auto& p : json_paths) cpaths.push_back(p.c_str());
+  for (const auto& path : json_paths) cpaths.push_back(path.c_str());
   check(fdy_archive_open(cpaths.data(), (uint32_t)cpaths.size(), (uint32_t)std::max(1, num_threads),
-                         &impl->archive->a),
+                         &impl.archive->a),
         "start_graph_builds (open)");
-  fdy_archive* a = impl->archive->a;
+  fdy_archive* a = impl.archive->a;
   const uint32_t G = (uint32_t)json_paths.size();
 
   // A graph_manifest.json beside the first path groups the graphs
   // (csrc/CUDAGraphParallel.cpp:1720-1786); otherwise the saved keys do.
   std::string manifest;
+  bool used_manifest = false;
   if (read_file(dirname_of(json_paths[0]) + "/graph_manifest.json", &manifest)) {
     std::vector<std::string> names;
-    for (const auto& p : json_paths) names.push_back(basename_of(p));
+    for (const auto& path : json_paths) names.push_back(basename_of(path));
     std::vector<const char*> cnames;
     for (const auto& n : names) cnames.push_back(n.c_str());
     int used = 0;
     check(fdy_archive_set_manifest(a, manifest.data(), manifest.size(), cnames.data(), &used),
           "start_graph_builds (manifest)");
-    pending->used_manifest = used != 0;
+    used_manifest = used != 0;
   }
+  if (!impl.iv_lo.empty())
+    check(fdy_archive_set_relocation(a, impl.iv_lo.data(), impl.iv_hi.data(), impl.iv_new.data(), impl.iv_lo.size(),
+                                     FDY_RELOC_HALF_OPEN),
+          "start_graph_builds (relocation)");
+  check(fdy_restore(a, s), "start_graph_builds (restore)");
+  std::vector<uint32_t> template_of(G);
+  check(fdy_get_groups(a, s, template_of.data()), "start_graph_builds (groups)");
+  for (uint32_t t : template_of) {
+    if (impl.groups.count(t)) continue;
+    auto grp = std::make_shared<detail::Group>();
+    grp->archive = impl.archive;
+    check(fdy_group_graph_create(a, t, registry(), s, &grp->gg), "start_graph_builds (group graph)");
+    impl.groups.emplace(t, std::move(grp));
+  }
+  TORCH_CHECK(hipStreamSynchronize(s) == hipSuccess, "start_graph_builds: the restore stream failed");
+  PendingGraphLoads::Impl::link(p, template_of);
+  p->template_of = std::move(template_of);
+  p->used_manifest = used_manifest;
+}
+
+}  // namespace
+
+std::shared_ptr<PendingGraphLoads> CUDAGraph::start_graph_builds(const std::vector<std::string>& json_paths,
+                                                                 MempoolId_t pool, int num_threads) {
+  TORCH_CHECK(!json_paths.empty(), "start_graph_builds: no graphs given");
+  TORCH_CHECK(hipDeviceSynchronize() == hipSuccess, "start_graph_builds: device synchronization failed");
+  int dev = 0;
+  TORCH_CHECK(hipGetDevice(&dev) == hipSuccess, "start_graph_builds: no current device");
+  auto pending = std::make_shared<PendingGraphLoads>();
+  pending->pool = pool;
+  pending->dev = (c10::DeviceIndex)dev;
+  pending->registry = &global_generator_state_registry();
+  auto impl = std::make_shared<PendingGraphLoads::Impl>();
+  pending->impl = impl;
+  impl->archive = std::make_shared<detail::Archive>();
+  const uint32_t G = (uint32_t)json_paths.size();
+  // The graph shells exist at once (Phase 1b, csrc/CUDAGraphParallel.cpp:1622-1718).
+  for (uint32_t i = 0; i < G; ++i) {
+    auto g = std::make_shared<CUDAGraph>();
+    g->index_ = i;
+    g->pool_ = pool;
+    pending->graphs.push_back(std::move(g));
+  }
+  impl->finished.assign(G, false);
+  impl->results.resize(G);
   // A region placed away from its saved base relocates every saved pointer.
+  // The region is this thread's: its interval is read here, for the worker.
   if (t_region.r) {
     const fdy_region_info info = region_info();
     if (info.base != info.saved_base) {
@@ -397,37 +548,30 @@ std::shared_ptr<PendingGraphLoads> CUDAGraph::start_graph_builds(const std::vect
         check(fdy_region_intervals(t_region.r, FDY_REGION_IV_REGION, impl->iv_lo.data(), impl->iv_hi.data(),
                                    impl->iv_new.data(), n, &n),
               "start_graph_builds (intervals)");
-      check(fdy_archive_set_relocation(a, impl->iv_lo.data(), impl->iv_hi.data(), impl->iv_new.data(), n,
-                                       FDY_RELOC_HALF_OPEN),
-            "start_graph_builds (relocation)");
     }
   }
-  hipStream_t s = current_stream();
-  check(fdy_restore(a, s), "start_graph_builds (restore)");
-  pending->template_of.resize(G);
-  check(fdy_get_groups(a, s, pending->template_of.data()), "start_graph_builds (groups)");
-  for (uint32_t t : pending->template_of) {
-    if (impl->groups.count(t)) continue;
-    auto grp = std::make_shared<detail::Group>();
-    grp->archive = impl->archive;
-    check(fdy_group_graph_create(a, t, registry(), s, &grp->gg), "start_graph_builds (group graph)");
-    impl->groups.emplace(t, std::move(grp));
-  }
-  for (uint32_t i = 0; i < G; ++i) {
-    auto g = std::make_shared<CUDAGraph>();
-    g->index_ = i;
-    g->pool_ = pool;
-    g->group_ = impl->groups.at(pending->template_of[i]);
-    pending->graphs.push_back(std::move(g));
-  }
-  impl->finished.assign(G, false);
-  impl->results.resize(G);
+  // Everything else runs on a worker thread; its error reaches the finish
+  // calls through build_complete_ (2010-2015).
+  auto done = std::make_shared<std::promise<void>>();
+  pending->build_complete_ = done->get_future().share();
+  PendingGraphLoads* p = pending.get();
+  impl->worker = std::thread([p, json_paths, num_threads, done]() {
+    try {
+      build_graphs(p, json_paths, num_threads);
+      done->set_value();
+    } catch (...) {
+      done->set_exception(std::current_exception());
+    }
+  });
   return pending;
 }
 
 GraphLoadResult CUDAGraph::finish_one_graph_load(std::shared_ptr<PendingGraphLoads> pending, size_t index) {
   TORCH_CHECK(pending && pending->impl, "finish_one_graph_load: no pending loads");
   auto& impl = *pending->impl;
+  // Wait for the background build, and raise its error (2034-2038 waits
+  // without raising; get() keeps the error).
+  if (pending->build_complete_.valid()) pending->build_complete_.get();
   if (index >= pending->graphs.size())
     throw std::out_of_range("finish_one_graph_load: index " + std::to_string(index) +
                             " out of range (num_graphs=" + std::to_string(pending->graphs.size()) + ")");
@@ -440,7 +584,8 @@ GraphLoadResult CUDAGraph::finish_one_graph_load(std::shared_ptr<PendingGraphLoa
   for (size_t k = 0; k + 24 <= gens.size(); k += 24) {
     uint64_t row[3];
     std::memcpy(row, gens.data() + k, 24);
-    graph->register_generator_state(global_generator_state_registry().get_state_from_id(row[0], row[1]), row[2]);
+    CUDAGeneratorStateRegistry& reg = pending->registry ? *pending->registry : global_generator_state_registry();
+    graph->register_generator_state(reg.get_state_from_id(row[0], row[1]), row[2]);
   }
   // Allocator events in SAVE order (2060-2064).
   const std::string events = impl.section(g, FDY_SEC_ALLOC_EVENTS);
@@ -496,6 +641,7 @@ GraphLoadResult CUDAGraph::finish_one_graph_load(std::shared_ptr<PendingGraphLoa
 
 std::vector<GraphLoadResult> CUDAGraph::finish_graph_loads(std::shared_ptr<PendingGraphLoads> pending) {
   TORCH_CHECK(pending, "finish_graph_loads: no pending loads");
+  if (pending->build_complete_.valid()) pending->build_complete_.get();  // 2079-2088
   std::vector<GraphLoadResult> out;
   for (size_t i = 0; i < pending->graphs.size(); ++i) out.push_back(finish_one_graph_load(pending, i));
   return out;

@@ -9,6 +9,9 @@
 
 namespace fdy {
 
+// Default RestoreArgs::hash_wait_spins: about 1 ms of s_sleep.
+constexpr uint32_t kHashWaitSpins = 1u << 14;
+
 // Everything the restore kernels read or write for one archive.
 struct RestoreArgs {
   const uint8_t* img;         // .cugraph images, each 256-B aligned
@@ -25,6 +28,8 @@ struct RestoreArgs {
   const uint32_t* explicit_template;  // or null
   uint64_t* key_hash;                 // per graph: the grouping pass's published key hash (epoch-tagged)
   uint32_t epoch;                     // this restore's tag for published key hashes (1..65535)
+  uint32_t hash_wait_spins;           // s_sleep rounds the grouping scan waits for an unpublished hash
+                                      // before hashing that key itself (0: at once)
   uint32_t* template_of;
   uint32_t* status;
   uint32_t* gwords;

@@ -99,18 +99,17 @@ __device__ __forceinline__ uint64_t shift_share(const CrcConsts* cc, uint64_t z,
 //     64-bit atomic store, tagged with the restore's epoch in its low 16
 //     bits.  Nothing else is shared, so no fence is needed: only atomics
 //     touch the published hashes.
-//   - Its first wave then scans the lower graphs' hashes, 64 per step, with
-//     atomic loads; a hash not yet published this restore is waited for a
-//     bounded time and then computed by the wave itself, so no workgroup
-//     depends on another's progress.  The lowest j with i's hash and key
-//     length is confirmed byte for byte by the workgroup; on a difference
-//     scanning goes on past j.
+//   - The workgroup then scans the lower graphs' hashes, one per thread per
+//     step, with atomic loads; a hash not yet published this restore is
+//     waited for a bounded time (RestoreArgs::hash_wait_spins sleeps) and
+//     then computed by the wave itself, so no workgroup depends on another's
+//     progress.  The lowest j with i's hash and key length is confirmed byte
+//     for byte by the workgroup; on a difference scanning goes on past j.
 // The restore's first kernel: it also resets the counters later kernels
 // accumulate into and starts the key and dependency digests from their
 // finishing terms (the node pass's digest units XOR every slice's share in).
 constexpr uint32_t kGroupThreads = 512;
 constexpr uint32_t kHashBatch = 8;
-constexpr uint32_t kHashWaitSpins = 1u << 14;  // ~1 ms of s_sleep before a wave hashes a key itself
 
 // A 64-bit hash of a key for finding grouping candidates (not a digest the
 // restore reports): the XOR over the key's 8-byte words w_k (the last one
@@ -186,13 +185,14 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
       s_differs = 0;
     }
     __syncthreads();
+    uint32_t found = i;
     for (uint32_t base = from; base < i; base += kGroupThreads) {
       const uint32_t j = base + tid;
       const bool in = j < i;
       uint64_t hj = in ? __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
       const uint64_t Lj = in ? a.graphs[j].sec_size[FDY_SEC_TOPOLOGY_KEY] : ~0ull;
       // Hashes of this restore carry its epoch; wait (bounded) for the rest.
-      for (uint32_t spin = 0; __ballot(in && (hj & 0xFFFF) != a.epoch) && spin < kHashWaitSpins; ++spin) {
+      for (uint32_t spin = 0; __ballot(in && (hj & 0xFFFF) != a.epoch) && spin < a.hash_wait_spins; ++spin) {
         __builtin_amdgcn_s_sleep(2);
         if (in && (hj & 0xFFFF) != a.epoch)
           hj = __hip_atomic_load(a.key_hash + j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -213,9 +213,13 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
       const uint64_t mk = __ballot(m);
       if (mk && lane == 0) atomicMin(&s_found, base + (tid & ~63u) + (uint32_t)__ffsll((long long)mk) - 1);
       __syncthreads();
-      if (s_found != i) break;  // uniform over the workgroup
+      found = s_found;
+      // Every wave holds this step's minimum before any wave of the next
+      // step can lower s_found again.
+      __syncthreads();
+      if (found != i) break;  // uniform over the workgroup
     }
-    const uint32_t j = s_found;
+    const uint32_t j = found;
     if (j == i) break;  // uniform over the workgroup
     const uint8_t* pj = a.img + a.graphs[j].sec_off[FDY_SEC_TOPOLOGY_KEY];
     // Both keys start 8-byte aligned: compare whole words, kHashBatch per

@@ -364,9 +364,9 @@ int check_switchable(fdy_archive* a, uint32_t g, uint32_t* t_out) {
 
 // The scatter that moves the live image of g's group from its current graph
 // to g.
-SwitchArgs switch_args(const fdy_archive* a, uint32_t g, uint8_t* dirty) {
+// The switch of g's group from its graph c to g.
+SwitchArgs switch_args(const fdy_archive* a, uint32_t g, uint8_t* dirty, uint32_t c) {
   const uint32_t t = a->h_tmpl[g];
-  const uint32_t c = a->h_current[t];
   SwitchArgs w{};
   w.ovr_cur = a->ovr.as<fdy_override>() + ovr_base(a, c);
   w.n_cur = a->h_ovr_off[c + 1] - a->h_ovr_off[c];
@@ -382,6 +382,9 @@ SwitchArgs switch_args(const fdy_archive* a, uint32_t g, uint8_t* dirty) {
   w.target = g;
   w.tmpl = t;
   return w;
+}
+SwitchArgs switch_args(const fdy_archive* a, uint32_t g, uint8_t* dirty) {
+  return switch_args(a, g, dirty, a->h_current[a->h_tmpl[g]]);
 }
 
 int enqueue_switch(fdy_archive* a, uint32_t g, hipStream_t s, uint8_t* dirty, bool set_device) {
@@ -712,6 +715,7 @@ int fdy_restore(fdy_archive* a, void* stream) {
   r.key_hash = a->key_hash.as<uint64_t>();
   a->epoch = a->epoch % 65535 + 1;
   r.epoch = a->epoch;
+  r.hash_wait_spins = a->hash_wait_spins;
   r.template_of = a->tmpl.as<uint32_t>();
   r.status = a->status.as<uint32_t>();
   r.gwords = a->gwords.as<uint32_t>();
@@ -762,6 +766,12 @@ int fdy_restore(fdy_archive* a, void* stream) {
 int fdy_set_timing(fdy_archive* a, int enabled) {
   if (!a) return err(FDY_E_INVALID, "null archive");
   a->timing = enabled != 0;
+  return FDY_OK;
+}
+
+int fdy_set_group_wait(fdy_archive* a, uint32_t spins) {
+  if (!a) return err(FDY_E_INVALID, "null archive");
+  a->hash_wait_spins = spins;
   return FDY_OK;
 }
 
@@ -897,19 +907,35 @@ int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, voi
     if (!rc) rc = check_switchable(a, targets[i], &t);
     if (rc) return rc;
   }
+  const bool bound = a->bound.size() == a->G;
+  // Every switch's launch size depends on the group's current graph at that
+  // point of the sequence: follow the sequence on a copy first, so that a
+  // switch too large for one launch refuses the whole sequence before
+  // anything is enqueued.
+  {
+    std::vector<uint32_t> cur = a->h_current;
+    for (uint64_t i = 0; i < n; ++i) {
+      const uint32_t g = targets[i], t = a->h_tmpl[g];
+      if ((bound && a->bound[t]) || cur[t] == g) continue;
+      if (switch_blocks(switch_args(a, g, nullptr, cur[t])) >= 0x7FFFFFFFull)
+        return err(FDY_E_CAPACITY, "override sets too large for one switch launch (target " +
+                                       std::to_string(g) + ")");
+      cur[t] = g;
+    }
+  }
   FDY_HIP(hipSetDevice(a->device));
   // Consecutive switches of different groups touch disjoint live images and
   // node sources: up to kSwitchBatch of them share one launch.  A switch of
   // a group already in the batch, or of a group whose live image a group
   // graph holds, first launches the batch so far (stream order keeps the
-  // sequence's order where it matters).
-  const bool bound = a->bound.size() == a->G;
+  // sequence's order where it matters).  A group's current graph is recorded
+  // once its switch is enqueued.
   SwitchBatch b{};
-  std::vector<uint32_t> in_batch;
+  uint32_t batch_t[kSwitchBatch], batch_g[kSwitchBatch];
   auto flush = [&]() -> int {
     if (b.n) FDY_HIP(launch_switch_many(b, s));
+    for (uint32_t k = 0; k < b.n; ++k) a->h_current[batch_t[k]] = batch_g[k];
     b.n = 0;
-    in_batch.clear();
     return FDY_OK;
   };
   for (uint64_t i = 0; i < n; ++i) {
@@ -921,20 +947,26 @@ int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, voi
       if (rc) return rc;
       continue;
     }
+    if (std::find(batch_t, batch_t + b.n, t) != batch_t + b.n) {
+      rc = flush();
+      if (rc) return rc;
+    }
     if (a->h_current[t] == g) continue;
+    if (b.n == kSwitchBatch) {
+      rc = flush();
+      if (rc) return rc;
+    }
     const SwitchArgs w = switch_args(a, g, nullptr);
-    const uint64_t blocks = switch_blocks(w);
-    if (blocks >= 0x7FFFFFFFull) return err(FDY_E_CAPACITY, "override sets too large for one switch launch");
-    if (b.n == kSwitchBatch || std::find(in_batch.begin(), in_batch.end(), t) != in_batch.end() ||
-        (b.n && b.end[b.n - 1] + blocks >= 0x7FFFFFFFull)) {
+    const uint32_t blocks = (uint32_t)switch_blocks(w);  // below 2^31: checked above
+    if (b.n && b.end[b.n - 1] + (uint64_t)blocks >= 0x7FFFFFFFull) {
       rc = flush();
       if (rc) return rc;
     }
     b.sw[b.n] = w;
-    b.end[b.n] = (b.n ? b.end[b.n - 1] : 0u) + (uint32_t)blocks;
+    b.end[b.n] = (b.n ? b.end[b.n - 1] : 0u) + blocks;
+    batch_t[b.n] = t;
+    batch_g[b.n] = g;
     ++b.n;
-    in_batch.push_back(t);
-    a->h_current[t] = g;
   }
   return flush();
 }
@@ -1025,6 +1057,23 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch[kMaxDevices] = {};
 
+// The table whose index each device's array holds, so that a call with the
+// same table uses it as it stands: no host build, no copy, no wait.
+struct StaticTable {
+  bool valid = false;
+  uint32_t policy = 0;
+  std::vector<uint64_t> lo, hi, nlo;
+  RelocDev dev{};
+};
+StaticTable g_static_table[kMaxDevices];
+
+bool same_table(const StaticTable& t, const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n,
+                uint32_t policy) {
+  if (!t.valid || t.policy != policy || t.lo.size() != n) return false;
+  const size_t b = 8 * n;
+  return !n || (!std::memcmp(t.lo.data(), lo, b) && !std::memcmp(t.hi.data(), hi, b) && !std::memcmp(t.nlo.data(), nlo, b));
+}
+
 // The device address of `scratch` on device `dev` (current), looked up on
 // the first call on that device.
 int scratch_on(int dev, uint8_t** out) {
@@ -1048,26 +1097,58 @@ int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint
   if ((!in && n) || (!out && n)) return err(FDY_E_INVALID, "null word array");
   if (((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 7) != 0)
     return err(FDY_E_INVALID, "word arrays must be 8-byte aligned");
-  HostIndex x;
-  int rc = build_reloc_index(lo, hi, nlo, n_iv, policy, &x);
-  if (rc) return rc;
-  const uint64_t total = x.line.size() * sizeof(RelocLine);
-  if (total > FDY_STATIC_INDEX_BYTES)
-    return err(FDY_E_CAPACITY, "the index of " + std::to_string(n_iv) + " intervals takes " + std::to_string(total) +
-                                   " bytes; the static index holds " + std::to_string(FDY_STATIC_INDEX_BYTES));
+  if (n_iv && (!lo || !hi || !nlo)) return err(FDY_E_INVALID, "null interval array");
   int dev = 0;
-  FDY_HIP(hipGetDevice(&dev));
+  const hipError_t ge = hipGetDevice(&dev);
+  bool same = false;
+  if (ge == hipSuccess && dev >= 0 && dev < kMaxDevices) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    same = same_table(g_static_table[dev], lo, hi, nlo, n_iv, policy);
+  }
+  // A new table: its index is built and checked against the array's size
+  // (on the host, so an oversized table is refused with or without a GPU).
+  HostIndex x;
+  if (!same) {
+    int rc = build_reloc_index(lo, hi, nlo, n_iv, policy, &x);
+    if (rc) return rc;
+    const uint64_t total = x.line.size() * sizeof(RelocLine);
+    if (total > FDY_STATIC_INDEX_BYTES)
+      return err(FDY_E_CAPACITY, "the index of " + std::to_string(n_iv) + " intervals takes " + std::to_string(total) +
+                                     " bytes; the static index holds " + std::to_string(FDY_STATIC_INDEX_BYTES));
+  }
+  FDY_HIP(ge);
   uint8_t* base = nullptr;
-  rc = scratch_on(dev, &base);
+  int rc = scratch_on(dev, &base);
   if (rc) return rc;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  RelocDev d = x.dev;
-  if (n_iv) {
-    // In stream order, so after any earlier call's kernel on this stream;
-    // then wait for the copies, after which the host arrays may go.
-    FDY_HIP(hipMemcpyAsync(base, x.line.data(), total, hipMemcpyHostToDevice, s));
-    FDY_HIP(hipStreamSynchronize(s));
-    d.line = reinterpret_cast<const RelocLine*>(base);
+  RelocDev d{};
+  {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    StaticTable& st = g_static_table[dev];
+    if (!same_table(st, lo, hi, nlo, n_iv, policy)) {
+      if (same) {  // another thread replaced the table meanwhile
+        rc = build_reloc_index(lo, hi, nlo, n_iv, policy, &x);
+        if (rc) return rc;
+        if (x.line.size() * sizeof(RelocLine) > FDY_STATIC_INDEX_BYTES)
+          return err(FDY_E_CAPACITY, "the static index cannot hold this table");
+      }
+      st.valid = false;
+      d = x.dev;
+      if (n_iv) {
+        // In stream order, so after any earlier call's kernel on this
+        // stream; then wait for the copy, after which the host index may go.
+        FDY_HIP(hipMemcpyAsync(base, x.line.data(), x.line.size() * sizeof(RelocLine), hipMemcpyHostToDevice, s));
+        FDY_HIP(hipStreamSynchronize(s));
+        d.line = reinterpret_cast<const RelocLine*>(base);
+      }
+      st.lo.assign(lo, lo + n_iv);
+      st.hi.assign(hi, hi + n_iv);
+      st.nlo.assign(nlo, nlo + n_iv);
+      st.policy = policy;
+      st.dev = d;
+      st.valid = true;
+    }
+    d = st.dev;
   }
   FDY_HIP(launch_reloc_words(d, in, out, n, s));
   return FDY_OK;

@@ -27,6 +27,7 @@ build: they raise NotImplementedError.
 from __future__ import annotations
 
 import atexit
+import concurrent.futures
 import ctypes as C
 import json
 import os
@@ -402,42 +403,109 @@ def generators_of(section: bytes) -> list[tuple[int, int, int]]:
 
 
 class PendingGraphLoads:
-    """The split-load state (include/CUDAGraphInternal.h:13-28): the restored
-    archive, one group graph per topology group, and one CUDAGraph per graph."""
+    """The split-load state (include/CUDAGraphInternal.h:13-28): one CUDAGraph
+    shell per graph at once, and, once the background build is complete, the
+    restored archive and one group graph per topology group.
 
-    def __init__(self, json_paths: Sequence[str], num_threads: int, stream, pool=None):
+    start_graph_builds returns while a worker thread opens the archives,
+    restores them on the GPU and builds the group graphs (the reference's
+    detached Phase 2 thread, csrc/CUDAGraphParallel.cpp:1861-2017, which also
+    overlaps the caller's own initialisation).  `build_complete` is that
+    work's future; the finish calls, `archive`, `template_of`,
+    `used_manifest` and `group_graphs` wait for it and raise the worker's
+    error, every time they are asked (the reference's finish_graph_loads uses
+    get(), which rethrows; its finish_one_graph_load only waits)."""
+
+    def __init__(self, json_paths: Sequence[str], num_threads: int, pool=None):
         self.pool = pool if pool is not None else (0, 0)
         self.json_paths = list(json_paths)
         self.names = [os.path.basename(p) for p in self.json_paths]
-        self.archive = Archive.open(self.json_paths, max(1, int(num_threads)))
-        self.used_manifest = False
-        manifest = os.path.join(os.path.dirname(self.json_paths[0]) or ".", "graph_manifest.json")
-        if os.path.exists(manifest):
-            with open(manifest, "rb") as f:
-                self.used_manifest = self.archive.set_manifest(f.read(), self.names)
+        self.num_threads = max(1, int(num_threads))
+        self.graphs = [CUDAGraph._restored(self, i) for i in range(len(self.json_paths))]
+        self.finished = [False] * len(self.json_paths)
+        self.outputs: list = [None] * len(self.json_paths)
+        # The allocation region is per thread: its intervals are read here,
+        # on the caller's thread, for the worker.
         r = _region()
         self.intervals = (np.zeros(0, np.uint64),) * 3
         if r is not None:
             info = r.info()
             if info["base"] != info["saved_base"]:
                 self.intervals = r.intervals()
-                self.archive.set_relocation(*self.intervals)
-        self.archive.restore(stream)
-        self.template_of = self.archive.groups(stream)
-        self.group_graphs = {int(t): GroupGraph(self.archive, int(t), registry(), stream)
-                             for t in sorted(set(int(x) for x in self.template_of))}
-        self.graphs = [CUDAGraph._restored(self, i) for i in range(len(self.json_paths))]
-        self.finished = [False] * len(self.json_paths)
-        self.outputs: list = [None] * len(self.json_paths)
+        self.device = torch.cuda.current_device()
+        self._archive: Archive | None = None
+        self._template_of = None
+        self._used_manifest = False
+        self._group_graphs: dict[int, GroupGraph] = {}
+        self.build_complete: concurrent.futures.Future = concurrent.futures.Future()
+        self._worker = threading.Thread(target=self._build, name="foundry-graph-build", daemon=False)
+        self._worker.start()
+
+    def _build(self) -> None:
+        """The worker: open, restore and build on a stream of its own (the
+        reference's bg thread makes the context current first, 1895-1897)."""
+        archive, ggs = None, {}
+        try:
+            torch.cuda.set_device(self.device)
+            stream = torch.cuda.Stream(device=self.device)
+            archive = Archive.open(self.json_paths, self.num_threads)
+            used = False
+            manifest = os.path.join(os.path.dirname(self.json_paths[0]) or ".", "graph_manifest.json")
+            if os.path.exists(manifest):
+                with open(manifest, "rb") as f:
+                    used = archive.set_manifest(f.read(), self.names)
+            if len(self.intervals[0]):
+                archive.set_relocation(*self.intervals)
+            archive.restore(stream)
+            template_of = archive.groups(stream)
+            for t in sorted(set(int(x) for x in template_of)):
+                ggs[t] = GroupGraph(archive, t, registry(), stream)
+            stream.synchronize()
+        except BaseException as e:  # handed to the finish calls
+            for gg in ggs.values():
+                gg.close()
+            if archive is not None:
+                archive.close()
+            self.build_complete.set_exception(e)
+            return
+        self._archive, self._template_of, self._used_manifest, self._group_graphs = archive, template_of, used, ggs
+        self.build_complete.set_result(None)
+
+    def wait(self) -> None:
+        """Wait for the background build; raises its error."""
+        self.build_complete.result()
+
+    @property
+    def archive(self) -> Archive:
+        self.wait()
+        return self._archive
+
+    @property
+    def template_of(self) -> np.ndarray:
+        self.wait()
+        return self._template_of
+
+    @property
+    def used_manifest(self) -> bool:
+        self.wait()
+        return self._used_manifest
+
+    @property
+    def group_graphs(self) -> dict:
+        self.wait()
+        return self._group_graphs
 
     def group_graph(self, index: int) -> GroupGraph:
         return self.group_graphs[int(self.template_of[index])]
 
     def close(self) -> None:
-        for gg in self.group_graphs.values():
+        self._worker.join()
+        for gg in self._group_graphs.values():
             gg.close()
-        self.group_graphs = {}
-        self.archive.close()
+        self._group_graphs = {}
+        if self._archive is not None:
+            self._archive.close()
+            self._archive = None
 
 
 class CUDAGraph:
@@ -545,15 +613,17 @@ class CUDAGraph:
     # ---- split load -------------------------------------------------------
     @staticmethod
     def start_graph_builds(json_paths: Sequence[str], pool=None, num_threads: int = 4) -> PendingGraphLoads:
-        """Open and restore every archive on the GPU and build one exec per
-        topology group (csrc/CUDAGraphParallel.cpp:1543-2015).  A
-        graph_manifest.json beside the first path groups the graphs; without
-        it, graphs group by their saved topology keys.  Everything is done
-        when this returns."""
+        """Start opening and restoring every archive on the GPU and building
+        one exec per topology group (csrc/CUDAGraphParallel.cpp:1543-2015),
+        and return while that runs on a worker thread: the caller goes on
+        with its own initialisation, and the finish calls wait for the
+        build.  A graph_manifest.json beside the first path groups the
+        graphs; without it, graphs group by their saved topology keys.  Open,
+        restore and build errors are raised by the finish calls."""
         if not json_paths:
             raise RuntimeError("start_graph_builds: no graphs given")
         torch.cuda.synchronize()
-        return PendingGraphLoads(json_paths, num_threads, torch.cuda.current_stream(), pool)
+        return PendingGraphLoads(json_paths, num_threads, pool)
 
     @staticmethod
     def finish_one_graph_load(pending: PendingGraphLoads, index: int):
@@ -562,6 +632,7 @@ class CUDAGraph:
         (in SAVE order), then rebuild its output tensors.  Raises IndexError
         out of range, as the reference's std::out_of_range does through
         pybind."""
+        pending.wait()
         if index < 0 or index >= len(pending.graphs):
             raise IndexError(f"finish_one_graph_load: index {index} out of range "
                              f"(num_graphs={len(pending.graphs)})")
@@ -583,6 +654,9 @@ class CUDAGraph:
 
     @staticmethod
     def finish_graph_loads(pending: PendingGraphLoads):
+        """csrc/CUDAGraphParallel.cpp:2071-2099: wait for the background
+        build (raising its error), then finish every graph in index order."""
+        pending.wait()
         return [CUDAGraph.finish_one_graph_load(pending, i) for i in range(len(pending.graphs))]
 
     @staticmethod

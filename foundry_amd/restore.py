@@ -115,6 +115,11 @@ class Archive:
     def set_timing(self, enabled: bool = True) -> None:
         check(restore_lib().fdy_set_timing(self._h, 1 if enabled else 0))
 
+    def set_group_wait(self, spins: int) -> None:
+        """Rounds of s_sleep the grouping step waits for a lower graph's
+        unpublished key hash before hashing that key itself (0: at once)."""
+        check(restore_lib().fdy_set_group_wait(self._h, int(spins)))
+
     # ---- the restore -----------------------------------------------------
     def restore(self, stream=None) -> None:
         check(restore_lib().fdy_restore(self._h, _stream(stream)))

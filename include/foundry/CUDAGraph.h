@@ -11,16 +11,21 @@
 // Loading restores every archive on the GPU in one pass, builds one hipGraph
 // exec per topology group, and shares it among the group's graphs (the
 // reference's SharedGraphExec); replay() switches the exec to the graph and
-// launches it on the current HIP stream.  Capture and SAVE are not part of
-// this library.  Errors throw c10::Error (TORCH_CHECK), an index out of
-// range std::out_of_range, as in the reference.
+// launches it on the current HIP stream.  start_graph_builds returns while a
+// worker thread does that work; the finish calls wait for it.  Capture and
+// SAVE are not part of this library.  Errors throw c10::Error (TORCH_CHECK),
+// an index out of range std::out_of_range, as in the reference.
 #pragma once
 
 #include <ATen/Tensor.h>
+#include <ATen/core/Generator.h>
+#include <ATen/hip/HIPGeneratorImpl.h>  // at::CUDAGeneratorState (the ROCm build's header for it)
 #include <c10/core/Allocator.h>
+#include <c10/util/intrusive_ptr.h>
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <future>
 #include <memory>
 #include <string>
 #include <utility>
@@ -72,36 +77,27 @@ int load_cuda_modules_and_libraries(const std::string& dir);
 // Write the registry's code objects into the packed pair in `dir`.
 void pack_fatbins_to_folder(const std::string& dir);
 
+// ---- BLAS handles (csrc/CUDAGraph.cpp:165-174) --------------------------------
+// Create the current stream's hipBLAS and hipBLASLt handles and the hipBLASLt
+// workspace (through torch) before graphs that use them are loaded, so that
+// they are not allocated inside the graphs' region later.
+void preallocate_cublas_workspaces();
+
 // ---- generator state (csrc/CUDAGraph.cpp:35-97, 133-160) ---------------------
-// The graph-safe Philox seed and offset words a restored graph's random
-// kernels read: a 2 MiB segment (an allocation of this thread's region when
-// one is enabled, else a torch tensor), seed at +0, offset at +512.
-struct GeneratorState {
-  GeneratorState(uint64_t seed, uint64_t philox_offset_per_thread);
-  ~GeneratorState();
-  GeneratorState(const GeneratorState&) = delete;
-  GeneratorState& operator=(const GeneratorState&) = delete;
-  // Allocates the words on first use (register_graph, 35-46).
-  void register_graph();
-  // Writes seed and offset on the current stream, then advances the offset
-  // by the increment rounded up to a multiple of 4 (79-86, 60-77).
-  void replay_prologue(uint64_t wholegraph_increment);
-  uint64_t seed() const { return seed_; }
-  uint64_t offset() const { return offset_; }
-  uint64_t seed_ptr() const { return seed_ptr_; }
-  uint64_t offset_ptr() const { return seed_ptr_ ? seed_ptr_ + 512 : 0; }
-
- private:
-  uint64_t seed_, offset_;
-  uint64_t seed_ptr_ = 0;
-  bool in_region_ = false;
-  at::Tensor words_;  // without a region
-};
-
+// A restored graph's random kernels read torch's graph-safe Philox seed and
+// offset words, seed_extragraph_ and offset_extragraph_ of an
+// at::CUDAGeneratorState.  When the first graph registers a state, the two
+// words are one 2 MiB segment (an allocation of this thread's region when one
+// is enabled, else a torch tensor), seed at +0 and offset at +512, where
+// torch's caching allocator puts two one-element tensors in a fresh segment;
+// they are released when the last graph unregisters.
 struct CUDAGeneratorStateRegistry {
+  // The id a state is known under: the id get_state_from_id made it for, else
+  // a new one (query_state_id, csrc/CUDAGraph.cpp:133-145).
+  uint64_t query_state_id(at::CUDAGeneratorState* state);
   // The state saved under `id`; a new id makes one of `seed` and offset 0
   // (get_state_from_id, csrc/CUDAGraph.cpp:147-160).
-  std::shared_ptr<GeneratorState> get_state_from_id(uint64_t id, uint64_t seed);
+  c10::intrusive_ptr<at::CUDAGeneratorState> get_state_from_id(uint64_t id, uint64_t seed);
   struct Impl;
   std::shared_ptr<Impl> impl_;
 };
@@ -116,9 +112,15 @@ struct CUDAGraph {
   explicit CUDAGraph(bool keep_graph = false);
   ~CUDAGraph();
 
-  // Run `state`'s replay prologue with this increment before every replay
-  // (csrc/CUDAGraph.cpp:185-194).
-  void register_generator_state(std::shared_ptr<GeneratorState> state, uint64_t wholegraph_increment);
+  // Run `state`'s replay prologue with this increment before every replay:
+  // seed and offset written on the current stream, then the offset advanced
+  // by the increment rounded up to a multiple of 4 (csrc/CUDAGraph.cpp:
+  // 60-86, 185-194).  The one-argument form registers with increment 0.
+  void register_generator_state(c10::intrusive_ptr<at::CUDAGeneratorState> state, uint64_t wholegraph_increment);
+  void register_generator_state(c10::intrusive_ptr<at::CUDAGeneratorState> state);
+  // A torch generator is registered while capturing (csrc/CUDAGraph.cpp:
+  // 180-183); capture is not part of this library, so this throws.
+  void register_generator_state(const at::Generator& generator);
   // Switch the group's exec to this graph (only nodes that differ are
   // re-set), run the generator prologues, launch on the current stream
   // (csrc/CUDAGraph.cpp:330-483).
@@ -145,17 +147,24 @@ struct CUDAGraph {
   int64_t index_ = -1;
   MempoolId_t pool_{0, 0};
   std::shared_ptr<detail::Group> group_;
-  std::vector<std::pair<std::shared_ptr<GeneratorState>, uint64_t>> generators_;
+  std::vector<std::pair<c10::intrusive_ptr<at::CUDAGeneratorState>, uint64_t>> generators_;
 };
 
-// The split-load state (include/CUDAGraphInternal.h:13-28).
+// The split-load state (include/CUDAGraphInternal.h:13-28).  The graphs exist
+// when start_graph_builds returns; the rest is filled in by the worker thread,
+// whose completion (or error) build_complete_ carries.
 struct PendingGraphLoads {
   std::vector<std::shared_ptr<CUDAGraph>> graphs;
+  MempoolId_t pool{0, 0};
+  c10::DeviceIndex dev = 0;
+  CUDAGeneratorStateRegistry* registry = nullptr;  // for the deferred generator registration
+  std::shared_future<void> build_complete_;
+  // Valid once build_complete_ is ready (after a finish call has returned).
   std::vector<uint32_t> template_of;  // per graph: its topology group's template
   bool used_manifest = false;
-  MempoolId_t pool{0, 0};
   struct Impl;
   std::shared_ptr<Impl> impl;
+  ~PendingGraphLoads();  // waits for the worker
 };
 
 }  // namespace foundry

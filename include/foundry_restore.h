@@ -236,9 +236,13 @@ int fdy_switch(fdy_archive* a, uint32_t graph, void* stream);
  * same end state and the same scatter work per switch, with the checks and
  * the device selection done once for the whole sequence instead of per call
  * (for callers that switch graphs many times between launches, and for
- * measuring sustained switches).  Every target is checked before any switch
- * is enqueued; on an error nothing is enqueued.  Counterpart of n calls of
- * the on-demand branch of csrc/CUDAGraph.cpp:330-461. */
+ * measuring sustained switches).  Every target, and every switch's launch
+ * size, is checked before any switch is enqueued: an invalid target or a
+ * switch too large for one launch enqueues nothing.  A HIP failure while
+ * enqueueing (or in a bound group graph's exec update) returns at once:
+ * the switches before it stay enqueued and recorded as current, none after
+ * it is.  Counterpart of n calls of the on-demand branch of
+ * csrc/CUDAGraph.cpp:330-461. */
 int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, void* stream);
 /* Live state of the group whose template is `template_graph`.  Synchronizes.
  * node_src[n] = graph whose own image supplies node n (template unless the
@@ -268,11 +272,14 @@ int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* 
  * An index larger than the array (past 65,536 intervals spread like the
  * relocation-heavy workload's: 64-byte lines, two root lines per interval
  * rounded down to a power of two, plus about a line per four intervals in
- * crowded ranges) is FDY_E_CAPACITY before anything is enqueued.  The index is copied in `stream`'s order and the call waits for
- * those copies, then enqueues the relocation.  Every call on one GPU shares
- * the array: calls on different streams that overlap race (the later index
- * can replace the earlier one under its running kernel); calls in one
- * stream's order do not. */
+ * crowded ranges) is FDY_E_CAPACITY before anything is enqueued.  A table
+ * that differs from the one the array holds has its index built on the
+ * host, copied in `stream`'s order and waited for; a call with the same
+ * table (the same policy and the same lo, hi and new_lo words, compared
+ * exactly) reuses the index as it stands and only enqueues the relocation.
+ * Every call on one GPU shares the array: calls on different streams that
+ * overlap race (the later index can replace the earlier one under its
+ * running kernel); calls in one stream's order do not. */
 #define FDY_STATIC_INDEX_BYTES (8u << 20)
 int fdy_relocate_words_static(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
                               uint32_t policy, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
@@ -299,6 +306,16 @@ typedef struct fdy_restore_timing {
 } fdy_restore_timing;
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
 int fdy_set_timing(fdy_archive* a, int enabled);
+
+/* How long the grouping step of fdy_restore waits for a lower graph's key
+ * hash that its own workgroup has not yet published, in rounds of s_sleep
+ * (about 64 ns each; default 16384, about 1 ms), before the waiting
+ * workgroup hashes that key itself.  0 hashes every unpublished key at
+ * once.  Results do not depend on it; it bounds how long one workgroup can
+ * wait on another that is not resident.  No counterpart in the reference
+ * (its grouping is a single-threaded map, csrc/CUDAGraphParallel.cpp:
+ * 1788-1851). */
+int fdy_set_group_wait(fdy_archive* a, uint32_t spins);
 
 #ifdef __cplusplus
 } /* extern "C" */

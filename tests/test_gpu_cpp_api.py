@@ -38,6 +38,12 @@ def test_cpp_caller_loads_replays_and_outputs(tmp_path):
     lines = [json.loads(x) for x in p.stdout.splitlines() if x.startswith("{")]
     meta = {k: v for d in lines if "graph" not in d for k, v in d.items()}
     assert meta["code_objects"] >= 1
+    # start_graph_builds returns before its worker is done (a 4-graph load
+    # takes milliseconds); reported, not asserted: the decode-style load in
+    # test_gpu_split_load asserts it with a margin of tens of milliseconds.
+    print("C++ start_graph_builds: build complete at return:", meta["ready_at_return"])
+    assert meta["ready_at_return"] in (0, 1)
+    assert meta["corrupt_raised_in_finish"] == 3  # each finish call raises the worker's error
     assert meta["used_manifest"] == 1 and meta["template_of"] == [0, 0, 0, 0]
     assert meta["out_of_range_throws"] == 1
     assert meta["raw_graph_needs_keep_graph"] == 1
@@ -48,6 +54,13 @@ def test_cpp_caller_loads_replays_and_outputs(tmp_path):
     out = saved_out - SAVED_BASE + base
     assert meta["out_ptr"] == out, "the output tensor is a view at the relocated buffer"
     assert meta["done"] == 1
+    # Typed generator state: id 77 made once, its words a 2 MiB region
+    # segment (seed at +0, offset at +512); graph 0 replays twice with
+    # increment 5 (rounded up to 8).
+    assert meta["state_id"] == 77 and meta["same_state"] == 1 and meta["torch_generator_refused"] == 1
+    assert base <= meta["seed_ptr"] < base + SIZE and meta["offset_ptr"] == meta["seed_ptr"] + 512
+    assert meta["rng_seed"] == 1234 and meta["rng_offset"] == 8 and meta["philox_offset"] == 16
+    assert meta["words_released"] == 1
     runs = [d for d in lines if "graph" in d]
     assert [d["graph"] for d in runs] == ORDER
     for d in runs:

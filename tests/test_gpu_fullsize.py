@@ -12,6 +12,7 @@ the interval table alone, not on which other graphs are open.
 import numpy as np
 import pytest
 
+import oracle
 from foundry_amd import synth
 from foundry_amd.restore import Archive
 from oracle import Restore
@@ -105,3 +106,42 @@ def test_1024_graph_archive_switch_sequence(c5):
         w2, src2, cur2 = ref.live(0)
         np.testing.assert_array_equal(w, w2, err_msg=f"live words of group {t} (last graph {g})")
         np.testing.assert_array_equal(src, np.array(pair, dtype=np.uint32)[src2], err_msg=f"node sources of group {t}")
+
+
+@pytest.mark.parametrize("spins", [0, 1])
+def test_1024_graph_grouping_when_keys_are_hashed_by_waiters(c5, spins):
+    """The grouping scan's fallback: a workgroup that finds a lower graph's
+    key hash unpublished hashes that key itself after `spins` rounds of
+    sleep (0: at once, so nearly every lookup takes the fallback).  Graphs
+    above 512 scan the lower graphs in more than one step.  Groups and
+    digests must equal the oracle's key grouping of all 1024 graphs and the
+    default restore's digests; runs after the switch sequence, and leaves
+    the default wait behind."""
+    p, s, arch, _ = c5
+    print(f"[case] preset5-full: grouping with a wait of {spins} spins", flush=True)
+    keys = [oracle.topology_key_saved(s.image(g)) for g in range(s.num_graphs)]
+    want = oracle.group_by_keys(keys)
+    digests = arch.digests()
+    arch.set_group_wait(spins)
+    try:
+        arch.restore()
+        np.testing.assert_array_equal(arch.groups(), want, err_msg="template_of")
+        np.testing.assert_array_equal(arch.digests(), digests, err_msg="digests")
+    finally:
+        arch.set_group_wait(1 << 14)
+        arch.restore()
+    np.testing.assert_array_equal(arch.groups(), want, err_msg="template_of (default wait)")
+
+
+def test_decode_style_grouping_when_keys_are_hashed_by_waiters(cuda):
+    p = synth.preset(2)
+    _case("preset2-full, grouping wait 0", p)
+    s = synth.SynthArchive(p)
+    lo, hi, new_lo = s.intervals()
+    arch = Archive.from_synth(s)
+    arch.set_relocation(lo, hi, new_lo)
+    arch.set_group_wait(0)
+    arch.restore()
+    ref = Restore(s.images(), (lo, hi, new_lo), threads=16)
+    assert_restore_parity(arch, ref, graphs=range(0, s.num_graphs, 17))
+    arch.close()

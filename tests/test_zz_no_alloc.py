@@ -51,3 +51,47 @@ def test_static_relocation_matches_the_plan(cuda):
             torch.cuda.synchronize()
             np.testing.assert_array_equal(d_in.cpu().numpy(), want)
             assert (want != words.view(np.int64)).any()  # the table moved some words
+
+
+@pytest.mark.gpu
+def test_static_relocation_allocates_no_device_memory(cuda):
+    """After a first call on the device, further calls (the same table, a
+    smaller one, then the first again) leave the device's free memory and
+    torch's allocation counts exactly as they were, and each call's words
+    equal the plan's."""
+    torch = cuda
+    big_words, big_iv = _case(1 << 18, 20_000, 0x51A9)
+    small_words, small_iv = _case(50_001, 700, 0x51AA)
+    d_big = torch.from_numpy(big_words.view(np.int64)).to("cuda")
+    d_small = torch.from_numpy(small_words.view(np.int64)).to("cuda")
+    want = {}
+    for name, d, (lo, hi, nlo), n in (("big", d_big, big_iv, len(big_words)),
+                                      ("small", d_small, small_iv, len(small_words))):
+        out = torch.empty_like(d)
+        plan = RelocPlan(lo, hi, nlo, 0)
+        plan.relocate(d.data_ptr(), out.data_ptr(), n)
+        torch.cuda.synchronize()
+        plan.close()
+        want[name] = out.cpu().numpy()
+    out_big = torch.full_like(d_big, -1)
+    out_small = torch.full_like(d_small, -1)
+    relocate_words_static(*big_iv, d_big.data_ptr(), out_big.data_ptr(), len(big_words), 0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out_big.cpu().numpy(), want["big"])
+    free0 = torch.cuda.mem_get_info()[0]
+
+    def requests():  # torch's cumulative counts of device allocation requests and segments
+        return {k: v for k, v in torch.cuda.memory_stats().items()
+                if k.startswith(("allocation.", "segment.")) and k.endswith(".allocated")}
+
+    stats0 = requests()
+    for name, d, dst, iv, n in (("big", d_big, out_big, big_iv, len(big_words)),
+                                ("small", d_small, out_small, small_iv, len(small_words)),
+                                ("big", d_big, out_big, big_iv, len(big_words))):
+        print(f"[case] static relocation, {name} table again: words={n} intervals={len(iv[0])}", flush=True)
+        dst.fill_(-1)
+        relocate_words_static(*iv, d.data_ptr(), dst.data_ptr(), n, 0)
+        torch.cuda.synchronize()
+        assert torch.cuda.mem_get_info()[0] == free0, "device free memory changed"
+        assert requests() == stats0, "torch allocated device memory"
+        np.testing.assert_array_equal(dst.cpu().numpy(), want[name])
