@@ -1721,7 +1721,11 @@ __device__ __forceinline__ void window_node(const uint2* s_gt, uint32_t nwin, ui
   }
 }
 
-__global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
+// Six waves per SIMD: the slots' prefix in scalar registers (readlane)
+// keeps the pass at 80 VGPRs, so the decode-style archive's 5824 slot waves
+// are resident at once (five per SIMD left some for a second round: 26.2 ->
+// 24.5 us).
+__global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
   static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
   // Per wave: {first graph word, first template word} of its window's nodes.
@@ -1751,7 +1755,7 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   }
   uint32_t start[kSubsPerSlot];  // exclusive prefix of the candidate counts, the same in every lane
 #pragma unroll
-  for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __shfl(incl - cnt, q, 64) & 0xFFFFu;
+  for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __builtin_amdgcn_readlane(incl - cnt, q) & 0xFFFFu;
   // Batch b's K candidates per lane, loaded unconditionally (a list index
   // past the end reads the first candidate and is masked off later) so that
   // they are issued together rather than each behind its own branch.  The

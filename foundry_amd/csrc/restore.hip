@@ -3,8 +3,10 @@
 // Host work is limited to what cannot run on the device: reading files,
 // validating section bounds (so device code never indexes outside an image),
 // sizing buffers, and enqueueing the kernels of kernels.hip.
+#include <fcntl.h>
 #include <hip/hip_runtime.h>
 #include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <atomic>
@@ -61,25 +63,129 @@ void parallel_for(uint32_t n, uint32_t threads, F&& f) {
 
 uint32_t default_threads() { return std::max(1u, std::min(16u, std::thread::hardware_concurrency())); }
 
-// Host staging buffer: pinned when possible so the upload runs at full PCIe rate.
-struct HostStage {
-  uint8_t* p = nullptr;
+// The upload of archive images to HBM.  Bytes reach the device through a
+// ring of pinned host slots that the process allocates once and every open
+// reuses (pinning and unpinning an image-sized buffer per open cost more than
+// the copy itself): each upload thread owns two slots and a stream, fills
+// one slot (pread from the file, or memcpy from memory) while the other's
+// copy is in flight, and waits for a slot's previous copy before refilling
+// it.  One upload uses the ring at a time.
+constexpr uint64_t kUploadSlot = 8ull << 20;
+constexpr uint32_t kUploadThreads = 8;
+
+struct UploadRing {
+  std::mutex mu;
+  uint8_t* host = nullptr;  // 2 * kUploadThreads slots, pinned
   bool pinned = false;
-  ~HostStage() {
-    if (!p) return;
-    if (pinned) (void)hipHostFree(p);
-    else std::free(p);
-  }
-  int alloc(size_t bytes) {
-    if (hipHostMalloc(reinterpret_cast<void**>(&p), bytes, hipHostMallocDefault) == hipSuccess) {
-      pinned = true;
-      return FDY_OK;
-    }
-    (void)hipGetLastError();
-    p = static_cast<uint8_t*>(std::malloc(bytes));
-    return p ? FDY_OK : err(FDY_E_NOMEM, "host staging buffer of " + std::to_string(bytes) + " bytes");
-  }
 };
+UploadRing g_ring;
+
+// A stretch of the device image: `len` bytes at `dst`, read from file
+// descriptor `fd` at `foff`, or copied from `src`; `zero` bytes of zeros
+// follow (padding to the next graph).
+struct UploadPiece {
+  uint64_t dst, len, zero;
+  int fd;
+  uint64_t foff;
+  const uint8_t* src;
+};
+
+// Split graph i's bytes (and its padding) into pieces of at most one slot.
+void add_pieces(std::vector<UploadPiece>& out, uint64_t dst, uint64_t len, uint64_t pad, int fd, const uint8_t* src) {
+  if (len == 0 && pad == 0) return;
+  uint64_t at = 0;
+  do {
+    const uint64_t n = std::min(len - at, kUploadSlot);
+    const uint64_t z = at + n == len ? std::min(pad, kUploadSlot - n) : 0;
+    out.push_back({dst + at, n, z, fd, at, src ? src + at : nullptr});
+    if (at + n == len && pad > z) out.push_back({dst + len + z, 0, pad - z, -1, 0, nullptr});
+    at += n;
+  } while (at < len);
+}
+
+int upload(uint8_t* dev, const std::vector<UploadPiece>& pieces, uint32_t threads) {
+  std::lock_guard<std::mutex> lk(g_ring.mu);
+  if (!g_ring.host) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, 2 * kUploadThreads * kUploadSlot, hipHostMallocPortable) == hipSuccess) {
+      g_ring.pinned = true;
+    } else {
+      (void)hipGetLastError();
+      p = std::malloc(2 * kUploadThreads * kUploadSlot);
+      if (!p) return err(FDY_E_NOMEM, "upload ring of " + std::to_string(2 * kUploadThreads * kUploadSlot) + " bytes");
+    }
+    g_ring.host = static_cast<uint8_t*>(p);
+  }
+  int dev_id = 0;
+  FDY_HIP(hipGetDevice(&dev_id));
+  threads = std::max(1u, std::min({threads, kUploadThreads, (uint32_t)pieces.size()}));
+  std::atomic<size_t> next{0};
+  std::vector<std::string> errs(threads);
+  std::vector<int> codes(threads, FDY_OK);
+  auto work = [&](uint32_t t) {
+    auto fail = [&](int code, const std::string& m) {
+      if (codes[t] == FDY_OK) {
+        codes[t] = code;
+        errs[t] = m;
+      }
+    };
+    if (hipSetDevice(dev_id) != hipSuccess) return fail(FDY_E_HIP, "hipSetDevice failed on an upload thread");
+    hipStream_t st = nullptr;
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    if (hipStreamCreateWithFlags(&st, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&ev[0], hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&ev[1], hipEventDisableTiming) != hipSuccess) {
+      fail(FDY_E_HIP, "cannot create an upload stream or event");
+    }
+    bool used[2] = {false, false};
+    for (uint32_t k = 0; codes[t] == FDY_OK;) {
+      const size_t i = next.fetch_add(1);
+      if (i >= pieces.size()) break;
+      const UploadPiece& pc = pieces[i];
+      const uint32_t b = k++ & 1;
+      uint8_t* slot = g_ring.host + (2ull * t + b) * kUploadSlot;
+      if (used[b] && hipEventSynchronize(ev[b]) != hipSuccess) {
+        fail(FDY_E_HIP, "upload copy failed");
+        break;
+      }
+      if (pc.src) {
+        std::memcpy(slot, pc.src, pc.len);
+      } else if (pc.len) {
+        uint64_t got = 0;
+        while (got < pc.len) {
+          const ssize_t r = pread(pc.fd, slot + got, pc.len - got, (off_t)(pc.foff + got));
+          if (r <= 0) break;
+          got += (uint64_t)r;
+        }
+        if (got != pc.len) {
+          fail(FDY_E_IO, "short read");
+          break;
+        }
+      }
+      std::memset(slot + pc.len, 0, pc.zero);
+      if (hipMemcpyAsync(dev + pc.dst, slot, pc.len + pc.zero, hipMemcpyHostToDevice, st) != hipSuccess ||
+          hipEventRecord(ev[b], st) != hipSuccess) {
+        fail(FDY_E_HIP, "upload copy failed");
+        break;
+      }
+      used[b] = true;
+    }
+    if (st && hipStreamSynchronize(st) != hipSuccess) fail(FDY_E_HIP, "upload copy failed");
+    for (hipEvent_t e : ev)
+      if (e) (void)hipEventDestroy(e);
+    if (st) (void)hipStreamDestroy(st);
+  };
+  std::vector<std::thread> pool;
+  for (uint32_t t = 1; t < threads; ++t) pool.emplace_back(work, t);
+  work(0);
+  for (auto& th : pool) th.join();
+  for (uint32_t t = 0; t < threads; ++t)
+    if (codes[t] != FDY_OK) {
+      (void)hipGetLastError();
+      return err(codes[t], "uploading the archive images: " + errs[t]);
+    }
+  return FDY_OK;
+}
 
 int build_reloc_index(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
                       HostIndex* out, uint64_t root_lines_per_interval = kRootLinesPerInterval) {
@@ -115,15 +221,22 @@ struct fdy_reloc_plan {
 
 namespace {
 
-int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& off,
-                const std::vector<uint64_t>& sizes, const std::vector<std::string>& names) {
+// Bytes of a graph's file the host reads before its upload: the header and
+// the section directory, all that validation and the layout need.
+constexpr uint64_t kHeadBytes = sizeof(fdy_file_header) + FDY_SEC_COUNT * sizeof(fdy_section);
+
+// heads[i]: the first min(sizes[i], kHeadBytes) bytes of graph i.  The
+// images themselves reach HBM through `pieces` (the upload ring).
+int finish_open(fdy_archive* a, const std::vector<std::vector<uint8_t>>& heads, const std::vector<uint64_t>& off,
+                const std::vector<uint64_t>& sizes, const std::vector<std::string>& names,
+                const std::vector<UploadPiece>& pieces, uint32_t threads) {
   const uint32_t G = a->G;
   a->graphs.resize(G);
   std::vector<std::string> errs(G);
   const X2nTable x2n = make_x2n_table();
   parallel_for(G, default_threads(), [&](uint32_t i) {
     GraphView v;
-    errs[i] = validate_image(stage.p + off[i], sizes[i], &v);
+    errs[i] = validate_image(heads[i].data(), sizes[i], &v);
     if (!errs[i].empty()) return;
     DevGraph& d = a->graphs[i];
     std::memset(&d, 0, sizeof(d));
@@ -217,7 +330,8 @@ int finish_open(fdy_archive* a, HostStage& stage, const std::vector<uint64_t>& o
   if (!rc) rc = alloc_restore_buffers(a);
   if (rc) return rc;
 
-  FDY_HIP(hipMemcpy(a->img.p, stage.p, a->img_bytes, hipMemcpyHostToDevice));
+  rc = upload(static_cast<uint8_t*>(a->img.p), pieces, threads);
+  if (rc) return rc;
   FDY_HIP(hipMemset(static_cast<uint8_t*>(a->img.p) + a->img_bytes, 0, 4096));
   FDY_HIP(hipMemcpy(a->dgraphs.p, a->graphs.data(), G * sizeof(DevGraph), hipMemcpyHostToDevice));
   auto consts = std::make_unique<CrcConsts>();
@@ -424,28 +538,47 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
   std::vector<std::string> names(n);
   std::vector<uint64_t> sizes(n), off(n);
   std::vector<std::vector<uint8_t>> converted(n);  // graphs read from their JSON document
+  std::vector<std::vector<uint8_t>> heads(n);      // header and section directory of each graph
+  std::vector<int> fds(n, -1);
+  struct Fds {
+    std::vector<int>& v;
+    ~Fds() {
+      for (int fd : v)
+        if (fd >= 0) ::close(fd);
+    }
+  } close_fds{fds};
   std::vector<std::string> errs(n);
   std::vector<int> codes(n, FDY_OK);
   // Which file holds each graph: the .cugraph if it opens with a v1 header
   // (csrc/BinaryGraphIO.cpp:710-737), else the JSON document at the path
   // (csrc/CUDAGraphParallel.cpp:1606-1617), converted as save_binary would.
+  // Phase 1a's reads (csrc/CUDAGraphParallel.cpp:1583-1620) are split: the
+  // header and section directory here, the rest streamed to HBM below.
   parallel_for(n, threads, [&](uint32_t i) {
     const std::string path = paths[i] ? paths[i] : "";
     std::string p = path;
     if (p.size() >= 5 && p.compare(p.size() - 5, 5, ".json") == 0) p = p.substr(0, p.size() - 5) + ".cugraph";
+    heads[i].assign(kHeadBytes, 0);
     struct stat st;
-    if (!p.empty() && stat(p.c_str(), &st) == 0 && S_ISREG(st.st_mode) && (uint64_t)st.st_size >= sizeof(fdy_file_header)) {
+    const int fd = p.empty() ? -1 : ::open(p.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd >= 0 && fstat(fd, &st) == 0 && S_ISREG(st.st_mode) && (uint64_t)st.st_size >= sizeof(fdy_file_header)) {
+      const uint64_t want = std::min<uint64_t>((uint64_t)st.st_size, kHeadBytes);
+      uint64_t got = 0;
+      while (got < want) {
+        const ssize_t r = pread(fd, heads[i].data() + got, want - got, (off_t)got);
+        if (r <= 0) break;
+        got += (uint64_t)r;
+      }
       fdy_file_header h;
-      FILE* f = std::fopen(p.c_str(), "rb");
-      const bool ok = f && std::fread(&h, 1, sizeof h, f) == sizeof h && std::memcmp(h.magic, "CUGRAPH", 8) == 0 &&
-                      h.version == FDY_FORMAT_VERSION;
-      if (f) std::fclose(f);
-      if (ok) {
+      std::memcpy(&h, heads[i].data(), sizeof h);
+      if (got == want && std::memcmp(h.magic, "CUGRAPH", 8) == 0 && h.version == FDY_FORMAT_VERSION) {
         names[i] = p;
         sizes[i] = (uint64_t)st.st_size;
+        fds[i] = fd;
         return;
       }
     }
+    if (fd >= 0) ::close(fd);
     names[i] = path;
     std::string text;
     FILE* f = path.empty() ? nullptr : std::fopen(path.c_str(), "rb");
@@ -459,42 +592,28 @@ int fdy_archive_open(const char* const* paths, uint32_t n, uint32_t num_threads,
     while ((got = std::fread(buf, 1, sizeof buf, f)) > 0) text.append(buf, got);
     std::fclose(f);
     codes[i] = fdy::cugraph_for_load(text.data(), text.size(), converted[i], errs[i]);
-    if (codes[i] == FDY_OK) sizes[i] = converted[i].size();
-    else errs[i] = path + ": " + errs[i];
+    if (codes[i] == FDY_OK) {
+      sizes[i] = converted[i].size();
+      std::memcpy(heads[i].data(), converted[i].data(), std::min<uint64_t>(sizes[i], kHeadBytes));
+    } else {
+      errs[i] = path + ": " + errs[i];
+    }
   });
   for (uint32_t i = 0; i < n; ++i)
     if (codes[i] != FDY_OK) return err(codes[i], errs[i]);
   uint64_t at = 0;
+  std::vector<UploadPiece> pieces;
   for (uint32_t i = 0; i < n; ++i) {
     off[i] = at;
-    at = align_up(at + sizes[i], 256);
+    const uint64_t end = align_up(at + sizes[i], 256);
+    add_pieces(pieces, at, sizes[i], end - at - sizes[i], fds[i], converted[i].empty() ? nullptr : converted[i].data());
+    at = end;
   }
   auto a = std::make_unique<fdy_archive>();
   (void)hipGetDevice(&a->device);
   a->G = n;
   a->img_bytes = at;
-  HostStage stage;
-  int rc = stage.alloc(at ? at : 256);
-  if (rc) return rc;
-  // Phase 1a: parallel reads (csrc/CUDAGraphParallel.cpp:1583-1620), straight into the staging buffer.
-  parallel_for(n, threads, [&](uint32_t i) {
-    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
-    if (!converted[i].empty() || sizes[i] == 0) {
-      if (sizes[i]) std::memcpy(stage.p + off[i], converted[i].data(), sizes[i]);
-      return;
-    }
-    FILE* f = std::fopen(names[i].c_str(), "rb");
-    if (!f) {
-      errs[i] = "cannot open";
-      return;
-    }
-    size_t got = std::fread(stage.p + off[i], 1, sizes[i], f);
-    std::fclose(f);
-    if (got != sizes[i]) errs[i] = "short read";
-  });
-  for (uint32_t i = 0; i < n; ++i)
-    if (!errs[i].empty()) return err(FDY_E_IO, names[i] + ": " + errs[i]);
-  rc = finish_open(a.get(), stage, off, sizes, names);
+  const int rc = finish_open(a.get(), heads, off, sizes, names, pieces, std::max(threads, default_threads()));
   if (rc) return rc;
   *out = a.release();
   return FDY_OK;
@@ -505,25 +624,24 @@ int fdy_archive_open_images(const uint8_t* const* images, const uint64_t* sizes_
   *out = nullptr;
   std::vector<std::string> names(n);
   std::vector<uint64_t> sizes(sizes_in, sizes_in + n), off(n);
+  std::vector<std::vector<uint8_t>> heads(n);
+  std::vector<UploadPiece> pieces;
   uint64_t at = 0;
   for (uint32_t i = 0; i < n; ++i) {
     if (!images[i] && sizes[i]) return err(FDY_E_INVALID, "null image " + std::to_string(i));
     names[i] = "image " + std::to_string(i);
+    heads[i].assign(kHeadBytes, 0);
+    if (sizes[i]) std::memcpy(heads[i].data(), images[i], std::min<uint64_t>(sizes[i], kHeadBytes));
     off[i] = at;
-    at = align_up(at + sizes[i], 256);
+    const uint64_t end = align_up(at + sizes[i], 256);
+    add_pieces(pieces, at, sizes[i], end - at - sizes[i], -1, images[i]);
+    at = end;
   }
   auto a = std::make_unique<fdy_archive>();
   (void)hipGetDevice(&a->device);
   a->G = n;
   a->img_bytes = at;
-  HostStage stage;
-  int rc = stage.alloc(at ? at : 256);
-  if (rc) return rc;
-  parallel_for(n, default_threads(), [&](uint32_t i) {
-    if (sizes[i]) std::memcpy(stage.p + off[i], images[i], sizes[i]);
-    std::memset(stage.p + off[i] + sizes[i], 0, align_up(sizes[i], 256) - sizes[i]);
-  });
-  rc = finish_open(a.get(), stage, off, sizes, names);
+  const int rc = finish_open(a.get(), heads, off, sizes, names, pieces, default_threads());
   if (rc) return rc;
   *out = a.release();
   return FDY_OK;
