@@ -61,7 +61,7 @@ class ArchiveInfo(C.Structure):
         ("num_intervals", C.c_uint64),
         ("device_bytes", C.c_uint64),
         ("serving_layout", C.c_uint32),
-        ("pad_", C.c_uint32),
+        ("scratch", C.c_uint32),
     ]
 
 

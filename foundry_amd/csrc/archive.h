@@ -87,16 +87,25 @@ struct fdy_archive {
   fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
   fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_gt, units, chunks, slot_desc, live_cur, tslots;
-  fdy::DevBuf aux, image, live, ovr, cand, sub_count, slot_rec, gaps, node_pbytes, key_hash;
+  fdy::DevBuf aux, image, live, ovr, cand, sub_count, slot_rec, restore_flags, node_pbytes, key_hash;
+  fdy::DevBuf slot_spill, sub_off;
 
   fdy::RelocPlan reloc;
-  // Serving layout, taken when the first group graph is bound (no restore
+  // Restoring layout: R_g at word_base(g); graph g's override records from
+  // word_base(g) >> rec_shift; the scratch (candidate regions and spill
+  // space, ragged-word sources once a restore has found a ragged node) at
+  // the archive's scratch level.  Live images exist for the templates only (template t's
+  // from h_live_base[t]), filled from R_t when results are first read after
+  // a restore.
+  //   Serving layout, taken when the first group graph is bound (no restore
   // can run until the last is destroyed): override records packed in
-  // canonical order (graph g's from h_ovr_off[g]), live images for the
-  // templates only (template t's from h_live_base[t]), each R_g packed to
-  // its words (from h_r_base[g]), and the restore's scratch (candidates,
-  // ragged-word sources) freed.  Otherwise all three start at word_base.
+  // canonical order (graph g's from h_ovr_off[g]), each R_g packed to its
+  // words (from h_r_base[g]), and the restore's scratch freed.
   bool compact = false;
+  uint32_t scratch_level = 0;  // kScratchLevels index: raised by a restore that overflowed, kept from then on
+  bool need_aux = false;       // a restore found a ragged node: ragged-word sources from then on
+  uint32_t rec_shift = 0, cand_cap = 0, spill_cap = 0;
+  bool live_ready = false;    // live images filled from this restore's R
   std::vector<uint64_t> h_live_base, h_r_base;  // h_r_base[g]: first word of R_g, packed to its words
   bool use_explicit = false;
   bool restored = false;
@@ -145,20 +154,20 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
 // First override record of graph g, first live word of template t, and
 // first word of R_g, in the current layout.
 inline uint64_t ovr_base(const fdy_archive* a, uint32_t g) {
-  return a->compact ? a->h_ovr_off[g] : a->graphs[g].word_base;
+  return a->compact ? a->h_ovr_off[g] : a->graphs[g].word_base >> a->rec_shift;
 }
-inline uint64_t live_base(const fdy_archive* a, uint32_t t) {
-  return a->compact ? a->h_live_base[t] : a->graphs[t].word_base;
-}
+inline uint64_t live_base(const fdy_archive* a, uint32_t t) { return a->h_live_base[t]; }
 inline uint64_t r_base(const fdy_archive* a, uint32_t g) {
   return a->compact ? a->h_r_base[g] : a->graphs[g].word_base;
 }
 // Take the serving layout (after a restore, before the first group graph is
 // bound); synchronizes `s`.
 int compact_for_serving(fdy_archive* a, hipStream_t s);
-// The restore's buffers at full capacity: override records and live images
-// at word_base, candidates and ragged-word sources.
+// The restore's override records and scratch at the archive's scratch
+// level, with ragged-word sources when need_aux.
 int alloc_restore_buffers(fdy_archive* a);
+// Enqueue the restore kernels on `s` (fdy_restore after its checks).
+int enqueue_restore(fdy_archive* a, hipStream_t s);
 // Device bytes the archive holds.
 uint64_t held_bytes(const fdy_archive* a);
 

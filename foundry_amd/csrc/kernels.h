@@ -41,16 +41,21 @@ struct RestoreArgs {
   uint32_t* tslots;           // slots of template graphs holding words (capacity: num_slots)
   uint32_t* tslot_count;      // entries of tslots
   SlotDesc* slot_desc;        // per slot
-  uint64_t* aux;              // ragged-word sources (per word)
+  uint64_t* aux;              // ragged-word sources (per word), or null until a restore finds a ragged node
   uint64_t* image;            // relocated param images R
-  uint64_t* live;             // live images (template graphs)
   uint32_t* live_src;         // per node
   uint32_t* live_cur;         // per graph
-  fdy_override* ovr;          // override records: graph g's in canonical order from index word_base(g)
-  Candidate* cand;            // per (slot, sub-range): kSubWords candidates, then as many records
+  fdy_override* ovr;          // override records: graph g's in canonical order from index word_base(g) >> rec_shift,
+                              // at most ((word_base + word_cap) >> rec_shift) - (word_base >> rec_shift) of them
+  uint32_t rec_shift;         // 0: a record per capacity word; kCompactShift: one per 2^kCompactShift
+  uint32_t cand_cap;          // candidates in a sub-range's own region (kSubWords, or fewer with spill space)
+  uint32_t spill_cap;         // candidates a slot's sub-ranges can spill past their own regions (0: none)
+  Candidate* cand;            // per slot: kSubsPerSlot regions of cand_cap candidates, then spill_cap more
+  uint32_t* slot_spill;       // per slot: spill entries taken by this restore
+  uint32_t* sub_off;          // per (slot, sub-range): first entry of its candidate list in the slot's area
   uint32_t* sub_count;        // per (slot, sub-range): candidates | compared candidates << 16
   uint32_t* slot_rec;         // records per slot
-  uint32_t* gaps;             // nonzero: some slot made fewer records than its bound
+  uint32_t* restore_flags;    // kFlag* raised by this restore
   uint64_t* node_pbytes;      // param bytes per node (nodes the first node pass handles itself)
   RelocDev reloc;
 };
@@ -68,6 +73,7 @@ struct RepackArgs {
   const uint32_t* slot_rec;
   fdy_override* ovr;
   uint32_t num_graphs;
+  uint32_t rec_shift;
 };
 hipError_t launch_repack(const RepackArgs& a, hipStream_t s);
 

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
   const uint32_t i = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (i == 0 && tid == 0) {
     *a.tslot_count = 0;  // the node pass lists template slots here
-    *a.gaps = 0;         // the search pass flags gapped override arrays here
+    *a.restore_flags = 0;  // kFlag* raised by the later passes
   }
   const DevGraph& Gi = a.graphs[i];
   if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
@@ -1179,7 +1179,8 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
           bool same_;
           side_header(img, Gg, RawEntry{eg}, sd_);
           scan_params(img, Gg, sd_, true, Gg, none_, false, &same_);
-          write_aux(img, Gg, eg, sd_, a.aux, gword);
+          if (a.aux) write_aux(img, Gg, eg, sd_, a.aux, gword);
+          else atomicOr(a.restore_flags, kFlagNeedAux);  // the host restores again with ragged-word sources
         }
       }
     }
@@ -1236,6 +1237,7 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     sd.pad[0] = sd.pad[1] = 0;
     sd.t_word_base = Gt.word_base;
     a.slot_desc[Gg.tile_base + k] = sd;
+    a.slot_spill[Gg.tile_base + k] = 0;
     if (is_t && k < first_unused) a.tslots[s_tbase + k] = Gg.tile_base + k;
   }
 }
@@ -1337,6 +1339,10 @@ __device__ inline NodeDesc window_desc(const NodeDesc* s_nd, const NodeWindow& n
 __device__ inline uint64_t load_word(const RestoreArgs& a, const DevGraph& G, const NodeDesc& d, uint64_t w,
                                      bool ragged, uint64_t src, uint32_t* width) {
   if (ragged) {
+    if (!a.aux) {  // flagged by the node pass: this restore's results are discarded and it runs again
+      *width = 8;
+      return 0;
+    }
     const uint64_t x = a.aux[G.word_base + w];
     *width = (uint32_t)(x & 15);
     return load_bytes(a.img, x >> 4, *width);
@@ -1464,14 +1470,10 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
 #pragma unroll
     for (uint32_t q = 0; q < kTWords; ++q) r[q] = ((need >> q) & 1) ? sq[rank[q]] : v[q];
     uint64_t* img_out = a.image + sd.word_base;
-    uint64_t* live_out = a.live + sd.word_base;
 #pragma unroll
     for (uint32_t q = 0; q < kTWords; ++q) {
       const uint64_t w = ubeg + q * kTThreads + tid;
-      if (w < uend) {
-        img_out[w] = r[q];
-        live_out[w] = r[q];
-      }
+      if (w < uend) img_out[w] = r[q];
     }
   }
   // The collision report, one graph per workgroup in turn, from the last
@@ -1641,7 +1643,6 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   // words: one or two wide stores per wave where storing each word's
   // candidate directly took two narrow stores per word (measured: 91 -> 86 us
   // for the 256-graph decode-style archive).
-  Candidate* out = a.cand + ((uint64_t)slot * kSubsPerSlot + wave) * kSubWords;
   const uint64_t lt = (1ull << lane) - 1;
   if (!flat) __syncthreads();  // every wave of the workgroup is done with the node window
   Candidate* stage = reinterpret_cast<Candidate*>(s_nd) + (tid >> 6) * kSubWords;
@@ -1660,17 +1661,40 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
     }
     run += (uint32_t)__popcll(mk);
   }
+  // The first cand_cap candidates go to the sub-range's own region, the
+  // rest to the slot's spill space (taken with one atomic, by the few waves
+  // whose sub-range has that many; never with the full layout, whose
+  // regions hold a whole sub-range).  Spill space that runs out raises the
+  // overflow flag and keeps the region's share, so every later read stays
+  // in bounds.
+  const uint32_t C = a.cand_cap;
+  uint32_t keep = run, spill = 0;
+  if (run > C) {  // uniform over the wave
+    uint32_t at = 0;
+    if (lane == 0) at = atomicAdd(a.slot_spill + slot, run - C);
+    at = __shfl(at, 0, 64);
+    if (at + (run - C) <= a.spill_cap) {
+      spill = kSubsPerSlot * C + at;
+    } else {
+      keep = C;
+      if (lane == 0) atomicOr(a.restore_flags, kFlagOverflow);
+    }
+  }
   {
     static_assert(sizeof(Candidate) % 8 == 0, "candidates copy as 8-byte words");
     constexpr uint32_t kCandWords = sizeof(Candidate) / 8;
     const uint64_t* src = reinterpret_cast<const uint64_t*>(stage);
-    uint64_t* dst = reinterpret_cast<uint64_t*>(out);
-    for (uint32_t i = lane; i < run * kCandWords; i += 64) dst[i] = src[i];
+    uint64_t* area = reinterpret_cast<uint64_t*>(a.cand + (uint64_t)slot * (kSubsPerSlot * C + a.spill_cap));
+    for (uint32_t i = lane; i < keep * kCandWords; i += 64)
+      area[i < C * kCandWords ? wave * C * kCandWords + i : (spill - C) * kCandWords + i] = src[i];
   }
   // Candidates in the low half, compared candidates (a bound on the
   // records they make) in the high half: the search pass places a slot's
   // records after the bounds of its graph's earlier slots.
-  if (lane == 0) sub_count[wave] = run | (ncmp << 16);
+  if (lane == 0) {
+    sub_count[wave] = keep | (ncmp << 16);
+    if (keep > C) a.sub_off[(uint64_t)slot * kSubsPerSlot + wave] = spill;  // where the rest went
+  }
   if (tid == 0 && part == 0 && (sd.flags & kSlotFirst)) {
     if (a.digests[4ull * g + 2] != a.digests[4ull * t + 2]) atomicOr(&a.status[g], FDY_GRAPH_TYPE_MISMATCH);
   }
@@ -1721,15 +1745,15 @@ __device__ __forceinline__ void window_node(const uint2* s_gt, uint32_t nwin, ui
   }
 }
 
-// Six waves per SIMD: the slots' prefix in scalar registers (readlane)
-// keeps the pass at 80 VGPRs, so the decode-style archive's 5824 slot waves
-// are resident at once (five per SIMD left some for a second round: 26.2 ->
-// 24.5 us).
-__global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
+// Five waves per SIMD (88 VGPRs).  Six need 80, and the spills that takes
+// cost more than the residency gains (27.6 against 26.2 us on the
+// decode-style archive).
+__global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
   static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
   // Per wave: {first graph word, first template word} of its window's nodes.
   __shared__ uint2 s_win[kSThreads / 64][kDiffWindow];
+  __shared__ uint32_t s_off[kSThreads / 64][kSubsPerSlot];
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t slot = blockIdx.x * (kSThreads / 64) + (threadIdx.x >> 6);
   if (slot >= a.num_slots) return;  // per wave: this kernel has no barrier
@@ -1737,6 +1761,12 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   uint32_t* counts = a.sub_count + (uint64_t)slot * kSubsPerSlot;
   // What depends on the slot alone is loaded first.
   const uint32_t cnt = lane < kSubsPerSlot ? counts[lane] : 0;
+  // A sub-range's list is its own region, continued in the slot's spill
+  // space where the member pass recorded (only for lists longer than the
+  // region).
+  const uint32_t C = a.cand_cap;
+  const uint32_t so =
+      lane < kSubsPerSlot && (cnt & 0xFFFFu) > C ? a.sub_off[(uint64_t)slot * kSubsPerSlot + lane] : 0u;
   const SlotDesc sd = load_slot(a.slot_desc + slot);
   const uint32_t n0 = a.tile_node[slot];
   const uint32_t n_after = slot + 1 < a.num_slots ? a.tile_node[slot + 1] : kNoTile;
@@ -1753,15 +1783,24 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
     if (lane == 0) a.slot_rec[slot] = 0;
     return;
   }
-  uint32_t start[kSubsPerSlot];  // exclusive prefix of the candidate counts, the same in every lane
+  // Per sub-range: the exclusive prefix of the candidate counts (the same
+  // in every lane), and where its list continues in the slot's spill space
+  // (in the wave's LDS: a select over sixteen of them per candidate cost
+  // spills).
+  uint32_t start[kSubsPerSlot];
 #pragma unroll
   for (uint32_t q = 0; q < kSubsPerSlot; ++q) start[q] = __builtin_amdgcn_readlane(incl - cnt, q) & 0xFFFFu;
+  uint32_t* const s_o = s_off[threadIdx.x >> 6];
+  if (lane < kSubsPerSlot) s_o[lane] = so;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   // Batch b's K candidates per lane, loaded unconditionally (a list index
   // past the end reads the first candidate and is masked off later) so that
   // they are issued together rather than each behind its own branch.  The
   // first batch is loaded before the bounds and the node window, the next
   // one before the current one's searches, so no load waits alone.
-  const Candidate* base = a.cand + (uint64_t)slot * kSubsPerSlot * kSubWords;
+  const Candidate* base = a.cand + (uint64_t)slot * (kSubsPerSlot * a.cand_cap + a.spill_cap);
   auto load_batch = [&](uint32_t b, Candidate* cand) {
 #pragma unroll
     for (uint32_t kk = 0; kk < K; ++kk) {
@@ -1773,7 +1812,8 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
       uint32_t sq = start[0];
 #pragma unroll
       for (uint32_t s = 1; s < kSubsPerSlot; ++s) sq = q == s ? start[s] : sq;
-      cand[kk] = base[(uint64_t)q * kSubWords + (i - sq)];
+      const uint32_t j = i - sq;
+      cand[kk] = base[j < C ? q * C + j : s_o[q] + (j - C)];
     }
   };
   Candidate cur[K];
@@ -1808,7 +1848,19 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   uint64_t* img_out = a.image + sd.word_base;
-  fdy_override* rec = a.ovr + sd.word_base + before;
+  // The graph's record region: in the compact layout it can be smaller than
+  // the records' bound, and then nothing is written and the restore runs
+  // again with full-capacity scratch.
+  const uint64_t rb = G.word_base >> a.rec_shift;
+  const uint64_t rcap = ((G.word_base + G.word_cap) >> a.rec_shift) - rb;
+  if ((uint64_t)before + bound > rcap) {  // uniform over the wave
+    if (lane == 0) {
+      a.slot_rec[slot] = 0;
+      atomicOr(a.restore_flags, kFlagOverflow);
+    }
+    return;
+  }
+  fdy_override* rec = a.ovr + rb + before;
   const uint64_t lt = (1ull << lane) - 1;
   uint32_t run = 0;
   for (uint32_t b = 0; b < total; b += kSBatch) {
@@ -1849,7 +1901,7 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   }
   if (lane == 0) {
     a.slot_rec[slot] = run;
-    if (run != bound) atomicOr(a.gaps, 1u);  // rare: a compared word equal once relocated
+    if (run != bound) atomicOr(a.restore_flags, kFlagGaps);  // rare: a compared word equal once relocated
   }
 }
 
@@ -1879,7 +1931,7 @@ __global__ __launch_bounds__(kRepackThreads) void k_repack(RepackArgs a) {
 #pragma unroll
   for (uint32_t w = 0; w < kRepackThreads / 64; ++w) gap |= s_part[w];
   if (!gap) return;  // uniform over the workgroup
-  fdy_override* ovr = a.ovr + G.word_base;
+  fdy_override* ovr = a.ovr + (G.word_base >> a.rec_shift);
   uint32_t bound_at = 0, rec_at = 0;  // the slot's place by the bounds, and its canonical place
   for (uint32_t k = 0; k < G.tile_cap; ++k) {
     const uint32_t slot = G.tile_base + k;

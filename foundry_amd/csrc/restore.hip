@@ -311,7 +311,8 @@ int finish_open(fdy_archive* a, const std::vector<std::vector<uint8_t>>& heads, 
       {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
       {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
       {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->slot_rec, 4 * slots},
-      {&a->gaps, 4},
+      {&a->restore_flags, 4},               {&a->slot_spill, 4 * slots},
+      {&a->sub_off, 4 * slots * kSubsPerSlot},
   };
   uint64_t arena_bytes = 0;
   for (const auto& pt : parts) arena_bytes += (pt.second + 255) / 256 * 256;
@@ -350,12 +351,46 @@ namespace fdy {
 
 int alloc_restore_buffers(fdy_archive* a) {
   const uint64_t words = a->total_cap;
-  int rc = dev_alloc(a->cand, sizeof(Candidate) * (uint64_t)kTileWords * a->num_slots, "candidate and record regions");
-  if (!rc) rc = dev_alloc(a->aux, 8 * words, "ragged word sources");
-  if (!rc) rc = dev_alloc(a->live, 8 * words, "live images");
-  if (!rc) rc = dev_alloc(a->ovr, sizeof(fdy_override) * words, "override records");
+  const ScratchLevel& L = kScratchLevels[a->scratch_level];
+  a->ovr.release();
+  a->cand.release();
+  a->aux.release();
+  a->rec_shift = L.rec_shift;
+  a->cand_cap = L.cand_cap;
+  a->spill_cap = L.spill_cap;
+  int rc = dev_alloc(a->cand, sizeof(Candidate) * ((uint64_t)a->cand_cap * kSubsPerSlot + a->spill_cap) * a->num_slots,
+                     "candidate regions");
+  if (!rc && a->need_aux) rc = dev_alloc(a->aux, 8 * words, "ragged word sources");
+  if (!rc) rc = dev_alloc(a->ovr, sizeof(fdy_override) * std::max<uint64_t>(1, words >> a->rec_shift), "override records");
   if (!rc) a->compact = false;
   return rc;
+}
+
+// The templates' live images, filled from R (after a restore, once its
+// results are settled).
+int fill_live(fdy_archive* a, hipStream_t s) {
+  const uint32_t G = a->G;
+  std::vector<uint64_t> lbase(G, 0);
+  uint64_t live_words = 0;
+  for (uint32_t g = 0; g < G; ++g)
+    if (a->h_tmpl[g] == g) {
+      lbase[g] = live_words;
+      live_words += a->graphs[g].word_cap;
+    }
+  const uint64_t bytes = 8 * std::max<uint64_t>(1, live_words);
+  if (a->live.bytes != bytes) {
+    a->live.release();
+    int rc = dev_alloc(a->live, bytes, "template live images");
+    if (rc) return rc;
+  }
+  for (uint32_t g = 0; g < G; ++g)
+    if (a->h_tmpl[g] == g && a->h_gwords[g])
+      FDY_HIP(hipMemcpyAsync(a->live.as<uint64_t>() + lbase[g], a->image.as<uint64_t>() + r_base(a, g),
+                             8ull * a->h_gwords[g], hipMemcpyDeviceToDevice, s));
+  FDY_HIP(hipStreamSynchronize(s));
+  a->h_live_base = std::move(lbase);
+  a->live_ready = true;
+  return FDY_OK;
 }
 
 int compact_for_serving(fdy_archive* a, hipStream_t s) {
@@ -363,41 +398,31 @@ int compact_for_serving(fdy_archive* a, hipStream_t s) {
   int rc = ensure_cache(a, s);
   if (rc) return rc;
   const uint32_t G = a->G;
-  std::vector<uint64_t> lbase(G, 0), rbase(G, 0);
-  uint64_t live_words = 0, r_words = 0;
+  std::vector<uint64_t> rbase(G, 0);
+  uint64_t r_words = 0;
   for (uint32_t g = 0; g < G; ++g) {
     rbase[g] = r_words;
     r_words += a->h_gwords[g];
-    if (a->h_tmpl[g] == g) {
-      lbase[g] = live_words;
-      live_words += a->graphs[g].word_cap;
-    }
   }
-  DevBuf ovr, live, image;
+  DevBuf ovr, image;
   rc = dev_alloc(ovr, sizeof(fdy_override) * std::max<uint64_t>(1, a->h_ovr_off[G]), "packed override records");
-  if (!rc) rc = dev_alloc(live, 8 * std::max<uint64_t>(1, live_words), "template live images");
   if (!rc) rc = dev_alloc(image, 8 * std::max<uint64_t>(1, r_words), "packed param images");
   if (rc) return rc;
   FDY_HIP(hipSetDevice(a->device));
   for (uint32_t g = 0; g < G; ++g) {
     const uint64_t n = a->h_ovr_off[g + 1] - a->h_ovr_off[g];
     if (n)
-      FDY_HIP(hipMemcpyAsync(ovr.as<fdy_override>() + a->h_ovr_off[g], a->ovr.as<fdy_override>() + a->graphs[g].word_base,
+      FDY_HIP(hipMemcpyAsync(ovr.as<fdy_override>() + a->h_ovr_off[g], a->ovr.as<fdy_override>() + ovr_base(a, g),
                              sizeof(fdy_override) * n, hipMemcpyDeviceToDevice, s));
-    if (a->h_tmpl[g] == g && a->graphs[g].word_cap)
-      FDY_HIP(hipMemcpyAsync(live.as<uint64_t>() + lbase[g], a->live.as<uint64_t>() + a->graphs[g].word_base,
-                             8ull * a->graphs[g].word_cap, hipMemcpyDeviceToDevice, s));
     if (a->h_gwords[g])
       FDY_HIP(hipMemcpyAsync(image.as<uint64_t>() + rbase[g], a->image.as<uint64_t>() + a->graphs[g].word_base,
                              8ull * a->h_gwords[g], hipMemcpyDeviceToDevice, s));
   }
   FDY_HIP(hipStreamSynchronize(s));
   a->ovr.swap(ovr);
-  a->live.swap(live);
   a->image.swap(image);
   a->cand.release();
   a->aux.release();
-  a->h_live_base = std::move(lbase);
   a->h_r_base = std::move(rbase);
   a->compact = true;
   return FDY_OK;
@@ -416,6 +441,26 @@ int ensure_cache(fdy_archive* a, hipStream_t s) {
   if (a->cached) return FDY_OK;
   FDY_HIP(hipStreamSynchronize(s));
   const uint32_t G = a->G;
+  uint32_t flags = 0;
+  FDY_HIP(hipMemcpy(&flags, a->restore_flags.p, 4, hipMemcpyDeviceToHost));
+  while (flags & (kFlagNeedAux | kFlagOverflow)) {
+    // The restore found a ragged node without ragged-word sources, or ran
+    // out of scratch: its results are discarded, and it runs again with what
+    // it lacked (kept for every later restore of this archive).
+    if (flags & kFlagNeedAux) {
+      if (a->need_aux) return err(FDY_E_STATE, "the restore asked again for ragged-word sources it had");
+      a->need_aux = true;
+    }
+    if (flags & kFlagOverflow) {
+      if (a->scratch_level == kScratchFull) return err(FDY_E_STATE, "the restore overflowed full-capacity scratch");
+      ++a->scratch_level;
+    }
+    int rc = alloc_restore_buffers(a);
+    if (!rc) rc = enqueue_restore(a, s);
+    if (rc) return rc;
+    FDY_HIP(hipStreamSynchronize(s));
+    FDY_HIP(hipMemcpy(&flags, a->restore_flags.p, 4, hipMemcpyDeviceToHost));
+  }
   a->h_tmpl.resize(G);
   a->h_status.resize(G);
   a->h_gwords.resize(G);
@@ -425,11 +470,9 @@ int ensure_cache(fdy_archive* a, hipStream_t s) {
   // record and leaves a gap where the search pass placed its slot's records
   // by their bounds: such override arrays are closed up before anything
   // reads them (rare; never in archives without such words).
-  uint32_t gaps = 0;
-  FDY_HIP(hipMemcpy(&gaps, a->gaps.p, 4, hipMemcpyDeviceToHost));
-  if (gaps) {
+  if (flags & kFlagGaps) {
     RepackArgs rp{a->dgraphs.as<DevGraph>(), a->sub_count.as<uint32_t>(), a->slot_rec.as<uint32_t>(),
-                  a->ovr.as<fdy_override>(), G};
+                  a->ovr.as<fdy_override>(), G, a->rec_shift};
     FDY_HIP(launch_repack(rp, s));
     FDY_HIP(hipStreamSynchronize(s));
   }
@@ -450,6 +493,8 @@ int ensure_cache(fdy_archive* a, hipStream_t s) {
   }
   a->h_current.resize(G);
   for (uint32_t i = 0; i < G; ++i) a->h_current[i] = i;
+  int rc = fill_live(a, s);
+  if (rc) return rc;
   a->cached = true;
   return FDY_OK;
 }
@@ -525,6 +570,80 @@ int copy_out(const void* dev, uint64_t n, T* out, uint64_t cap, uint64_t* n_out)
 }
 
 }  // namespace
+
+namespace fdy {
+
+int enqueue_restore(fdy_archive* a, hipStream_t s) {
+  RestoreArgs r{};
+  r.img = a->img.as<uint8_t>();
+  r.graphs = a->dgraphs.as<DevGraph>();
+  r.cc = a->cc.as<CrcConsts>();
+  r.num_graphs = a->G;
+  r.num_slots = a->num_slots;
+  r.num_chunks = a->num_chunks;
+  r.chunk_gt = a->chunk_gt.as<uint2>();
+  r.num_units = a->num_units;
+  r.units = a->units.as<DigestUnit>();
+  r.chunks = a->chunks.as<NodeChunk>();
+  r.digests = a->digests.as<uint64_t>();
+  r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
+  r.key_hash = a->key_hash.as<uint64_t>();
+  a->epoch = a->epoch % 65535 + 1;
+  r.epoch = a->epoch;
+  r.hash_wait_spins = a->hash_wait_spins;
+  r.template_of = a->tmpl.as<uint32_t>();
+  r.status = a->status.as<uint32_t>();
+  r.gwords = a->gwords.as<uint32_t>();
+  r.pbytes = a->pbytes.as<uint64_t>();
+  r.node_flags = a->nflags.as<uint8_t>();
+  r.node_desc = a->ndesc.as<NodeDesc>();
+  r.node_ptrs = a->nptrs.as<uint64_t>();
+  r.tile_node = a->tile_node.as<uint32_t>();
+  r.tslots = a->tslots.as<uint32_t>();
+  r.tslot_count = a->tslots.as<uint32_t>() + a->num_slots;
+  r.slot_desc = a->slot_desc.as<SlotDesc>();
+  r.aux = a->aux.as<uint64_t>();
+  r.image = a->image.as<uint64_t>();
+  r.live_src = a->live_src.as<uint32_t>();
+  r.live_cur = a->live_cur.as<uint32_t>();
+  r.ovr = a->ovr.as<fdy_override>();
+  r.rec_shift = a->rec_shift;
+  r.cand_cap = a->cand_cap;
+  r.spill_cap = a->spill_cap;
+  r.cand = a->cand.as<Candidate>();
+  r.slot_spill = a->slot_spill.as<uint32_t>();
+  r.sub_off = a->sub_off.as<uint32_t>();
+  r.sub_count = a->sub_count.as<uint32_t>();
+  r.slot_rec = a->slot_rec.as<uint32_t>();
+  r.restore_flags = a->restore_flags.as<uint32_t>();
+  r.node_pbytes = a->node_pbytes.as<uint64_t>();
+  r.reloc = a->reloc.dev;
+  if (a->timing) {
+    for (hipEvent_t& e : a->ev)
+      if (!e) FDY_HIP(hipEventCreate(&e));
+    FDY_HIP(hipEventRecord(a->ev[0], s));
+  }
+  // Grouping first (the key and dependency digests run beside the second
+  // node pass).
+  FDY_HIP(launch_group(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
+  FDY_HIP(launch_node(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
+  FDY_HIP(launch_diff_templates(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
+  FDY_HIP(launch_diff_members(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
+  FDY_HIP(launch_diff_search(r, s));
+  if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
+  a->timed = a->timing;
+  a->restored = true;
+  a->cached = false;
+  a->live_ready = false;
+  a->last_stream = s;
+  return FDY_OK;
+}
+
+}  // namespace fdy
 
 extern "C" {
 
@@ -664,10 +783,8 @@ int fdy_archive_info_get(fdy_archive* a, fdy_archive_info* o) {
   o->total_nodes = a->total_nodes;
   o->file_bytes = a->img_bytes;
   o->num_intervals = a->reloc.dev.n;
-  o->device_bytes = held_bytes(a);
-  o->serving_layout = a->compact ? 1u : 0u;
   if (a->restored) {
-    int rc = ensure_cache(a, a->last_stream);
+    int rc = ensure_cache(a, a->last_stream);  // settles the restore (a second run if it lacked scratch)
     if (rc) return rc;
     for (uint32_t i = 0; i < a->G; ++i) {
       o->num_groups += a->h_tmpl[i] == i;
@@ -676,6 +793,9 @@ int fdy_archive_info_get(fdy_archive* a, fdy_archive_info* o) {
     }
     o->total_overrides = a->h_ovr_off[a->G];
   }
+  o->device_bytes = held_bytes(a);
+  o->serving_layout = a->compact ? 1u : 0u;
+  o->scratch = a->scratch_level | (a->need_aux ? FDY_SCRATCH_RAGGED : 0u);
   return FDY_OK;
 }
 
@@ -810,75 +930,12 @@ int fdy_restore(fdy_archive* a, void* stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   FDY_HIP(hipSetDevice(a->device));
   if (a->compact) {  // group graphs were bound and are gone: back to the restore's layout
-    a->ovr.release();
-    a->live.release();
     a->image.release();
     int rc = dev_alloc(a->image, 8 * a->total_cap, "param images");
     if (!rc) rc = alloc_restore_buffers(a);
     if (rc) return rc;
   }
-  RestoreArgs r{};
-  r.img = a->img.as<uint8_t>();
-  r.graphs = a->dgraphs.as<DevGraph>();
-  r.cc = a->cc.as<CrcConsts>();
-  r.num_graphs = a->G;
-  r.num_slots = a->num_slots;
-  r.num_chunks = a->num_chunks;
-  r.chunk_gt = a->chunk_gt.as<uint2>();
-  r.num_units = a->num_units;
-  r.units = a->units.as<DigestUnit>();
-  r.chunks = a->chunks.as<NodeChunk>();
-  r.digests = a->digests.as<uint64_t>();
-  r.explicit_template = a->use_explicit ? a->explicit_tmpl.as<uint32_t>() : nullptr;
-  r.key_hash = a->key_hash.as<uint64_t>();
-  a->epoch = a->epoch % 65535 + 1;
-  r.epoch = a->epoch;
-  r.hash_wait_spins = a->hash_wait_spins;
-  r.template_of = a->tmpl.as<uint32_t>();
-  r.status = a->status.as<uint32_t>();
-  r.gwords = a->gwords.as<uint32_t>();
-  r.pbytes = a->pbytes.as<uint64_t>();
-  r.node_flags = a->nflags.as<uint8_t>();
-  r.node_desc = a->ndesc.as<NodeDesc>();
-  r.node_ptrs = a->nptrs.as<uint64_t>();
-  r.tile_node = a->tile_node.as<uint32_t>();
-  r.tslots = a->tslots.as<uint32_t>();
-  r.tslot_count = a->tslots.as<uint32_t>() + a->num_slots;
-  r.slot_desc = a->slot_desc.as<SlotDesc>();
-  r.aux = a->aux.as<uint64_t>();
-  r.image = a->image.as<uint64_t>();
-  r.live = a->live.as<uint64_t>();
-  r.live_src = a->live_src.as<uint32_t>();
-  r.live_cur = a->live_cur.as<uint32_t>();
-  r.ovr = a->ovr.as<fdy_override>();
-  r.cand = a->cand.as<Candidate>();
-  r.sub_count = a->sub_count.as<uint32_t>();
-  r.slot_rec = a->slot_rec.as<uint32_t>();
-  r.gaps = a->gaps.as<uint32_t>();
-  r.node_pbytes = a->node_pbytes.as<uint64_t>();
-  r.reloc = a->reloc.dev;
-  if (a->timing) {
-    for (hipEvent_t& e : a->ev)
-      if (!e) FDY_HIP(hipEventCreate(&e));
-    FDY_HIP(hipEventRecord(a->ev[0], s));
-  }
-  // Grouping first (the key and dependency digests run beside the second
-  // node pass).
-  FDY_HIP(launch_group(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[1], s));
-  FDY_HIP(launch_node(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[2], s));
-  FDY_HIP(launch_diff_templates(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[3], s));
-  FDY_HIP(launch_diff_members(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[4], s));
-  FDY_HIP(launch_diff_search(r, s));
-  if (a->timing) FDY_HIP(hipEventRecord(a->ev[5], s));
-  a->timed = a->timing;
-  a->restored = true;
-  a->cached = false;
-  a->last_stream = s;
-  return FDY_OK;
+  return enqueue_restore(a, s);
 }
 
 int fdy_set_timing(fdy_archive* a, int enabled) {

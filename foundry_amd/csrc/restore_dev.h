@@ -22,6 +22,30 @@ constexpr uint32_t kDiffWindow = 384;    // node descriptors staged in LDS per t
                                          // to five waves per SIMD, 83.8 against 81.6 us)
 constexpr uint32_t kNoTile = 0xFFFFFFFFu;
 
+// The restore's flag word (RestoreArgs::restore_flags), read by the host
+// before any result is.
+constexpr uint32_t kFlagGaps = 1;      // a slot made fewer records than its bound: close the gaps (k_repack)
+constexpr uint32_t kFlagNeedAux = 2;   // a ragged node found no ragged-word sources: restore again with them
+constexpr uint32_t kFlagOverflow = 4;  // a slot's candidate spill space or a graph's record region ran out:
+                                       // restore again with the next scratch level
+
+// Scratch levels.  Each sub-range has a region of candidates, each slot spill
+// space its sub-ranges continue their lists in, and each graph one override
+// record per 2^rec_shift capacity words.  A restore that overflows a level
+// runs again at the next; the last (full) holds a candidate and a record per
+// word, so it cannot overflow.
+struct ScratchLevel {
+  uint32_t cand_cap;   // candidates per sub-range region
+  uint32_t spill_cap;  // spill candidates per slot
+  uint32_t rec_shift;
+};
+constexpr ScratchLevel kScratchLevels[] = {
+    {kSubWords / 8, kTileWords / 16, 3},  // 768 candidates per 4096 words, a record per 8 words
+    {kSubWords / 4, kTileWords / 4, 2},   // 2048 candidates per 4096 words, a record per 4 words
+    {kSubWords, 0, 0},                    // full capacity
+};
+constexpr uint32_t kScratchFull = 2;
+
 // Internal node flag bits beyond the public FDY_NODE_* bits (0x0F).
 constexpr uint32_t kNodeRaggedT = 0x10;  // template's node n is ragged
 constexpr uint32_t kNodeCompare = 0x20;  // compare words against the template
@@ -47,7 +71,7 @@ struct DevGraph {
   uint32_t flags;        // header flags
   uint32_t word_cap;     // param-image capacity in words
   uint64_t node_base;    // global index of node 0
-  uint64_t word_base;    // global index of word 0 in R / live / aux
+  uint64_t word_base;    // global index of word 0 in R and aux (the override records: word_base >> rec_shift)
   uint32_t tile_base;    // first diff-tile slot
   uint32_t tile_cap;     // number of diff-tile slots
   uint64_t crc_fin[4];   // CRC-64/XZ finishing terms of the key, edge, type, kernel-entry streams
@@ -82,12 +106,12 @@ static_assert(sizeof(NodeChunk) == 32, "NodeChunk is 32 B");
 // Per-slot work description written by the node pass for the diff pass.
 constexpr uint32_t kSlotFlat = 1;      // every word of the tile sits at kg + 8w (and kt + 8w)
 constexpr uint32_t kSlotCompare = 2;   // flat tile whose words are compared with the template
-constexpr uint32_t kSlotTemplate = 4;  // tile of a template graph (also writes the live image)
+constexpr uint32_t kSlotTemplate = 4;  // tile of a template graph
 constexpr uint32_t kSlotFirst = 8;     // the graph's first slot
 struct SlotDesc {
   uint64_t kg;           // flat: byte offset of image word 0 of the graph in the file image
   uint64_t kt;           // flat + compare: the same for the template
-  uint64_t word_base;    // the graph's first word in R / live / aux
+  uint64_t word_base;    // the graph's first word in R and aux
   uint64_t t_word_base;  // the template's first word in R
   uint32_t wbeg, wend;   // graph-local word range of the tile (empty: inactive slot)
   uint32_t graph;

@@ -79,6 +79,20 @@ typedef struct fdy_override {
   uint64_t value;
 } fdy_override;
 
+/* ---- restore scratch (fdy_archive_info.scratch) --------------------------
+ * A restore keeps a bounded share of candidate words per diff sub-range
+ * (continued in spill space shared by the sub-ranges of a 4096-word tile)
+ * and a bounded override region per graph, and no ragged-word sources.  A
+ * restore that runs out of either, or meets a node whose params are not
+ * whole aligned words, is run again with what it lacked before any of its
+ * results is read (the results are the same; the earlier run's time is
+ * lost), and the archive keeps that layout for later restores.  Levels:
+ *   0  768 candidates per 4096 words, an override record per 8 words
+ *   1  2048 candidates per 4096 words, a record per 4 words
+ *   2  a candidate and a record per word (cannot overflow) */
+#define FDY_SCRATCH_LEVEL 0x3u   /* scratch level, 0..2 */
+#define FDY_SCRATCH_RAGGED 0x4u  /* ragged-word sources held (one word per image word) */
+
 typedef struct fdy_archive_info {
   uint32_t num_graphs;
   uint32_t num_groups;      /* valid after fdy_restore */
@@ -90,7 +104,7 @@ typedef struct fdy_archive_info {
   uint64_t num_intervals;
   uint64_t device_bytes;       /* device memory the archive holds */
   uint32_t serving_layout;     /* 1 while in the serving layout (see fdy_group_graph_create) */
-  uint32_t pad_;
+  uint32_t scratch;            /* FDY_SCRATCH_* bits: how the restore's scratch is laid out */
 } fdy_archive_info;
 
 typedef struct fdy_archive fdy_archive;
