@@ -50,6 +50,7 @@ WORKLOADS = {
 }
 SWITCHES = 10000
 GRAPH_SWITCHES = 200  # switches timed through group graphs
+CACHED_EXECS = 4      # execs per group in the exec-cache measurement
 PROBE_CO = os.path.join(ROOT, "tests", "native", "_build", "probe.co")
 
 
@@ -269,6 +270,7 @@ def bench_group_graphs(preset, torch, np, stream, diff_node_pct=0):
         gg = GroupGraph(arch, int(t), reg, stream)
         build_ms.append(1e3 * (time.perf_counter() - t0))
         inst_ms.append(gg.info()["instantiate_ms"])
+        gg.set_exec_cache(1)  # one exec per group (the reference's shape) for the sparse-update figures
         ggs[int(t)] = gg
     nodes = int(gg.info()["num_nodes"])
     # First selection of each graph: includes fetching its host copies
@@ -290,6 +292,30 @@ def bench_group_graphs(preset, torch, np, stream, diff_node_pct=0):
     for i in range(40):
         st = ggs[int(groups[seq[i]])].reset_all(stream)
         full_us.append(st["reset_us"])
+    # The exec cache: CACHED_EXECS execs per group, switching among as many
+    # graphs of each group (a serving loop's hot batch sizes).  The first
+    # round instantiates the execs (their device memory measured with
+    # hipMemGetInfo); after it every switch finds its exec.
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    hot = {int(t): [int(g) for g in np.flatnonzero(groups == t)[:CACHED_EXECS]] for t in ggs}
+    inst_us = []
+    for t, gg in ggs.items():
+        gg.set_exec_cache(CACHED_EXECS)
+        for g in hot[t]:
+            st = gg.select(g, stream)
+            if st["instantiate_us"]:
+                inst_us.append(st["instantiate_us"])
+    torch.cuda.synchronize()
+    exec_bytes = (free0 - torch.cuda.mem_get_info()[0]) / max(1, len(inst_us))
+    rng = np.random.default_rng(params.seed ^ 0xCAC)
+    hit_us, hits = [], 0
+    for _ in range(GRAPH_SWITCHES):
+        t = int(rng.choice(list(ggs)))
+        st = ggs[t].select(int(rng.choice(hot[t])), stream)
+        hits += st["cache_hit"]
+        hit_us.append(st["host_us"])
+    torch.cuda.synchronize()
     for gg in ggs.values():
         gg.close()
     arch.close()
@@ -307,6 +333,15 @@ def bench_group_graphs(preset, torch, np, stream, diff_node_pct=0):
         "nodes_reset_mean": round(statistics.mean(reset_n), 1),
         "nodes_per_graph": nodes,
         "all_node_reset_us_p50": round(_pct(full_us, 0.5), 1),
+        "exec_cache": {
+            "execs_per_group": CACHED_EXECS,
+            "sample": f"{GRAPH_SWITCHES} seeded switches among {CACHED_EXECS} graphs of each group, "
+                      f"{hits} of them found their exec",
+            "cached_switch_us_p50": round(_pct(hit_us, 0.5), 1),
+            "cached_switch_us_p99": round(_pct(hit_us, 0.99), 1),
+            "instantiate_ms_per_exec": round(statistics.mean(inst_us) / 1e3, 3) if inst_us else None,
+            "device_bytes_per_exec": int(exec_bytes),
+        },
     }
 
 

@@ -87,7 +87,7 @@ class GroupGraphInfo(C.Structure):
         ("num_event_nodes", C.c_uint32),
         ("num_deps", C.c_uint32),
         ("num_events", C.c_uint32),
-        ("pad_", C.c_uint32),
+        ("num_execs", C.c_uint32),
         ("build_ms", C.c_double),
         ("instantiate_ms", C.c_double),
     ]
@@ -100,6 +100,9 @@ class SelectStats(C.Structure):
         ("words_scattered", C.c_uint64),
         ("host_us", C.c_double),
         ("reset_us", C.c_double),
+        ("instantiate_us", C.c_double),
+        ("cache_hit", C.c_uint32),
+        ("pad_", C.c_uint32),
     ]
 
 
@@ -214,6 +217,7 @@ _GRAPH_SIGS = {
     "fdy_group_graph_destroy": (C.c_int, [_vp]),
     "fdy_group_graph_select": (C.c_int, [_vp, C.c_uint32, _vp, C.POINTER(SelectStats)]),
     "fdy_group_graph_reset_all": (C.c_int, [_vp, _vp, C.POINTER(SelectStats)]),
+    "fdy_group_graph_set_exec_cache": (C.c_int, [_vp, C.c_uint32]),
     "fdy_group_graph_launch": (C.c_int, [_vp, _vp]),
     "fdy_group_graph_info_get": (C.c_int, [_vp, C.POINTER(GroupGraphInfo)]),
     "fdy_group_graph_handles": (C.c_int, [_vp, C.POINTER(_vp), C.POINTER(_vp)]),

@@ -408,13 +408,32 @@ struct Member {
 
 using namespace fdy;
 
+// One instantiated exec of a group graph, holding one graph's params.
+struct ExecSlot {
+  hipGraphExec_t exec = nullptr;
+  uint32_t graph = 0;          // graph whose params the exec holds
+  uint64_t used = 0;           // selection tick of its last selection
+  hipEvent_t done = nullptr;   // recorded after each launch
+  bool launched = false;
+  bool stale = false;          // an update failed part-way: re-set every node next time
+};
+
+// Execs a group graph keeps by default (fdy_group_graph_set_exec_cache).
+constexpr uint32_t kDefaultExecs = 4;
+
 struct fdy_group_graph {
   fdy_archive* a = nullptr;
   fdy_registry* reg = nullptr;
   uint32_t t = 0;
   uint32_t N = 0;
   hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  // Execs of recently selected graphs: selecting a graph that holds one
+  // makes it current with no node update; otherwise the least recently
+  // selected exec (or a new one, below max_execs) is updated to the graph.
+  std::vector<ExecSlot> slots;
+  uint32_t cur = 0;            // the current exec (launched by fdy_group_graph_launch)
+  uint32_t max_execs = kDefaultExecs;
+  uint64_t tick = 0;
   std::vector<GNode> nodes;
   HostGraph th;                                 // the template
   UpdateSet tset;                               // the template's updates, one per node
@@ -425,18 +444,17 @@ struct fdy_group_graph {
   uint64_t* d_live = nullptr;                   // device addresses of the two
   uint8_t* d_dirty = nullptr;
   DevBuf dirty;                                 // per node, device memory: the scatter's marks
-  hipEvent_t done = nullptr;                    // recorded after each launch
-  bool launched = false;
-  bool stale = false;                           // an update failed part-way: re-set every node next time
   fdy_group_graph_info info{};
 
   ~fdy_group_graph() {
     (void)hipSetDevice(a ? a->device : 0);
-    if (done && launched) (void)hipEventSynchronize(done);
-    if (exec) (void)hipGraphExecDestroy(exec);
+    for (ExecSlot& x : slots) {
+      if (x.done && x.launched) (void)hipEventSynchronize(x.done);
+      if (x.exec) (void)hipGraphExecDestroy(x.exec);
+      if (x.done) (void)hipEventDestroy(x.done);
+    }
     if (graph) (void)hipGraphDestroy(graph);
     for (auto& e : events) (void)hipEventDestroy(e.second);
-    if (done) (void)hipEventDestroy(done);
     if (h_live) (void)hipHostFree(h_live);
     if (h_dirty) (void)hipHostFree(h_dirty);
   }
@@ -486,27 +504,27 @@ int make_update(fdy_group_graph* gg, const HostGraph& h, uint32_t n, uint64_t* w
   }
 }
 
-int apply_update(fdy_group_graph* gg, const GNode& x, NodeUpdate& u, void** params) {
+int apply_update(hipGraphExec_t exec, const GNode& x, NodeUpdate& u, void** params) {
   switch (x.type) {
     case FDY_NODE_KERNEL: {
       hipKernelNodeParams p = kernel_params(u, params);
-      FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
+      FDY_HIP(hipGraphExecKernelNodeSetParams(exec, x.h, &p));
       return FDY_OK;
     }
     case FDY_NODE_MEMSET: {
       hipKernelNodeParams p = fill_params(u);
-      FDY_HIP(hipGraphExecKernelNodeSetParams(gg->exec, x.h, &p));
+      FDY_HIP(hipGraphExecKernelNodeSetParams(exec, x.h, &p));
       return FDY_OK;
     }
     case FDY_NODE_MEMCPY:
-      if (u.copy3d) FDY_HIP(hipGraphExecMemcpyNodeSetParams(gg->exec, x.h, &u.p3));
-      else FDY_HIP(hipGraphExecMemcpyNodeSetParams1D(gg->exec, x.h, u.dst, u.src, u.bytes, hipMemcpyDeviceToDevice));
+      if (u.copy3d) FDY_HIP(hipGraphExecMemcpyNodeSetParams(exec, x.h, &u.p3));
+      else FDY_HIP(hipGraphExecMemcpyNodeSetParams1D(exec, x.h, u.dst, u.src, u.bytes, hipMemcpyDeviceToDevice));
       return FDY_OK;
     case FDY_NODE_EVENT_RECORD:
-      FDY_HIP(hipGraphExecEventRecordNodeSetEvent(gg->exec, x.h, u.event));
+      FDY_HIP(hipGraphExecEventRecordNodeSetEvent(exec, x.h, u.event));
       return FDY_OK;
     case FDY_NODE_EVENT_WAIT:
-      FDY_HIP(hipGraphExecEventWaitNodeSetEvent(gg->exec, x.h, u.event));
+      FDY_HIP(hipGraphExecEventWaitNodeSetEvent(exec, x.h, u.event));
       return FDY_OK;
     default:
       return FDY_OK;
@@ -573,6 +591,21 @@ Member* member(fdy_group_graph* gg, uint32_t g, int* rc) {
   return p;
 }
 
+// A new exec of the group's graph (which holds the template's params).
+int add_exec(fdy_group_graph* gg) {
+  ExecSlot x;
+  x.graph = gg->t;
+  FDY_HIP(hipGraphInstantiate(&x.exec, gg->graph, nullptr, nullptr, 0));
+  const hipError_t e = hipEventCreateWithFlags(&x.done, hipEventDisableTiming);
+  if (e != hipSuccess) {
+    (void)hipGraphExecDestroy(x.exec);
+    FDY_HIP(e);
+  }
+  gg->slots.push_back(x);
+  gg->info.num_execs = (uint32_t)gg->slots.size();
+  return FDY_OK;
+}
+
 int build(fdy_group_graph* gg) {
   const auto t0 = Clock::now();
   fdy_archive* a = gg->a;
@@ -601,7 +634,6 @@ int build(fdy_group_graph* gg) {
   rc = dev_alloc(gg->dirty, std::max<uint32_t>(N, 1), "group graph dirty marks");
   if (rc) return rc;
   FDY_HIP(hipMemset(gg->dirty.p, 0, std::max<uint32_t>(N, 1)));
-  FDY_HIP(hipEventCreateWithFlags(&gg->done, hipEventDisableTiming));
 
   FDY_HIP(hipGraphCreate(&gg->graph, 0));
   fdy_group_graph_info& info = gg->info;
@@ -679,7 +711,8 @@ int build(fdy_group_graph* gg) {
     FDY_HIP(hipGraphAddDependencies(gg->graph, from.data(), to.data(), from.size()));
   }
   const auto ti = Clock::now();
-  FDY_HIP(hipGraphInstantiate(&gg->exec, gg->graph, nullptr, nullptr, 0));
+  rc = add_exec(gg);
+  if (rc) return rc;
   info.instantiate_ms = us_since(ti) / 1000.0;
   info.template_graph = t;
   info.current_graph = t;
@@ -708,8 +741,24 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
     return err(FDY_E_MISMATCH, "graph " + std::to_string(g) + " has node types other than its template's");
   if (a->h_status[g] & FDY_GRAPH_BAD_PARAMS)
     return err(FDY_E_FORMAT, "graph " + std::to_string(g) + " has ranges outside its sections");
-  const uint32_t c = a->h_current[t];
-  if (c == g && !gg->stale) {
+  const uint32_t c = a->h_current[t];  // the live image's graph
+  ++gg->tick;
+  // An exec that holds g already: it becomes current, with no node update;
+  // the live image follows (the scatter, enqueued on `s`, marks nothing).
+  for (uint32_t i = 0; i < gg->slots.size(); ++i) {
+    ExecSlot& x = gg->slots[i];
+    if (x.graph != g || x.stale) continue;
+    if (c != g) {
+      FDY_HIP(hipSetDevice(a->device));
+      st.words_scattered = (a->h_ovr_off[c + 1] - a->h_ovr_off[c]) + (a->h_ovr_off[g + 1] - a->h_ovr_off[g]);
+      rc = enqueue_switch(a, g, s, nullptr);
+      if (rc) return rc;
+    }
+    x.used = gg->tick;
+    gg->cur = i;
+    gg->info.current_graph = g;
+    st.cache_hit = 1;
+    st.host_us = us_since(t0);
     if (stats_v) *static_cast<fdy_select_stats*>(stats_v) = st;
     return FDY_OK;
   }
@@ -719,11 +768,36 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
     if (!m) return rc;
   }
   FDY_HIP(hipSetDevice(a->device));
-  if (gg->launched) FDY_HIP(hipEventSynchronize(gg->done));
+  // The exec to update: a new one while there are fewer than max_execs,
+  // else the least recently selected.
+  uint32_t v = 0;
+  if (gg->slots.size() < gg->max_execs) {
+    const auto ti = Clock::now();
+    rc = add_exec(gg);
+    if (rc) return rc;
+    st.instantiate_us = us_since(ti);
+    v = (uint32_t)gg->slots.size() - 1;
+  } else {
+    for (uint32_t i = 1; i < gg->slots.size(); ++i)
+      if (gg->slots[i].used < gg->slots[v].used) v = i;
+  }
+  ExecSlot& x = gg->slots[v];
+  if (x.launched) FDY_HIP(hipEventSynchronize(x.done));
+  // The nodes whose params differ between the exec's graph h and g are
+  // those of O_h, O_g and the two graphs' own descriptors and layouts: the
+  // live image moves to h first when h is not its graph (c), so that the
+  // scatters' marks cover all of them (and O_c's, which take g's params
+  // too).
+  const uint32_t h = x.graph;
   st.words_scattered = (a->h_ovr_off[c + 1] - a->h_ovr_off[c]) + (a->h_ovr_off[g + 1] - a->h_ovr_off[g]);
+  if (h != c && h != g) {
+    st.words_scattered += 2 * (a->h_ovr_off[h + 1] - a->h_ovr_off[h]);
+    rc = enqueue_switch(a, h, s, gg->dirty.as<uint8_t>());
+    if (rc) return rc;
+  }
   rc = enqueue_switch(a, g, s, gg->dirty.as<uint8_t>());
   if (rc) return rc;
-  const bool all = gg->stale;
+  const bool all = x.stale;
   MirrorArgs mr{};
   mr.live = a->live.as<uint64_t>() + live_base(a, t);
   mr.desc = a->ndesc.as<NodeDesc>() + a->graphs[t].node_base;
@@ -735,18 +809,21 @@ int group_graph_select(fdy_group_graph* gg, uint32_t g, hipStream_t s, void* sta
   FDY_HIP(launch_mirror(mr, s));
   FDY_HIP(hipStreamSynchronize(s));
   const auto tr = Clock::now();
-  gg->stale = true;  // until every node below is set
+  x.stale = true;  // until every node below is set
+  gg->cur = v;
   for (uint32_t n = 0; n < gg->N; ++n) {
     if (!gg->h_dirty[n]) continue;
     gg->h_dirty[n] = 0;
     const int32_t k = m ? m->own[n] : -1;
-    if (k >= 0) rc = apply_update(gg, gg->nodes[n], *m->set.u[k], m->set.params.data());
-    else rc = apply_update(gg, gg->nodes[n], *gg->tset.u[n], gg->tset.params.data());
+    if (k >= 0) rc = apply_update(x.exec, gg->nodes[n], *m->set.u[k], m->set.params.data());
+    else rc = apply_update(x.exec, gg->nodes[n], *gg->tset.u[n], gg->tset.params.data());
     if (rc) return rc;
     ++st.nodes_reset;
     st.kernel_nodes_reset += gg->nodes[n].type == FDY_NODE_KERNEL;
   }
-  gg->stale = false;
+  x.stale = false;
+  x.graph = g;
+  x.used = gg->tick;
   gg->info.current_graph = g;
   st.reset_us = us_since(tr);
   st.host_us = us_since(t0);
@@ -1073,25 +1150,56 @@ int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fd
 
 int fdy_group_graph_reset_all(fdy_group_graph* gg, void* stream, fdy_select_stats* stats) {
   if (!gg) return err(FDY_E_INVALID, "null group graph");
-  gg->stale = true;
-  return group_graph_select(gg, gg->a->h_current[gg->t], static_cast<hipStream_t>(stream), stats);
+  // The current exec re-set from its graph, every node (the other execs stay).
+  ExecSlot& x = gg->slots[gg->cur];
+  x.stale = true;
+  x.used = 0;  // the least recently selected: the update below takes it
+  for (ExecSlot& y : gg->slots)
+    if (&y != &x) y.used = std::max<uint64_t>(y.used, 1);
+  const uint32_t keep = gg->max_execs;
+  gg->max_execs = (uint32_t)gg->slots.size();  // no new exec for this
+  const int rc = group_graph_select(gg, x.graph, static_cast<hipStream_t>(stream), stats);
+  gg->max_execs = keep;
+  return rc;
+}
+
+int fdy_group_graph_set_exec_cache(fdy_group_graph* gg, uint32_t max_execs) {
+  if (!gg) return err(FDY_E_INVALID, "null group graph");
+  if (max_execs == 0) return err(FDY_E_INVALID, "a group graph keeps at least one exec");
+  FDY_HIP(hipSetDevice(gg->a->device));
+  // Execs past the new limit go, least recently selected first; the current one stays.
+  while (gg->slots.size() > max_execs) {
+    uint32_t v = gg->cur == 0 ? 1 : 0;
+    for (uint32_t i = 0; i < gg->slots.size(); ++i)
+      if (i != gg->cur && gg->slots[i].used < gg->slots[v].used) v = i;
+    ExecSlot& x = gg->slots[v];
+    if (x.launched) FDY_HIP(hipEventSynchronize(x.done));
+    FDY_HIP(hipGraphExecDestroy(x.exec));
+    FDY_HIP(hipEventDestroy(x.done));
+    gg->slots.erase(gg->slots.begin() + v);
+    if (gg->cur > v) --gg->cur;
+  }
+  gg->max_execs = max_execs;
+  gg->info.num_execs = (uint32_t)gg->slots.size();
+  return FDY_OK;
 }
 
 int fdy_group_graph_launch(fdy_group_graph* gg, void* stream) {
   if (!gg) return err(FDY_E_INVALID, "null group graph");
-  if (gg->stale) return err(FDY_E_STATE, "the last select failed part-way; select a graph again before launching");
+  ExecSlot& x = gg->slots[gg->cur];
+  if (x.stale) return err(FDY_E_STATE, "the last select failed part-way; select a graph again before launching");
   hipStream_t s = static_cast<hipStream_t>(stream);
   FDY_HIP(hipSetDevice(gg->a->device));
-  FDY_HIP(hipGraphLaunch(gg->exec, s));
-  FDY_HIP(hipEventRecord(gg->done, s));
-  gg->launched = true;
+  FDY_HIP(hipGraphLaunch(x.exec, s));
+  FDY_HIP(hipEventRecord(x.done, s));
+  x.launched = true;
   return FDY_OK;
 }
 
 int fdy_group_graph_handles(fdy_group_graph* gg, void** graph, void** exec) {
   if (!gg) return err(FDY_E_INVALID, "null group graph");
   if (graph) *graph = gg->graph;
-  if (exec) *exec = gg->exec;
+  if (exec) *exec = gg->slots[gg->cur].exec;
   return FDY_OK;
 }
 

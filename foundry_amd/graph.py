@@ -101,12 +101,16 @@ class GroupGraph:
     def select(self, graph: int, stream=None) -> dict:
         st = SelectStats()
         check(restore_lib().fdy_group_graph_select(self._h, graph, _stream(stream), C.byref(st)))
-        return {k: getattr(st, k) for k, _ in SelectStats._fields_}
+        return {k: getattr(st, k) for k, _ in SelectStats._fields_ if k != "pad_"}
+
+    def set_exec_cache(self, max_execs: int) -> None:
+        """Execs kept for recently selected graphs (at least 1; default 4)."""
+        check(restore_lib().fdy_group_graph_set_exec_cache(self._h, int(max_execs)))
 
     def reset_all(self, stream=None) -> dict:
         st = SelectStats()
         check(restore_lib().fdy_group_graph_reset_all(self._h, _stream(stream), C.byref(st)))
-        return {k: getattr(st, k) for k, _ in SelectStats._fields_}
+        return {k: getattr(st, k) for k, _ in SelectStats._fields_ if k != "pad_"}
 
     def launch(self, stream=None) -> None:
         check(restore_lib().fdy_group_graph_launch(self._h, _stream(stream)))

@@ -105,7 +105,7 @@ typedef struct fdy_group_graph_info {
   uint32_t num_event_nodes;
   uint32_t num_deps;
   uint32_t num_events;         /* distinct saved event ids */
-  uint32_t pad_;
+  uint32_t num_execs;          /* execs instantiated (fdy_group_graph_set_exec_cache) */
   double build_ms;             /* host time of fdy_group_graph_create */
   double instantiate_ms;       /* of which hipGraphInstantiate */
 } fdy_group_graph_info;
@@ -113,9 +113,12 @@ typedef struct fdy_group_graph_info {
 typedef struct fdy_select_stats {
   uint32_t nodes_reset;   /* nodes re-set in the exec */
   uint32_t kernel_nodes_reset;
-  uint64_t words_scattered;  /* override records applied by the scatter: |O_prev| + |O_new| */
+  uint64_t words_scattered;  /* override records applied by the scatter(s) */
   double host_us;            /* wall time of the call, including the scatter's synchronization */
   double reset_us;           /* of which the exec node updates */
+  double instantiate_us;     /* of which instantiating a new exec (0 unless the cache grew) */
+  uint32_t cache_hit;        /* 1: an exec held the graph already; nothing was re-set or waited for */
+  uint32_t pad_;
 } fdy_select_stats;
 
 /* Build the group graph of template graph `template_graph` after
@@ -134,22 +137,36 @@ typedef struct fdy_select_stats {
 int fdy_group_graph_create(fdy_archive* a, uint32_t template_graph, fdy_registry* r, void* stream,
                            fdy_group_graph** out);
 int fdy_group_graph_destroy(fdy_group_graph* gg);
-/* Make the exec run graph `graph` (a member of the group): the override
- * scatter on `stream`, then the exec updates of the changed nodes.  Waits
- * for the group graph's previous launch and for the scatter.  No-op if
- * `graph` is current.  `stats` may be NULL.  Counterpart of the on-demand
- * branch of csrc/CUDAGraph.cpp:330-461, which re-sets every node. */
+/* Make the group graph run graph `graph` (a member of the group).  A group
+ * graph keeps up to max_execs instantiated execs (default 4), each holding
+ * one graph's params.  If one holds `graph`, it becomes current: the
+ * override scatter is enqueued on `stream` so that the group's live image
+ * follows, and nothing else runs (no node update, no wait).  Otherwise the
+ * least recently selected exec -- or a new one while there are fewer than
+ * max_execs -- waits for its previous launch and takes `graph`'s params:
+ * the scatter(s) on `stream` mark the nodes that differ between the two
+ * graphs, then those nodes are re-set (after one synchronisation of
+ * `stream`).  `stats` may be NULL.  Counterpart of the on-demand branch of
+ * csrc/CUDAGraph.cpp:330-461, which has one exec per group and re-sets
+ * every node on every switch. */
 int fdy_group_graph_select(fdy_group_graph* gg, uint32_t graph, void* stream, fdy_select_stats* stats);
-/* Re-set every node of the exec from the current graph, as the reference
+/* Re-set every node of the current exec from its graph, as the reference
  * does on every switch (csrc/CUDAGraph.cpp:345-441).  Use after an update
  * failed part-way; the bench uses it as the all-node baseline. */
 int fdy_group_graph_reset_all(fdy_group_graph* gg, void* stream, fdy_select_stats* stats);
-/* Launch the exec on `stream` (csrc/CUDAGraph.cpp:476-477). */
+/* The number of execs the group graph keeps (at least 1; 1 is the
+ * reference's one exec per group).  Lowering it destroys the least recently
+ * selected execs past the limit (never the current one).  Each exec holds a
+ * copy of every node's params (the driver's kernel-argument buffers). No
+ * counterpart in the reference. */
+int fdy_group_graph_set_exec_cache(fdy_group_graph* gg, uint32_t max_execs);
+/* Launch the current exec on `stream` (csrc/CUDAGraph.cpp:476-477). */
 int fdy_group_graph_launch(fdy_group_graph* gg, void* stream);
 int fdy_group_graph_info_get(fdy_group_graph* gg, fdy_group_graph_info* out);
-/* The group graph's hipGraph_t and hipGraphExec_t (either pointer may be
- * NULL), owned by the group graph: CUDAGraph::raw_cuda_graph and
- * raw_cuda_graph_exec (csrc/CUDAGraph.cpp:537-551) of every member. */
+/* The group graph's hipGraph_t and its current hipGraphExec_t (either
+ * pointer may be NULL), owned by the group graph: CUDAGraph::raw_cuda_graph
+ * and raw_cuda_graph_exec (csrc/CUDAGraph.cpp:537-551) of every member.
+ * The current exec changes with fdy_group_graph_select. */
 int fdy_group_graph_handles(fdy_group_graph* gg, void** graph, void** exec);
 /* hipGraphDebugDotPrint of the group graph, verbose, to `path`
  * (CUDAGraph::debug_dump, csrc/CUDAGraph.cpp:515-532). */

@@ -192,13 +192,59 @@ def test_each_member_runs_its_own_params(env):
 
 
 def test_only_changed_nodes_are_reset(env):
+    """With one exec (the reference's shape), every switch updates it: only
+    the nodes that differ between the two graphs are re-set."""
     with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        gg.set_exec_cache(1)
         prev = 0
         for g in [1, 2, 3, 4, 1, 0, 4, 3, 2]:
             st = env.run(gg, g)
             assert st["nodes_reset"] == env.expected_resets(prev, g), (prev, g)
             prev = g
         assert gg.select(prev, env.stream)["nodes_reset"] == 0  # already current
+
+
+@pytest.mark.parametrize("execs", [1, 2, 4])
+def test_exec_cache(env, execs):
+    """Up to `execs` execs hold recently selected graphs.  A graph one of
+    them holds becomes current with nothing re-set.  Otherwise the least
+    recently selected exec (or a new one, which starts from the template's
+    params) takes the graph: the re-set nodes are those whose params differ
+    among the live image's graph (the previous selection), the exec's graph
+    and the new one.  Every launch runs the selected graph's params,
+    whatever exec holds them."""
+    def own(g):
+        o = {int(x) for x in env.arch.overrides(g, env.stream)["node"]}
+        fl = env.arch.node_flags(g, env.stream)
+        return o | {n for n in range(len(fl)) if fl[n] & (_lib.NODE_LAYOUT | _lib.NODE_DESC)}
+
+    order = [1, 2, 1, 3, 2, 4, 0, 1, 4, 4, 3, 0, 2, 1]
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        gg.set_exec_cache(execs)
+        slots = [[0, 0]]  # per exec: [graph, tick of its last selection]
+        prev = 0
+        for tick, g in enumerate(order, start=1):
+            st = env.run(gg, g)
+            hit = [x for x in slots if x[0] == g]
+            if hit:
+                assert st["cache_hit"] == 1 and st["nodes_reset"] == 0, (tick, g, slots)
+                hit[0][1] = tick
+            else:
+                if len(slots) < execs:
+                    slots.append([0, 0])
+                    x = slots[-1]
+                else:
+                    x = min(slots, key=lambda y: y[1])
+                h = x[0]
+                want = own(h) | own(g) | (own(prev) if prev != h else set())
+                assert st["cache_hit"] == 0 and st["nodes_reset"] == len(want), (tick, g, h, prev)
+                x[:] = [g, tick]
+            assert gg.info()["num_execs"] == len(slots)
+            prev = g
+        gg.set_exec_cache(1)  # the current exec stays
+        assert gg.info()["num_execs"] == 1 and gg.info()["current_graph"] == prev
+        env.run(gg, prev)
+        env.run(gg, 3)
 
 
 def test_seeded_switch_sequence(env):
@@ -278,6 +324,8 @@ def test_synthetic_groups_build_and_switch_without_launch(env, diff_node_pct):
     temps = sorted(set(int(t) for t in groups))
     assert len(temps) == 3
     ggs = {t: GroupGraph(arch, t, env.reg, env.stream) for t in temps}
+    for gg in ggs.values():
+        gg.set_exec_cache(1)  # one exec per group: every switch updates it
 
     def touched(g):
         o = {int(x) for x in arch.overrides(g, env.stream)["node"]}
