@@ -86,7 +86,12 @@ def bench_relocation(args, s, iv, torch, np, stream):
     n = int(words_host.size)
     w = torch.from_numpy(words_host.view(np.int64)).to("cuda")
     o = torch.empty_like(w)
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    t0 = time.perf_counter()
     plan = RelocPlan(*iv)
+    plan_build_s = time.perf_counter() - t0  # the interval index, built on the host and uploaded
+    plan_bytes = free0 - torch.cuda.mem_get_info()[0]
     if args.profile_loop:
         for _ in range(args.profile_loop):
             plan.relocate(w.data_ptr(), o.data_ptr(), n, stream)
@@ -119,6 +124,8 @@ def bench_relocation(args, s, iv, torch, np, stream):
                      "traffic": _measured_traffic(RELOC_TRAFFIC_FILE) if n == 1 << 27 else None,
                      "algorithmic_bytes": b_r},
         "cpu_baseline": None,
+        "plan_build_s": round(plan_build_s, 3),
+        "plan_device_bytes": int(plan_bytes),
     }
     if not args.no_cpu_baseline:
         import oracle
@@ -394,7 +401,9 @@ def main():
             reopen.append(time.perf_counter() - t0)
             other.close()
     open_s = statistics.median(reopen) if reopen else first_open_s
+    t0 = time.perf_counter()
     arch.set_relocation(*iv)
+    index_build_s = time.perf_counter() - t0  # the archive's interval index, built on the host and uploaded
 
     if args.profile_loop:
         for _ in range(args.profile_loop):
@@ -489,6 +498,7 @@ def main():
         "open_upload_s": round(open_s, 4),
         "open_upload_GBps": round(int(info["file_bytes"]) / open_s / 1e9, 2),
         "open_first_s": round(first_open_s, 4),
+        "interval_index_build_s": round(index_build_s, 4),
         "first_host_to_device_copy_ms": round(first_copy_ms, 2),
         "roofline": {
             "bound": "hbm",

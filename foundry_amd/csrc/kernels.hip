@@ -41,8 +41,6 @@ namespace {
 constexpr uint32_t kNodeThreads = 1024;
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
-constexpr uint32_t kRelocBatch = 4;  // words searched in lockstep (8 and 2 measured no faster)
-static_assert(kRelocBatch % 2 == 0 && (2 * kRelocPairs) % kRelocBatch == 0, "whole pairs per batch");
 
 __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
   uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
@@ -2140,40 +2138,86 @@ __global__ __launch_bounds__(kFillThreads) void k_fill(FillArgs a) {
 
 // `in` and `out` may be the same array: each word is read and then written
 // by one thread, so in-place relocation needs no ordering between threads.
+// Standalone relocation of packed words.  Each thread owns kRelocPairs
+// 16-byte pairs per chunk (coalesced across the workgroup).  The words
+// inside the table's range (the pointers: 40% on the relocation-heavy
+// workload) are compacted per wave in LDS and searched kRelocSearch per lane
+// in lockstep, then read back in place, so no lane holds index lines for
+// words that need no search: 90 VGPRs and five waves per SIMD, where
+// searching every word in batches of four took 148 VGPRs and three.
+constexpr uint32_t kRelocSearch = 2;
+static_assert((64 * 2 * kRelocPairs) % (64 * kRelocSearch) == 0, "whole search batches per wave");
+
 __global__ __launch_bounds__(kRelocThreads) void k_reloc(RelocDev R, const uint64_t* in, uint64_t* out, uint64_t n,
                                                          int vec) {
-  // Each thread owns kRelocPairs 16-byte pairs per chunk (coalesced across
-  // the workgroup): all loads first, then the searches, then the stores, so
-  // the searches of 2 * kRelocPairs words overlap.
+  constexpr uint32_t kW = 2 * kRelocPairs;  // words per lane per chunk
+  __shared__ uint64_t s_q[kRelocThreads / 64][64 * kW];
   const uint64_t chunk = (uint64_t)kRelocThreads * kRelocPairs;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t lt = (1ull << lane) - 1;
+  uint64_t* sq = s_q[threadIdx.x >> 6];
   if (vec) {
     const uint64_t pairs = n / 2;
     const ulonglong2* in2 = reinterpret_cast<const ulonglong2*>(in);
     ulonglong2* out2 = reinterpret_cast<ulonglong2*>(out);
     for (uint64_t c = (uint64_t)blockIdx.x * chunk; c < pairs; c += (uint64_t)gridDim.x * chunk) {
-      ulonglong2 v[kRelocPairs];
+      uint64_t w[kW];
 #pragma unroll
       for (uint32_t q = 0; q < kRelocPairs; ++q) {
         const uint64_t p = c + q * kRelocThreads + threadIdx.x;
-        v[q] = p < pairs ? in2[p] : ulonglong2{0, 0};
+        const ulonglong2 v = p < pairs ? in2[p] : ulonglong2{0, 0};
+        w[2 * q] = v.x;
+        w[2 * q + 1] = v.y;
+      }
+      uint32_t need = 0, rank[kW], cnt = 0;
+      if (R.n != 0) {
+#pragma unroll
+        for (uint32_t j = 0; j < kW; ++j)
+          if (w[j] >= R.lo_min && (R.policy ? w[j] <= R.hi_max : w[j] < R.hi_max)) need |= 1u << j;
       }
 #pragma unroll
-      for (uint32_t q = 0; q < kRelocPairs; q += kRelocBatch / 2) {
-        uint64_t w[kRelocBatch], r[kRelocBatch];
+      for (uint32_t j = 0; j < kW; ++j) {
+        const uint64_t mk = __ballot((need >> j) & 1);
+        rank[j] = cnt + (uint32_t)__popcll(mk & lt);
+        if ((need >> j) & 1) sq[rank[j]] = w[j];
+        cnt += (uint32_t)__popcll(mk);
+      }
+      // The wave's own LDS words: its writes precede its reads in program order.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      for (uint32_t b = 0; b < cnt; b += 64 * kRelocSearch) {
+        uint64_t x[kRelocSearch], y[kRelocSearch];
+        uint32_t mm = 0;
 #pragma unroll
-        for (uint32_t k = 0; k < kRelocBatch / 2; ++k) {
-          w[2 * k] = v[q + k].x;
-          w[2 * k + 1] = v[q + k].y;
+        for (uint32_t k = 0; k < kRelocSearch; ++k) {
+          const uint32_t i = b + 64 * k + lane;
+          x[k] = i < cnt ? sq[i] : 0;
+          mm |= (i < cnt ? 1u : 0u) << k;
         }
-        reloc_batch<kRelocBatch>(R, w, r, (1u << kRelocBatch) - 1);
+        reloc_batch<kRelocSearch>(R, x, y, mm);
 #pragma unroll
-        for (uint32_t k = 0; k < kRelocBatch / 2; ++k) v[q + k] = ulonglong2{r[2 * k], r[2 * k + 1]};
+        for (uint32_t k = 0; k < kRelocSearch; ++k) {
+          const uint32_t i = b + 64 * k + lane;
+          if (i < cnt) sq[i] = y[k];
+        }
       }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (uint32_t j = 0; j < kW; ++j)
+        if ((need >> j) & 1) w[j] = sq[rank[j]];
 #pragma unroll
       for (uint32_t q = 0; q < kRelocPairs; ++q) {
         const uint64_t p = c + q * kRelocThreads + threadIdx.x;
-        if (p < pairs) out2[p] = v[q];
+        if (p < pairs) out2[p] = ulonglong2{w[2 * q], w[2 * q + 1]};
       }
+      // The next chunk's compaction overwrites this wave's LDS words only
+      // after every lane has read its own back (program order in the wave).
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     if (blockIdx.x == 0 && threadIdx.x == 0 && (n & 1)) out[n - 1] = reloc_word(R, in[n - 1]);
   } else {
