@@ -33,6 +33,8 @@
 //   k_mirror  dirty nodes' live words -> a group graph's host mirror.
 //   k_fill    memset node of a restored graph, as a kernel node.
 //   k_reloc   streaming relocation of packed words.
+#include <type_traits>
+
 #include "kernels.h"
 
 namespace fdy {
@@ -264,10 +266,42 @@ struct Side {
 // image in global memory; every field of an entry is 4-byte aligned).
 struct RawEntry {
   const uint8_t* e;
+  __device__ explicit RawEntry(const uint8_t* p) : e(p) {}
   __device__ uint32_t u32(uint32_t off) const { return f32(e, off); }
   __device__ uint64_t u64(uint32_t off) const { return f64(e, off); }
   __device__ uint8_t type() const { return e[FDY_NODE_OFF_TYPE]; }
 };
+
+// A node entry whose type and kernel fields (bytes 4-7, 36-51, 64-91 and
+// 128-143: type, binary hash, name, required and per-node cluster dims, KNA
+// flags, param and arg-buffer references) are loaded together up front, so
+// that the per-node path waits for them once, where reading each field at
+// its first use (behind the branches on the type and flags) waited once per
+// group of fields.  Other fields are read in place.
+struct PreEntry {
+  const uint8_t* e;
+  uint32_t w1, k36[4], k64[7], k128[4];
+  __device__ explicit PreEntry(const uint8_t* p) : e(p) {
+    w1 = f32(p, 4);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) k36[i] = f32(p, 36 + 4 * i);
+#pragma unroll
+    for (uint32_t i = 0; i < 7; ++i) k64[i] = f32(p, 64 + 4 * i);
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) k128[i] = f32(p, 128 + 4 * i);
+  }
+  // Offsets are compile-time constants at every use, so the selection folds away.
+  __device__ uint32_t u32(uint32_t off) const {
+    if (off == 4) return w1;
+    if (off >= 36 && off < 52) return k36[(off - 36) / 4];
+    if (off >= 64 && off < 92) return k64[(off - 64) / 4];
+    if (off >= 128 && off < 144) return k128[(off - 128) / 4];
+    return f32(e, off);
+  }
+  __device__ uint64_t u64(uint32_t off) const { return (uint64_t)u32(off) | ((uint64_t)u32(off + 4) << 32); }
+  __device__ uint8_t type() const { return (uint8_t)w1; }
+};
+static_assert(FDY_NODE_OFF_TYPE == 4, "the type is the low byte of entry bytes 4-7");
 
 // The param references of kernel node entry e: the name, param-index and
 // arg-buffer bounds; an extra-style node's blob.  Per-param nodes are
@@ -455,8 +489,8 @@ struct Strings {
 };
 
 // Equal kernel names, compared through 8-byte windows.
-template <class E>
-__device__ __forceinline__ bool names_equal(const Strings& A, const E& ea, const Strings& B, const E& eb) {
+template <class EA, class EB>
+__device__ __forceinline__ bool names_equal(const Strings& A, const EA& ea, const Strings& B, const EB& eb) {
   const uint32_t ao = ea.u32(FDY_KOFF_NAME_OFFSET), al = ea.u32(FDY_KOFF_NAME_LENGTH);
   const uint32_t bo = eb.u32(FDY_KOFF_NAME_OFFSET), bl = eb.u32(FDY_KOFF_NAME_LENGTH);
   if (al != bl) return false;
@@ -501,8 +535,8 @@ __device__ __forceinline__ void node_pointers(const E& e, const RelocDev& r, uin
   }
 }
 
-template <class E>
-__device__ __forceinline__ bool u64_range_differs(const E& a, const E& b, uint32_t off, uint32_t n) {
+template <class EA, class EB>
+__device__ __forceinline__ bool u64_range_differs(const EA& a, const EB& b, uint32_t off, uint32_t n) {
   bool d = false;
   for (uint32_t i = 0; i < n; i += 8) d |= a.u64(off + i) != b.u64(off + i);
   return d;
@@ -513,10 +547,10 @@ __device__ __forceinline__ bool u64_range_differs(const E& a, const E& b, uint32
 // same_ctx: both graphs have byte-identical string sections and common
 // attrs, so equal entry bytes [8, 128) (launch config, function hash, name
 // offset and length, function attrs, per-node attrs) mean equal descriptors.
-template <class E>
-__device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const E& ea, const Strings& B,
-                             const uint8_t* cb, const E& eb, uint64_t pa0, uint64_t pa1, uint64_t pb0,
-                             uint64_t pb1, bool same_ctx) {
+template <class EA, class EB>
+__device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca, const EA& ea, const Strings& B,
+                                             const uint8_t* cb, const EB& eb, uint64_t pa0, uint64_t pa1,
+                                             uint64_t pb0, uint64_t pb1, bool same_ctx) {
   const uint8_t ta = ea.type(), tb = eb.type();
   if (ta != tb) return true;
   switch (ta) {
@@ -621,7 +655,8 @@ __device__ __forceinline__ uint32_t node_chunks(uint32_t N) { return max(1u, (N 
 // The node-type record (type, then the key's cluster dims for a kernel
 // node, csrc/CUDAGraphParallel.cpp:1807-1833) and the kernel-entry record
 // (binary hash, CRC-64/XZ of the name) of node entry e.
-__device__ __forceinline__ void node_records(const RawEntry& e, const uint8_t* common, const Strings& str,
+template <class E>
+__device__ __forceinline__ void node_records(const E& e, const uint8_t* common, const Strings& str,
                                              const uint64_t (*slice)[256], uint64_t r[4]) {
   const uint8_t type = e.type();
   r[0] = type;
@@ -658,13 +693,17 @@ struct NodeOut {
   uint64_t rec[4];  // node-type record (2 words), kernel-entry record (2 words)
 };
 
-__device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& Gg, const DevGraph& Gt, bool is_t,
-                                          uint32_t n, const Strings& sg_str, const Strings& st_str,
-                                          const uint8_t* common_g, const uint8_t* common_t, bool same_ctx,
-                                          bool xor_t, const uint64_t (*slice)[256], NodeOut& o) {
+// A template's nodes (is_t) read their entry's kernel fields up front: no
+// template side to compare with leaves registers free for them.
+template <bool is_t>
+__device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& Gg, const DevGraph& Gt, uint32_t n,
+                                          const Strings& sg_str, const Strings& st_str, const uint8_t* common_g,
+                                          const uint8_t* common_t, bool same_ctx, bool xor_t,
+                                          const uint64_t (*slice)[256], NodeOut& o) {
   const uint8_t* img = a.img;
   const uint32_t NT = Gt.num_nodes;
-  const RawEntry eg{img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n};
+  using Entry = typename std::conditional<is_t, PreEntry, RawEntry>::type;
+  const Entry eg(img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n);
   const bool has_t = !is_t && n < NT;
   const RawEntry et{img + Gt.sec_off[FDY_SEC_NODES] + 168ull * (has_t ? n : 0)};
   uint32_t words_g = 0, words_t = 0, flags = 0;
@@ -686,7 +725,10 @@ __device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& 
     if (sg.bad) flags |= kNodeBad;
     if (sg.extra) flags |= kNodeExtra;
   }
-  node_pointers(eg, a.reloc, &o.p0, &o.p1);
+  // A template's node reads its type from the prefetched fields; a member's
+  // reads the entry in place (the fields need not stay live this long).
+  if (is_t) node_pointers(eg, a.reloc, &o.p0, &o.p1);
+  else node_pointers(RawEntry{eg.e}, a.reloc, &o.p0, &o.p1);
   if (is_t) {
     flags |= FDY_NODE_TEMPLATE;
   } else if (has_t) {
@@ -701,7 +743,9 @@ __device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& 
     }
     if (layout) flags |= FDY_NODE_LAYOUT;
     else if (words_g) flags |= kNodeCompare;
-    if (desc_differs(sg_str, common_g, eg, st_str, common_t, et, o.p0, o.p1, q0, q1, same_ctx)) flags |= FDY_NODE_DESC;
+    // Read in place: the prefetched fields need not stay live this long.
+    if (desc_differs(sg_str, common_g, RawEntry{eg.e}, st_str, common_t, et, o.p0, o.p1, q0, q1, same_ctx))
+      flags |= FDY_NODE_DESC;
     if (xor_t) {
       uint64_t rt[4];
       node_records(et, common_t, st_str, slice, rt);
@@ -718,6 +762,26 @@ __device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& 
   o.d.src_g = src_g;
   o.d.src_t = src_t;
   o.pbytes = pbytes;
+}
+
+// A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
+// does not first wait for the workgroup's outstanding global stores, which
+// no thread of the workgroup reads back.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The CRC slice tables (16 KB) into LDS by a workgroup of kNodeChunk
+// threads: eight loads per thread, all issued before any store.
+__device__ __forceinline__ void stage_slice(uint64_t (*dst)[256], const uint64_t (*src)[256]) {
+  static_assert(8 * 256 == 8 * kNodeChunk, "eight words per thread");
+  uint64_t v[8];
+#pragma unroll
+  for (uint32_t k = 0; k < 8; ++k) v[k] = src[k][threadIdx.x];
+#pragma unroll
+  for (uint32_t k = 0; k < 8; ++k) dst[k][threadIdx.x] = v[k];
 }
 
 // Five waves per SIMD (registers held to 96 for that; LDS under 32 KB).
@@ -738,7 +802,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   __shared__ uint16_t s_list[kNodeChunk];
   __shared__ uint32_t s_wave_n[kNodeChunk / 64];
   __shared__ uint64_t s_pb[kNodeChunk / 64];
-  __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax;
+  __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax, s_umin, s_umax;
 
   const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint2 gt = a.chunk_gt[chunk];  // {graph, template}: the grouping pass filled in the template
@@ -759,6 +823,12 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
                     Gg.sec_size[FDY_SEC_PARAM_DATA] == Gt.sec_size[FDY_SEC_PARAM_DATA] &&
                     Gg.sec_size[FDY_SEC_ARG_DATA] == Gt.sec_size[FDY_SEC_ARG_DATA];
 
+  // Record fields used past the first barrier, kept in registers: each
+  // barrier's fence would have a later use load the field again.
+  const uint64_t pidx_size = Gg.sec_size[FDY_SEC_PARAM_INDEX];
+  const uint64_t node_base = Gg.node_base;
+  const uint64_t* pg = reinterpret_cast<const uint64_t*>(img + Gg.sec_off[FDY_SEC_PARAM_INDEX]);
+  const uint64_t* pt = reinterpret_cast<const uint64_t*>(img + Gt.sec_off[FDY_SEC_PARAM_INDEX]);
   const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
   const int64_t first = (int64_t)c * kNodeChunk - pad;  // node of thread 0
   // The chunk's entries against the template's: word w of the chunk is word
@@ -797,56 +867,124 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
       if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg[m] == FDY_NO_ARG_BUFFER;
     }
   };
-  // A member's first batch of entry loads goes out before the staging below.
-  uint64_t vg0[kCompareBatch], vt0[kCompareBatch];
-  if (fast) load_batch(0, vg0, vt0);
+  const int64_t ns = first + tid;
+  const bool valid = ns >= 0 && ns < (int64_t)N;
+  const uint32_t n = valid ? (uint32_t)ns : 0;
+  // A member's first two batches of entry loads go out before the staging
+  // below, with each thread's own node's type and param-index fields (the
+  // same lines), which bound the param entries the chunk may compare.
+  uint64_t vg0[kCompareBatch], vt0[kCompareBatch], vg1[kCompareBatch], vt1[kCompareBatch];
+  uint64_t own_type = 0, own_pidx = 0;
+  if (fast) {
+    load_batch(0, vg0, vt0);
+    load_batch(kCompareBatch, vg1, vt1);
+    own_type = *reinterpret_cast<const uint64_t*>(eg0 + 168ull * n);
+    own_pidx = *reinterpret_cast<const uint64_t*>(eg0 + 168ull * n + FDY_KOFF_PARAM_INDEX);
+  }
 
   if (tid == 0) {
     s_flags = 0;
     s_status = 0;
-    s_pmin = 0xFFFFFFFFu;
-    s_pmax = 0;
+    s_pmin = s_umin = 0xFFFFFFFFu;
+    s_pmax = s_umax = 0;
   }
   s_dirty[tid] = 0;
   s_launch[tid] = 0;
 
   // The (small) string sections and the common attrs in LDS (sections start
-  // 8-byte aligned); the CRC tables too, unless the chunk is a member's,
-  // which needs them only if some node takes the per-node path.
-  auto stage_strings = [&](const DevGraph& G, uint64_t* buf) -> Strings {
-    Strings S{img + G.sec_off[FDY_SEC_STRINGS], G.sec_size[FDY_SEC_STRINGS]};
-    if (S.size <= kStrStage) {
-      stage_words(buf, reinterpret_cast<const uint64_t*>(S.p), (uint32_t)((S.size + 7) / 8));
-      S.p = reinterpret_cast<const uint8_t*>(buf);
-    }
-    return S;
-  };
-  auto stage_common = [&](bool on, const DevGraph& G, uint64_t* buf) -> const uint8_t* {
-    if (!on) return nullptr;
-    if (tid < 7) buf[tid] = reinterpret_cast<const uint64_t*>(img + G.sec_off[FDY_SEC_COMMON_ATTRS])[tid];
-    return reinterpret_cast<const uint8_t*>(buf);
-  };
-  const Strings sg_str = stage_strings(Gg, s_str[0]);
-  const Strings st_str = is_t ? sg_str : stage_strings(Gt, s_str[1]);
-  const uint8_t* common_g = stage_common(common_g_on, Gg, s_common[0]);
-  const uint8_t* common_t = is_t ? common_g : stage_common(common_t_on, Gt, s_common[1]);
-  if (!fast) stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);
+  // 8-byte aligned).
+  // All of these loads are issued before any LDS store, so the staging costs
+  // one round trip, not one per piece.
+  Strings sg_str{img + Gg.sec_off[FDY_SEC_STRINGS], Gg.sec_size[FDY_SEC_STRINGS]};
+  Strings st_str{img + Gt.sec_off[FDY_SEC_STRINGS], Gt.sec_size[FDY_SEC_STRINGS]};
+  const bool str_g = sg_str.size <= kStrStage, str_t = !is_t && st_str.size <= kStrStage;
+  static_assert(kStrStage / 8 <= kNodeChunk, "one string word per thread");
+  const uint32_t nsg = (uint32_t)((sg_str.size + 7) / 8), nst = (uint32_t)((st_str.size + 7) / 8);
+  const bool cm_t = !is_t && common_t_on;
+  uint64_t xg = 0, xt = 0, yg = 0, yt = 0;
+  if (str_g && tid < nsg) xg = reinterpret_cast<const uint64_t*>(sg_str.p)[tid];
+  if (str_t && tid < nst) xt = reinterpret_cast<const uint64_t*>(st_str.p)[tid];
+  if (common_g_on && tid < 7) yg = reinterpret_cast<const uint64_t*>(img + Gg.sec_off[FDY_SEC_COMMON_ATTRS])[tid];
+  if (cm_t && tid < 7) yt = reinterpret_cast<const uint64_t*>(img + Gt.sec_off[FDY_SEC_COMMON_ATTRS])[tid];
+  // Every node of a chunk that is not a member's takes the per-node path: the
+  // CRC tables, in LDS.
+  uint64_t sl[8];
+  if (!fast) {
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) sl[k] = a.cc->slice.t[k][tid];
+  }
+  if (str_g && tid < nsg) s_str[0][tid] = xg;
+  if (str_t && tid < nst) s_str[1][tid] = xt;
+  if (common_g_on && tid < 7) s_common[0][tid] = yg;
+  if (cm_t && tid < 7) s_common[1][tid] = yt;
+  if (!fast) {
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) s_slice[k][tid] = sl[k];
+  }
+  if (str_g) sg_str.p = reinterpret_cast<const uint8_t*>(s_str[0]);
+  if (str_t) st_str.p = reinterpret_cast<const uint8_t*>(s_str[1]);
+  if (is_t) st_str = sg_str;
+  const uint8_t* common_g = common_g_on ? reinterpret_cast<const uint8_t*>(s_common[0]) : nullptr;
+  const uint8_t* common_t = is_t ? common_g : cm_t ? reinterpret_cast<const uint8_t*>(s_common[1]) : nullptr;
   __syncthreads();  // the marks are zero before any thread sets one
 
+  static_assert(kEntryWords == 3 * kCompareBatch, "three batches: two, then one with the param entries");
   if (fast) {
+    // Opaque from here on: left to itself the compiler tests the fields
+    // right after their loads, which waits for every load issued before them.
+    asm volatile("" : "+v"(own_type), "+v"(own_pidx));
     take_batch(0, vg0, vt0);
+    take_batch(kCompareBatch, vg1, vt1);
+    // The chunk's kernel nodes' param entries (in bounds) span [umin, umax):
+    // a superset of the clean per-param nodes' range checked below.
+    uint32_t umin = 0xFFFFFFFFu, umax = 0;
+    const uint32_t pio = (uint32_t)own_pidx, np = (uint32_t)(own_pidx >> 32);
+    const uint64_t end = (uint64_t)pio + 8ull * np;
+    if (valid && (uint8_t)(own_type >> 32) == FDY_NODE_KERNEL && np && end <= pidx_size) {
+      umin = pio;
+      umax = (uint32_t)end;
+    }
 #pragma unroll
-    for (uint32_t mb = kCompareBatch; mb < kEntryWords; mb += kCompareBatch) {
-      uint64_t vg[kCompareBatch], vt[kCompareBatch];
-      load_batch(mb, vg, vt);
-      take_batch(mb, vg, vt);
+    for (int dd = 32; dd >= 1; dd >>= 1) {
+      umin = min(umin, (uint32_t)__shfl_down(umin, (unsigned)dd, 64));
+      umax = max(umax, (uint32_t)__shfl_down(umax, (unsigned)dd, 64));
+    }
+    if (lane == 0 && umax) {
+      atomicMin(&s_umin, umin);
+      atomicMax(&s_umax, umax);
+    }
+  }
+  __syncthreads();
+  // The last entry batch, and the first kPidxSpec * kNodeChunk param-entry
+  // words of [umin, umax) on both sides, compared once loaded; which of the
+  // differing words count is settled once the clean nodes are known.  (The
+  // section sizes are equal and 8-byte aligned, so the words covering the
+  // range lie inside both.)
+  constexpr uint32_t kPidxSpec = 9;
+  const uint32_t u0 = s_umin / 8, u1 = s_umax > s_umin ? (s_umax + 7) / 8 : u0;
+  uint32_t pdiff = 0;  // bit m: word u0 + tid + m * kNodeChunk differs
+  if (fast) {
+    uint64_t vg[kCompareBatch], vt[kCompareBatch];
+    load_batch(2 * kCompareBatch, vg, vt);
+    uint64_t wg[kPidxSpec], wt[kPidxSpec];
+    if (u1 > u0) {  // uniform
+#pragma unroll
+      for (uint32_t m = 0; m < kPidxSpec; ++m) {
+        const uint32_t q = u0 + tid + m * kNodeChunk;
+        const uint32_t qc = q < u1 ? q : u1 - 1;  // a word inside the range stands in past its end
+        wg[m] = pg[qc];
+        wt[m] = pt[qc];
+      }
+    }
+    take_batch(2 * kCompareBatch, vg, vt);
+    if (u1 > u0) {
+#pragma unroll
+      for (uint32_t m = 0; m < kPidxSpec; ++m)
+        if (u0 + tid + m * kNodeChunk < u1 && wg[m] != wt[m]) pdiff |= 1u << m;
     }
   }
   __syncthreads();
 
-  const int64_t ns = first + tid;
-  const bool valid = ns >= 0 && ns < (int64_t)N;
-  const uint32_t n = valid ? (uint32_t)ns : 0;
   if (fast) {
     // Identical string sections and common attrs.
     bool d = false;
@@ -862,7 +1000,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     uint32_t pmin = 0xFFFFFFFFu, pmax = 0;
     if (valid && !s_dirty[tid] && s_type[tid] == FDY_NODE_KERNEL && s_perparam[tid] && s_np[tid]) {
       const uint64_t end = (uint64_t)s_pio[tid] + 8ull * s_np[tid];
-      if (end > Gg.sec_size[FDY_SEC_PARAM_INDEX]) {
+      if (end > pidx_size) {
         s_dirty[tid] = 1;  // out of bounds: the per-node path reports it
       } else {
         pmin = s_pio[tid];
@@ -882,17 +1020,19 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   }
   __syncthreads();
   if (fast && s_pmax > s_pmin) {
-    // The section sizes are equal and 8-byte aligned, so the words that
-    // cover [pmin, pmax) lie inside both.
-    const uint64_t* pg = reinterpret_cast<const uint64_t*>(img + Gg.sec_off[FDY_SEC_PARAM_INDEX]);
-    const uint64_t* pt = reinterpret_cast<const uint64_t*>(img + Gt.sec_off[FDY_SEC_PARAM_INDEX]);
-    // kPidxBatch words per side in flight per thread: one word per loop
-    // turn waited for each pair of loads in turn (9 us of a 31 us member
-    // chunk on the 256 x 1200 archive).
-    constexpr uint32_t kPidxBatch = 8;
+    // The words covering [pmin, pmax) inside [u0, u1): their compare is in
+    // pdiff.
+    const uint32_t p0 = s_pmin / 8, q1 = (s_pmax + 7) / 8;
     bool d = false;
-    const uint32_t q1 = (s_pmax + 7) / 8;
-    for (uint32_t q0 = s_pmin / 8 + tid; q0 < q1; q0 += kPidxBatch * kNodeChunk) {
+#pragma unroll
+    for (uint32_t m = 0; m < kPidxSpec; ++m) {
+      const uint32_t q = u0 + tid + m * kNodeChunk;
+      d |= ((pdiff >> m) & 1) && q >= p0 && q < q1;
+    }
+    // Words past the ones compared above (a chunk with more param entries),
+    // kPidxBatch per side in flight per thread.
+    constexpr uint32_t kPidxBatch = 8;
+    for (uint32_t q0 = max(p0, u0 + kPidxSpec * kNodeChunk) + tid; q0 < q1; q0 += kPidxBatch * kNodeChunk) {
       uint64_t vg[kPidxBatch], vt[kPidxBatch];
 #pragma unroll
       for (uint32_t m = 0; m < kPidxBatch; ++m) {
@@ -919,9 +1059,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   if (valid && !mine) {
     NodeDesc d{};
     d.flags = kNodeClean | (s_launch[tid] ? FDY_NODE_DESC : 0u);
-    a.node_desc[Gg.node_base + n] = d;
+    a.node_desc[node_base + n] = d;
   }
-  __syncthreads();
+  lds_barrier();  // the clean nodes' descriptors are not read back here
   uint32_t before = 0, total = 0;
 #pragma unroll
   for (uint32_t w = 0; w < kNodeChunk / 64; ++w) {
@@ -929,7 +1069,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     total += s_wave_n[w];
   }
   if (mine) s_list[before + (uint32_t)__popcll(mb & ((1ull << lane) - 1))] = (uint16_t)tid;
-  if (fast && total) stage_words(&s_slice[0][0], &a.cc->slice.t[0][0], 8 * 256);  // uniform
+  if (fast && total) stage_slice(s_slice, a.cc->slice.t);  // uniform
   __syncthreads();
 
   uint64_t pbytes = 0;
@@ -937,8 +1077,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
     const uint32_t slot = s_list[k];
     const uint32_t nn = (uint32_t)(first + slot);
     NodeOut o;
-    node_full(a, Gg, Gt, is_t, nn, sg_str, st_str, common_g, common_t, same_ctx, diff, s_slice, o);
-    const uint64_t gi = Gg.node_base + nn;
+    if (is_t) node_full<true>(a, Gg, Gt, nn, sg_str, st_str, common_g, common_t, same_ctx, diff, s_slice, o);
+    else node_full<false>(a, Gg, Gt, nn, sg_str, st_str, common_g, common_t, same_ctx, diff, s_slice, o);
+    const uint64_t gi = node_base + nn;
     a.node_desc[gi] = o.d;
     a.node_flags[gi] = (uint8_t)(o.d.flags & 0x0F);
     a.node_ptrs[2 * gi] = o.p0;
@@ -955,7 +1096,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
 #pragma unroll
   for (int d = 32; d >= 1; d >>= 1) pbytes += shfl_down64(pbytes, d);
   if (lane == 0) s_pb[wave] = pbytes;
-  __syncthreads();
+  lds_barrier();  // nor are the per-node outputs
   if (tid >= 64) return;
   if (total == 0) {  // every record is zero (clean member chunk, or padding only): so are their CRCs
     if (tid == 0) {
@@ -1230,9 +1371,10 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     sd.wend = (uint32_t)min((uint64_t)(k + 1) * kTileWords, (uint64_t)words);
     sd.graph = g;
     sd.tmpl = t;
-    sd.flags = sflags | (k == 0 ? kSlotFirst : 0u);
+    sd.flags = sflags | (k == 0 ? kSlotFirst : 0u) | (k + 1 == Gg.tile_cap ? kSlotLast : 0u);
     sd.t_cap = Gt.word_cap;
-    sd.pad[0] = sd.pad[1] = 0;
+    sd.node_base = (uint32_t)Gg.node_base;
+    sd.num_nodes = N;
     sd.t_word_base = Gt.word_base;
     a.slot_desc[Gg.tile_base + k] = sd;
     a.slot_spill[Gg.tile_base + k] = 0;
@@ -1279,15 +1421,16 @@ struct NodeWindow {
   uint32_t n0, N, nwin;
 };
 
-__device__ inline NodeWindow stage_window(const RestoreArgs& a, const DevGraph& G, uint32_t slot, NodeDesc* s_nd) {
+// The slot descriptor carries the graph's node range, so the window's loads
+// wait only for it and the tile -> node table.
+__device__ inline NodeWindow stage_window(const RestoreArgs& a, const SlotDesc& sd, uint32_t slot, NodeDesc* s_nd) {
   NodeWindow nw;
-  const uint32_t k = slot - G.tile_base;
   nw.n0 = a.tile_node[slot];
-  nw.N = G.num_nodes;
-  const uint32_t n_next = k + 1 < G.tile_cap ? a.tile_node[slot + 1] : kNoTile;
+  nw.N = sd.num_nodes;
+  const uint32_t n_next = (sd.flags & kSlotLast) ? kNoTile : a.tile_node[slot + 1];
   const uint32_t n_last = n_next == kNoTile ? nw.N - 1 : n_next;
   nw.nwin = min(kDiffWindow, n_last - nw.n0 + 1);
-  nw.nd = a.node_desc + G.node_base;
+  nw.nd = a.node_desc + sd.node_base;
   for (uint32_t i = threadIdx.x; i < nw.nwin; i += blockDim.x) s_nd[i] = nw.nd[nw.n0 + i];
   return nw;
 }
@@ -1403,7 +1546,7 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
     } else {
       const DevGraph& G = a.graphs[sd.graph];
       __syncthreads();  // the previous unit's lookups are done with s_nd
-      const NodeWindow nw = stage_window(a, G, slot, s_nd);
+      const NodeWindow nw = stage_window(a, sd, slot, s_nd);
       __syncthreads();
       uint64_t wv[kTWords];
       uint32_t node[kTWords];
@@ -1569,7 +1712,7 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   if (!flat && wend > wbeg) {  // uniform over the workgroup
     const DevGraph& G = a.graphs[g];
     const DevGraph& T = a.graphs[t];
-    const NodeWindow nw = stage_window(a, G, slot, s_nd);
+    const NodeWindow nw = stage_window(a, sd, slot, s_nd);
     __syncthreads();
     uint64_t wv[J];
     uint32_t node[J];
@@ -1743,10 +1886,12 @@ __device__ __forceinline__ void window_node(const uint2* s_gt, uint32_t nwin, ui
   }
 }
 
-// Five waves per SIMD (88 VGPRs).  Six need 80, and the spills that takes
-// cost more than the residency gains (27.6 against 26.2 us on the
-// decode-style archive).
-__global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
+// Six waves per SIMD (78 VGPRs, no spills): a batch's candidates are loaded
+// at its start rather than during the previous batch's searches, which most
+// slots (one batch) never used and which took the registers of the sixth
+// wave (search pass 26.5 -> 25.5 us on the decode-style archive, 272 -> 260
+// us on the MoE-style one).
+__global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   constexpr uint32_t K = kSBatch / 64;
   static_assert(kSubsPerSlot <= 64, "one lane per sub-range count");
   // Per wave: {first graph word, first template word} of its window's nodes.
@@ -1796,8 +1941,8 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   // Batch b's K candidates per lane, loaded unconditionally (a list index
   // past the end reads the first candidate and is masked off later) so that
   // they are issued together rather than each behind its own branch.  The
-  // first batch is loaded before the bounds and the node window, the next
-  // one before the current one's searches, so no load waits alone.
+  // first batch is loaded before the bounds and the node window, so its
+  // loads wait together with theirs.
   const Candidate* base = a.cand + (uint64_t)slot * (kSubsPerSlot * a.cand_cap + a.spill_cap);
   auto load_batch = [&](uint32_t b, Candidate* cand) {
 #pragma unroll
@@ -1827,11 +1972,12 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
     const uint4 v = earlier[j];
     before += (v.x >> 16) + (v.y >> 16) + (v.z >> 16) + (v.w >> 16);
   }
-  const DevGraph& G = a.graphs[sd.graph];
-  const uint32_t N = G.num_nodes;
-  const NodeDesc* nd = a.node_desc + G.node_base;
-  const uint32_t n_next = k + 1 < G.tile_cap ? n_after : kNoTile;
-  const uint32_t n_last = n_next == kNoTile ? N - 1 : n_next;
+  const uint32_t word_cap = a.graphs[sd.graph].word_cap;
+  const uint32_t N = sd.num_nodes;
+  const NodeDesc* nd = a.node_desc + sd.node_base;
+  // The graph's last slot, or its last slot holding words (the next one's
+  // table entry is kNoTile), ends at its last node.
+  const uint32_t n_last = ((sd.flags & kSlotLast) || n_after == kNoTile) ? N - 1 : n_after;
   const uint32_t nwin = min(kDiffWindow, n_last - n0 + 1);
   for (uint32_t i = lane; i < nwin; i += 64) {
     const uint4 v = *reinterpret_cast<const uint4*>(nd + n0 + i);  // gword, nwords, tword, flags
@@ -1849,8 +1995,8 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   // The graph's record region: in the compact layout it can be smaller than
   // the records' bound, and then nothing is written and the restore runs
   // again with full-capacity scratch.
-  const uint64_t rb = G.word_base >> a.rec_shift;
-  const uint64_t rcap = ((G.word_base + G.word_cap) >> a.rec_shift) - rb;
+  const uint64_t rb = sd.word_base >> a.rec_shift;
+  const uint64_t rcap = ((sd.word_base + word_cap) >> a.rec_shift) - rb;
   if ((uint64_t)before + bound > rcap) {  // uniform over the wave
     if (lane == 0) {
       a.slot_rec[slot] = 0;
@@ -1862,6 +2008,7 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
   const uint64_t lt = (1ull << lane) - 1;
   uint32_t run = 0;
   for (uint32_t b = 0; b < total; b += kSBatch) {
+    if (b) load_batch(b, cur);  // uniform over the wave
     uint64_t raw[K], tval[K], res[K];
     uint32_t word[K], fl[K], m = 0;
 #pragma unroll
@@ -1873,7 +2020,6 @@ __global__ __launch_bounds__(kSThreads, 5) void k_diff_s(RestoreArgs a) {
       fl[kk] = in ? cur[kk].flags : 0;
       if (fl[kk] & kCandReloc) m |= 1u << kk;
     }
-    if (b + kSBatch < total) load_batch(b + kSBatch, cur);  // uniform over the wave
     reloc_batch<K>(a.reloc, raw, res, m);
     // The member pass stored each candidate's raw word; only the words the
     // relocation moved are stored again (a scattered 8-byte store costs a

@@ -277,6 +277,7 @@ int finish_open(fdy_archive* a, const std::vector<std::vector<uint8_t>>& heads, 
     slots += d.tile_cap;
     chunks += std::max<uint64_t>(1, (d.num_nodes + kNodeChunk - 1) / kNodeChunk);  // at least one per graph
   }
+  if (nodes >= (1ull << 32)) return err(FDY_E_FORMAT, "archive too large (2^32 nodes or more)");
   // The member pass launches 1024 threads per tile, and a launch holds fewer than 2^32 threads.
   if (slots >= (1ull << 22)) return err(FDY_E_FORMAT, "archive too large (more than 2^22 diff tiles, 128 GiB of params)");
   a->total_nodes = nodes;

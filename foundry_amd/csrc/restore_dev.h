@@ -108,6 +108,7 @@ constexpr uint32_t kSlotFlat = 1;      // every word of the tile sits at kg + 8w
 constexpr uint32_t kSlotCompare = 2;   // flat tile whose words are compared with the template
 constexpr uint32_t kSlotTemplate = 4;  // tile of a template graph
 constexpr uint32_t kSlotFirst = 8;     // the graph's first slot
+constexpr uint32_t kSlotLast = 16;     // the graph's last slot
 struct SlotDesc {
   uint64_t kg;           // flat: byte offset of image word 0 of the graph in the file image
   uint64_t kt;           // flat + compare: the same for the template
@@ -118,7 +119,8 @@ struct SlotDesc {
   uint32_t tmpl;         // the graph's template
   uint32_t flags;        // kSlot*
   uint32_t t_cap;        // the template's image capacity in words
-  uint32_t pad[2];
+  uint32_t node_base;    // the graph's node 0 in the node arrays (an archive holds fewer than 2^32 nodes)
+  uint32_t num_nodes;    // the graph's node count
 };
 static_assert(sizeof(SlotDesc) == 64, "SlotDesc is one 64-byte line");
 
