@@ -764,6 +764,10 @@ __device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& 
   o.pbytes = pbytes;
 }
 
+// Two consecutive 8-byte words as one 16-byte access at 8-byte alignment
+// (gfx950 serves a 16-byte global access at any 4-byte alignment).
+typedef uint64_t u64x2a8 __attribute__((ext_vector_type(2), aligned(8)));
+
 // A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
 // does not first wait for the workgroup's outstanding global stores, which
 // no thread of the workgroup reads back.
@@ -1637,7 +1641,7 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
 // The other graphs: kMSplit workgroups per slot, each of kMThreads / 64
 // waves; wave v of the slot (counted over its workgroups) owns the slot's
 // sub-range v (kSubWords consecutive words), lane l its words
-// v*kSubWords + j*64 + l for j < kMWords.  Small workgroups retire and are
+// v*kSubWords + 128h + 2l and the one after, for h < kMWords / 2.  Small workgroups retire and are
 // replaced wave by wave, where one workgroup per slot left its CU idle
 // while its last waves finished (measured: 91 us against 100 us for the
 // 256-graph decode-style archive).  Relocation is a function of the
@@ -1671,7 +1675,12 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   }
   const uint32_t g = sd.graph, t = sd.tmpl;
   const uint64_t wbeg = sd.wbeg, wend = sd.wend;
-  const uint64_t w0 = wbeg + (uint64_t)wave * kSubWords + lane;  // word j is w0 + 64j
+  // Lane l holds words 2l and 2l + 1 of each 128-word half of the sub-range:
+  // word j is wb + 128 (j / 2) + j % 2, so a flat tile's pairs load and store
+  // as 16-byte accesses (half the address-unit work of one word per lane).
+  static_assert(J % 2 == 0 && kSubWords == 64 * J, "pairs of words per lane");
+  const uint64_t wb = wbeg + (uint64_t)wave * kSubWords + 2 * lane;
+  auto word_of = [&](uint32_t j) -> uint64_t { return wb + 128 * (j >> 1) + (j & 1); };
   const bool flat = (sd.flags & kSlotFlat) != 0;
   const RelocDev& R = a.reloc;
   // Issued ahead of the word loads so that its wait does not follow theirs.
@@ -1693,19 +1702,36 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
     const uint8_t* pg = a.img + sd.kg;
     const uint8_t* pt = a.img + sd.kt;
 #pragma unroll
-    for (uint32_t j = 0; j < J; ++j) {
-      const uint64_t w = w0 + 64 * j;
-      fg[j] = ft[j] = fr[j] = 0;
-      if (w < wend) {
-        valid |= 1u << j;
-        fg[j] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
-        ft[j] = *reinterpret_cast<const uint64_t*>(pt + 8 * w);
+    for (uint32_t q = 0; q < J / 2; ++q) {
+      const uint64_t w = word_of(2 * q);
+      fg[2 * q] = ft[2 * q] = fr[2 * q] = fg[2 * q + 1] = ft[2 * q + 1] = fr[2 * q + 1] = 0;
+      if (w + 1 < wend) {
+        valid |= 3u << (2 * q);
+        const u64x2a8 g2 = *reinterpret_cast<const u64x2a8*>(pg + 8 * w);
+        const u64x2a8 t2 = *reinterpret_cast<const u64x2a8*>(pt + 8 * w);
+        fg[2 * q] = g2.x;
+        fg[2 * q + 1] = g2.y;
+        ft[2 * q] = t2.x;
+        ft[2 * q + 1] = t2.y;
+      } else if (w < wend) {
+        valid |= 1u << (2 * q);
+        fg[2 * q] = *reinterpret_cast<const uint64_t*>(pg + 8 * w);
+        ft[2 * q] = *reinterpret_cast<const uint64_t*>(pt + 8 * w);
       }
     }
     if (R.n != 0) {
 #pragma unroll
-      for (uint32_t j = 0; j < J; ++j)
-        if ((valid >> j) & 1) fr[j] = rimg_t[min(w0 + 64 * j, (uint64_t)t_last)];
+      for (uint32_t q = 0; q < J / 2; ++q) {
+        const uint64_t w = word_of(2 * q);
+        if (((valid >> (2 * q)) & 3) == 3 && w + 1 <= t_last) {
+          const u64x2a8 r2 = *reinterpret_cast<const u64x2a8*>(rimg_t + w);
+          fr[2 * q] = r2.x;
+          fr[2 * q + 1] = r2.y;
+        } else {
+          if ((valid >> (2 * q)) & 1) fr[2 * q] = rimg_t[min(w, (uint64_t)t_last)];
+          if ((valid >> (2 * q + 1)) & 1) fr[2 * q + 1] = rimg_t[min(w + 1, (uint64_t)t_last)];
+        }
+      }
     }
     cmp = full = valid;
   }
@@ -1717,7 +1743,7 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
     uint64_t wv[J];
     uint32_t node[J];
 #pragma unroll
-    for (uint32_t j = 0; j < J; ++j) wv[j] = w0 + 64 * j;
+    for (uint32_t j = 0; j < J; ++j) wv[j] = word_of(j);
     find_nodes<J>(s_nd, nw, wv, node);
 #pragma unroll
     for (uint32_t j = 0; j < J; ++j) {
@@ -1764,13 +1790,26 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   // k_diff_s writes the relocated one, so each word takes one
   // unconditional store.
   uint32_t cand = 0, creloc = 0;
+  uint64_t res[J];
+#pragma unroll
+  for (uint32_t j = 0; j < J; ++j) res[j] = ((cmp >> j) & 1) && fg[j] == ft[j] ? fr[j] : fg[j];
+#pragma unroll
+  for (uint32_t q = 0; q < J / 2; ++q) {
+    const uint64_t w = word_of(2 * q);
+    if (((valid >> (2 * q)) & 3) == 3) {
+      u64x2a8 r2;
+      r2.x = res[2 * q];
+      r2.y = res[2 * q + 1];
+      *reinterpret_cast<u64x2a8*>(img_out + w) = r2;
+    } else if ((valid >> (2 * q)) & 1) {
+      img_out[w] = res[2 * q];
+    }
+  }
 #pragma unroll
   for (uint32_t j = 0; j < J; ++j) {
     if (!((valid >> j) & 1)) continue;
-    const uint64_t w = w0 + 64 * j;
     const bool c = (cmp >> j) & 1;
     const bool same = c && fg[j] == ft[j];
-    img_out[w] = same ? fr[j] : fg[j];
     if (same) continue;
     if (!((full >> j) & 1)) {
       if (c && fg[j] != fr[j]) cand |= 1u << j;
@@ -1787,20 +1826,28 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   const uint64_t lt = (1ull << lane) - 1;
   if (!flat) __syncthreads();  // every wave of the workgroup is done with the node window
   Candidate* stage = reinterpret_cast<Candidate*>(s_nd) + (tid >> 6) * kSubWords;
+  // In word order: within a 128-word half, lane l's two words follow the
+  // candidates of the lanes below it.
   uint32_t run = 0, ncmp = 0;
 #pragma unroll
-  for (uint32_t j = 0; j < J; ++j) {
-    const uint64_t mk = __ballot((cand >> j) & 1);
-    ncmp += (uint32_t)__popcll(__ballot(((cand & cmp) >> j) & 1));
-    if ((cand >> j) & 1) {
-      Candidate c;
-      c.word = (uint32_t)(w0 + 64 * j);
-      c.flags = (((creloc >> j) & 1) ? kCandReloc : 0u) | (((cmp >> j) & 1) ? kCandCompare : 0u);
-      c.raw = fg[j];
-      c.tval = fr[j];
-      stage[run + (uint32_t)__popcll(mk & lt)] = c;
+  for (uint32_t q = 0; q < J / 2; ++q) {
+    const uint64_t m0 = __ballot((cand >> (2 * q)) & 1), m1 = __ballot((cand >> (2 * q + 1)) & 1);
+    ncmp += (uint32_t)__popcll(__ballot(((cand & cmp) >> (2 * q)) & 1)) +
+            (uint32_t)__popcll(__ballot(((cand & cmp) >> (2 * q + 1)) & 1));
+    const uint32_t below = (uint32_t)__popcll(m0 & lt) + (uint32_t)__popcll(m1 & lt);
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t j = 2 * q + h;
+      if ((cand >> j) & 1) {
+        Candidate c;
+        c.word = (uint32_t)word_of(j);
+        c.flags = (((creloc >> j) & 1) ? kCandReloc : 0u) | (((cmp >> j) & 1) ? kCandCompare : 0u);
+        c.raw = fg[j];
+        c.tval = fr[j];
+        stage[run + below + (h ? (uint32_t)((m0 >> lane) & 1) : 0u)] = c;
+      }
     }
-    run += (uint32_t)__popcll(mk);
+    run += (uint32_t)__popcll(m0) + (uint32_t)__popcll(m1);
   }
   // The first cand_cap candidates go to the sub-range's own region, the
   // rest to the slot's spill space (taken with one atomic, by the few waves
