@@ -645,8 +645,6 @@ __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* 
 // flatness, status, digests and the slot descriptors of the diff pass.
 
 constexpr uint32_t kEntryWords = 168 / 8;  // 8-byte words of a node entry
-constexpr uint32_t kCompareBatch = 7;      // entry words per side whose loads are issued together
-static_assert(kEntryWords % kCompareBatch == 0, "whole batches");
 constexpr uint32_t kStrStage = 2048;       // string sections up to this size are staged in LDS
 constexpr uint32_t kChunkCtxDiff = 1, kChunkPidxDiff = 2;
 
@@ -806,7 +804,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   __shared__ uint16_t s_list[kNodeChunk];
   __shared__ uint32_t s_wave_n[kNodeChunk / 64];
   __shared__ uint64_t s_pb[kNodeChunk / 64];
-  __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax, s_umin, s_umax;
+  __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax, s_umin;
 
   const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const uint2 gt = a.chunk_gt[chunk];  // {graph, template}: the grouping pass filled in the template
@@ -836,61 +834,76 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   const uint32_t pad = (kNodeChunk - N % kNodeChunk) % kNodeChunk;
   const int64_t first = (int64_t)c * kNodeChunk - pad;  // node of thread 0
   // The chunk's entries against the template's: word w of the chunk is word
-  // w % 21 of its node w / 21 (168 = 21 * 8), read coalesced.
+  // w % 21 of its node w / 21 (168 = 21 * 8), read coalesced, two words
+  // (16 bytes) per lane per load: pair p = tid + 256 m holds words 2p, 2p + 1.
   const uint8_t* eg0 = img + Gg.sec_off[FDY_SEC_NODES];
   const uint8_t* et0 = img + Gt.sec_off[FDY_SEC_NODES];
   const int64_t b0 = first * 168, bend = 168 * (int64_t)N;
-  auto load_batch = [&](uint32_t mb, uint64_t* vg, uint64_t* vt) {
-#pragma unroll
-    for (uint32_t m = 0; m < kCompareBatch; ++m) {
-      const int64_t off = b0 + 8 * (int64_t)(tid + kNodeChunk * (mb + m));
-      const bool ok = off >= 0 && off < bend;
-      vg[m] = ok ? *reinterpret_cast<const uint64_t*>(eg0 + off) : 0;
-      vt[m] = ok ? *reinterpret_cast<const uint64_t*>(et0 + off) : 0;
-    }
+  static_assert(kEntryWords * kNodeChunk % 2 == 0, "whole pairs");
+  constexpr uint32_t kPairs = kEntryWords * kNodeChunk / 2;  // per side
+  // Loaded without a branch (a branch per pair made each wait for the one
+  // before): a pair wholly before the chunk's first node (its padded front)
+  // reads the section's first pair instead, and the one straddling the
+  // section start reads the 8 bytes before it, which the file's header and
+  // directory precede; take_pair drops the words before the first node.  A
+  // chunk's pairs never pass its last node.
+  auto pair_off = [&](uint32_t m) -> int64_t { return b0 + 16 * (int64_t)(tid + kNodeChunk * m); };
+  auto load_pair = [&](uint32_t m, uint64_t* vg, uint64_t* vt) {
+    const int64_t off = pair_off(m);
+    const int64_t offl = off < -8 ? 0 : off;
+    const u64x2a8 g2 = *reinterpret_cast<const u64x2a8*>(eg0 + offl);
+    const u64x2a8 t2 = *reinterpret_cast<const u64x2a8*>(et0 + offl);
+    vg[0] = g2.x;
+    vg[1] = g2.y;
+    vt[0] = t2.x;
+    vt[1] = t2.y;
   };
-  auto take_batch = [&](uint32_t mb, const uint64_t* vg, const uint64_t* vt) {
-#pragma unroll
-    for (uint32_t m = 0; m < kCompareBatch; ++m) {
-      const uint32_t w = tid + kNodeChunk * (mb + m), node = w / kEntryWords, k = w % kEntryWords;
-      // Words 1-3 and the low half of word 4 of a kernel entry are its
-      // launch dimensions and shared memory (bytes 8-36): a difference there
-      // alone changes the node's descriptor and nothing else.
-      const uint64_t x = vg[m] ^ vt[m];
-      if (x) {
-        if ((k >= 1 && k <= 3) || (k == 4 && (x >> 32) == 0)) s_launch[node] = 1;
-        else s_dirty[node] = 1;
-      }
-      // Fields the param-entry check needs: type (word 0), param index
-      // offset and count (word 16), arg buffer offset (word 17).
-      if (k == 0) s_type[node] = (uint8_t)(vg[m] >> 32);
-      if (k == FDY_KOFF_PARAM_INDEX / 8) {
-        s_pio[node] = (uint32_t)vg[m];
-        s_np[node] = (uint32_t)(vg[m] >> 32);
-      }
-      if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg[m] == FDY_NO_ARG_BUFFER;
+  auto take_word = [&](uint32_t w, uint64_t vg, uint64_t vt) {
+    const uint32_t node = w / kEntryWords, k = w % kEntryWords;
+    // Words 1-3 and the low half of word 4 of a kernel entry are its
+    // launch dimensions and shared memory (bytes 8-36): a difference there
+    // alone changes the node's descriptor and nothing else.
+    const uint64_t x = vg ^ vt;
+    if (x) {
+      if ((k >= 1 && k <= 3) || (k == 4 && (x >> 32) == 0)) s_launch[node] = 1;
+      else s_dirty[node] = 1;
     }
+    // Fields the param-entry check needs: type (word 0), param index
+    // offset and count (word 16), arg buffer offset (word 17).
+    if (k == 0) s_type[node] = (uint8_t)(vg >> 32);
+    if (k == FDY_KOFF_PARAM_INDEX / 8) {
+      s_pio[node] = (uint32_t)vg;
+      s_np[node] = (uint32_t)(vg >> 32);
+    }
+    if (k == FDY_KOFF_ARG_OFFSET / 8) s_perparam[node] = (uint32_t)vg == FDY_NO_ARG_BUFFER;
   };
+  auto take_pair = [&](uint32_t m, const uint64_t* vg, const uint64_t* vt) {
+    const uint32_t w = 2 * (tid + kNodeChunk * m);
+    const int64_t off = pair_off(m);
+    if (off >= 0) take_word(w, vg[0], vt[0]);
+    if (off >= -8) take_word(w + 1, vg[1], vt[1]);
+  };
+  // Pairs 0-6 in the first round, 7-10 in the second (pair 10 for the first
+  // half of the threads).
+  constexpr uint32_t kPairs1 = 7, kPairs2 = (kPairs + kNodeChunk - 1) / kNodeChunk - kPairs1;
+  static_assert(kPairs2 == 4 && kPairs - (kPairs1 + kPairs2 - 1) * kNodeChunk == kNodeChunk / 2, "pair rounds");
+  // The nodes whose param-index field (entry word 16) the first round holds.
+  constexpr uint32_t kSpecNodes = (2 * kPairs1 * kNodeChunk - FDY_KOFF_PARAM_INDEX / 8 - 1) / kEntryWords + 1;
   const int64_t ns = first + tid;
   const bool valid = ns >= 0 && ns < (int64_t)N;
   const uint32_t n = valid ? (uint32_t)ns : 0;
-  // A member's first two batches of entry loads go out before the staging
-  // below, with each thread's own node's type and param-index fields (the
-  // same lines), which bound the param entries the chunk may compare.
-  uint64_t vg0[kCompareBatch], vt0[kCompareBatch], vg1[kCompareBatch], vt1[kCompareBatch];
-  uint64_t own_type = 0, own_pidx = 0;
+  // A member's first round of entry loads goes out before the staging below.
+  uint64_t vg0[2 * kPairs1], vt0[2 * kPairs1];
   if (fast) {
-    load_batch(0, vg0, vt0);
-    load_batch(kCompareBatch, vg1, vt1);
-    own_type = *reinterpret_cast<const uint64_t*>(eg0 + 168ull * n);
-    own_pidx = *reinterpret_cast<const uint64_t*>(eg0 + 168ull * n + FDY_KOFF_PARAM_INDEX);
+#pragma unroll
+    for (uint32_t m = 0; m < kPairs1; ++m) load_pair(m, vg0 + 2 * m, vt0 + 2 * m);
   }
 
   if (tid == 0) {
     s_flags = 0;
     s_status = 0;
     s_pmin = s_umin = 0xFFFFFFFFu;
-    s_pmax = s_umax = 0;
+    s_pmax = 0;
   }
   s_dirty[tid] = 0;
   s_launch[tid] = 0;
@@ -932,44 +945,39 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   const uint8_t* common_t = is_t ? common_g : cm_t ? reinterpret_cast<const uint8_t*>(s_common[1]) : nullptr;
   __syncthreads();  // the marks are zero before any thread sets one
 
-  static_assert(kEntryWords == 3 * kCompareBatch, "three batches: two, then one with the param entries");
   if (fast) {
-    // Opaque from here on: left to itself the compiler tests the fields
-    // right after their loads, which waits for every load issued before them.
-    asm volatile("" : "+v"(own_type), "+v"(own_pidx));
-    take_batch(0, vg0, vt0);
-    take_batch(kCompareBatch, vg1, vt1);
-    // The chunk's kernel nodes' param entries (in bounds) span [umin, umax):
-    // a superset of the clean per-param nodes' range checked below.
-    uint32_t umin = 0xFFFFFFFFu, umax = 0;
-    const uint32_t pio = (uint32_t)own_pidx, np = (uint32_t)(own_pidx >> 32);
-    const uint64_t end = (uint64_t)pio + 8ull * np;
-    if (valid && (uint8_t)(own_type >> 32) == FDY_NODE_KERNEL && np && end <= pidx_size) {
-      umin = pio;
-      umax = (uint32_t)end;
-    }
 #pragma unroll
-    for (int dd = 32; dd >= 1; dd >>= 1) {
-      umin = min(umin, (uint32_t)__shfl_down(umin, (unsigned)dd, 64));
-      umax = max(umax, (uint32_t)__shfl_down(umax, (unsigned)dd, 64));
-    }
-    if (lane == 0 && umax) {
-      atomicMin(&s_umin, umin);
-      atomicMax(&s_umax, umax);
-    }
+    for (uint32_t m = 0; m < kPairs1; ++m) take_pair(m, vg0 + 2 * m, vt0 + 2 * m);
+  }
+  lds_barrier();
+  if (fast) {
+    // The first in-bounds param entry of the kernel nodes whose fields the
+    // first round held: where the chunk's param entries most likely start.
+    uint32_t umin = 0xFFFFFFFFu;
+    if (valid && tid < kSpecNodes && s_type[tid] == FDY_NODE_KERNEL && s_np[tid] &&
+        (uint64_t)s_pio[tid] + 8ull * s_np[tid] <= pidx_size)
+      umin = s_pio[tid];
+#pragma unroll
+    for (int dd = 32; dd >= 1; dd >>= 1) umin = min(umin, (uint32_t)__shfl_down(umin, (unsigned)dd, 64));
+    if (lane == 0 && umin != 0xFFFFFFFFu) atomicMin(&s_umin, umin);
   }
   __syncthreads();
-  // The last entry batch, and the first kPidxSpec * kNodeChunk param-entry
-  // words of [umin, umax) on both sides, compared once loaded; which of the
-  // differing words count is settled once the clean nodes are known.  (The
-  // section sizes are equal and 8-byte aligned, so the words covering the
-  // range lie inside both.)
+  // The last entry pairs, and kPidxSpec * kNodeChunk param-entry words from
+  // there on both sides (within the section: the sizes are equal and 8-byte
+  // aligned), compared once loaded; which of the differing words count is
+  // settled once the clean nodes are known.
   constexpr uint32_t kPidxSpec = 9;
-  const uint32_t u0 = s_umin / 8, u1 = s_umax > s_umin ? (s_umax + 7) / 8 : u0;
+  const uint32_t pidx_words = (uint32_t)(pidx_size / 8);
+  const uint32_t u0 = s_umin == 0xFFFFFFFFu ? 0 : s_umin / 8;
+  const uint32_t u1 = s_umin == 0xFFFFFFFFu ? 0 : min(u0 + kPidxSpec * kNodeChunk, pidx_words);
   uint32_t pdiff = 0;  // bit m: word u0 + tid + m * kNodeChunk differs
   if (fast) {
-    uint64_t vg[kCompareBatch], vt[kCompareBatch];
-    load_batch(2 * kCompareBatch, vg, vt);
+    uint64_t vg[2 * kPairs2], vt[2 * kPairs2];
+#pragma unroll
+    for (uint32_t m = 0; m < kPairs2; ++m) {
+      vg[2 * m] = vg[2 * m + 1] = vt[2 * m] = vt[2 * m + 1] = 0;
+      if (tid + kNodeChunk * (kPairs1 + m) < kPairs) load_pair(kPairs1 + m, vg + 2 * m, vt + 2 * m);
+    }
     uint64_t wg[kPidxSpec], wt[kPidxSpec];
     if (u1 > u0) {  // uniform
 #pragma unroll
@@ -980,7 +988,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
         wt[m] = pt[qc];
       }
     }
-    take_batch(2 * kCompareBatch, vg, vt);
+#pragma unroll
+    for (uint32_t m = 0; m < kPairs2; ++m)
+      if (tid + kNodeChunk * (kPairs1 + m) < kPairs) take_pair(kPairs1 + m, vg + 2 * m, vt + 2 * m);
     if (u1 > u0) {
 #pragma unroll
       for (uint32_t m = 0; m < kPidxSpec; ++m)
@@ -1033,20 +1043,29 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
       const uint32_t q = u0 + tid + m * kNodeChunk;
       d |= ((pdiff >> m) & 1) && q >= p0 && q < q1;
     }
-    // Words past the ones compared above (a chunk with more param entries),
-    // kPidxBatch per side in flight per thread.
+    // Words outside the ones compared above (before them, or past them in a
+    // chunk with more param entries), kPidxBatch per side in flight per
+    // thread.
     constexpr uint32_t kPidxBatch = 8;
-    for (uint32_t q0 = max(p0, u0 + kPidxSpec * kNodeChunk) + tid; q0 < q1; q0 += kPidxBatch * kNodeChunk) {
-      uint64_t vg[kPidxBatch], vt[kPidxBatch];
+    auto compare_words = [&](uint32_t r0, uint32_t r1) {
+      for (uint32_t q0 = r0 + tid; q0 < r1; q0 += kPidxBatch * kNodeChunk) {
+        uint64_t vg[kPidxBatch], vt[kPidxBatch];
 #pragma unroll
-      for (uint32_t m = 0; m < kPidxBatch; ++m) {
-        const uint32_t q = q0 + m * kNodeChunk;
-        const uint32_t qc = q < q1 ? q : q1 - 1;  // a word inside the range stands in past its end
-        vg[m] = pg[qc];
-        vt[m] = pt[qc];
+        for (uint32_t m = 0; m < kPidxBatch; ++m) {
+          const uint32_t q = q0 + m * kNodeChunk;
+          const uint32_t qc = q < r1 ? q : r1 - 1;  // a word inside the range stands in past its end
+          vg[m] = pg[qc];
+          vt[m] = pt[qc];
+        }
+#pragma unroll
+        for (uint32_t m = 0; m < kPidxBatch; ++m) d |= vg[m] != vt[m];
       }
-#pragma unroll
-      for (uint32_t m = 0; m < kPidxBatch; ++m) d |= vg[m] != vt[m];
+    };
+    if (u1 > u0) {
+      compare_words(p0, min(q1, u0));
+      compare_words(max(p0, u1), q1);
+    } else {
+      compare_words(p0, q1);
     }
     if (d) atomicOr(&s_flags, kChunkPidxDiff);
   }

@@ -260,3 +260,83 @@ def test_members_of_an_overflowed_template(cuda):
         np.testing.assert_array_equal(a, b0, err_msg=f"node-0 overrides g={g}")
         with pytest.raises(FoundryError):
             arch.switch(g)
+
+
+def _reorder_param_index(img: bytes, order) -> bytes:
+    """The archive with its param-index entries regrouped node by node in
+    `order` (every kernel node's entries kept together and in their own
+    order; each entry's param-index offset updated): the same params, laid
+    out other than in node order, which the format allows."""
+    import struct
+
+    img = bytearray(img)
+    sec = lambda i: struct.unpack_from("<QQ", img, 64 + 24 * i + 8)  # (offset, size)
+    nodes_off, _ = sec(1)
+    pidx_off, pidx_size = sec(3)
+    n_nodes = struct.unpack_from("<I", img, 16)[0]
+    old = bytes(img[pidx_off:pidx_off + pidx_size])
+    at = 0
+    for n in order:
+        e = nodes_off + 168 * n
+        if img[e + 4] != 0:
+            continue
+        pio, np_ = struct.unpack_from("<II", img, e + 128)
+        img[pidx_off + at:pidx_off + at + 8 * np_] = old[pio:pio + 8 * np_]
+        struct.pack_into("<I", img, e + 128, at)
+        at += 8 * np_
+    assert at == pidx_size and n_nodes > max(order)
+    return bytes(img)
+
+
+def test_param_entries_out_of_node_order(cuda):
+    # Param-index entries laid out in reverse node order: a member chunk's
+    # first nodes then hold the highest offsets, so the param entries it
+    # compares start below the range its first loads suggest.  Members differ
+    # from their template in param data, and two of them in the param entries
+    # of one node (two params' offsets swapped) below and inside that range;
+    # every output must equal the oracle's.
+    import struct
+
+    import cugraph_writer as W
+
+    print("[case] param entries in reverse node order: 300 kernel nodes, template + 3 members", flush=True)
+    N, base, size = 300, 0x7F0000000000, 1 << 32
+    rng = np.random.default_rng(11)
+
+    def words(k):
+        return [int(base + 16 * rng.integers(0, size // 16)) if rng.random() < 0.4 else int(rng.integers(0, 1 << 62))
+                for _ in range(k)]
+
+    tvals = [words(4) for _ in range(N)]
+
+    def graph(vals, swap_node=None):
+        nodes = [W.Kernel(f"k{n % 7}", 0x1234 + n % 3, params=[W.le(v) for v in vals[n]]) for n in range(N)]
+        img = _reorder_param_index(W.write(nodes), list(range(N - 1, -1, -1)))
+        if swap_node is not None:  # the node's first two params read each other's bytes
+            img = bytearray(img)
+            nodes_off = struct.unpack_from("<Q", img, 64 + 24 * 1 + 8)[0]
+            pidx_off = struct.unpack_from("<Q", img, 64 + 24 * 3 + 8)[0]
+            pio = struct.unpack_from("<I", img, nodes_off + 168 * swap_node + 128)[0]
+            a, b = struct.unpack_from("<8s8s", img, pidx_off + pio)
+            struct.pack_into("<8s8s", img, pidx_off + pio, b, a)
+            img = bytes(img)
+        return img
+
+    images = [graph(tvals)]
+    for swap in (250, 100, None):
+        vals = [list(v) for v in tvals]
+        for n in range(0, N, 7):
+            vals[n][n % 4] = words(1)[0]
+        images.append(graph(vals, swap))
+    lo = np.array([base], dtype=np.uint64)
+    hi = np.array([base + size], dtype=np.uint64)
+    nlo = np.array([0x7E0000000000], dtype=np.uint64)
+    arch = Archive.from_images(images)
+    arch.set_relocation(lo, hi, nlo)
+    arch.restore()
+    ref = oracle.Restore(images, (lo, hi, nlo))
+    assert ref.groups().tolist() == [0, 0, 0, 0]
+    # The swapped entries change what those nodes' first two params read.
+    for g, n in ((1, 250), (2, 100)):
+        assert (ref.overrides(g)["node"] == n).any(), (g, n)
+    assert_restore_parity(arch, ref)
