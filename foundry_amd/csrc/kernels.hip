@@ -40,7 +40,7 @@
 namespace fdy {
 namespace {
 
-constexpr uint32_t kNodeThreads = 1024;
+constexpr uint32_t kNodeThreads = 512;
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
 
@@ -578,26 +578,49 @@ __device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca
   }
 }
 
-// Exclusive block-wide prefix sum of 256 u32 values; *total gets the sum.
-__device__ uint32_t block_excl_scan(uint32_t v, uint32_t* s_tmp, uint32_t* total) {
+// A graph record read through the constant address space (scalar loads).
+typedef __attribute__((address_space(4))) const DevGraph ConstGraph;
+
+// A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
+// does not first wait for the workgroup's outstanding global stores, which
+// no thread of the workgroup reads back.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Exclusive block-wide prefix sums of two u32 values per thread (over
+// blockDim.x <= 1024 threads); tot[0..1] get the sums.  The workgroup's two
+// barriers order its LDS only.
+__device__ void block_excl_scan2(const uint32_t v[2], uint32_t (*s_tmp)[16], uint32_t out[2], uint32_t tot[2]) {
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  uint32_t x = v;
+  uint32_t x[2] = {v[0], v[1]};
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    uint32_t y = shfl_up32(x, d);
-    if (lane >= (uint32_t)d) x += y;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t y = shfl_up32(x[k], d);
+      if (lane >= (uint32_t)d) x[k] += y;
+    }
   }
-  if (lane == 63) s_tmp[wave] = x;
-  __syncthreads();
-  uint32_t before = 0, sum = 0;
-  for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
-    uint32_t t = s_tmp[w];
-    if (w < wave) before += t;
-    sum += t;
+  if (lane == 63) {
+    s_tmp[0][wave] = x[0];
+    s_tmp[1][wave] = x[1];
   }
-  __syncthreads();
-  *total = sum;
-  return before + x - v;
+  lds_barrier();
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    uint32_t before = 0, sum = 0;
+    for (uint32_t w = 0; w < blockDim.x / 64; ++w) {
+      const uint32_t t = s_tmp[k][w];
+      if (w < wave) before += t;
+      sum += t;
+    }
+    out[k] = before + x[k] - v[k];
+    tot[k] = sum;
+  }
+  lds_barrier();
 }
 
 __device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* e, const Side& s, uint64_t* aux,
@@ -765,15 +788,6 @@ __device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& 
 // Two consecutive 8-byte words as one 16-byte access at 8-byte alignment
 // (gfx950 serves a 16-byte global access at any 4-byte alignment).
 typedef uint64_t u64x2a8 __attribute__((ext_vector_type(2), aligned(8)));
-
-// A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
-// does not first wait for the workgroup's outstanding global stores, which
-// no thread of the workgroup reads back.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // The CRC slice tables (16 KB) into LDS by a workgroup of kNodeChunk
 // threads: eight loads per thread, all issued before any store.
@@ -1160,8 +1174,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   }
 }
 
-__global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
-  __shared__ uint32_t s_tmp[kNodeThreads / 64];
+__global__ __launch_bounds__(kNodeThreads, 6) void k_node_b(RestoreArgs a) {
+  static_assert(kNodeThreads <= 1024, "a scan step holds 16 waves");
+  __shared__ uint32_t s_tmp[2][16];
   __shared__ uint64_t s_x[4][kNodeThreads / 64];
   __shared__ unsigned long long s_pb;
   __shared__ uint32_t s_status, s_words, s_flat, s_tbase;
@@ -1174,10 +1189,12 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     // the digest (XOR is order-free).  Every load that does not depend on
     // the slice's bytes is issued with them, before the tables are staged.
     __shared__ uint64_t s_slice[8][256];
-    static_assert(8 * 256 == 2 * kNodeThreads, "two table words per thread");
+    static_assert(8 * 256 == 4 * kNodeThreads, "four table words per thread");
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t* tab = &a.cc->slice.t[0][0];
-    const uint64_t t0 = tab[threadIdx.x], t1 = tab[threadIdx.x + kNodeThreads];
+    uint64_t tw[4];
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) tw[k] = tab[threadIdx.x + k * kNodeThreads];
     const uint32_t u = (blockIdx.x - a.num_graphs) * (kNodeThreads / 64) + (threadIdx.x >> 6);
     const bool on = u < a.num_units;
     const DigestUnit du = a.units[on ? u : 0];
@@ -1197,8 +1214,8 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     }
     uint64_t pm = a.cc->pos64[kPosLanes - 64 + lane];
     const uint64_t cs = a.cc->chunk_shift[min(du.back, (uint32_t)kChunkShifts - 1)][lane];
-    (&s_slice[0][0])[threadIdx.x] = t0;
-    (&s_slice[0][0])[threadIdx.x + kNodeThreads] = t1;
+#pragma unroll
+    for (uint32_t k = 0; k < 4; ++k) (&s_slice[0][0])[threadIdx.x + k * kNodeThreads] = tw[k];
     __syncthreads();
     if (!on) return;
     // pm opaque from here: otherwise the multiply's 64 per-bit masks of pm
@@ -1225,34 +1242,78 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
   const uint32_t t = a.template_of[g];
   const bool is_t = t == g;
   const DevGraph& Gg = a.graphs[g];
-  const DevGraph& Gt = a.graphs[t];
-  const uint32_t N = Gg.num_nodes, NT = Gt.num_nodes;
+  // The record fields this pass uses, read through the constant address
+  // space: nothing writes the records during the restore, so these are
+  // scalar loads, which neither wait for the vector loads in flight nor
+  // are repeated after a barrier's fence (as loads of a record that might
+  // be written would be).
+  const ConstGraph* cg = (const ConstGraph*)(a.graphs + g);
+  const ConstGraph* ct = (const ConstGraph*)(a.graphs + t);
+  const uint32_t N = cg->num_nodes, NT = ct->num_nodes;
+  const uint64_t g_node_base = cg->node_base, t_node_base = ct->node_base;
+  const uint32_t g_chunk_base = cg->chunk_base, t_chunk_base = ct->chunk_base;
+  const uint64_t g_sec_param = cg->sec_off[FDY_SEC_PARAM_DATA], g_sec_arg = cg->sec_off[FDY_SEC_ARG_DATA];
+  const uint64_t t_sec_param = ct->sec_off[FDY_SEC_PARAM_DATA], t_sec_arg = ct->sec_off[FDY_SEC_ARG_DATA];
+  const uint32_t g_word_cap = cg->word_cap, t_word_cap = ct->word_cap;
+  const uint32_t g_tile_base = cg->tile_base, g_tile_cap = cg->tile_cap;
+  const uint64_t g_word_base = cg->word_base, t_word_base = ct->word_base;
   const uint8_t* img = a.img;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  if (threadIdx.x == 0) {
-    s_status = 0;
-    s_pb = 0;
-    s_flat = 1;
-  }
-  __syncthreads();
+  // A block of kNodeThreads nodes' inputs: the node's first-pass results
+  // and, for a member, its template node's (loaded for every node, not only
+  // the clean ones, so that they need not wait for the node's flags), one
+  // block ahead of the block being completed.
+  struct NodeIn {
+    NodeDesc d;
+    uint4 th;            // the template node's gword, nwords, tword, flags
+    uint64_t ts, q0, q1, tpb;
+  };
+  auto load_in = [&](uint32_t base, NodeIn& in) {
+    const uint32_t n = base + threadIdx.x;
+    in.d = NodeDesc{};
+    in.th = make_uint4(0, 0, 0, 0);
+    in.ts = in.q0 = in.q1 = in.tpb = 0;
+    if (n < N) {
+      in.d = a.node_desc[g_node_base + n];
+      if (!is_t && n < NT) {
+        const uint64_t ti = t_node_base + n;
+        in.th = *reinterpret_cast<const uint4*>(a.node_desc + ti);
+        in.ts = a.node_desc[ti].src_g;
+        in.q0 = a.node_ptrs[2 * ti];
+        in.q1 = a.node_ptrs[2 * ti + 1];
+        in.tpb = a.node_pbytes[ti];
+      }
+    }
+  };
+  NodeIn cur;
+  load_in(0, cur);
 
   // Chunk results, one wave per chunk: the node-type and kernel-entry CRCs
   // (of a diff chunk: XORed with the template chunk's) shifted past the
-  // chunks after them; param bytes and status bits.
+  // chunks after them; param bytes and status bits.  The chunk, its
+  // template chunk and the lane's shift multiple load together, before the
+  // workgroup's first barrier.
   static_assert(kNodeChunk == kPosRecords, "chunk shift tables are built for kPosRecords records per chunk");
-  const uint32_t nch = node_chunks(N);
+  const uint32_t nch = node_chunks(N), ncht = node_chunks(NT);
   uint64_t x[4] = {0, 0, 0, 0}, pb = 0;
   uint32_t st = 0;
   for (uint32_t c = wave; c < nch; c += kNodeThreads / 64) {
-    const NodeChunk ch = a.chunks[Gg.chunk_base + c];
+    const uint32_t k = nch - 1 - c;
+    const NodeChunk ch = a.chunks[g_chunk_base + c];
+    const NodeChunk ctc = a.chunks[t_chunk_base + (c < ncht ? c : 0)];  // used for a diff chunk only
+    const uint64_t row = a.cc->chunk_shift[k < (uint32_t)kChunkShifts ? k : 0][lane];
     uint64_t rt = ch.crc_type, rk = ch.crc_kent;
     if (ch.mode & kChunkDiff) {
-      const NodeChunk& ct = a.chunks[Gt.chunk_base + c];
-      rt ^= ct.crc_type;
-      rk ^= ct.crc_kent;
+      rt ^= ctc.crc_type;
+      rk ^= ctc.crc_kent;
     }
-    x[2] ^= shift_share(a.cc, rt, nch - 1 - c, lane);
-    x[3] ^= shift_share(a.cc, rk, nch - 1 - c, lane);
+    if (k < (uint32_t)kChunkShifts) {
+      x[2] ^= ((rt >> (63 - lane)) & 1) ? row : 0ull;
+      x[3] ^= ((rk >> (63 - lane)) & 1) ? row : 0ull;
+    } else {
+      x[2] ^= shift_share(a.cc, rt, k, lane);
+      x[3] ^= shift_share(a.cc, rk, k, lane);
+    }
     if (lane == 0) {
       pb += ch.pbytes;
       st |= ch.status;
@@ -1265,6 +1326,12 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
   if (lane == 0)
 #pragma unroll
     for (int k = 0; k < 4; ++k) s_x[k][wave] = x[k];
+  if (threadIdx.x == 0) {
+    s_status = 0;
+    s_pb = 0;
+    s_flat = 1;
+  }
+  lds_barrier();
 
   // Word offsets of every node in the graph's and in the template's image;
   // clean nodes first take their template node's results (its first pass
@@ -1272,18 +1339,17 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
   // template's word offsets).
   uint32_t gcarry = 0, tcarry = 0;
   for (uint32_t base = 0; base < N; base += kNodeThreads) {
+    NodeIn nxt;
+    if (base + kNodeThreads < N) load_in(base + kNodeThreads, nxt);  // uniform
     const uint32_t n = base + threadIdx.x;
     const bool valid = n < N;
-    const uint64_t gi = Gg.node_base + n;
-    NodeDesc d{};
-    if (valid) d = a.node_desc[gi];
+    const uint64_t gi = g_node_base + n;
+    NodeDesc d = cur.d;
     if (valid && (d.flags & kNodeClean)) {
-      const uint64_t ti = Gt.node_base + n;
-      const NodeDesc* dt = a.node_desc + ti;
-      const uint32_t tw = dt->nwords, tf = dt->flags;
-      const uint64_t ts = dt->src_g;
-      const uint64_t q0 = a.node_ptrs[2 * ti], q1 = a.node_ptrs[2 * ti + 1];
-      pb += a.node_pbytes[ti];
+      const uint32_t tw = cur.th.y, tf = cur.th.w;
+      const uint64_t ts = cur.ts;
+      const uint64_t q0 = cur.q0, q1 = cur.q1;
+      pb += cur.tpb;
       uint32_t f = (tf & kNodeExtra) | (d.flags & FDY_NODE_DESC);  // launch dimensions differ: DESC
       if (tf & kNodeBad) {
         f |= FDY_NODE_LAYOUT | kNodeBad;
@@ -1297,28 +1363,32 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
       d.tword = tw;
       d.flags = f;
       d.src_t = ts;
-      d.src_g = ts ? ts - Gt.sec_off[sec] + Gg.sec_off[sec] : 0;
+      d.src_g = ts ? ts - (sec == FDY_SEC_ARG_DATA ? t_sec_arg : t_sec_param) +
+                         (sec == FDY_SEC_ARG_DATA ? g_sec_arg : g_sec_param)
+                   : 0;
       a.node_flags[gi] = (uint8_t)(f & 0x0F);
       a.node_ptrs[2 * gi] = q0;
       a.node_ptrs[2 * gi + 1] = q1;
     }
     const uint32_t words_g = d.nwords, words_t = d.tword;
     uint32_t flags = d.flags;
-    uint32_t tot_g, tot_t;
-    const uint32_t gword = gcarry + block_excl_scan(words_g, s_tmp, &tot_g);
-    const uint32_t tword = tcarry + block_excl_scan(words_t, s_tmp, &tot_t);
+    const uint32_t wv[2] = {words_g, words_t};
+    uint32_t ex[2], tot[2];
+    block_excl_scan2(wv, s_tmp, ex, tot);
+    const uint32_t gword = gcarry + ex[0], tword = tcarry + ex[1];
+    const uint32_t tot_g = tot[0], tot_t = tot[1];
     // A template whose image overflows its capacity (overlapping param
     // ranges) has no usable words past the capacity; never index them.
-    if ((flags & kNodeCompare) && (uint64_t)tword + words_t > Gt.word_cap) flags &= ~kNodeCompare;
+    if ((flags & kNodeCompare) && (uint64_t)tword + words_t > t_word_cap) flags &= ~kNodeCompare;
     if (valid) {
       // The graph's image is flat when every node with words is aligned and
       // placed canonically (word w of the image at param-data byte 8w), and
       // likewise in the template's image for every compared node.
       if (words_g) {
         const bool ok = !(flags & (FDY_NODE_RAGGED | kNodeRaggedT)) &&
-                        d.src_g == Gg.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword &&
+                        d.src_g == g_sec_param + 8ull * gword &&
                         (is_t || ((flags & kNodeCompare) && tword == gword &&
-                                  d.src_t == Gt.sec_off[FDY_SEC_PARAM_DATA] + 8ull * gword));
+                                  d.src_t == t_sec_param + 8ull * gword));
         if (!ok) s_flat = 0;
       }
       if (is_t) {
@@ -1334,7 +1404,7 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
       if (words_g) {
         uint64_t k = ((uint64_t)gword + kTileWords - 1) / kTileWords;
         const uint64_t k_last = ((uint64_t)gword + words_g - 1) / kTileWords;
-        for (; k <= k_last && k < Gg.tile_cap; ++k) a.tile_node[Gg.tile_base + k] = n;
+        for (; k <= k_last && k < g_tile_cap; ++k) a.tile_node[g_tile_base + k] = n;
         if (flags & FDY_NODE_RAGGED) {
           const uint8_t* eg = img + Gg.sec_off[FDY_SEC_NODES] + 168ull * n;
           Side sd_{}, none_{};
@@ -1348,6 +1418,7 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     }
     gcarry += tot_g;
     tcarry += tot_t;
+    cur = nxt;
   }
   // One LDS atomic per wave: every thread's own atomic on one address
   // serialised (about 8 us of the pass at 1024 threads).
@@ -1360,12 +1431,12 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     if (pb) atomicAdd(&s_pb, (unsigned long long)pb);
     if (st) atomicOr(&s_status, st);
   }
-  __syncthreads();
+  lds_barrier();
   if (threadIdx.x == 0) {
     uint64_t acc[4] = {0, 0, 0, 0};
     for (uint32_t w = 0; w < kNodeThreads / 64; ++w)
       for (int k = 0; k < 4; ++k) acc[k] ^= s_x[k][w];
-    const bool overflow = gcarry > Gg.word_cap;
+    const bool overflow = gcarry > g_word_cap;
     s_words = overflow ? 0 : gcarry;
     uint32_t stat = s_status;
     if (!is_t && N != NT) stat |= kGraphNodeCount;
@@ -1373,35 +1444,35 @@ __global__ __launch_bounds__(kNodeThreads, 8) void k_node_b(RestoreArgs a) {
     a.status[g] = stat;
     a.gwords[g] = s_words;
     a.pbytes[g] = s_pb;
-    for (int k = 2; k < 4; ++k) a.digests[4ull * g + k] = acc[k] ^ Gg.crc_fin[k];  // 0, 1: the digest units
+    for (int k = 2; k < 4; ++k) a.digests[4ull * g + k] = acc[k] ^ cg->crc_fin[k];  // 0, 1: the digest units
     if (is_t) {
       a.live_cur[g] = g;
       // List the template's slots that hold words for k_diff_t.
       s_tbase = atomicAdd(a.tslot_count, (s_words + kTileWords - 1) / kTileWords);
     }
   }
-  __syncthreads();
+  lds_barrier();
   const uint32_t words = s_words;
   const uint32_t first_unused = (words + kTileWords - 1) / kTileWords;
   const uint32_t sflags = (s_flat ? kSlotFlat | (is_t ? 0u : kSlotCompare) : 0u) | (is_t ? kSlotTemplate : 0u);
-  for (uint32_t k = threadIdx.x; k < Gg.tile_cap; k += kNodeThreads) {
-    if (k >= first_unused) a.tile_node[Gg.tile_base + k] = kNoTile;
+  for (uint32_t k = threadIdx.x; k < g_tile_cap; k += kNodeThreads) {
+    if (k >= first_unused) a.tile_node[g_tile_base + k] = kNoTile;
     SlotDesc sd;
-    sd.kg = Gg.sec_off[FDY_SEC_PARAM_DATA];
-    sd.kt = Gt.sec_off[FDY_SEC_PARAM_DATA];
-    sd.word_base = Gg.word_base;
+    sd.kg = g_sec_param;
+    sd.kt = t_sec_param;
+    sd.word_base = g_word_base;
     sd.wbeg = (uint32_t)min((uint64_t)k * kTileWords, (uint64_t)words);
     sd.wend = (uint32_t)min((uint64_t)(k + 1) * kTileWords, (uint64_t)words);
     sd.graph = g;
     sd.tmpl = t;
-    sd.flags = sflags | (k == 0 ? kSlotFirst : 0u) | (k + 1 == Gg.tile_cap ? kSlotLast : 0u);
-    sd.t_cap = Gt.word_cap;
-    sd.node_base = (uint32_t)Gg.node_base;
+    sd.flags = sflags | (k == 0 ? kSlotFirst : 0u) | (k + 1 == g_tile_cap ? kSlotLast : 0u);
+    sd.t_cap = t_word_cap;
+    sd.node_base = (uint32_t)g_node_base;
     sd.num_nodes = N;
-    sd.t_word_base = Gt.word_base;
-    a.slot_desc[Gg.tile_base + k] = sd;
-    a.slot_spill[Gg.tile_base + k] = 0;
-    if (is_t && k < first_unused) a.tslots[s_tbase + k] = Gg.tile_base + k;
+    sd.t_word_base = t_word_base;
+    a.slot_desc[g_tile_base + k] = sd;
+    a.slot_spill[g_tile_base + k] = 0;
+    if (is_t && k < first_unused) a.tslots[s_tbase + k] = g_tile_base + k;
   }
 }
 
