@@ -40,6 +40,19 @@
 namespace fdy {
 namespace {
 
+// A graph record read through the constant address space (scalar loads).
+typedef __attribute__((address_space(4))) const DevGraph ConstGraph;
+
+// Memory that no workgroup writes during the kernel at hand (the records,
+// or what an earlier pass of the restore wrote), read through the constant
+// address space: a wave-uniform address becomes a scalar load, which
+// neither waits for the vector loads in flight nor is repeated after a
+// barrier's fence.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* readonly(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+
 constexpr uint32_t kNodeThreads = 512;
 constexpr uint32_t kRelocThreads = 256;
 constexpr uint32_t kRelocPairs = 4;  // 16-byte word pairs per thread per iteration
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
     *a.tslot_count = 0;  // the node pass lists template slots here
     *a.restore_flags = 0;  // kFlag* raised by the later passes
   }
-  const DevGraph& Gi = a.graphs[i];
+  const ConstGraph& Gi = *readonly(a.graphs + i);
   if (tid < 2) a.digests[4ull * i + tid] = Gi.crc_fin[tid];
   // The node pass reads {graph, template} per node chunk.
   const uint32_t nch = Gi.num_nodes ? (Gi.num_nodes + kNodeChunk - 1) / kNodeChunk : 1;
@@ -202,7 +215,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(RestoreArgs a) {
       while (miss) {
         const uint32_t l = (uint32_t)__ffsll((long long)miss) - 1;
         miss &= miss - 1;
-        const DevGraph& Gj = a.graphs[base + (tid & ~63u) + l];
+        const ConstGraph& Gj = *readonly(a.graphs + base + (tid & ~63u) + l);
         uint64_t y = key_share(a.img + Gj.sec_off[FDY_SEC_TOPOLOGY_KEY], Gj.sec_size[FDY_SEC_TOPOLOGY_KEY], lane, 64);
 #pragma unroll
         for (int d = 32; d >= 1; d >>= 1) y ^= shfl_down64(y, d);
@@ -306,8 +319,8 @@ static_assert(FDY_NODE_OFF_TYPE == 4, "the type is the low byte of entry bytes 4
 // The param references of kernel node entry e: the name, param-index and
 // arg-buffer bounds; an extra-style node's blob.  Per-param nodes are
 // completed by scan_params.
-template <class E>
-__device__ __forceinline__ void side_header(const uint8_t* img, const DevGraph& G, const E& e, Side& s) {
+template <class E, class GR>
+__device__ __forceinline__ void side_header(const uint8_t* img, const GR& G, const E& e, Side& s) {
   s = Side{};
   const uint32_t pio = e.u32(FDY_KOFF_PARAM_INDEX), np = e.u32(FDY_KOFF_NUM_PARAMS);
   const uint32_t ao = e.u32(FDY_KOFF_ARG_OFFSET), as = e.u32(FDY_KOFF_ARG_SIZE);
@@ -333,7 +346,8 @@ __device__ __forceinline__ void side_header(const uint8_t* img, const DevGraph& 
 }
 
 // Param entry j ({u32 offset, u32 size}) into a side's running totals.
-__device__ inline void side_param(const DevGraph& G, Side& s, uint32_t j, uint64_t entry, uint64_t& prev,
+template <class GR>
+__device__ inline void side_param(const GR& G, Side& s, uint32_t j, uint64_t entry, uint64_t& prev,
                                   uint64_t& words) {
   const uint32_t o = (uint32_t)entry, sz = (uint32_t)(entry >> 32);
   if ((uint64_t)o + sz > G.sec_size[FDY_SEC_PARAM_DATA]) {
@@ -356,8 +370,9 @@ __device__ inline void side_param(const DevGraph& G, Side& s, uint32_t j, uint64
 // and sizes.
 constexpr uint32_t kParamBatch = 8;
 
-__device__ __forceinline__ void scan_params(const uint8_t* img, const DevGraph& Gg, Side& g, bool with_g,
-                                            const DevGraph& Gt, Side& t, bool with_t, bool* same_sizes) {
+template <class GA, class GB>
+__device__ __forceinline__ void scan_params(const uint8_t* img, const GA& Gg, Side& g, bool with_g,
+                                            const GB& Gt, Side& t, bool with_t, bool* same_sizes) {
   const bool wg = with_g && !g.bad && !g.extra;
   const bool wt = with_t && !t.bad && !t.extra;
   const uint32_t ng = wg ? g.num_params : 0, nt = wt ? t.num_params : 0;
@@ -578,9 +593,6 @@ __device__ __forceinline__ bool desc_differs(const Strings& A, const uint8_t* ca
   }
 }
 
-// A graph record read through the constant address space (scalar loads).
-typedef __attribute__((address_space(4))) const DevGraph ConstGraph;
-
 // A workgroup barrier ordering LDS accesses only: unlike __syncthreads it
 // does not first wait for the workgroup's outstanding global stores, which
 // no thread of the workgroup reads back.
@@ -623,7 +635,8 @@ __device__ void block_excl_scan2(const uint32_t v[2], uint32_t (*s_tmp)[16], uin
   lds_barrier();
 }
 
-__device__ void write_aux(const uint8_t* img, const DevGraph& G, const uint8_t* e, const Side& s, uint64_t* aux,
+template <class GR>
+__device__ void write_aux(const uint8_t* img, const GR& G, const uint8_t* e, const Side& s, uint64_t* aux,
                           uint32_t gword) {
   uint32_t idx = 0;
   auto put = [&](uint64_t byte, uint32_t size) {
@@ -716,8 +729,8 @@ struct NodeOut {
 
 // A template's nodes (is_t) read their entry's kernel fields up front: no
 // template side to compare with leaves registers free for them.
-template <bool is_t>
-__device__ __forceinline__ void node_full(const RestoreArgs& a, const DevGraph& Gg, const DevGraph& Gt, uint32_t n,
+template <bool is_t, class GR>
+__device__ __forceinline__ void node_full(const RestoreArgs& a, const GR& Gg, const GR& Gt, uint32_t n,
                                           const Strings& sg_str, const Strings& st_str, const uint8_t* common_g,
                                           const uint8_t* common_t, bool same_ctx, bool xor_t,
                                           const uint64_t (*slice)[256], NodeOut& o) {
@@ -821,11 +834,16 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   __shared__ uint32_t s_flags, s_status, s_pmin, s_pmax, s_umin;
 
   const uint32_t chunk = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint2 gt = a.chunk_gt[chunk];  // {graph, template}: the grouping pass filled in the template
-  const uint32_t g = gt.x, t = gt.y;
+  // {graph, template}: the grouping pass filled in the template.
+  const auto* gt = readonly(reinterpret_cast<const uint32_t*>(a.chunk_gt + chunk));
+  const uint32_t g = gt[0], t = gt[1];
   const bool is_t = t == g;
-  const DevGraph& Gg = a.graphs[g];
-  const DevGraph& Gt = a.graphs[t];
+  // The records through the constant address space: nothing writes them
+  // during the restore, so their fields are scalar loads, which neither
+  // wait for the vector loads in flight nor are repeated after a barrier's
+  // fence.
+  const ConstGraph& Gg = *readonly(a.graphs + g);
+  const ConstGraph& Gt = *readonly(a.graphs + t);
   const uint32_t N = Gg.num_nodes;
   const uint32_t c = chunk - Gg.chunk_base;
   const uint8_t* img = a.img;
@@ -1239,7 +1257,7 @@ __global__ __launch_bounds__(kNodeThreads, 6) void k_node_b(RestoreArgs a) {
   }
 
   const uint32_t g = blockIdx.x;
-  const uint32_t t = a.template_of[g];
+  const uint32_t t = *readonly(a.template_of + g);  // written by the grouping pass
   const bool is_t = t == g;
   const DevGraph& Gg = a.graphs[g];
   // The record fields this pass uses, read through the constant address
@@ -1247,8 +1265,8 @@ __global__ __launch_bounds__(kNodeThreads, 6) void k_node_b(RestoreArgs a) {
   // scalar loads, which neither wait for the vector loads in flight nor
   // are repeated after a barrier's fence (as loads of a record that might
   // be written would be).
-  const ConstGraph* cg = (const ConstGraph*)(a.graphs + g);
-  const ConstGraph* ct = (const ConstGraph*)(a.graphs + t);
+  const ConstGraph* cg = readonly(a.graphs + g);
+  const ConstGraph* ct = readonly(a.graphs + t);
   const uint32_t N = cg->num_nodes, NT = ct->num_nodes;
   const uint64_t g_node_base = cg->node_base, t_node_base = ct->node_base;
   const uint32_t g_chunk_base = cg->chunk_base, t_chunk_base = ct->chunk_base;
@@ -1490,16 +1508,29 @@ __device__ inline uint64_t load_bytes(const uint8_t* img, uint64_t byte, uint32_
   return width >= 8 ? v : v & ((1ull << (8 * width)) - 1);
 }
 
-// A slot descriptor, loaded whole before any branch: left to itself the
+// A slot descriptor, loaded whole before any branch (left to itself the
 // compiler loads each field at its first use, behind branches, and every
-// such load is another serial round trip before the tile's loads can start.
+// such load is another serial round trip before the tile's loads can start),
+// by scalar loads: the node pass wrote it and nothing writes it here.
 __device__ inline SlotDesc load_slot(const SlotDesc* p) {
+  const auto* q = readonly(reinterpret_cast<const uint64_t*>(p));  // written by the node pass, read-only here
+  SlotDesc d;
+  static_assert(sizeof(SlotDesc) == 8 * sizeof(uint64_t), "SlotDesc is eight 8-byte words");
+  uint64_t* o = reinterpret_cast<uint64_t*>(&d);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = q[i];
+  return d;
+}
+
+// The same by vector loads, for a descriptor prefetched across LDS work:
+// a scalar load's wait shares its counter with LDS accesses, so every LDS
+// wait in between would wait for the prefetch too.
+__device__ inline SlotDesc load_slot_v(const SlotDesc* p) {
   const uint4* q = reinterpret_cast<const uint4*>(p);
   const uint4 v0 = q[0], v1 = q[1], v2 = q[2], v3 = q[3];
   asm volatile("" ::"s"(v0.x), "s"(v0.y), "s"(v0.z), "s"(v0.w), "s"(v1.x), "s"(v1.y), "s"(v1.z), "s"(v1.w),
                "s"(v2.x), "s"(v2.y), "s"(v2.z), "s"(v2.w), "s"(v3.x), "s"(v3.y), "s"(v3.z), "s"(v3.w));
   SlotDesc d;
-  static_assert(sizeof(SlotDesc) == 4 * sizeof(uint4), "SlotDesc is four 16-byte words");
   uint4* o = reinterpret_cast<uint4*>(&d);
   o[0] = v0;
   o[1] = v1;
@@ -1519,9 +1550,9 @@ struct NodeWindow {
 // wait only for it and the tile -> node table.
 __device__ inline NodeWindow stage_window(const RestoreArgs& a, const SlotDesc& sd, uint32_t slot, NodeDesc* s_nd) {
   NodeWindow nw;
-  nw.n0 = a.tile_node[slot];
+  nw.n0 = *readonly(a.tile_node + slot);
   nw.N = sd.num_nodes;
-  const uint32_t n_next = (sd.flags & kSlotLast) ? kNoTile : a.tile_node[slot + 1];
+  const uint32_t n_next = (sd.flags & kSlotLast) ? kNoTile : *readonly(a.tile_node + slot + 1);
   const uint32_t n_last = n_next == kNoTile ? nw.N - 1 : n_next;
   nw.nwin = min(kDiffWindow, n_last - nw.n0 + 1);
   nw.nd = a.node_desc + sd.node_base;
@@ -1571,7 +1602,8 @@ __device__ inline NodeDesc window_desc(const NodeDesc* s_nd, const NodeWindow& n
 
 // Raw word w of a graph whose node descriptor is d (general path): ragged
 // words through their recorded byte position and width.
-__device__ inline uint64_t load_word(const RestoreArgs& a, const DevGraph& G, const NodeDesc& d, uint64_t w,
+template <class GR>
+__device__ inline uint64_t load_word(const RestoreArgs& a, const GR& G, const NodeDesc& d, uint64_t w,
                                      bool ragged, uint64_t src, uint32_t* width) {
   if (ragged) {
     if (!a.aux) {  // flagged by the node pass: this restore's results are discarded and it runs again
@@ -1612,15 +1644,15 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint64_t lt = (1ull << lane) - 1;
   const RelocDev& R = a.reloc;
-  const uint32_t units = *a.tslot_count * kTUnitsPerTile;
+  const uint32_t units = *readonly(a.tslot_count) * kTUnitsPerTile;
   // The next unit's slot descriptor is loaded while this unit is worked on
   // (with eight words per thread: MoE-style 105 -> 97 us).
   SlotDesc next{};
-  if (blockIdx.x < units) next = load_slot(a.slot_desc + a.tslots[blockIdx.x / kTUnitsPerTile]);
+  if (blockIdx.x < units) next = load_slot_v(a.slot_desc + a.tslots[blockIdx.x / kTUnitsPerTile]);
   for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
     const SlotDesc sd = next;
     const uint32_t slot = a.tslots[u / kTUnitsPerTile];
-    if (u + gridDim.x < units) next = load_slot(a.slot_desc + a.tslots[(u + gridDim.x) / kTUnitsPerTile]);
+    if (u + gridDim.x < units) next = load_slot_v(a.slot_desc + a.tslots[(u + gridDim.x) / kTUnitsPerTile]);
     const uint64_t ubeg = (uint64_t)sd.wbeg + (u % kTUnitsPerTile) * kTUnit;
     const uint64_t uend = min((uint64_t)sd.wend, ubeg + kTUnit);
     if (ubeg >= uend) continue;  // uniform over the block
@@ -1638,7 +1670,7 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
         }
       }
     } else {
-      const DevGraph& G = a.graphs[sd.graph];
+      const ConstGraph& G = *readonly(a.graphs + sd.graph);
       __syncthreads();  // the previous unit's lookups are done with s_nd
       const NodeWindow nw = stage_window(a, sd, slot, s_nd);
       __syncthreads();
@@ -1774,7 +1806,7 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
   const bool flat = (sd.flags & kSlotFlat) != 0;
   const RelocDev& R = a.reloc;
   // Issued ahead of the word loads so that its wait does not follow theirs.
-  const uint32_t t_status = a.status[t];
+  const uint32_t t_status = *readonly(a.status + t);  // a template's status: final after the node pass
   uint64_t* img_out = a.image + sd.word_base;
   // The template's relocated image (read within the template's capacity;
   // with relocation off it equals the raw image and is not read).  Its
@@ -1826,8 +1858,8 @@ __global__ __launch_bounds__(kMThreads, 6) void k_diff_m(RestoreArgs a) {
     cmp = full = valid;
   }
   if (!flat && wend > wbeg) {  // uniform over the workgroup
-    const DevGraph& G = a.graphs[g];
-    const DevGraph& T = a.graphs[t];
+    const ConstGraph& G = *readonly(a.graphs + g);
+    const ConstGraph& T = *readonly(a.graphs + t);
     const NodeWindow nw = stage_window(a, sd, slot, s_nd);
     __syncthreads();
     uint64_t wv[J];
@@ -2048,8 +2080,8 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
   const uint32_t so =
       lane < kSubsPerSlot && (cnt & 0xFFFFu) > C ? a.sub_off[(uint64_t)slot * kSubsPerSlot + lane] : 0u;
   const SlotDesc sd = load_slot(a.slot_desc + slot);
-  const uint32_t n0 = a.tile_node[slot];
-  const uint32_t n_after = slot + 1 < a.num_slots ? a.tile_node[slot + 1] : kNoTile;
+  const uint32_t n0 = *readonly(a.tile_node + slot);
+  const uint32_t n_after = slot + 1 < a.num_slots ? *readonly(a.tile_node + slot + 1) : kNoTile;
   // Lane q < kSubsPerSlot holds sub-range q's count; inclusive prefix over lanes.
   uint32_t incl = cnt;
 #pragma unroll
@@ -2109,7 +2141,7 @@ __global__ __launch_bounds__(kSThreads, 6) void k_diff_s(RestoreArgs a) {
     const uint4 v = earlier[j];
     before += (v.x >> 16) + (v.y >> 16) + (v.z >> 16) + (v.w >> 16);
   }
-  const uint32_t word_cap = a.graphs[sd.graph].word_cap;
+  const uint32_t word_cap = readonly(a.graphs + sd.graph)->word_cap;
   const uint32_t N = sd.num_nodes;
   const NodeDesc* nd = a.node_desc + sd.node_base;
   // The graph's last slot, or its last slot holding words (the next one's
