@@ -851,7 +851,9 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   const bool common_t_on = (Gt.flags & FDY_HAS_COMMON_ATTRS) && Gt.sec_size[FDY_SEC_COMMON_ATTRS] >= 52;
   // Equal node counts, section sizes (bounds then agree node for node) and
   // common-attr presence: the byte compare may decide nodes.
-  const bool fast = !is_t && N == Gt.num_nodes && common_g_on == common_t_on &&
+  // (A graph without nodes has one empty chunk and nothing to compare: its
+  // entry pairs, loaded without bounds checks, would read past the section.)
+  const bool fast = !is_t && N != 0 && N == Gt.num_nodes && common_g_on == common_t_on &&
                     Gg.sec_size[FDY_SEC_STRINGS] == Gt.sec_size[FDY_SEC_STRINGS] &&
                     Gg.sec_size[FDY_SEC_PARAM_INDEX] == Gt.sec_size[FDY_SEC_PARAM_INDEX] &&
                     Gg.sec_size[FDY_SEC_PARAM_DATA] == Gt.sec_size[FDY_SEC_PARAM_DATA] &&

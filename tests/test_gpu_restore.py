@@ -340,3 +340,23 @@ def test_param_entries_out_of_node_order(cuda):
     for g, n in ((1, 250), (2, 100)):
         assert (ref.overrides(g)["node"] == n).any(), (g, n)
     assert_restore_parity(arch, ref)
+
+
+def test_graphs_without_nodes(cuda):
+    # Two graphs without nodes (one the other's template) among two kernel
+    # graphs, the last image of the archive empty: every output must equal
+    # the oracle's, and nothing is read past an image.
+    import cugraph_writer as W
+
+    print("[case] two graphs without nodes among two 40-node graphs, the last image empty", flush=True)
+    rng = np.random.default_rng(3)
+
+    def kern(n):
+        return W.Kernel(f"k{n % 3}", 0x99, params=[W.le(int(rng.integers(0, 1 << 62))) for _ in range(3)])
+
+    images = [W.write([kern(n) for n in range(40)]), W.write([]), W.write([kern(n) for n in range(40)]), W.write([])]
+    arch = Archive.from_images(images)
+    arch.restore()
+    ref = oracle.Restore(images, None)
+    assert ref.groups().tolist() == [0, 1, 0, 1]
+    assert_restore_parity(arch, ref)
