@@ -872,7 +872,7 @@ __global__ __launch_bounds__(kNodeChunk, 5) void k_node_a(RestoreArgs a) {
   // (16 bytes) per lane per load: pair p = tid + 256 m holds words 2p, 2p + 1.
   const uint8_t* eg0 = img + Gg.sec_off[FDY_SEC_NODES];
   const uint8_t* et0 = img + Gt.sec_off[FDY_SEC_NODES];
-  const int64_t b0 = first * 168, bend = 168 * (int64_t)N;
+  const int64_t b0 = first * 168;
   static_assert(kEntryWords * kNodeChunk % 2 == 0, "whole pairs");
   constexpr uint32_t kPairs = kEntryWords * kNodeChunk / 2;  // per side
   // Loaded without a branch (a branch per pair made each wait for the one

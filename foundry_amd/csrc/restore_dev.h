@@ -227,25 +227,6 @@ __device__ __forceinline__ uint64_t f64(const uint8_t* e, uint32_t off) {
   return (uint64_t)f32(e, off) | ((uint64_t)f32(e, off + 4) << 32);
 }
 
-// Copy n 8-byte words into LDS, kBatch loads per thread issued before any
-// store (a plain copy loop waits for each load in turn).
-template <uint32_t kBatch = 8>
-__device__ inline void stage_words(uint64_t* dst, const uint64_t* src, uint32_t n) {
-  for (uint32_t base = 0; base < n; base += kBatch * blockDim.x) {
-    uint64_t v[kBatch];
-#pragma unroll
-    for (uint32_t k = 0; k < kBatch; ++k) {
-      const uint32_t i = base + k * blockDim.x + threadIdx.x;
-      v[k] = i < n ? src[i] : 0;
-    }
-#pragma unroll
-    for (uint32_t k = 0; k < kBatch; ++k) {
-      const uint32_t i = base + k * blockDim.x + threadIdx.x;
-      if (i < n) dst[i] = v[k];
-    }
-  }
-}
-
 // Relocate K words at once (the words whose bit is set in `mask`; the others
 // pass through): the interval containing w (the last one with lo <= w)
 // moves w if w < hi (w <= hi under the inclusive policy).  The K searches
