@@ -86,7 +86,8 @@ struct fdy_archive {
   // restore's scratch, as parts (one allocation instead of some twenty).
   fdy::DevBuf arena;
   fdy::DevBuf img, dgraphs, cc, digests, tmpl, explicit_tmpl, status, gwords, pbytes;
-  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_gt, units, chunks, slot_desc, live_cur, tslots;
+  fdy::DevBuf nflags, ndesc, nptrs, live_src, tile_node, chunk_gt, units, chunks, slot_desc, live_cur, tslot_desc;
+  fdy::DevBuf tslot_count;
   fdy::DevBuf aux, image, live, ovr, cand, sub_count, slot_rec, restore_flags, node_pbytes, key_hash;
   fdy::DevBuf slot_spill, sub_off;
 

@@ -38,8 +38,8 @@ struct RestoreArgs {
   NodeDesc* node_desc;
   uint64_t* node_ptrs;        // 2 per node
   uint32_t* tile_node;        // per slot
-  uint32_t* tslots;           // slots of template graphs holding words (capacity: num_slots)
-  uint32_t* tslot_count;      // entries of tslots
+  SlotDesc* tslot_desc;       // descriptors of the template graphs' slots holding words (capacity: num_slots)
+  uint32_t* tslot_count;      // entries of tslot_desc
   SlotDesc* slot_desc;        // per slot
   uint64_t* aux;              // ragged-word sources (per word), or null until a restore finds a ragged node
   uint64_t* image;            // relocated param images R

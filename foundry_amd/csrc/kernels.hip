@@ -1492,7 +1492,7 @@ __global__ __launch_bounds__(kNodeThreads, 6) void k_node_b(RestoreArgs a) {
     sd.t_word_base = t_word_base;
     a.slot_desc[g_tile_base + k] = sd;
     a.slot_spill[g_tile_base + k] = 0;
-    if (is_t && k < first_unused) a.tslots[s_tbase + k] = g_tile_base + k;
+    if (is_t && k < first_unused) a.tslot_desc[s_tbase + k] = sd;
   }
 }
 
@@ -1648,13 +1648,14 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
   const RelocDev& R = a.reloc;
   const uint32_t units = *readonly(a.tslot_count) * kTUnitsPerTile;
   // The next unit's slot descriptor is loaded while this unit is worked on
-  // (with eight words per thread: MoE-style 105 -> 97 us).
+  // (with eight words per thread: MoE-style 105 -> 97 us).  The node pass
+  // lists the template slots' descriptors themselves, so the first one is
+  // a single load.
   SlotDesc next{};
-  if (blockIdx.x < units) next = load_slot_v(a.slot_desc + a.tslots[blockIdx.x / kTUnitsPerTile]);
+  if (blockIdx.x < units) next = load_slot_v(a.tslot_desc + blockIdx.x / kTUnitsPerTile);
   for (uint32_t u = blockIdx.x; u < units; u += gridDim.x) {
     const SlotDesc sd = next;
-    const uint32_t slot = a.tslots[u / kTUnitsPerTile];
-    if (u + gridDim.x < units) next = load_slot_v(a.slot_desc + a.tslots[(u + gridDim.x) / kTUnitsPerTile]);
+    if (u + gridDim.x < units) next = load_slot_v(a.tslot_desc + (u + gridDim.x) / kTUnitsPerTile);
     const uint64_t ubeg = (uint64_t)sd.wbeg + (u % kTUnitsPerTile) * kTUnit;
     const uint64_t uend = min((uint64_t)sd.wend, ubeg + kTUnit);
     if (ubeg >= uend) continue;  // uniform over the block
@@ -1673,6 +1674,7 @@ __global__ __launch_bounds__(kTThreads) void k_diff_t(RestoreArgs a) {
       }
     } else {
       const ConstGraph& G = *readonly(a.graphs + sd.graph);
+      const uint32_t slot = G.tile_base + sd.wbeg / kTileWords;
       __syncthreads();  // the previous unit's lookups are done with s_nd
       const NodeWindow nw = stage_window(a, sd, slot, s_nd);
       __syncthreads();

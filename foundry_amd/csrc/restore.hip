@@ -310,7 +310,7 @@ int finish_open(fdy_archive* a, const std::vector<std::vector<uint8_t>>& heads, 
       {&a->chunk_gt, 8 * chunks},          {&a->node_pbytes, 8 * nodes},
       {&a->units, sizeof(DigestUnit) * units.size()},
       {&a->key_hash, 8ull * G},             {&a->chunks, sizeof(NodeChunk) * chunks},
-      {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslots, 4 * (slots + 1)},
+      {&a->slot_desc, sizeof(SlotDesc) * slots}, {&a->tslot_desc, sizeof(SlotDesc) * slots}, {&a->tslot_count, 4},
       {&a->sub_count, 4 * slots * kSubsPerSlot}, {&a->slot_rec, 4 * slots},
       {&a->restore_flags, 4},               {&a->slot_spill, 4 * slots},
       {&a->sub_off, 4 * slots * kSubsPerSlot},
@@ -600,8 +600,8 @@ int enqueue_restore(fdy_archive* a, hipStream_t s) {
   r.node_desc = a->ndesc.as<NodeDesc>();
   r.node_ptrs = a->nptrs.as<uint64_t>();
   r.tile_node = a->tile_node.as<uint32_t>();
-  r.tslots = a->tslots.as<uint32_t>();
-  r.tslot_count = a->tslots.as<uint32_t>() + a->num_slots;
+  r.tslot_desc = a->tslot_desc.as<SlotDesc>();
+  r.tslot_count = a->tslot_count.as<uint32_t>();
   r.slot_desc = a->slot_desc.as<SlotDesc>();
   r.aux = a->aux.as<uint64_t>();
   r.image = a->image.as<uint64_t>();
