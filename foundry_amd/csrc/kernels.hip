@@ -808,14 +808,12 @@ typedef uint64_t u64x2a8 __attribute__((ext_vector_type(2), aligned(8)));
 // so: otherwise they evict from the L2s and the 256 MB MALL the node tables,
 // template words and interval lines that the passes read again (measured on
 // the decode-style archive: restore 165 -> 158 us; MoE-style 1163 -> 1095 us).
-template <class T>
-__device__ __forceinline__ void st_stream(T* p, T v) {
-  __builtin_nontemporal_store(v, p);
-}
-template <class T>
-__device__ __forceinline__ T ld_stream(const T* p) {
-  return __builtin_nontemporal_load(p);
-}
+// (Overloads rather than a template: a template parameter would drop the
+// pair type's 8-byte alignment.)
+__device__ __forceinline__ void st_stream(uint64_t* p, uint64_t v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ void st_stream(u64x2a8* p, u64x2a8 v) { __builtin_nontemporal_store(v, p); }
+__device__ __forceinline__ uint64_t ld_stream(const uint64_t* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ u64x2a8 ld_stream(const u64x2a8* p) { return __builtin_nontemporal_load(p); }
 
 // The CRC slice tables (16 KB) into LDS by a workgroup of kNodeChunk
 // threads: eight loads per thread, all issued before any store.

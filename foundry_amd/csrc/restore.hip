@@ -1100,12 +1100,62 @@ int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, voi
     }
   }
   FDY_HIP(hipSetDevice(a->device));
-  // Consecutive switches of different groups touch disjoint live images and
-  // node sources: up to kSwitchBatch of them share one launch.  A switch of
-  // a group already in the batch, or of a group whose live image a group
-  // graph holds, first launches the batch so far (stream order keeps the
-  // sequence's order where it matters).  A group's current graph is recorded
-  // once its switch is enqueued.
+  // Switches of different groups touch disjoint live images and node
+  // sources, so only each group's own switches need their order.  Unless a
+  // group graph holds one of the groups involved, the sequence runs in
+  // layers: layer k holds every group's k-th switch (no-op switches, to the
+  // group's current graph, left out), up to kSwitchBatch per launch, and
+  // the layers launch in order.  A group's state after the sequence, and
+  // after each of its own switches, is the same as in sequence order; where
+  // consecutive switches often hit one group (32 groups, uniform targets:
+  // about 7 in a row before a repeat) a launch holds up to kSwitchBatch
+  // instead of those 7.
+  bool layered = true;
+  if (bound)
+    for (uint64_t i = 0; i < n && layered; ++i) layered = !a->bound[a->h_tmpl[targets[i]]];
+  if (layered) {
+    std::vector<uint32_t> cur = a->h_current, depth(a->G, 0);
+    std::vector<std::vector<std::pair<uint32_t, uint32_t>>> layers;  // {target, its group's graph before it}
+    for (uint64_t i = 0; i < n; ++i) {
+      const uint32_t g = targets[i], t = a->h_tmpl[g];
+      if (cur[t] == g) continue;
+      const uint32_t k = depth[t]++;
+      if (k == layers.size()) layers.emplace_back();
+      layers[k].push_back({g, cur[t]});
+      cur[t] = g;
+    }
+    // A launch's switches are recorded as their groups' current graphs once
+    // it is enqueued.
+    SwitchBatch lb{};
+    auto launch = [&]() -> int {
+      if (lb.n) FDY_HIP(launch_switch_many(lb, s));
+      for (uint32_t k = 0; k < lb.n; ++k) a->h_current[lb.sw[k].tmpl] = lb.sw[k].target;
+      lb.n = 0;
+      return FDY_OK;
+    };
+    for (const auto& layer : layers) {
+      for (const auto& gc : layer) {
+        const SwitchArgs w = switch_args(a, gc.first, nullptr, gc.second);
+        const uint32_t blocks = (uint32_t)switch_blocks(w);  // below 2^31: checked above
+        if (lb.n == kSwitchBatch || (lb.n && lb.end[lb.n - 1] + (uint64_t)blocks >= 0x7FFFFFFFull)) {
+          rc = launch();
+          if (rc) return rc;
+        }
+        lb.sw[lb.n] = w;
+        lb.end[lb.n] = (lb.n ? lb.end[lb.n - 1] : 0u) + blocks;
+        ++lb.n;
+      }
+      rc = launch();  // the next layer's switches follow this layer's in their groups
+      if (rc) return rc;
+    }
+    return FDY_OK;
+  }
+  // With a group graph involved: consecutive switches of different groups,
+  // up to kSwitchBatch, share one launch.  A switch of a group already in
+  // the batch, or of a group whose live image a group graph holds, first
+  // launches the batch so far (stream order keeps the sequence's order where
+  // it matters).  A group's current graph is recorded once its switch is
+  // enqueued.
   SwitchBatch b{};
   uint32_t batch_t[kSwitchBatch], batch_g[kSwitchBatch];
   auto flush = [&]() -> int {

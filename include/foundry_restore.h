@@ -250,13 +250,16 @@ int fdy_switch(fdy_archive* a, uint32_t graph, void* stream);
  * same end state and the same scatter work per switch, with the checks and
  * the device selection done once for the whole sequence instead of per call
  * (for callers that switch graphs many times between launches, and for
- * measuring sustained switches).  Every target, and every switch's launch
- * size, is checked before any switch is enqueued: an invalid target or a
- * switch too large for one launch enqueues nothing.  A HIP failure while
- * enqueueing (or in a bound group graph's exec update) returns at once:
- * the switches before it stay enqueued and recorded as current, none after
- * it is.  Counterpart of n calls of the on-demand branch of
- * csrc/CUDAGraph.cpp:330-461. */
+ * measuring sustained switches).  Every group goes through its own switches
+ * in sequence order; switches of different groups, which touch disjoint
+ * state, share launches (unless a group graph holds one of the groups:
+ * then the sequence's order is kept throughout).  Every target, and every
+ * switch's launch size, is checked before any switch is enqueued: an
+ * invalid target or a switch too large for one launch enqueues nothing.  A
+ * HIP failure while enqueueing (or in a bound group graph's exec update)
+ * returns at once: the switches already enqueued are recorded as their
+ * groups' current graphs, none after them.  Counterpart of n calls of the
+ * on-demand branch of csrc/CUDAGraph.cpp:330-461. */
 int fdy_switch_sequence(fdy_archive* a, const uint32_t* targets, uint64_t n, void* stream);
 /* Live state of the group whose template is `template_graph`.  Synchronizes.
  * node_src[n] = graph whose own image supplies node n (template unless the

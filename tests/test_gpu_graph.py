@@ -254,6 +254,25 @@ def test_seeded_switch_sequence(env):
             env.run(gg, rng.choice(GC.GROUP_A))
 
 
+def test_switch_sequence_with_a_bound_group_keeps_its_order(env):
+    # A switch sequence that touches a group held by a group graph keeps the
+    # sequence's order (no layering) and selects each target through the
+    # group graph: afterwards the exec runs the last target's params.
+    rng = random.Random(0x5EED + 7)
+    seq = [rng.choice(GC.GROUP_A) for _ in range(12)]
+    with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
+        env.arch.switch_sequence(seq, env.stream)
+        torch.cuda.synchronize()
+        assert gg.info()["current_graph"] == seq[-1]
+        torch.cuda.synchronize()
+        env.buf.zero_()
+        env.poison_slot2()
+        torch.cuda.synchronize()
+        gg.launch(env.stream)
+        torch.cuda.synchronize()
+        env.check(seq[-1])
+
+
 def test_archive_switch_goes_through_the_group_graph(env):
     with GroupGraph(env.arch, 0, env.reg, env.stream) as gg:
         for g in (3, 1, 0):
