@@ -195,6 +195,7 @@ _SIGS = {
     "fdy_get_live": (C.c_int, [_vp, _vp, C.c_uint32, u64p, C.c_uint64, u32p, C.c_uint64, u32p]),
     "fdy_reloc_plan_create": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, C.POINTER(_vp)]),
     "fdy_reloc_plan_destroy": (C.c_int, [_vp]),
+    "fdy_reloc_plan_lines": (C.c_int, [_vp, _vp, C.c_uint64, C.POINTER(C.c_uint64)]),
     "fdy_relocate_words": (C.c_int, [_vp, _vp, _vp, C.c_uint64, _vp]),
     "fdy_relocate_words_static": (C.c_int, [u64p, u64p, u64p, C.c_uint64, C.c_uint32, _vp, _vp, C.c_uint64, _vp]),
     "fdy_restore_timing_get": (C.c_int, [_vp, C.POINTER(RestoreTiming)]),

@@ -122,6 +122,27 @@ hipError_t launch_mirror(const MirrorArgs& a, hipStream_t s);
 
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s);
 
+// The interval index built on the device (the builder of reloc_index.h, one
+// thread per root line): launch_index_count writes each workgroup's first
+// line below its roots into block_sum (one per kIndexThreads root lines) and
+// the index's line count into *total; launch_index_place then writes the
+// lines (line holds *total of them).
+constexpr uint32_t kIndexThreads = 64;  // one wave: 24 KB of LDS for the subtree counts
+struct IndexArgs {
+  const uint64_t* lo;   // the table, on the device
+  const uint64_t* hi;
+  const uint64_t* nlo;
+  uint64_t n;           // intervals (> 0)
+  uint64_t nb;          // root lines
+  uint32_t shift;       // root line width: 2^shift bytes
+  uint32_t pad_;
+  uint64_t* block_sum;  // ceil(nb / kIndexThreads) entries
+  uint64_t* total;
+  RelocLine* line;
+};
+hipError_t launch_index_count(const IndexArgs& a, hipStream_t s);
+hipError_t launch_index_place(const IndexArgs& a, hipStream_t s);
+
 // A memset node of a restored graph, run as a kernel node: `height` rows of
 // `row_bytes` bytes, `pitch` bytes apart, each byte k of a row taking byte
 // k % 4 of `pattern` (the value replicated to 32 bits).

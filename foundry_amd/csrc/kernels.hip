@@ -36,6 +36,7 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "reloc_index.h"
 
 namespace fdy {
 namespace {
@@ -65,6 +66,12 @@ __device__ inline uint64_t shfl_down64(uint64_t v, int d) {
 }
 
 __device__ inline uint32_t shfl_up32(uint32_t v, int d) { return __shfl_up(v, (unsigned)d, 64); }
+__device__ inline uint64_t shfl_up64(uint64_t v, int d) {
+  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+  lo = __shfl_up(lo, (unsigned)d, 64);
+  hi = __shfl_up(hi, (unsigned)d, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
 
 // Word qi (bytes [8 qi, 8 qi + 8)) of the L-byte stream at p (8-aligned,
 // inside the archive-image buffer), with bytes outside [0, L) read as zero.
@@ -2422,6 +2429,88 @@ __global__ __launch_bounds__(kSwitchThreads) void k_switch_many(SwitchBatch b) {
   switch_block(b.sw[k], blockIdx.x - first, b.end[k] - first, s_sample, s_seg);
 }
 
+// ---- interval index, built on the device ------------------------------
+
+// Exclusive prefix over the workgroup of one u64 per thread (kWaves waves);
+// *tot gets the sum.
+template <uint32_t kWaves>
+__device__ inline uint64_t index_block_scan(uint64_t v, uint64_t* s_part, uint64_t* tot) {
+  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  uint64_t x = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint64_t y = shfl_up64(x, d);
+    if (lane >= (uint32_t)d) x += y;
+  }
+  if (lane == 63) s_part[wave] = x;
+  __syncthreads();
+  uint64_t before = 0, sum = 0;
+  for (uint32_t w = 0; w < kWaves; ++w) {
+    if (w < wave) before += s_part[w];
+    sum += s_part[w];
+  }
+  __syncthreads();  // s_part is free again
+  *tot = sum;
+  return before + x - v;
+}
+
+// Root line b's range and the lines below it (st: this thread's
+// 2 * kSubtreeStack words of LDS).
+__device__ inline uint64_t index_root(const IndexArgs& a, uint64_t b, uint64_t* s0, uint64_t* i, uint64_t* j,
+                                      uint64_t* st) {
+  *s0 = root_start(a.lo[0], a.shift, b);
+  root_range(a.lo, a.n, *s0, root_start(a.lo[0], a.shift, b + 1), i, j);
+  return subtree_lines(*j - *i + 1, st, st + kSubtreeStack);
+}
+
+// Pass 1, one thread per root line: the lines below each workgroup's roots.
+__global__ __launch_bounds__(kIndexThreads) void k_index_count(IndexArgs a) {
+  __shared__ uint64_t s_part[kIndexThreads / 64];
+  __shared__ uint64_t s_st[kIndexThreads][2 * kSubtreeStack];
+  const uint64_t b = (uint64_t)blockIdx.x * kIndexThreads + threadIdx.x;
+  uint64_t sub = 0;
+  if (b < a.nb) {
+    uint64_t s0, i, j;
+    sub = index_root(a, b, &s0, &i, &j, s_st[threadIdx.x]);
+  }
+  uint64_t tot;
+  (void)index_block_scan<kIndexThreads / 64>(sub, s_part, &tot);
+  if (threadIdx.x == 0) a.block_sum[blockIdx.x] = tot;
+}
+
+// Pass 2, one workgroup of kIndexScanThreads: each root workgroup's first
+// line below its roots (after the nb root lines), and the index's line
+// count.  Each thread sums, then rewrites, a contiguous run of the counts.
+constexpr uint32_t kIndexScanThreads = 1024;
+__global__ __launch_bounds__(kIndexScanThreads) void k_index_scan(IndexArgs a, uint64_t nblocks) {
+  __shared__ uint64_t s_part[kIndexScanThreads / 64];
+  const uint64_t per = (nblocks + kIndexScanThreads - 1) / kIndexScanThreads;
+  const uint64_t k0 = min(nblocks, (uint64_t)threadIdx.x * per), k1 = min(nblocks, k0 + per);
+  uint64_t v = 0;
+#pragma unroll 8
+  for (uint64_t k = k0; k < k1; ++k) v += a.block_sum[k];
+  uint64_t tot;
+  uint64_t at = a.nb + index_block_scan<kIndexScanThreads / 64>(v, s_part, &tot);
+  for (uint64_t k = k0; k < k1; ++k) {
+    const uint64_t x = a.block_sum[k];
+    a.block_sum[k] = at;
+    at += x;
+  }
+  if (threadIdx.x == 0) *a.total = a.nb + tot;
+}
+
+// Pass 3, one thread per root line: the root line and the lines below it.
+__global__ __launch_bounds__(kIndexThreads) void k_index_place(IndexArgs a) {
+  __shared__ uint64_t s_part[kIndexThreads / 64];
+  __shared__ uint64_t s_st[kIndexThreads][2 * kSubtreeStack];
+  const uint64_t b = (uint64_t)blockIdx.x * kIndexThreads + threadIdx.x;
+  uint64_t sub = 0, s0 = 0, i = 0, j = 0;
+  if (b < a.nb) sub = index_root(a, b, &s0, &i, &j, s_st[threadIdx.x]);
+  uint64_t tot;
+  const uint64_t base = a.block_sum[blockIdx.x] + index_block_scan<kIndexThreads / 64>(sub, s_part, &tot);
+  if (b < a.nb) place_root(a.line, b, s0, i, j, a.lo, a.hi, a.nlo, base);
+}
+
 // ---- host mirror of a group graph's live image ---------------------------
 
 // Block b covers nodes [64b, 64b + 64): the first wave moves their marks to
@@ -2652,6 +2741,23 @@ dim3 fill_grid(const FillArgs& f) {
   const uint64_t x = std::min<uint64_t>((vec + kFillThreads - 1) / kFillThreads, 1024);
   const uint64_t y = std::min<uint64_t>(std::max<uint64_t>(f.height, 1), 65535);
   return dim3((uint32_t)std::max<uint64_t>(x, 1), (uint32_t)y);
+}
+
+hipError_t launch_index_count(const IndexArgs& a, hipStream_t s) {
+  const uint64_t nblocks = (a.nb + kIndexThreads - 1) / kIndexThreads;
+  if (nblocks == 0 || nblocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_index_count, dim3((uint32_t)nblocks), dim3(kIndexThreads), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_index_scan, dim3(1), dim3(kIndexScanThreads), 0, s, a, nblocks);
+  return hipGetLastError();
+}
+
+hipError_t launch_index_place(const IndexArgs& a, hipStream_t s) {
+  const uint64_t nblocks = (a.nb + kIndexThreads - 1) / kIndexThreads;
+  if (nblocks == 0 || nblocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_index_place, dim3((uint32_t)nblocks), dim3(kIndexThreads), 0, s, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_reloc_words(const RelocDev& r, const uint64_t* in, uint64_t* out, uint64_t n, hipStream_t s) {

@@ -194,16 +194,51 @@ int build_reloc_index(const uint64_t* lo, const uint64_t* hi, const uint64_t* nl
   return rc ? err(rc, why) : FDY_OK;
 }
 
+// A table's index on the device: checked and shaped on the host, its lines
+// counted, placed and written on the device (one thread per root line,
+// kernels.hip), so only the table travels over PCIe.  Synchronizes.
 int build_reloc_plan(const uint64_t* lo, const uint64_t* hi, const uint64_t* nlo, uint64_t n, uint32_t policy,
                      RelocPlan* out, uint64_t root_lines_per_interval = kRootLinesPerInterval) {
-  HostIndex x;
-  int rc = build_reloc_index(lo, hi, nlo, n, policy, &x, root_lines_per_interval);
-  out->dev = x.dev;
-  if (rc || n == 0) return rc;
-  rc = dev_alloc(out->line, x.line.size() * sizeof(RelocLine), "interval index lines");
+  std::memset(&out->dev, 0, sizeof(out->dev));
+  out->line.release();
+  std::string why;
+  IndexShape sh;
+  int rc = index_shape(lo, hi, nlo, n, policy, root_lines_per_interval, &sh, &why);
+  if (rc) return err(rc, why);
+  out->dev.policy = policy;
+  if (n == 0) return FDY_OK;
+  const uint64_t nblocks = (sh.nb + kIndexThreads - 1) / kIndexThreads;
+  DevBuf table, sums;
+  rc = dev_alloc(table, 24 * n, "interval table");
+  if (!rc) rc = dev_alloc(sums, 8 * (nblocks + 1), "interval index counts");
   if (rc) return rc;
-  FDY_HIP(hipMemcpy(out->line.p, x.line.data(), x.line.size() * sizeof(RelocLine), hipMemcpyHostToDevice));
+  uint64_t* t = table.as<uint64_t>();
+  FDY_HIP(hipMemcpy(t, lo, 8 * n, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(t + n, hi, 8 * n, hipMemcpyHostToDevice));
+  FDY_HIP(hipMemcpy(t + 2 * n, nlo, 8 * n, hipMemcpyHostToDevice));
+  IndexArgs ia{};
+  ia.lo = t;
+  ia.hi = t + n;
+  ia.nlo = t + 2 * n;
+  ia.n = n;
+  ia.nb = sh.nb;
+  ia.shift = sh.shift;
+  ia.block_sum = sums.as<uint64_t>();
+  ia.total = sums.as<uint64_t>() + nblocks;
+  FDY_HIP(launch_index_count(ia, nullptr));
+  uint64_t total = 0;
+  FDY_HIP(hipMemcpy(&total, ia.total, 8, hipMemcpyDeviceToHost));
+  if (total > kMaxIndexLines) return err(FDY_E_INVALID, "interval index too large");
+  rc = dev_alloc(out->line, total * sizeof(RelocLine), "interval index lines");
+  if (rc) return rc;
+  ia.line = out->line.as<RelocLine>();
+  FDY_HIP(launch_index_place(ia, nullptr));
+  FDY_HIP(hipStreamSynchronize(nullptr));  // before the table and counts are freed
   out->dev.line = out->line.as<RelocLine>();
+  out->dev.n = n;
+  out->dev.lo_min = lo[0];
+  out->dev.hi_max = hi[n - 1];
+  out->dev.shift = sh.shift;
   return FDY_OK;
 }
 
@@ -1388,6 +1423,18 @@ int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t
   int rc = build_reloc_plan(lo, hi, nlo, n, policy, &p->plan, kPlanRootLinesPerInterval);
   if (rc) return rc;
   *out = p.release();
+  return FDY_OK;
+}
+
+int fdy_reloc_plan_lines(const fdy_reloc_plan* p, void* lines, uint64_t cap, uint64_t* n_lines) {
+  if (!p) return err(FDY_E_INVALID, "null plan");
+  const uint64_t n = p->plan.dev.n ? p->plan.line.bytes / sizeof(RelocLine) : 0;
+  if (n_lines) *n_lines = n;
+  if (!lines) return FDY_OK;
+  if (cap < n) return err(FDY_E_CAPACITY, "output holds " + std::to_string(cap) + " lines, the index has " +
+                                              std::to_string(n));
+  FDY_HIP(hipSetDevice(p->device));
+  if (n) FDY_HIP(hipMemcpy(lines, p->plan.line.p, n * sizeof(RelocLine), hipMemcpyDeviceToHost));
   return FDY_OK;
 }
 

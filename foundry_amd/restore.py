@@ -257,6 +257,14 @@ class RelocPlan:
         """Relocate n_words u64 words at device address d_in into d_out."""
         check(restore_lib().fdy_relocate_words(self._h, C.c_void_p(d_in), C.c_void_p(d_out), n_words, _stream(stream)))
 
+    def lines(self) -> np.ndarray:
+        """The plan's interval index: one row of eight u64 words per 64-byte line."""
+        n = C.c_uint64()
+        check(restore_lib().fdy_reloc_plan_lines(self._h, None, 0, C.byref(n)))
+        out = np.zeros((n.value, 8), dtype=np.uint64)
+        check(restore_lib().fdy_reloc_plan_lines(self._h, out.ctypes.data_as(C.c_void_p), n.value, C.byref(n)))
+        return out
+
     def close(self) -> None:
         if self._h:
             check(restore_lib().fdy_reloc_plan_destroy(self._h))

@@ -271,12 +271,21 @@ int fdy_get_live(fdy_archive* a, void* stream, uint32_t template_graph, uint64_t
  * (in and out may alias).  The plan holds the interval search structure:
  * about 16 root lines of 64 B per interval (2M intervals: about 2 GB of device
  * memory), built once for many relocations, against about 2 per interval for
- * the index beside a restored archive. */
+ * the index beside a restored archive.  The table is checked on the host and
+ * the index built on the current device (only the table is uploaded);
+ * returns when it is built. */
 int fdy_reloc_plan_create(const uint64_t* lo, const uint64_t* hi, const uint64_t* new_lo, uint64_t n,
                           uint32_t policy, fdy_reloc_plan** out);
 int fdy_reloc_plan_destroy(fdy_reloc_plan* p);
 int fdy_relocate_words(const fdy_reloc_plan* p, const uint64_t* d_in, uint64_t* d_out, uint64_t n_words,
                        void* stream);
+/* The plan's interval index: its 64-byte lines (the root lines first, then
+ * the lines below them), copied to `lines` (room for cap of them) with their
+ * count in *n_lines (lines may be null to ask for the count).  The index is
+ * built on the device, one thread per root line.  No counterpart in the
+ * reference; for inspecting a plan and checking the device build against
+ * the host build of the same index. */
+int fdy_reloc_plan_lines(const fdy_reloc_plan* p, void* lines, uint64_t cap, uint64_t* n_lines);
 
 /* fdy_relocate_words without any device allocation.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (serving

@@ -3,10 +3,11 @@
 // kernels run) executed on the CPU, so the index can be checked without a
 // GPU.
 //
-//   reloc_index_check TABLE WORDS OUT
+//   reloc_index_check TABLE WORDS OUT [ROOT_LINES_PER_INTERVAL [INDEX_OUT]]
 //
 // TABLE: u64 n, u64 policy, then n lo, n hi, n new_lo (little endian).
-// WORDS: u64 words.  OUT: the relocated words, then one JSON line on stdout
+// WORDS: u64 words.  INDEX_OUT: the index's 64-byte lines.  OUT: the relocated
+// words, then one JSON line on stdout
 // with the index's shape (lines, root lines, root shift, fence lines, and
 // `bad_refs`: fence lines naming children outside the index or not after
 // themselves, or fences out of order) and the line reads the searches took.
@@ -32,8 +33,8 @@ static std::vector<uint64_t> read_all(const char* path) {
 }
 
 int main(int argc, char** argv) {
-  if (argc != 4 && argc != 5) {
-    std::fprintf(stderr, "usage: %s TABLE WORDS OUT [ROOT_LINES_PER_INTERVAL]\n", argv[0]);
+  if (argc < 4 || argc > 6) {
+    std::fprintf(stderr, "usage: %s TABLE WORDS OUT [ROOT_LINES_PER_INTERVAL [INDEX_OUT]]\n", argv[0]);
     return 2;
   }
   const std::vector<uint64_t> t = read_all(argv[1]);
@@ -50,12 +51,20 @@ int main(int argc, char** argv) {
 
   HostIndex x;
   std::string why;
-  const uint64_t per = argc == 5 ? std::strtoull(argv[4], nullptr, 10) : kRootLinesPerInterval;
+  const uint64_t per = argc >= 5 ? std::strtoull(argv[4], nullptr, 10) : kRootLinesPerInterval;
   const int rc = build_reloc_index(lo, hi, nlo, n, policy, &x, &why, per);
   if (rc) {
     std::printf("{\"error\": %d}\n", rc);
     std::fprintf(stderr, "%s\n", why.c_str());
     return 0;
+  }
+  if (argc == 6) {  // the index itself, for comparing with the device build
+    FILE* f = std::fopen(argv[5], "wb");
+    if (!f || std::fwrite(x.line.data(), sizeof(RelocLine), x.line.size(), f) != x.line.size()) {
+      std::perror(argv[5]);
+      return 2;
+    }
+    std::fclose(f);
   }
   RelocDev d = x.dev;
   d.line = x.line.data();
