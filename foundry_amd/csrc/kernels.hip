@@ -33,6 +33,9 @@
 //   k_mirror  dirty nodes' live words -> a group graph's host mirror.
 //   k_fill    memset node of a restored graph, as a kernel node.
 //   k_reloc   streaming relocation of packed words.
+//   k_index_count, k_index_scan, k_index_place
+//             the interval index of a relocation table, one thread per root
+//             line (the builder of reloc_index.h).
 #include <type_traits>
 
 #include "kernels.h"
