@@ -73,6 +73,8 @@ class RestoreTiming(C.Structure):
         ("diff_ms", C.c_float),
         ("search_ms", C.c_float),
         ("total_ms", C.c_float),
+        ("prepare_ms", C.c_float),
+        ("diff_phase_ms", C.c_float),
     ]
 
 

@@ -124,10 +124,10 @@ struct fdy_archive {
   std::vector<fdy_group_graph*> bound;
   uint32_t num_bound = 0;
 
-  bool timing = false;
+  int timing = 0;  // fdy_set_timing: 0 off, 1 every kernel, 2 the two phases only
   uint32_t epoch = 0;  // tag of the last restore's published key hashes (1..65535)
   uint32_t hash_wait_spins = fdy::kHashWaitSpins;  // fdy_set_group_wait
-  bool timed = false;
+  int timed = 0;  // the mode the last restore was timed in
   hipEvent_t ev[6] = {};
 
   ~fdy_archive() {

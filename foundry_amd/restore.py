@@ -112,8 +112,11 @@ class Archive:
         check(restore_lib().fdy_archive_set_manifest(self._h, data, len(data), arr, C.byref(used)))
         return bool(used.value)
 
-    def set_timing(self, enabled: bool = True) -> None:
-        check(restore_lib().fdy_set_timing(self._h, 1 if enabled else 0))
+    def set_timing(self, enabled: bool = True, phases_only: bool = False) -> None:
+        """Time the following restores with HIP events after every kernel,
+        or (phases_only) only around the grouping + node passes and the diff
+        phase, which leaves the kernels within each phase back to back."""
+        check(restore_lib().fdy_set_timing(self._h, (2 if phases_only else 1) if enabled else 0))
 
     def set_group_wait(self, spins: int) -> None:
         """Rounds of s_sleep the grouping step waits for a lower graph's

@@ -321,7 +321,11 @@ void* fdy_dlpack_view(uint64_t ptr, int32_t device_type, int32_t device_id, int3
                       const int64_t* strides, uint8_t code, uint8_t bits);
 
 /* Timing of the last fdy_restore, from HIP events recorded on its stream
- * around each kernel (milliseconds).  Synchronizes. */
+ * (milliseconds).  Synchronizes.  fdy_set_timing(a, 1) records an event
+ * after every kernel; fdy_set_timing(a, 2) only at the start, between the
+ * grouping + node passes and the diff phase, and at the end, so that no
+ * event's wait for the kernel before it stretches a phase (the per-kernel
+ * fields then read -1); 0 records none. */
 typedef struct fdy_restore_timing {
   float group_ms;   /* key hashes and template assignment */
   float node_ms;    /* per-node compare, layout, and the four digests */
@@ -329,6 +333,8 @@ typedef struct fdy_restore_timing {
   float diff_ms;    /* fused diff + relocate of every other graph's param words */
   float search_ms;  /* interval searches of the words left over by the diff; completed override records in place */
   float total_ms;
+  float prepare_ms;     /* grouping and both node passes */
+  float diff_phase_ms;  /* template, member and search passes */
 } fdy_restore_timing;
 int fdy_restore_timing_get(fdy_archive* a, fdy_restore_timing* out);
 int fdy_set_timing(fdy_archive* a, int enabled);

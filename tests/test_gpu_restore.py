@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 
 import oracle
-from foundry_amd._lib import FoundryError
+from foundry_amd._lib import FoundryError, check, restore_lib
 from foundry_amd.restore import Archive
 
 from foundry_amd import synth
@@ -124,6 +124,34 @@ def test_restore_twice_is_identical(cuda):
     arch.restore()
     for g in range(s.num_graphs):
         np.testing.assert_array_equal(arch.overrides(g), first[g])
+    assert_restore_parity(arch, ref)
+
+
+def test_timed_restores(cuda):
+    """Restores timed after every kernel, or only at the two phases'
+    boundaries, give the same results; each mode's fields add up."""
+    p = synth.preset(2, num_graphs=8, nodes_per_graph=200, num_groups=2)
+    s = synth.SynthArchive(p)
+    arch, ref = gpu_and_oracle(s)
+    with pytest.raises(FoundryError):
+        arch.timing()  # no timed restore yet
+    with pytest.raises(FoundryError):
+        check(restore_lib().fdy_set_timing(arch._h, 3))
+    arch.set_timing(True)
+    arch.restore()
+    t = arch.timing()
+    kernels = ("group_ms", "node_ms", "tmpl_ms", "diff_ms", "search_ms")
+    assert all(t[k] > 0 for k in kernels)
+    assert t["prepare_ms"] == pytest.approx(t["group_ms"] + t["node_ms"], abs=1e-3)
+    assert t["diff_phase_ms"] == pytest.approx(t["tmpl_ms"] + t["diff_ms"] + t["search_ms"], abs=1e-3)
+    arch.set_timing(True, phases_only=True)
+    arch.restore()
+    t = arch.timing()
+    assert all(t[k] == -1.0 for k in kernels)
+    assert t["prepare_ms"] > 0 and t["diff_phase_ms"] > 0
+    assert t["total_ms"] == pytest.approx(t["prepare_ms"] + t["diff_phase_ms"], abs=1e-3)
+    arch.set_timing(False)
+    arch.restore()
     assert_restore_parity(arch, ref)
 
 
