@@ -30,6 +30,15 @@ def _u64(a) -> np.ndarray:
     return np.ascontiguousarray(np.asarray(a, dtype=np.uint64))
 
 
+def _table(lo, hi, new_lo):
+    """An interval table as three contiguous u64 arrays of one length (the
+    library reads n entries of each)."""
+    lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+    if not (lo.ndim == hi.ndim == new_lo.ndim == 1 and len(lo) == len(hi) == len(new_lo)):
+        raise ValueError("lo, hi and new_lo must be 1-D with one entry per interval")
+    return lo, hi, new_lo
+
+
 class Archive:
     """A set of `.cugraph` archives resident in HBM, and their restore state."""
 
@@ -83,7 +92,7 @@ class Archive:
 
     # ---- configuration ---------------------------------------------------
     def set_relocation(self, lo, hi, new_lo, policy: int = _lib.RELOC_HALF_OPEN) -> None:
-        lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+        lo, hi, new_lo = _table(lo, hi, new_lo)
         self._reloc_keep = (lo, hi, new_lo)
         check(
             restore_lib().fdy_archive_set_relocation(
@@ -242,7 +251,8 @@ class RelocPlan:
     """Interval search structure for fdy_relocate_words."""
 
     def __init__(self, lo, hi, new_lo, policy: int = _lib.RELOC_HALF_OPEN):
-        lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
+        self._h = C.c_void_p()
+        lo, hi, new_lo = _table(lo, hi, new_lo)
         h = C.c_void_p()
         check(
             restore_lib().fdy_reloc_plan_create(
@@ -285,9 +295,7 @@ def relocate_words_static(lo, hi, new_lo, d_in: int, d_out: int, n_words: int, p
     """fdy_relocate_words_static: relocate device words by the table (lo, hi,
     new_lo) with no device allocation (the index lives in the library's
     static per-GPU array)."""
-    lo, hi, new_lo = _u64(lo), _u64(hi), _u64(new_lo)
-    if not (len(lo) == len(hi) == len(new_lo)):
-        raise ValueError("lo, hi and new_lo must have one entry per interval")
+    lo, hi, new_lo = _table(lo, hi, new_lo)
     check(restore_lib().fdy_relocate_words_static(lo.ctypes.data_as(_lib.u64p), hi.ctypes.data_as(_lib.u64p),
                                                   new_lo.ctypes.data_as(_lib.u64p), len(lo), policy, d_in, d_out,
                                                   n_words, _stream(stream)))

@@ -4,6 +4,7 @@ import pytest
 
 import oracle
 from foundry_amd import synth
+from foundry_amd._lib import FoundryError
 from foundry_amd.restore import RelocPlan
 
 pytestmark = pytest.mark.gpu
@@ -91,3 +92,41 @@ def test_relocate_full_size_round_trip(cuda):
     idx = slice(12_345_678, 12_345_678 + 200_000)
     want = oracle.relocate_words(np.asarray(words)[idx], lo, hi, nlo, 0, threads=8)
     np.testing.assert_array_equal(d_mid[idx].cpu().numpy().view(np.uint64), want)
+
+
+def test_empty_table_zero_words_and_refused_tables(cuda):
+    """A plan of no intervals leaves every word as it is (the reference's
+    relocation of a pointer outside every interval), a call for zero words
+    writes nothing, and tables that break the interval rules are refused
+    when the plan is made."""
+    print("[case] relocation: empty table, zero words, refused tables", flush=True)
+    rng = np.random.default_rng(5)
+    words = rng.integers(0, 1 << 63, 10_001, dtype=np.uint64) * np.uint64(2) + np.uint64(1)
+    words[:3] = [0, 1, np.uint64((1 << 64) - 1)]
+    empty = np.zeros(0, np.uint64)
+    for policy in (0, 1):
+        plan = RelocPlan(empty, empty, empty, policy)
+        assert plan.lines().shape == (0, 8)
+        d_in = cuda.from_numpy(words.view(np.int64)).to("cuda")
+        d_out = cuda.full_like(d_in, 7)
+        plan.relocate(d_in.data_ptr(), d_out.data_ptr(), 0)
+        cuda.cuda.synchronize()
+        assert (d_out.cpu().numpy() == 7).all()
+        plan.relocate(d_in.data_ptr(), d_out.data_ptr(), len(words))
+        cuda.cuda.synchronize()
+        got = d_out.cpu().numpy().view(np.uint64)
+        np.testing.assert_array_equal(got, words)
+        np.testing.assert_array_equal(got, oracle.relocate_words(words, empty, empty, empty, policy))
+        plan.close()
+    bad = {
+        "overlapping": ([100, 150], [200, 300]),
+        "unsorted": ([300, 100], [400, 200]),
+        "empty interval": ([100, 300], [100, 400]),
+        "ending at 2^64-1": ([100], [(1 << 64) - 1]),
+    }
+    for name, (lo, hi) in bad.items():
+        lo, hi = np.array(lo, np.uint64), np.array(hi, np.uint64)
+        with pytest.raises(FoundryError, match="interval"):
+            RelocPlan(lo, hi, lo)
+    with pytest.raises(FoundryError, match="policy"):
+        RelocPlan(np.array([100], np.uint64), np.array([200], np.uint64), np.array([0], np.uint64), 2)

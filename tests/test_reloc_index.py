@@ -152,3 +152,16 @@ def test_refused_tables(tmp_path):
     stats, _ = _run(tmp_path, np.array([100, 50], np.uint64), np.array([200, 60], np.uint64),
                     np.array([0, 0], np.uint64), np.array([1], np.uint64), 0)
     assert stats == {"error": -1}  # FDY_E_INVALID
+
+
+def test_tables_of_unequal_length_are_refused_before_the_library():
+    """The Python binding checks that lo, hi and new_lo have one entry per
+    interval: the library reads n entries of each."""
+    from foundry_amd.restore import Archive, RelocPlan, relocate_words_static
+    lo, hi = np.array([100, 300], np.uint64), np.array([200, 400], np.uint64)
+    with pytest.raises(ValueError):
+        RelocPlan(lo, hi, np.array([0], np.uint64))
+    with pytest.raises(ValueError):
+        relocate_words_static(lo, hi[:1], lo, 0, 0, 0)
+    with pytest.raises(ValueError):
+        Archive.set_relocation(None, lo, np.zeros((2, 1), np.uint64), lo)
