@@ -45,6 +45,14 @@ class Archive:
     def __init__(self, handle: C.c_void_p, keepalive=None):
         self._h = handle
         self._keep = keepalive
+        self._graphs = None
+
+    def _graph_count(self) -> int:
+        """The archive's graph count (fixed when it is opened): the length of
+        the per-graph arrays the library reads without a length argument."""
+        if self._graphs is None:
+            self._graphs = int(self.info()["num_graphs"])
+        return self._graphs
 
     # ---- opening ---------------------------------------------------------
     @classmethod
@@ -110,12 +118,16 @@ class Archive:
             check(restore_lib().fdy_archive_set_groups(self._h, None))
             return
         t = np.ascontiguousarray(np.asarray(template_of, dtype=np.uint32))
+        if t.ndim != 1 or len(t) != self._graph_count():
+            raise ValueError(f"template_of needs one entry per graph ({self._graph_count()})")
         check(restore_lib().fdy_archive_set_groups(self._h, t.ctypes.data_as(_lib.u32p)))
 
     def set_manifest(self, text, names: Sequence[str]) -> bool:
         """Group by a graph_manifest.json text; False if the reference would
         ignore it (and group by keys)."""
         data = text.encode() if isinstance(text, str) else bytes(text)
+        if len(names) != self._graph_count():
+            raise ValueError(f"set_manifest needs one name per graph ({self._graph_count()})")
         arr = (C.c_char_p * len(names))(*[n.encode() for n in names])
         used = C.c_int()
         check(restore_lib().fdy_archive_set_manifest(self._h, data, len(data), arr, C.byref(used)))

@@ -155,6 +155,23 @@ def test_timed_restores(cuda):
     assert_restore_parity(arch, ref)
 
 
+def test_per_graph_arrays_of_another_length_are_refused(cuda):
+    """fdy_archive_set_groups and fdy_archive_set_manifest read one entry
+    per graph: the binding refuses other lengths before the call, and the
+    archive still restores as before."""
+    p = synth.preset(1, num_graphs=6)
+    s = synth.SynthArchive(p)
+    arch, ref = gpu_and_oracle(s)
+    with pytest.raises(ValueError):
+        arch.set_groups(np.zeros(5, np.uint32))
+    with pytest.raises(ValueError):
+        arch.set_groups(np.zeros((6, 1), np.uint32))
+    with pytest.raises(ValueError):
+        arch.set_manifest("{}", [f"g{i}.json" for i in range(7)])
+    arch.restore()
+    assert_restore_parity(arch, ref)
+
+
 def test_switch_sequence(cuda):
     p = synth.preset(2, num_graphs=16, nodes_per_graph=250, num_groups=2, layout_var_pct=5)
     _print_case("switch", p)
