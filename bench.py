@@ -9,8 +9,12 @@ Prints one JSON line.  `value` is param bytes restored per second of wall
 time (inputs in HBM, K steps between two synchronisations).  `roofline`
 covers the dominant kernel (k_diff_m) from HIP events on the restore
 stream; its `traffic` is the HBM bytes per launch measured with rocprofv3
-counters (see profiles/).  `cpu_baseline` times the oracle (the CPU
-restatement) on the host's cores.
+counters (see profiles/).  `kernels_ms` times each kernel between HIP
+events; `prepare_phase` (grouping and node passes) and `diff_phase`
+(template, member and search passes) are timed with events only at the
+phases' ends, so their kernels run back to back as in an untimed restore,
+each against its algorithmic bytes.  `cpu_baseline` times the oracle (the
+CPU restatement) on the host's cores.
 """
 from __future__ import annotations
 
